@@ -1,0 +1,147 @@
+#!/usr/bin/env python3
+"""Benchmark of the Pet JSON codec on one MI355X.
+
+Headline line (the driver's contract): BASELINE.json configs[1] — flat
+encode of 10M Pets (id, name, status) from SoA columns already resident in
+HBM into one JSON array, records/s.  The same JSON object also carries the
+nested-encode and NDJSON-decode figures under
+"workloads", the roofline of the dominant kernel measured with HIP events on
+the codec's stream, and the CPU restatement timed on this host's cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload flat|nested|decode]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "micronaut3-bug_amd"))
+
+METRIC = "records/s and output GB/s (% of HBM peak) for 10M-Pet encode/decode, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def col_bytes(cols):
+    return cols.input_bytes()
+
+
+def run_encode(codec, cols_dev, fmt, steps, warmup):
+    import torch
+    import petjson as pj
+    need = codec.encode_size(cols_dev, fmt)
+    out = torch.empty(need + 4, dtype=torch.uint8, device="cuda")
+    for _ in range(warmup):
+        codec.encode(cols_dev, fmt, out=out)
+    torch.cuda.synchronize()
+    kern = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        codec.encode(cols_dev, fmt, out=out)
+        kern.append(codec.timings()[-1])     # k_encode, HIP events on the codec stream
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    return need, wall, sum(kern) / len(kern), out
+
+
+def encode_workload(codec, config, n, steps, warmup):
+    import petjson as pj
+    log(f"[bench] generating config {config}, {n} records")
+    cols = pj.generate(config, n)
+    dev = cols.to_device()
+    in_bytes = col_bytes(cols)
+    out_bytes, wall, kms, _ = run_encode(codec, dev, pj.FORMAT_ARRAY, steps, warmup)
+    alg = in_bytes + out_bytes
+    res = {
+        "records": n, "records_per_s": n / wall, "ms_per_step": wall * 1e3,
+        "output_bytes": out_bytes, "input_bytes": in_bytes,
+        "output_GBps": out_bytes / wall / 1e9, "output_frac_hbm": out_bytes / wall / 1e9 / HBM_PEAK_GBPS,
+        "kernel_ms": kms, "kernel_alg_GBps": alg / (kms * 1e-3) / 1e9,
+    }
+    return cols, res
+
+
+def cpu_baseline_encode(cols_full, n_sample, budget_s=10.0):
+    """Oracle (CPU restatement) encode on a bounded sample, one thread."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py as orc
+    import petjson as pj
+    sample = pj.generate(cols_full["_config"], n_sample) if isinstance(cols_full, dict) else None
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.encode(sample, pj.FORMAT_ARRAY)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": n_sample * reps / el, "unit": "records/s", "cores": 1, "kind": "port",
+            "sample": f"{n_sample} records of the same configuration, encoded {reps}x in {el:.1f}s "
+                      f"by oracle/pj_oracle.c (C restatement of the serde/Jackson rules; the reference is "
+                      f"Java and no JVM is available)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="flat", choices=["flat", "nested"])
+    ap.add_argument("--records", type=int, default=10_000_000)
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}); this codec's sharding is described "
+              f"in DESIGN.md and no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import petjson as pj
+    codec = pj.Codec(0)
+    cfg = 2 if a.workload == "flat" else 3
+    cols, head = encode_workload(codec, cfg, a.records, a.steps, a.warmup)
+    workloads = {a.workload + "_encode": head}
+    if not a.no_extra:
+        other = 3 if cfg == 2 else 2
+        _, r = encode_workload(codec, other, a.records, max(3, a.steps // 2), 1)
+        workloads[("nested" if other == 3 else "flat") + "_encode"] = r
+    del cols
+    torch.cuda.empty_cache()
+    cpu = cpu_baseline_encode({"_config": cfg}, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
+    alg = head["input_bytes"] + head["output_bytes"]
+    achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": head["records_per_s"],
+        "unit": "records/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic (seeded generator, BASELINE.json configs)",
+        "config": {"workload": ("configs[1] flat encode" if cfg == 2 else "configs[2] nested encode") +
+                               f", {a.records} Pets, SoA columns in HBM -> JSON array",
+                   "records": a.records, "format": "array"},
+        "output_GBps": head["output_GBps"],
+        "output_frac_hbm": head["output_frac_hbm"],
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "kernel": "k_encode", "kernel_ms": head["kernel_ms"],
+                     "alg_bytes_per_launch": alg},
+        "cpu_baseline": cpu,
+        "workloads": workloads,
+    }
+    print(json.dumps(line), flush=True)
+    codec.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,62 @@
+"""Builds the native libraries of the package in-tree.
+
+* ``libpetjson.so`` — the gfx950 HIP codec behind ``include/petjson.h``
+  (hipcc, ``--offload-arch=gfx950``, packed-FP32 instructions disabled).
+* ``libpjgen.so``  — the seeded synthetic-record generator (host C++).
+
+Usage: ``python micronaut3-bug_amd/build_lib.py`` (always recompiles).
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INC = os.path.join(ROOT, "include")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+HIP_SOURCES = ["pj_api.cpp", "pj_encode.hip", "pj_decode.hip"]
+HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wall", "-Wno-unused-function", f"-I{INC}", f"-I{CSRC}"]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops" not in l and "not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build(verbose=False):
+    objdir = os.path.join(PKG, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, src.replace(".", "_") + ".o")
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        return _run([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj]), obj
+
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        fut_gen = ex.submit(_run, ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-pthread",
+                                   f"-I{INC}", os.path.join(CSRC, "pj_gen.cpp"),
+                                   "-o", os.path.join(PKG, "libpjgen.so")])
+        results = list(ex.map(compile_one, srcs))
+        fut_gen.result()
+    objs = [o for _, o in results]
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs,
+          "-o", os.path.join(PKG, "libpetjson.so")])
+    if verbose:
+        for out, _ in results:
+            if out.strip():
+                print(out)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", os.path.join(PKG, "libpetjson.so"))

@@ -1,0 +1,369 @@
+// pj_api.cpp — the C ABI of libpetjson (include/petjson.h).
+//
+// A context owns one HIP stream on one gfx950 device plus growable device
+// scratch (look-back words, decode index arrays, host-path staging).  Every
+// entry point validates its arguments on the host (shapes the kernels and
+// their grids assume) before launching anything, synchronises its stream
+// before returning, and reports failures as pj_status plus pj_last_error().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "petjson.h"
+#include "pj_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+pj_status fail(pj_status s, const std::string &msg) {
+    g_err = msg;
+    return s;
+}
+
+#define PJ_HIP(call)                                                                      \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess)                                                             \
+            return fail(e_ == hipErrorOutOfMemory ? PJ_ERR_OUT_OF_MEMORY : PJ_ERR_DEVICE, \
+                        std::string(#call) + ": " + hipGetErrorString(e_));              \
+    } while (0)
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    hipError_t ensure(size_t want) {
+        if (want <= n) return hipSuccess;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+        size_t sz = std::max<size_t>(want + want / 8, 4096);
+        hipError_t e = hipMalloc(&p, sz);
+        if (e == hipSuccess) n = sz;
+        return e;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+constexpr int MAX_EV = 6;
+
+inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
+
+}  // namespace
+
+struct pj_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    pj_options opt{PJ_INCLUDE_NON_EMPTY, 1};
+    DevBuf scan;        // tickets, totals, look-back words
+    DevBuf index;       // decode: special bitmap, bad flags, line starts
+    DevBuf stage_in;    // host path: input staging
+    DevBuf stage_out;   // host path: output staging
+    uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
+    hipEvent_t ev[MAX_EV] = {};
+    int n_ev = 0;
+    float timings[MAX_EV] = {};
+    int n_timings = 0;
+};
+
+namespace {
+
+pj_status bind(pj_ctx *c) {
+    if (!c) return fail(PJ_ERR_INVALID_ARG, "null context");
+    PJ_HIP(hipSetDevice(c->device));
+    return PJ_OK;
+}
+
+pj_status mark(pj_ctx *c) {  // record the next timing event
+    if (c->n_ev < MAX_EV) PJ_HIP(hipEventRecord(c->ev[c->n_ev++], c->stream));
+    return PJ_OK;
+}
+
+pj_status finish_timing(pj_ctx *c) {
+    c->n_timings = 0;
+    if (c->n_ev >= 2) {
+        PJ_HIP(hipEventSynchronize(c->ev[c->n_ev - 1]));
+        float ms = 0;
+        PJ_HIP(hipEventElapsedTime(&ms, c->ev[0], c->ev[c->n_ev - 1]));
+        c->timings[c->n_timings++] = ms;
+        for (int k = 1; k < c->n_ev && c->n_timings < MAX_EV; k++) {
+            PJ_HIP(hipEventElapsedTime(&ms, c->ev[k - 1], c->ev[k]));
+            c->timings[c->n_timings++] = ms;
+        }
+    }
+    return PJ_OK;
+}
+
+bool nested_cols(const pj_pet_columns *c) { return c->cat_id || c->photo_off || c->tag_off; }
+
+pj_status check_enc_cols(const pj_pet_columns *c) {
+    if (c->n_pets == 0) return PJ_OK;
+    if (!c->name_off || !c->name_bytes) return fail(PJ_ERR_INVALID_ARG, "name_off / name_bytes required");
+    if (!c->id && (!c->flags)) return fail(PJ_ERR_INVALID_ARG, "id column NULL requires a flags column");
+    if (c->cat_id && (!c->cat_name_off || !c->cat_name_bytes))
+        return fail(PJ_ERR_INVALID_ARG, "category group incomplete");
+    if (c->photo_off && (!c->url_off || !c->url_bytes)) return fail(PJ_ERR_INVALID_ARG, "photoUrls group incomplete");
+    if (c->tag_off && (!c->tag_id || !c->tag_name_off || !c->tag_name_bytes))
+        return fail(PJ_ERR_INVALID_ARG, "tags group incomplete");
+    if (c->n_pets > (1ull << 40)) return fail(PJ_ERR_INVALID_ARG, "too many records");
+    return PJ_OK;
+}
+
+pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t cap,
+                      uint64_t *out_len, bool count_only) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    if (!count_only && cap > 0 && !out) return fail(PJ_ERR_INVALID_ARG, "null output with capacity");
+    if ((s = check_enc_cols(cols))) return s;
+    ctx->n_ev = 0;
+    const uint64_t n = cols->n_pets;
+    if (n == 0) {
+        uint64_t len = format == PJ_FORMAT_ARRAY ? 2 : 0;
+        *out_len = len;
+        if (!count_only && len && len <= cap) {
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(pj_launch_put_bytes(out, '[' | (']' << 8), 2, ctx->stream));
+            if ((s = mark(ctx))) return s;
+        }
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if ((s = finish_timing(ctx))) return s;
+        return len > cap && !count_only ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
+    }
+    const uint64_t nblk = (n + 255) / 256;
+    PJ_HIP(ctx->scan.ensure((nblk + 2) * sizeof(uint64_t)));
+    uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p);
+    EncParams P;
+    std::memset(&P, 0, sizeof P);
+    P.c = *cols;
+    P.n = n;
+    P.format = format;
+    P.incl = ctx->opt.inclusion;
+    P.hexa = ctx->opt.hex_upper ? 'A' : 'a';
+    P.count_only = count_only ? 1 : 0;
+    P.out = out;
+    P.cap = count_only ? 0 : cap;
+    P.ticket = reinterpret_cast<unsigned long long *>(sc);
+    P.total = sc + 1;
+    P.state = sc + 2;
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(hipMemcpyAsync(ctx->pinned, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if ((s = finish_timing(ctx))) return s;
+    *out_len = ctx->pinned[0];
+    if (!count_only && *out_len > cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    return PJ_OK;
+}
+
+// ---------------------------------------------------------- host staging
+struct Layout {  // byte offsets of each column inside one staging buffer
+    uint64_t off[17];
+    uint64_t size[17];
+    uint64_t total;
+};
+
+// Column sizes implied by a host column set (offset arrays give the counts).
+void host_layout(const pj_pet_columns *c, Layout *L) {
+    const uint64_t n = c->n_pets;
+    uint64_t nu = c->photo_off ? c->photo_off[n] : 0, nt = c->tag_off ? c->tag_off[n] : 0;
+    uint64_t sz[17] = {
+        c->id ? n * 8 : 0,
+        c->flags ? n : 0,
+        c->status ? n : 0,
+        c->name_off ? (n + 1) * 8 : 0,
+        c->name_bytes ? c->name_off[n] : 0,
+        c->cat_id ? n * 8 : 0,
+        c->cat_flags ? n : 0,
+        c->cat_name_off ? (n + 1) * 8 : 0,
+        c->cat_name_bytes ? c->cat_name_off[n] : 0,
+        c->photo_off ? (n + 1) * 8 : 0,
+        c->url_off ? (nu + 1) * 8 : 0,
+        c->url_bytes ? c->url_off[nu] : 0,
+        c->tag_off ? (n + 1) * 8 : 0,
+        c->tag_id ? nt * 8 : 0,
+        c->tag_flags ? nt : 0,
+        c->tag_name_off ? (nt + 1) * 8 : 0,
+        c->tag_name_bytes ? c->tag_name_off[nt] : 0,
+    };
+    uint64_t o = 0;
+    for (int k = 0; k < 17; k++) {
+        L->off[k] = o;
+        L->size[k] = sz[k];
+        o += align256(sz[k] + 4);  // +4: aligned-dword reads may touch the tail
+    }
+    L->total = o;
+}
+
+void **col_ptrs(pj_pet_columns *c, void **v) {
+    void *src[17] = {c->id, c->flags, c->status, c->name_off, c->name_bytes, c->cat_id, c->cat_flags,
+                     c->cat_name_off, c->cat_name_bytes, c->photo_off, c->url_off, c->url_bytes,
+                     c->tag_off, c->tag_id, c->tag_flags, c->tag_name_off, c->tag_name_bytes};
+    std::memcpy(v, src, sizeof src);
+    return v;
+}
+
+void set_col_ptrs(pj_pet_columns *c, void *const *v) {
+    c->id = (int64_t *)v[0]; c->flags = (uint8_t *)v[1]; c->status = (uint8_t *)v[2];
+    c->name_off = (uint64_t *)v[3]; c->name_bytes = (uint8_t *)v[4]; c->cat_id = (int64_t *)v[5];
+    c->cat_flags = (uint8_t *)v[6]; c->cat_name_off = (uint64_t *)v[7]; c->cat_name_bytes = (uint8_t *)v[8];
+    c->photo_off = (uint64_t *)v[9]; c->url_off = (uint64_t *)v[10]; c->url_bytes = (uint8_t *)v[11];
+    c->tag_off = (uint64_t *)v[12]; c->tag_id = (int64_t *)v[13]; c->tag_flags = (uint8_t *)v[14];
+    c->tag_name_off = (uint64_t *)v[15]; c->tag_name_bytes = (uint8_t *)v[16];
+}
+
+}  // namespace
+
+// ===================================================================== ABI
+extern "C" {
+
+const char *pj_last_error(void) { return g_err.c_str(); }
+
+void pj_default_options(pj_options *o) {
+    if (!o) return;
+    o->inclusion = PJ_INCLUDE_NON_EMPTY;
+    o->hex_upper = 1;
+}
+
+pj_ctx *pj_create(int device, pj_status *status) {
+    auto set = [&](pj_status s) { if (status) *status = s; };
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        g_err = "no HIP device";
+        set(PJ_ERR_NO_DEVICE);
+        return nullptr;
+    }
+    if (device < 0 || device >= n) {
+        g_err = "device index out of range";
+        set(PJ_ERR_INVALID_ARG);
+        return nullptr;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess || std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_err = std::string("libpetjson is built for gfx950; device is ") + prop.gcnArchName;
+        set(PJ_ERR_NO_DEVICE);
+        return nullptr;
+    }
+    pj_ctx *c = new pj_ctx();
+    c->device = device;
+    bool ok = hipSetDevice(device) == hipSuccess && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) == hipSuccess &&
+              hipHostMalloc((void **)&c->pinned, 64 * sizeof(uint64_t), hipHostMallocDefault) == hipSuccess;
+    for (int k = 0; ok && k < MAX_EV; k++) ok = hipEventCreate(&c->ev[k]) == hipSuccess;
+    if (!ok) {
+        g_err = "context set-up failed";
+        pj_destroy(c);
+        set(PJ_ERR_DEVICE);
+        return nullptr;
+    }
+    set(PJ_OK);
+    return c;
+}
+
+void pj_destroy(pj_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    c->scan.release();
+    c->index.release();
+    c->stage_in.release();
+    c->stage_out.release();
+    for (auto &e : c->ev) if (e) (void)hipEventDestroy(e);
+    if (c->pinned) (void)hipHostFree(c->pinned);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+pj_status pj_set_options(pj_ctx *c, const pj_options *o) {
+    if (!c || !o) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (o->inclusion < PJ_INCLUDE_NON_EMPTY || o->inclusion > PJ_INCLUDE_ALWAYS)
+        return fail(PJ_ERR_INVALID_ARG, "bad inclusion mode");
+    c->opt = *o;
+    c->opt.hex_upper = o->hex_upper ? 1 : 0;
+    return PJ_OK;
+}
+
+int pj_last_timings(const pj_ctx *c, float *ms, int cap) {
+    if (!c || !ms) return 0;
+    int k = std::min(cap, c->n_timings);
+    for (int i = 0; i < k; i++) ms[i] = c->timings[i];
+    return k;
+}
+
+pj_status pj_encode_device(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t out_cap,
+                           uint64_t *out_len) {
+    return encode_impl(ctx, cols, format, out, out_cap, out_len, false);
+}
+
+pj_status pj_encode_size_device(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint64_t *out_len) {
+    return encode_impl(ctx, cols, format, nullptr, 0, out_len, true);
+}
+
+pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t out_cap,
+                         uint64_t *out_len) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (cols->n_pets && (s = check_enc_cols(cols))) return s;
+    Layout L;
+    host_layout(cols, &L);
+    PJ_HIP(ctx->stage_in.ensure(L.total));
+    uint8_t *base = static_cast<uint8_t *>(ctx->stage_in.p);
+    void *hp[17], *dp[17];
+    pj_pet_columns hc = *cols, dc = *cols;
+    col_ptrs(&hc, hp);
+    for (int k = 0; k < 17; k++) {
+        dp[k] = hp[k] ? base + L.off[k] : nullptr;
+        if (hp[k] && L.size[k])
+            PJ_HIP(hipMemcpyAsync(dp[k], hp[k], L.size[k], hipMemcpyHostToDevice, ctx->stream));
+    }
+    set_col_ptrs(&dc, dp);
+    uint64_t need = 0;
+    if ((s = pj_encode_size_device(ctx, &dc, format, &need))) return s;
+    *out_len = need;
+    if (need > out_cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    if (need == 0) return PJ_OK;
+    if (!out) return fail(PJ_ERR_INVALID_ARG, "null output");
+    PJ_HIP(ctx->stage_out.ensure(need + 4));
+    uint64_t got = 0;
+    if ((s = pj_encode_device(ctx, &dc, format, static_cast<uint8_t *>(ctx->stage_out.p), need, &got))) return s;
+    PJ_HIP(hipMemcpyAsync(out, ctx->stage_out.p, got, hipMemcpyDeviceToHost, ctx->stream));
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    *out_len = got;
+    return PJ_OK;
+}
+
+void pj_decode_bounds(uint64_t len, pj_pet_columns *c) {
+    if (!c) return;
+    // a valid record needs at least {"name":"","photoUrls":[]} (26 bytes) + '\n'
+    c->cap_pets = len / 27 + 1;
+    c->cap_name_bytes = len;
+    c->cap_cat_name_bytes = len;
+    c->cap_urls = len / 3 + 1;      // each url needs "" and a separator
+    c->cap_url_bytes = len;
+    c->cap_tags = len / 3 + 1;      // each tag needs {} and a separator
+    c->cap_tag_name_bytes = len;
+}
+
+}  // extern "C"
+
+extern "C" pj_status pj_decode_device(pj_ctx *ctx, const uint8_t *, uint64_t, pj_pet_columns *, uint64_t *,
+                                      uint8_t *, uint64_t, pj_decode_result *) {
+    pj_status s = bind(ctx);
+    return s ? s : fail(PJ_ERR_DEVICE, "decode kernels not built");
+}
+extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *, uint64_t, pj_pet_columns *, uint64_t *,
+                                    uint8_t *, uint64_t, pj_decode_result *) {
+    pj_status s = bind(ctx);
+    return s ? s : fail(PJ_ERR_DEVICE, "decode kernels not built");
+}

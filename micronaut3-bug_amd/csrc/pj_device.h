@@ -1,0 +1,133 @@
+// pj_device.h — device helpers shared by the encode and decode kernels
+// (gfx950, wave64).  Block-wide scans, the decoupled look-back used to chain
+// workgroups in a single pass, and SWAR byte classification.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define PJ_BLOCK 256
+#define PJ_WAVES (PJ_BLOCK / 64)
+
+namespace pj {
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    lo = (uint32_t)__shfl_up((int)lo, (unsigned)d, 64);
+    hi = (uint32_t)__shfl_up((int)hi, (unsigned)d, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    lo = (uint32_t)__shfl((int)lo, src, 64);
+    hi = (uint32_t)__shfl((int)hi, src, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    lo = (uint32_t)__shfl_xor((int)lo, m, 64);
+    hi = (uint32_t)__shfl_xor((int)hi, m, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Inclusive wave scan (sum) of 64-bit values.
+__device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
+    const int l = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        uint64_t t = shfl_up_u64(v, d);
+        if (l >= d) v += t;
+    }
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_sum(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_u64(v, m);
+    return v;
+}
+
+// Block-wide exclusive scan of one 64-bit value per thread (all PJ_BLOCK
+// threads must call).  Returns the exclusive prefix; *total gets the block sum.
+// `sh` needs PJ_WAVES+1 entries of LDS.
+__device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t *sh, uint64_t *total) {
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    uint64_t inc = wave_incl_scan(v);
+    if (l == 63) sh[w] = inc;
+    __syncthreads();
+    uint64_t before = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < PJ_WAVES; k++) {
+        uint64_t s = sh[k];
+        before += (k < w) ? s : 0;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return before + inc - v;
+}
+
+// ----------------------------------------------------------- look-back
+// One 64-bit word per logical block: bits 63:62 = state, 61:0 = value.
+constexpr uint64_t LB_AGG = 1ull << 62;
+constexpr uint64_t LB_PRE = 2ull << 62;
+constexpr uint64_t LB_VAL = (1ull << 62) - 1;
+
+__device__ __forceinline__ void lb_store(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by ONE full wave of logical block `b` after the block aggregate is
+// known.  Publishes the aggregate, walks predecessors 64 at a time and
+// returns the exclusive prefix (identical in every lane); publishes the
+// inclusive prefix.  Predecessors hold smaller tickets, so they are resident
+// and the spin always ends.
+__device__ __forceinline__ uint64_t lookback(uint64_t *state, uint64_t b, uint64_t agg) {
+    const int l = lane_id();
+    if (b == 0) {
+        if (l == 0) lb_store(&state[0], LB_PRE | agg);
+        return 0;
+    }
+    if (l == 0) lb_store(&state[b], LB_AGG | agg);
+    uint64_t excl = 0;
+    int64_t j = (int64_t)b - 1;
+    for (;;) {
+        int64_t idx = j - l;
+        uint64_t s = idx >= 0 ? lb_load(&state[idx]) : LB_PRE;
+        uint32_t fl = (uint32_t)(s >> 62);
+        uint64_t notready = __ballot(fl == 0);
+        uint64_t isp = __ballot(fl == 2);
+        int fp = isp ? __builtin_ctzll(isp) : 64;
+        uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1);
+        if (notready & need) { __builtin_amdgcn_s_sleep(1); continue; }
+        excl += wave_sum(l <= fp ? (s & LB_VAL) : 0);
+        if (fp < 64) break;
+        j -= 64;
+    }
+    if (l == 0) lb_store(&state[b], LB_PRE | (excl + agg));
+    return excl;
+}
+
+// ----------------------------------------------------------- SWAR bytes
+// Nonzero iff some byte of x is < 0x20 (exact as an "any" test).
+__device__ __forceinline__ uint32_t any_lt20(uint32_t x) { return (x - 0x20202020u) & ~x & 0x80808080u; }
+__device__ __forceinline__ uint32_t any_zero(uint32_t x) { return (x - 0x01010101u) & ~x & 0x80808080u; }
+// Nonzero iff some byte needs a JSON output escape: < 0x20, '"' or '\\'.
+__device__ __forceinline__ uint32_t any_special(uint32_t x) {
+    return any_lt20(x) | any_zero(x ^ 0x22222222u) | any_zero(x ^ 0x5C5C5C5Cu);
+}
+
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p 4-byte aligned
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+
+// Compile-time packing of up to 4 literal bytes (little endian).
+constexpr uint32_t pack4(const char *s, int k) {
+    return (k > 0 ? (uint32_t)(uint8_t)s[0] : 0u) | (k > 1 ? (uint32_t)(uint8_t)s[1] << 8 : 0u) |
+           (k > 2 ? (uint32_t)(uint8_t)s[2] << 16 : 0u) | (k > 3 ? (uint32_t)(uint8_t)s[3] << 24 : 0u);
+}
+
+}  // namespace pj

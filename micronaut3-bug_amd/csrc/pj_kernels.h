@@ -1,0 +1,49 @@
+// pj_kernels.h — kernel parameter blocks and launchers (host <-> device).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "petjson.h"
+
+struct EncParams {
+    pj_pet_columns c;          // device column pointers
+    uint64_t n;                // records
+    int format;                // pj_format
+    int incl;                  // pj_inclusion
+    uint32_t hexa;             // 'A' or 'a': first letter of hex escapes
+    int count_only;            // 1: length pass only
+    uint8_t *out;
+    uint64_t cap;
+    uint64_t *state;           // look-back words, one per block (zeroed)
+    unsigned long long *ticket;// logical block counter (zeroed)
+    uint64_t *total;           // encoded size (written by the last block)
+};
+
+struct DecParams {
+    const uint8_t *in;
+    uint64_t len;
+    uint64_t nblk64;           // number of 64-byte blocks
+    // index stage outputs
+    uint64_t *special;         // [nblk64] unescaped quotes | backslashes
+    uint8_t *bad;              // [nblk64] 1 = string-content fault in block
+    uint64_t *line_start;      // [n_lines+1]
+    uint64_t *n_lines;         // device scalar
+    // parse stage
+    pj_pet_columns o;          // outputs with capacities
+    uint64_t *err_line;
+    uint8_t *err_code;
+    uint64_t err_cap;
+    uint64_t *totals;          // [PJ_DEC_NCNT] column totals (written by last block)
+    uint64_t *state_idx;       // look-back words of the index stage
+    uint64_t *state_parse;     // look-back words of the parse stage, PJ_DEC_NCNT per block
+    unsigned long long *tickets; // [2]
+    uint64_t lines;            // n_lines as known by the host for the parse stage
+};
+
+// counters carried through the parse-stage scan
+enum { C_PETS = 0, C_NAMEB, C_CATB, C_URLS, C_URLB, C_TAGS, C_TAGB, C_ERRS, PJ_DEC_NCNT };
+
+hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);
+hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st);
+hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
+hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
+hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);

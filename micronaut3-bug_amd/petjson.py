@@ -1,0 +1,356 @@
+"""ctypes binding of libpetjson (include/petjson.h) and of the record generator.
+
+Host columns are numpy arrays; device columns are torch tensors on the
+context's GPU (torch is only the device allocator here).  The product path
+always runs the gfx950 kernels of libpetjson.so: when that library is missing
+or no gfx950 device is present the calls raise, they never fall back to CPU.
+
+Reference interface mirrored: io.micronaut.serde.ObjectMapper
+(reference src/main/java/com/micronaut/bug/config/MyEntityConfig.java:8,34 and
+service/MyEntityService.java:45) — see ``mapper.py`` for the object surface.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT_DIR = os.path.dirname(PKG_DIR)
+
+# ----------------------------------------------------------------- constants
+PJ_OK, PJ_ERR_INVALID_ARG, PJ_ERR_CAPACITY, PJ_ERR_DEVICE, PJ_ERR_NO_DEVICE, PJ_ERR_OUT_OF_MEMORY = range(6)
+STATUS_NAMES = {0: "PJ_OK", 1: "PJ_ERR_INVALID_ARG", 2: "PJ_ERR_CAPACITY", 3: "PJ_ERR_DEVICE",
+                4: "PJ_ERR_NO_DEVICE", 5: "PJ_ERR_OUT_OF_MEMORY"}
+FORMAT_ARRAY, FORMAT_NDJSON = 0, 1
+INCLUDE_NON_EMPTY, INCLUDE_NON_NULL, INCLUDE_ALWAYS = 0, 1, 2
+STATUS_AVAILABLE, STATUS_PENDING, STATUS_SOLD, STATUS_NULL = 0, 1, 2, 255
+PET_HAS_ID, PET_HAS_CATEGORY, PET_HAS_NAME, PET_HAS_PHOTOURLS, PET_HAS_TAGS = 1, 2, 4, 8, 16
+PET_DEFAULT_FLAGS = PET_HAS_ID | PET_HAS_NAME | PET_HAS_PHOTOURLS
+SUB_HAS_ID, SUB_HAS_NAME = 1, 2
+SUB_DEFAULT_FLAGS = SUB_HAS_ID | SUB_HAS_NAME
+REC_OK, REC_SYNTAX, REC_STRING, REC_NUMBER, REC_TYPE, REC_MISSING_NAME, REC_MISSING_PHOTOURLS, \
+    REC_BAD_STATUS, REC_DEPTH, REC_EMPTY = range(10)
+MAX_DEPTH = 1000
+SEED_BASE = 0x5EED0000
+
+COLS = ["id", "flags", "status", "name_off", "name_bytes", "cat_id", "cat_flags", "cat_name_off",
+        "cat_name_bytes", "photo_off", "url_off", "url_bytes", "tag_off", "tag_id", "tag_flags",
+        "tag_name_off", "tag_name_bytes"]
+DTYPES = {"id": np.int64, "flags": np.uint8, "status": np.uint8, "name_off": np.uint64,
+          "name_bytes": np.uint8, "cat_id": np.int64, "cat_flags": np.uint8, "cat_name_off": np.uint64,
+          "cat_name_bytes": np.uint8, "photo_off": np.uint64, "url_off": np.uint64, "url_bytes": np.uint8,
+          "tag_off": np.uint64, "tag_id": np.int64, "tag_flags": np.uint8, "tag_name_off": np.uint64,
+          "tag_name_bytes": np.uint8}
+CAPS = ["cap_pets", "cap_name_bytes", "cap_cat_name_bytes", "cap_urls", "cap_url_bytes", "cap_tags",
+        "cap_tag_name_bytes"]
+
+
+class PetColumnsStruct(C.Structure):
+    _fields_ = [("n_pets", C.c_uint64)] + [(n, C.c_void_p) for n in COLS] + [(n, C.c_uint64) for n in CAPS]
+
+
+class Options(C.Structure):
+    _fields_ = [("inclusion", C.c_int32), ("hex_upper", C.c_int32)]
+
+
+class DecodeResult(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("n_lines", "n_pets", "n_errors", "name_bytes", "cat_name_bytes",
+                                          "n_urls", "url_bytes", "n_tags", "tag_name_bytes")]
+
+
+class PetJsonError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+# -------------------------------------------------------------------- loader
+_LIB = None
+_GEN = None
+
+EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "pj_last_error",
+           "pj_last_timings", "pj_encode_device", "pj_encode_size_device", "pj_encode_host",
+           "pj_decode_device", "pj_decode_host", "pj_decode_bounds"]
+
+
+def lib_path() -> str:
+    return os.path.join(PKG_DIR, "libpetjson.so")
+
+
+def load_lib():
+    """Load libpetjson.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        p = lib_path()
+        if not os.path.exists(p):
+            raise FileNotFoundError(f"{p} missing: run __graft_entry__.build() (no CPU fallback exists)")
+        L = C.CDLL(p)
+        vp, u64, i32 = C.c_void_p, C.c_uint64, C.c_int
+        L.pj_create.restype = vp
+        L.pj_create.argtypes = [i32, C.POINTER(i32)]
+        L.pj_destroy.argtypes = [vp]
+        L.pj_default_options.argtypes = [C.POINTER(Options)]
+        L.pj_set_options.argtypes = [vp, C.POINTER(Options)]
+        L.pj_set_options.restype = i32
+        L.pj_last_error.restype = C.c_char_p
+        L.pj_last_timings.argtypes = [vp, C.POINTER(C.c_float), i32]
+        L.pj_last_timings.restype = i32
+        for f in ("pj_encode_device", "pj_encode_host"):
+            getattr(L, f).argtypes = [vp, C.POINTER(PetColumnsStruct), i32, vp, u64, C.POINTER(u64)]
+            getattr(L, f).restype = i32
+        L.pj_encode_size_device.argtypes = [vp, C.POINTER(PetColumnsStruct), i32, C.POINTER(u64)]
+        L.pj_encode_size_device.restype = i32
+        for f in ("pj_decode_device", "pj_decode_host"):
+            getattr(L, f).argtypes = [vp, vp, u64, C.POINTER(PetColumnsStruct), vp, vp, u64,
+                                      C.POINTER(DecodeResult)]
+            getattr(L, f).restype = i32
+        L.pj_decode_bounds.argtypes = [u64, C.POINTER(PetColumnsStruct)]
+        _LIB = L
+    return _LIB
+
+
+def load_gen():
+    global _GEN
+    if _GEN is None:
+        p = os.path.join(PKG_DIR, "libpjgen.so")
+        if not os.path.exists(p):
+            raise FileNotFoundError(f"{p} missing: run __graft_entry__.build()")
+        G = C.CDLL(p)
+        G.pjg_generate.argtypes = [C.c_int, C.c_uint64, C.c_uint64, C.c_int, C.POINTER(PetColumnsStruct)]
+        G.pjg_generate.restype = C.c_int
+        G.pjg_free.argtypes = [C.POINTER(PetColumnsStruct)]
+        G.pjg_corrupt_ndjson.argtypes = [C.c_void_p, C.c_uint64, C.c_uint64, C.c_double, C.c_void_p,
+                                         C.c_void_p, C.c_uint64]
+        G.pjg_corrupt_ndjson.restype = C.c_uint64
+        _GEN = G
+    return _GEN
+
+
+# ------------------------------------------------------------------- columns
+def _ptr(a) -> Optional[int]:
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()  # torch tensor
+
+
+def _len(a) -> int:
+    return 0 if a is None else (a.shape[0] if isinstance(a, np.ndarray) else a.numel())
+
+
+@dataclass
+class Columns:
+    """SoA Pet columns (numpy on the host or torch tensors on a GPU).  A
+    missing group is None, with the meaning given in include/petjson.h."""
+    n_pets: int
+    arrays: Dict[str, object] = field(default_factory=dict)
+    caps: Dict[str, int] = field(default_factory=dict)
+    # logical lengths of device arrays that carry tail padding
+    lengths: Dict[str, int] = field(default_factory=dict)
+
+    def __getitem__(self, k):
+        v = self.arrays.get(k)
+        if v is not None and k in self.lengths:
+            v = v[: self.lengths[k]]
+        return v
+
+    def struct(self) -> PetColumnsStruct:
+        s = PetColumnsStruct()
+        s.n_pets = self.n_pets
+        for n in COLS:
+            setattr(s, n, _ptr(self.arrays.get(n)))
+        for n in CAPS:
+            setattr(s, n, int(self.caps.get(n, 0)))
+        return s
+
+    def to_device(self, device="cuda"):
+        import torch
+
+        def up(v):
+            # never a zero-size allocation (its data pointer would be NULL,
+            # which means "column group absent"), plus a few tail bytes
+            v = np.ascontiguousarray(v)
+            pad = max(1, 8 // v.itemsize)
+            buf = torch.empty(v.shape[0] + pad, dtype=torch.from_numpy(v[:0]).dtype, device=device)
+            if v.shape[0]:
+                buf[: v.shape[0]].copy_(torch.from_numpy(v))
+            return buf
+
+        arr, lens = {}, {}
+        for k in self.arrays:
+            v = self[k]
+            arr[k] = up(v) if v is not None else None
+            if v is not None:
+                lens[k] = v.shape[0]
+        return Columns(self.n_pets, arr, dict(self.caps), lens)
+
+    def to_host(self):
+        arr = {}
+        for k in self.arrays:
+            v = self[k]
+            arr[k] = v if isinstance(v, np.ndarray) or v is None else v.cpu().numpy()
+        return Columns(self.n_pets, arr, dict(self.caps))
+
+    # sizes implied by the offset arrays
+    def sizes(self):
+        h = self.to_host()
+        n = self.n_pets
+        get = lambda k, i: int(h.arrays[k][i]) if h.arrays.get(k) is not None else 0
+        nu, nt = get("photo_off", n), get("tag_off", n)
+        return {"n_pets": n, "name_bytes": get("name_off", n), "cat_name_bytes": get("cat_name_off", n),
+                "n_urls": nu, "url_bytes": get("url_off", nu) if nu or h.arrays.get("url_off") is not None else 0,
+                "n_tags": nt, "tag_name_bytes": get("tag_name_off", nt) if h.arrays.get("tag_name_off") is not None else 0}
+
+    def input_bytes(self) -> int:
+        """Bytes of all columns an encode reads (algorithmic input bytes)."""
+        tot = 0
+        for k in self.arrays:
+            v = self[k]
+            if v is None:
+                continue
+            tot += v.nbytes if isinstance(v, np.ndarray) else v.numel() * v.element_size()
+        return tot
+
+
+def columns_from_struct(s: PetColumnsStruct, copy=True) -> Columns:
+    """Copy columns described by a host struct into numpy arrays."""
+    n = s.n_pets
+    arrays = {}
+
+    def grab(name, count):
+        p = getattr(s, name)
+        if not p:
+            return None
+        dt = np.dtype(DTYPES[name])
+        if count == 0:
+            return np.zeros(0, dtype=dt)
+        buf = (C.c_uint8 * (count * dt.itemsize)).from_address(p)
+        a = np.frombuffer(buf, dtype=dt, count=count)
+        return a.copy() if copy else a
+
+    for k in ("id", "flags", "status", "cat_id", "cat_flags"):
+        arrays[k] = grab(k, n)
+    for k in ("name_off", "cat_name_off", "photo_off", "tag_off"):
+        arrays[k] = grab(k, n + 1)
+    arrays["name_bytes"] = grab("name_bytes", int(arrays["name_off"][n]) if arrays["name_off"] is not None else 0)
+    arrays["cat_name_bytes"] = grab("cat_name_bytes", int(arrays["cat_name_off"][n]) if arrays["cat_name_off"] is not None else 0)
+    nu = int(arrays["photo_off"][n]) if arrays["photo_off"] is not None else 0
+    nt = int(arrays["tag_off"][n]) if arrays["tag_off"] is not None else 0
+    arrays["url_off"] = grab("url_off", nu + 1)
+    arrays["url_bytes"] = grab("url_bytes", int(arrays["url_off"][nu]) if arrays["url_off"] is not None else 0)
+    arrays["tag_id"] = grab("tag_id", nt)
+    arrays["tag_flags"] = grab("tag_flags", nt)
+    arrays["tag_name_off"] = grab("tag_name_off", nt + 1)
+    arrays["tag_name_bytes"] = grab("tag_name_bytes", int(arrays["tag_name_off"][nt]) if arrays["tag_name_off"] is not None else 0)
+    return Columns(n, arrays)
+
+
+def generate(config: int, n: int, seed: Optional[int] = None, threads: int = 0) -> Columns:
+    """Seeded synthetic records of a benchmark configuration (1..5)."""
+    G = load_gen()
+    s = PetColumnsStruct()
+    if seed is None:
+        seed = SEED_BASE + config
+    rc = G.pjg_generate(config, n, seed, threads, C.byref(s))
+    if rc != 0:
+        raise ValueError(f"pjg_generate({config}, {n}) failed")
+    try:
+        return columns_from_struct(s)
+    finally:
+        G.pjg_free(C.byref(s))
+
+
+def corrupt_ndjson(buf: np.ndarray, seed: int, rate: float):
+    """Corrupt ~rate of the lines of an NDJSON uint8 array in place; returns
+    (line indices, expected codes)."""
+    G = load_gen()
+    cap = max(16, int(len(buf) // 20 * rate * 4) + 16)
+    lines = np.zeros(cap, dtype=np.uint64)
+    codes = np.zeros(cap, dtype=np.uint8)
+    k = G.pjg_corrupt_ndjson(buf.ctypes.data, len(buf), seed, rate, lines.ctypes.data, codes.ctypes.data, cap)
+    if k > cap:
+        raise RuntimeError("corruption list overflow")
+    return lines[:k].copy(), codes[:k].copy()
+
+
+def decode_bounds(length: int) -> Dict[str, int]:
+    s = PetColumnsStruct()
+    load_lib().pj_decode_bounds(length, C.byref(s))
+    return {k: int(getattr(s, k)) for k in CAPS}
+
+
+# --------------------------------------------------------------------- codec
+class Codec:
+    """One libpetjson context (one HIP stream on one gfx950 device)."""
+
+    def __init__(self, device: int = 0, inclusion: int = INCLUDE_NON_EMPTY, hex_upper: bool = True):
+        self.L = load_lib()
+        st = C.c_int(0)
+        self.ctx = self.L.pj_create(device, C.byref(st))
+        if not self.ctx:
+            raise PetJsonError(st.value, self.L.pj_last_error().decode())
+        self.device = device
+        self.set_options(inclusion, hex_upper)
+
+    def close(self):
+        if self.ctx:
+            self.L.pj_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc):
+        if rc != PJ_OK:
+            raise PetJsonError(rc, self.L.pj_last_error().decode())
+
+    def set_options(self, inclusion=INCLUDE_NON_EMPTY, hex_upper=True):
+        o = Options(inclusion, 1 if hex_upper else 0)
+        self._check(self.L.pj_set_options(self.ctx, C.byref(o)))
+
+    def timings(self):
+        buf = (C.c_float * 8)()
+        k = self.L.pj_last_timings(self.ctx, buf, 8)
+        return [buf[i] for i in range(k)]
+
+    # ---- encode
+    def encode_size(self, cols: Columns, fmt: int = FORMAT_ARRAY) -> int:
+        import torch
+        torch.cuda.synchronize()
+        s = cols.struct()
+        n = C.c_uint64(0)
+        self._check(self.L.pj_encode_size_device(self.ctx, C.byref(s), fmt, C.byref(n)))
+        return n.value
+
+    def encode(self, cols: Columns, fmt: int = FORMAT_ARRAY, out=None):
+        """Encode device columns; returns a uint8 torch tensor (a view of `out`
+        when given) holding exactly the JSON bytes."""
+        import torch
+        if out is None:
+            need = self.encode_size(cols, fmt)
+            out = torch.empty(need + 4, dtype=torch.uint8, device=f"cuda:{self.device}")
+        torch.cuda.synchronize()
+        s = cols.struct()
+        n = C.c_uint64(0)
+        cap = out.numel()
+        self._check(self.L.pj_encode_device(self.ctx, C.byref(s), fmt, C.c_void_p(out.data_ptr()), cap, C.byref(n)))
+        return out[: n.value]
+
+    def encode_host(self, cols: Columns, fmt: int = FORMAT_ARRAY) -> bytes:
+        s = cols.struct()
+        n = C.c_uint64(0)
+        rc = self.L.pj_encode_host(self.ctx, C.byref(s), fmt, None, 0, C.byref(n))
+        if rc not in (PJ_OK, PJ_ERR_CAPACITY):
+            self._check(rc)
+        out = np.empty(max(1, n.value), dtype=np.uint8)
+        self._check(self.L.pj_encode_host(self.ctx, C.byref(s), fmt, C.c_void_p(out.ctypes.data), out.size,
+                                          C.byref(n)))
+        return out[: n.value].tobytes()

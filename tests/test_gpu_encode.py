@@ -1,0 +1,115 @@
+"""GPU encode parity: libpetjson (gfx950) output is byte-identical to the CPU
+restatement on the same seeded records, for every configuration, both
+framings and every inclusion option, plus edge cases (empty input, one
+record, misaligned columns, capacity overflow)."""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_py as orc
+import petjson as pj
+from kat_util import load, pet_from_dict
+from model import to_columns
+
+pytestmark = pytest.mark.gpu
+INCL = {"NON_EMPTY": pj.INCLUDE_NON_EMPTY, "NON_NULL": pj.INCLUDE_NON_NULL, "ALWAYS": pj.INCLUDE_ALWAYS}
+
+
+def gpu_encode(codec, cols, fmt, incl=pj.INCLUDE_NON_EMPTY, hex_upper=True):
+    codec.set_options(incl, hex_upper)
+    try:
+        return codec.encode(cols.to_device(), fmt).cpu().numpy().tobytes()
+    finally:
+        codec.set_options()
+
+
+@pytest.mark.parametrize("case", load("encode_kat.json")["cases"], ids=lambda c: c["name"])
+def test_encode_kat_gpu(codec, case):
+    cols = to_columns([pet_from_dict(p) for p in case["pets"]])
+    fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
+    incl = INCL[case.get("inclusion", "NON_EMPTY")]
+    hx = case.get("hex_upper", True)
+    assert gpu_encode(codec, cols, fmt, incl, hx) == case["expected"].encode("utf-8")
+    codec.set_options(incl, hx)
+    assert codec.encode_host(cols, fmt) == case["expected"].encode("utf-8")
+    codec.set_options()
+
+
+@pytest.mark.parametrize("config,n", [(1, 100_000), (2, 200_000), (3, 100_000), (5, 20_000)])
+@pytest.mark.parametrize("fmt", [pj.FORMAT_ARRAY, pj.FORMAT_NDJSON])
+def test_encode_configs_match_oracle(codec, config, n, fmt):
+    print(f"[encode parity] config={config} n={n} fmt={fmt}", flush=True)
+    cols = pj.generate(config, n)
+    assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
+
+
+@pytest.mark.parametrize("incl", [pj.INCLUDE_NON_NULL, pj.INCLUDE_ALWAYS])
+def test_encode_inclusion_options_match_oracle(codec, incl):
+    cols = pj.generate(3, 30_000)
+    # knock out some fields so that nulls / empties occur
+    rng = np.random.default_rng(1)
+    cols.arrays["flags"] = cols["flags"] & rng.integers(0, 32, cols.n_pets, dtype=np.uint8) | pj.PET_HAS_NAME
+    cols.arrays["status"][rng.random(cols.n_pets) < 0.2] = pj.STATUS_NULL
+    cols.arrays["tag_flags"] = rng.integers(0, 4, cols["tag_flags"].shape[0], dtype=np.uint8)
+    assert gpu_encode(codec, cols, pj.FORMAT_ARRAY, incl, False) == \
+        orc.encode(cols, pj.FORMAT_ARRAY, incl, False)
+
+
+def test_encode_misaligned_string_columns(codec):
+    cols = pj.generate(3, 5000)
+    for shift in (1, 2, 3):
+        c2 = pj.Columns(cols.n_pets, dict(cols.arrays))
+        for k in ("name_bytes", "cat_name_bytes", "url_bytes", "tag_name_bytes"):
+            pad = np.concatenate([np.full(shift, 0x41, np.uint8), cols[k]])
+            c2.arrays[k] = pad
+        for k, kb in (("name_off", "name_bytes"), ("cat_name_off", "cat_name_bytes"), ("url_off", "url_bytes"),
+                      ("tag_name_off", "tag_name_bytes")):
+            c2.arrays[k] = cols[k] + np.uint64(shift)
+        assert gpu_encode(codec, c2, pj.FORMAT_ARRAY) == orc.encode(cols, pj.FORMAT_ARRAY)
+
+
+def test_encode_long_strings_and_all_bytes(codec):
+    big = bytes(range(256)) * 70 + b"x" * 3
+    pets = [pet_from_dict({"name": "n", "photoUrls": []})]
+    p = pets[0]
+    p.name = big
+    p.photo_urls = [big[: k] for k in range(0, 64)]
+    cols = to_columns(pets * 3)
+    assert gpu_encode(codec, cols, pj.FORMAT_NDJSON) == orc.encode(cols, pj.FORMAT_NDJSON)
+
+
+def test_encode_empty_and_single(codec):
+    cols = to_columns([])
+    assert gpu_encode(codec, cols, pj.FORMAT_ARRAY) == b"[]"
+    assert gpu_encode(codec, cols, pj.FORMAT_NDJSON) == b""
+    cols = pj.generate(3, 1)
+    assert gpu_encode(codec, cols, pj.FORMAT_ARRAY) == orc.encode(cols, pj.FORMAT_ARRAY)
+
+
+def test_encode_capacity_guard(codec):
+    cols = pj.generate(2, 10_000)
+    d = cols.to_device()
+    need = codec.encode_size(d, pj.FORMAT_ARRAY)
+    out = torch.full((need,), 0xEE, dtype=torch.uint8, device="cuda")
+    cap = need // 2
+    with pytest.raises(pj.PetJsonError) as ei:
+        codec.encode(d, pj.FORMAT_ARRAY, out=out[:cap])
+    assert ei.value.status == pj.PJ_ERR_CAPACITY
+    host = out.cpu().numpy()
+    assert (host[cap:] == 0xEE).all()          # nothing past the capacity
+    ref = np.frombuffer(orc.encode(cols, pj.FORMAT_ARRAY), np.uint8)
+    written = host[:cap] != 0xEE
+    assert (host[:cap][written] == ref[:cap][written]).all()
+
+
+@pytest.mark.parametrize("config", [2, 3])
+def test_encode_full_size_matches_oracle(codec, config):
+    """10M records (benchmark size): byte-identical to the CPU restatement."""
+    print(f"[encode full] config={config}", flush=True)
+    cols = pj.generate(config, 10_000_000)
+    gpu = codec.encode(cols.to_device(), pj.FORMAT_ARRAY).cpu().numpy()
+    ref = orc.encode(cols, pj.FORMAT_ARRAY)
+    assert gpu.size == len(ref)
+    assert hashlib.sha256(gpu.tobytes()).hexdigest() == hashlib.sha256(ref).hexdigest()

@@ -1,0 +1,142 @@
+"""Pins the CPU restatement (oracle/) before it is trusted as the checker.
+
+Each check is chosen so that a plausible mistake fails it:
+* hand-written known-answer vectors, one per rule (tests/golden/*.json);
+* Long.toString brute-forced against Python's int formatting;
+* string escaping cross-checked against Python's json module (a library
+  routine for the RFC 8259 grammar; it writes \\u00xx in lower case, so that
+  case is normalised);
+* decoded values cross-checked against json.loads on valid records;
+* decode(encode(x)) == x on generated records of every configuration.
+"""
+import json
+import random
+import re
+
+import numpy as np
+import pytest
+
+import oracle_py as orc
+import petjson as pj
+from kat_util import expected_pet, line_bytes, load, norm_pet, pet_from_dict
+from model import from_columns, to_columns
+
+INCL = {"NON_EMPTY": pj.INCLUDE_NON_EMPTY, "NON_NULL": pj.INCLUDE_NON_NULL, "ALWAYS": pj.INCLUDE_ALWAYS}
+
+
+@pytest.mark.parametrize("case", load("encode_kat.json")["cases"], ids=lambda c: c["name"])
+def test_encode_kat(case):
+    cols = to_columns([pet_from_dict(p) for p in case["pets"]])
+    fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
+    out = orc.encode(cols, fmt, INCL[case.get("inclusion", "NON_EMPTY")], case.get("hex_upper", True))
+    assert out == case["expected"].encode("utf-8")
+
+
+@pytest.mark.parametrize("case", load("decode_kat.json")["cases"], ids=lambda c: c["name"])
+def test_decode_kat(case):
+    line = line_bytes(case)
+    assert orc.decode_line_code(line) == case["code"]
+    cols, el, ec, res = orc.decode(line + b"\n")
+    assert res.n_lines == 1
+    if case["code"] == 0:
+        assert res.n_errors == 0 and res.n_pets == 1
+        got = from_columns(cols, as_bytes=True)[0]
+        assert norm_pet(got) == norm_pet(expected_pet(case))
+    else:
+        assert res.n_pets == 0 and list(el) == [0] and list(ec) == [case["code"]]
+
+
+def _nest(depth):
+    return "{\"x\":" + "[" * (depth - 1) + "]" * (depth - 1) + ",\"name\":\"a\",\"photoUrls\":[]}"
+
+
+def test_depth_limit():
+    # the pet object is depth 1; jackson's default limit is 1000 open containers
+    assert orc.decode_line_code(_nest(1000).encode()) == pj.REC_OK
+    assert orc.decode_line_code(_nest(1001).encode()) == pj.REC_DEPTH
+
+
+def test_long_format_bruteforce():
+    rnd = random.Random(7)
+    vals = [0, 1, -1, 9, 10, -10, 2**63 - 1, -2**63, 10**18, -10**18, 999999999999999999]
+    vals += [10**k for k in range(19)] + [10**k - 1 for k in range(1, 19)] + [-(10**k) for k in range(19)]
+    vals += [rnd.randrange(-2**63, 2**63) for _ in range(20000)]
+    vals += [rnd.randrange(0, 10**rnd.randrange(1, 19)) for _ in range(20000)]
+    for v in vals:
+        assert orc.format_long(v) == str(v)
+
+
+def _py_escape(b: bytes) -> bytes:
+    s = json.dumps(b.decode("utf-8"), ensure_ascii=False, separators=(",", ":"))
+    s = re.sub(r"\\u00([0-9a-f]{2})", lambda m: "\\u00" + m.group(1).upper(), s)
+    return s.encode("utf-8")
+
+
+def test_escape_matches_python_json_all_bytes():
+    # every single ASCII byte and a sample of UTF-8 sequences, alone and embedded
+    samples = [bytes([c]) for c in range(128)] + ["é€😀ü".encode()]
+    rnd = random.Random(3)
+    for _ in range(300):
+        samples.append(bytes(rnd.randrange(128) for _ in range(rnd.randrange(0, 40))))
+    pets = [pet_from_dict({"name": s.decode(), "photoUrls": []}) for s in samples]
+    out = orc.encode(to_columns(pets), pj.FORMAT_NDJSON).split(b"\n")[:-1]
+    for s, line in zip(samples, out):
+        assert line == b'{"name":' + _py_escape(s) + b',"photoUrls":[]}'
+
+
+def _schema_check(obj):
+    """Independent Python statement of the Pet binding rules on top of json.loads."""
+    assert isinstance(obj, dict)
+    assert isinstance(obj.get("name"), str) and isinstance(obj.get("photoUrls"), list)
+    return obj
+
+
+@pytest.mark.parametrize("config", [1, 3, 5])
+def test_encode_is_valid_json_and_roundtrips(config):
+    cols = generate_small(config)
+    out = orc.encode(cols, pj.FORMAT_NDJSON)
+    pets = from_columns(cols)
+    lines = out.split(b"\n")[:-1]
+    assert len(lines) == len(pets)
+    for p, line in zip(pets, lines):
+        obj = _schema_check(json.loads(line))
+        assert list(obj.keys()) == [k for k in ("id", "category", "name", "photoUrls", "tags", "status")
+                                    if k in obj]
+        assert obj["name"] == p.name and obj.get("id") == p.id
+        assert obj["photoUrls"] == p.photo_urls
+        assert obj.get("status") == (None if p.status is None else p.status.value)
+        if p.category is not None:
+            assert obj["category"] == {"id": p.category.id, "name": p.category.name}
+        assert obj.get("tags") == ([{"id": t.id, "name": t.name} for t in p.tags] if p.tags else None)
+    # array framing is the NDJSON records joined by ','
+    arr = orc.encode(cols, pj.FORMAT_ARRAY)
+    assert arr == b"[" + b",".join(lines) + b"]"
+    # decode(encode(x)) == x, column by column
+    dec, el, ec, res = orc.decode(out)
+    assert res.n_errors == 0 and res.n_pets == cols.n_pets
+    for k in pj.COLS:
+        if cols[k] is not None:
+            assert np.array_equal(dec[k], cols[k]), k
+
+
+def generate_small(config, n=3000):
+    return pj.generate(config, n)
+
+
+def test_decode_matches_json_loads_on_valid_lines():
+    cols = generate_small(3, 2000)
+    out = orc.encode(cols, pj.FORMAT_NDJSON)
+    dec, _, _, res = orc.decode(out)
+    for line, p in zip(out.split(b"\n")[:-1], from_columns(dec)):
+        obj = json.loads(line)
+        assert p.name == obj["name"] and p.photo_urls == obj["photoUrls"]
+
+
+def test_decode_corrupted_lines_report_expected_codes():
+    cols = generate_small(3, 20000)
+    buf = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), np.uint8).copy()
+    lines, codes = pj.corrupt_ndjson(buf, 99, 0.01)
+    assert len(lines) > 100
+    dec, el, ec, res = orc.decode(buf.tobytes())
+    assert list(el) == list(lines) and list(ec) == list(codes)
+    assert res.n_pets == cols.n_pets - len(lines)
