@@ -138,8 +138,9 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
         if ((s = finish_timing(ctx))) return s;
         return len > cap && !count_only ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
     }
-    const uint64_t nblk = (n + 255) / 256;
-    PJ_HIP(ctx->scan.ensure((nblk + 2) * sizeof(uint64_t)));
+    const uint64_t bt = (uint64_t)pj_encode_block_records(nested_cols(cols));
+    const uint64_t nblk = (n + bt - 1) / bt;
+    PJ_HIP(ctx->scan.ensure((nblk + 2 + 128) * sizeof(uint64_t)));
     uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p);
     EncParams P;
     std::memset(&P, 0, sizeof P);
@@ -153,6 +154,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.cap = count_only ? 0 : cap;
     P.ticket = reinterpret_cast<unsigned long long *>(sc);
     P.total = sc + 1;
+    P.dummy = reinterpret_cast<uint32_t *>(sc + 2 + nblk);   // 128 u64 = PJ_BLOCK dwords
     P.state = sc + 2;
     if ((s = mark(ctx))) return s;
     PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));

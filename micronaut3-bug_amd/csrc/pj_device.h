@@ -47,17 +47,23 @@ __device__ __forceinline__ uint64_t wave_sum(uint64_t v) {
     return v;
 }
 
-// Block-wide exclusive scan of one 64-bit value per thread (all PJ_BLOCK
-// threads must call).  Returns the exclusive prefix; *total gets the block sum.
-// `sh` needs PJ_WAVES+1 entries of LDS.
+// Block-wide exclusive scan of one 64-bit value per thread (all BT threads
+// must call).  Returns the exclusive prefix; *total gets the block sum.
+// `sh` needs BT/64 entries of LDS.
+template <int BT>
 __device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t *sh, uint64_t *total) {
+    constexpr int NW = BT / 64;
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     uint64_t inc = wave_incl_scan(v);
+    if (NW == 1) {
+        *total = shfl_u64(inc, 63);
+        return inc - v;
+    }
     if (l == 63) sh[w] = inc;
     __syncthreads();
     uint64_t before = 0, tot = 0;
 #pragma unroll
-    for (int k = 0; k < PJ_WAVES; k++) {
+    for (int k = 0; k < NW; k++) {
         uint64_t s = sh[k];
         before += (k < w) ? s : 0;
         tot += s;
@@ -80,18 +86,18 @@ __device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
     return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Called by ONE full wave of logical block `b` after the block aggregate is
-// known.  Publishes the aggregate, walks predecessors 64 at a time and
-// returns the exclusive prefix (identical in every lane); publishes the
-// inclusive prefix.  Predecessors hold smaller tickets, so they are resident
-// and the spin always ends.
-__device__ __forceinline__ uint64_t lookback(uint64_t *state, uint64_t b, uint64_t agg) {
+// Decoupled look-back in two halves.  lb_publish (one lane) announces the
+// block aggregate as early as possible; lb_resolve (one full wave) walks the
+// predecessors 64 at a time, returns the exclusive prefix (same in every
+// lane) and publishes the inclusive prefix.  Predecessors hold smaller
+// tickets, so they are resident and the spin always ends.
+__device__ __forceinline__ void lb_publish(uint64_t *state, uint64_t b, uint64_t agg) {
+    lb_store(&state[b], (b == 0 ? LB_PRE : LB_AGG) | agg);
+}
+
+__device__ __forceinline__ uint64_t lb_resolve(uint64_t *state, uint64_t b, uint64_t agg) {
     const int l = lane_id();
-    if (b == 0) {
-        if (l == 0) lb_store(&state[0], LB_PRE | agg);
-        return 0;
-    }
-    if (l == 0) lb_store(&state[b], LB_AGG | agg);
+    if (b == 0) return 0;
     uint64_t excl = 0;
     int64_t j = (int64_t)b - 1;
     for (;;) {
@@ -109,6 +115,12 @@ __device__ __forceinline__ uint64_t lookback(uint64_t *state, uint64_t b, uint64
     }
     if (l == 0) lb_store(&state[b], LB_PRE | (excl + agg));
     return excl;
+}
+
+// Both halves back to back (one full wave).
+__device__ __forceinline__ uint64_t lookback(uint64_t *state, uint64_t b, uint64_t agg) {
+    if (lane_id() == 0) lb_publish(state, b, agg);
+    return lb_resolve(state, b, agg);
 }
 
 // ----------------------------------------------------------- SWAR bytes

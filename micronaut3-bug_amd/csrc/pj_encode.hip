@@ -1,66 +1,142 @@
 // pj_encode.hip — single-pass columnar Pet -> JSON encoder for gfx950.
 //
-// One workgroup = PJ_BLOCK consecutive records, one record per thread:
-//   1. length pass: every thread measures its record's JSON bytes (integer
-//      digit counts, escape expansion of its strings, separators);
-//   2. block-wide exclusive scan of the lengths;
-//   3. decoupled look-back across workgroups (logical block ids from an
-//      atomic ticket) gives the block's output base;
-//   4. write pass: every thread emits its record at base + prefix.  Bytes are
-//      gathered in a 64-bit register and stored as aligned dwords; the few
-//      bytes a record shares with a neighbour's dword are byte stores.
-// Strings are read with aligned dword loads and funnel shifts; a SWAR test
-// takes four bytes at a time through the no-escape fast path.
+// A workgroup owns R consecutive records, hence a contiguous range of their
+// photoUrls and tags.  Phases (one kernel, one pass over the columns):
+//   1. item lengths: every url / tag item (`"url",` or `{...},`) is measured
+//      item-parallel by all BT threads, and block-scanned into LDS, so the
+//      Poisson-sized lists cost no divergence;
+//   2. record lengths: one thread per record measures its skeleton (integer
+//      digit counts, escape expansion of name / category, list sizes from
+//      the item scans); block scan -> record offsets in the tile; the block
+//      aggregate is published for the decoupled look-back right away;
+//   3. build the block's output tile in LDS: record threads write skeletons,
+//      all threads write the url / tag items, all with exact unaligned
+//      ds_write_b8..b64 (gfx950 runs LDS in unaligned mode);
+//   4. resolve the look-back (its latency hidden behind phase 3) and copy the
+//      tile to HBM with aligned 16-byte stores, so every cache line leaves
+//      the chip whole.
+// A block whose tile or item arrays do not fit falls back to writing each
+// record straight to global memory from one thread.
 //
 // Output rules (jackson UTF8JsonGenerator via micronaut-serde, reference
 // build.gradle:104) and property order / inclusion (petstore.json:872-922)
-// are the same as the CPU restatement in oracle/pj_oracle.c.
+// are the ones restated by the CPU checker in oracle/pj_oracle.c.
 #include "pj_device.h"
 #include "pj_kernels.h"
 
 namespace pj {
 
+// ------------------------------------------------------- memory helpers
+// Unaligned 8-byte global load (gfx950 global memory is in unaligned mode).
+__device__ __forceinline__ uint64_t ldu64(const uint8_t *p) { return *reinterpret_cast<const uint64_t *>(p); }
+
+// The n (1..7) bytes at p, touching only aligned qwords that hold some of
+// them (so never a page past the end of the buffer).
+__device__ __forceinline__ uint64_t ld_tail(const uint8_t *p, int n) {
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)7;
+    const int sh = (int)((uintptr_t)p & 7);
+    uint64_t v = *reinterpret_cast<const uint64_t *>(a) >> (8 * sh);
+    if (sh + n > 8) v |= *reinterpret_cast<const uint64_t *>(a + 8) << (64 - 8 * sh);
+    return v & ((1ull << (8 * n)) - 1);
+}
+
+constexpr uint64_t ONES = 0x0101010101010101ull;
+// Nonzero iff some byte of x needs an output escape (< 0x20, '"', '\\').
+__device__ __forceinline__ uint64_t special64(uint64_t x) {
+    const uint64_t q = x ^ (0x22 * ONES), b = x ^ (0x5C * ONES);
+    return (((x - 0x20 * ONES) & ~x) | ((q - ONES) & ~q) | ((b - ONES) & ~b)) & (0x80 * ONES);
+}
+
+constexpr uint64_t pack8(const char *s, int k) {
+    uint64_t v = 0;
+    for (int j = 0; j < k && j < 8; j++) v |= (uint64_t)(uint8_t)s[j] << (8 * j);
+    return v;
+}
+
 // ------------------------------------------------------------------ sinks
+// Every sink offers put(w, k) (k <= 4 bytes of w), put8(x, k) (k <= 8),
+// put_byte, skip(k) and pos().
 struct CountSink {
     uint64_t n = 0;
     __device__ __forceinline__ void put(uint32_t, int k) { n += (uint64_t)k; }
+    __device__ __forceinline__ void put8(uint64_t, int k) { n += (uint64_t)k; }
     __device__ __forceinline__ void put_byte(uint32_t) { n += 1; }
+    __device__ __forceinline__ void skip(uint32_t k) { n += k; }
+    __device__ __forceinline__ uint32_t pos() const { return (uint32_t)n; }
 };
 
+// Exact unaligned writes into the LDS tile.
+struct LdsSink {
+    uint8_t *t;
+    uint32_t o;
+    __device__ __forceinline__ void put8(uint64_t x, int k) {
+        uint8_t *q = t + o;
+        o += (uint32_t)k;
+        if (k & 8) { *reinterpret_cast<uint64_t *>(q) = x; return; }
+        if (k & 4) { *reinterpret_cast<uint32_t *>(q) = (uint32_t)x; q += 4; x >>= 32; }
+        if (k & 2) { *reinterpret_cast<uint16_t *>(q) = (uint16_t)x; q += 2; x >>= 16; }
+        if (k & 1) *q = (uint8_t)x;
+    }
+    __device__ __forceinline__ void put(uint32_t w, int k) { put8(w, k); }
+    __device__ __forceinline__ void put_byte(uint32_t b) { t[o++] = (uint8_t)b; }
+    __device__ __forceinline__ void skip(uint32_t k) { o += k; }
+    __device__ __forceinline__ uint32_t pos() const { return o; }
+};
+
+// Direct global writes (fallback for blocks whose tile does not fit LDS).
+// Bytes gather in a 64-bit accumulator that always describes an aligned
+// output dword; full dwords are stored whole, and the first dword (shared
+// with the previous record) is diverted to a per-thread dummy slot while the
+// record's own bytes of it, and the tail bytes, are stored one by one.
 struct WriteSink {
     uint8_t *out;
-    uint64_t ps;     // output position of the first pending byte
-    uint64_t acc;    // pending bytes, little endian
-    int nacc;        // number of pending bytes (<= 3 between calls)
+    uint32_t *dst;
+    uint64_t ps, ps0, acc;
+    uint32_t head;
+    int nacc, lead;
 
-    __device__ __forceinline__ void drain() {
-        while (nacc >= 4) {
-            if ((ps & 3) == 0) {
-                *reinterpret_cast<uint32_t *>(out + ps) = (uint32_t)acc;
-                acc >>= 32; nacc -= 4; ps += 4;
-            } else {
-                out[ps] = (uint8_t)acc;
-                acc >>= 8; nacc -= 1; ps += 1;
-            }
-        }
+    __device__ __forceinline__ void init(uint8_t *o, uint64_t p, uint32_t *dummy) {
+        out = o;
+        ps = ps0 = p & ~3ull;
+        lead = nacc = (int)(p & 3);
+        acc = 0;
+        head = 0;
+        dst = lead ? dummy : reinterpret_cast<uint32_t *>(out + ps);
     }
-    // append the low k (1..4) bytes of w
     __device__ __forceinline__ void put(uint32_t w, int k) {
-        uint64_t m = k == 4 ? 0xFFFFFFFFull : ((1ull << (8 * k)) - 1);
+        uint64_t m = (1ull << (8 * k)) - 1;
         acc |= ((uint64_t)w & m) << (8 * nacc);
         nacc += k;
-        drain();
+        if (nacc >= 4) {
+            *dst = (uint32_t)acc;
+            head = ps == ps0 ? (uint32_t)acc : head;
+            ps += 4;
+            dst = reinterpret_cast<uint32_t *>(out + ps);
+            acc >>= 32;
+            nacc -= 4;
+        }
+    }
+    __device__ __forceinline__ void put8(uint64_t x, int k) {
+        if (k > 4) { put((uint32_t)x, 4); put((uint32_t)(x >> 32), k - 4); }
+        else if (k > 0) put((uint32_t)x, k);
     }
     __device__ __forceinline__ void put_byte(uint32_t b) { put(b & 0xFF, 1); }
+    __device__ __forceinline__ void skip(uint32_t) {}
+    __device__ __forceinline__ uint32_t pos() const { return 0; }
     __device__ __forceinline__ void finish() {
-        while (nacc > 0) { out[ps] = (uint8_t)acc; acc >>= 8; nacc--; ps++; }
+        if (ps == ps0) {
+            for (int b = lead; b < nacc; b++) out[ps + b] = (uint8_t)(acc >> (8 * b));
+            return;
+        }
+        for (int b = lead; b > 0 && b < 4; b++) out[ps0 + b] = (uint8_t)(head >> (8 * b));
+        for (int b = 0; b < nacc; b++) out[ps + b] = (uint8_t)(acc >> (8 * b));
     }
 };
 
 template <class S, int N> __device__ __forceinline__ void lit(S &s, const char (&str)[N]) {
     constexpr int L = N - 1;
 #pragma unroll
-    for (int k = 0; k < L; k += 4) s.put(pack4(str + k, (L - k) < 4 ? (L - k) : 4), (L - k) < 4 ? (L - k) : 4);
+    for (int k = 0; k < L; k += 8) s.put8(pack8(str + k, L - k < 8 ? L - k : 8), L - k < 8 ? L - k : 8);
 }
 
 // ----------------------------------------------------------------- numbers
@@ -78,41 +154,47 @@ __device__ __forceinline__ uint32_t four_digits(uint32_t x) {
     return 0x30303030u | h1 | (h0 << 8) | (l1 << 16) | (l0 << 24);
 }
 
-// Long.toString(v): number of bytes.
-__device__ __forceinline__ int long_len(int64_t v) {
-    uint64_t u = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
-    int neg = v < 0;
-    if (u < 100000000ull) return neg + digits32((uint32_t)u);
-    if (u < 10000000000000000ull) return neg + 8 + digits32((uint32_t)(u / 100000000ull));
-    return neg + 16 + digits32((uint32_t)(u / 10000000000000000ull));
+__device__ __forceinline__ uint64_t eight_digits(uint32_t x) {  // x < 10^8
+    return (uint64_t)four_digits(x / 10000u) | ((uint64_t)four_digits(x % 10000u) << 32);
 }
 
+// Long.toString(v)
 template <class S> __device__ __forceinline__ void emit_long(S &s, int64_t v) {
     uint64_t u = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
     if (v < 0) s.put_byte('-');
-    uint32_t ch[5];   // 20 digits, most significant chunk first
-    uint32_t c0, c1, c2;
-    c2 = (uint32_t)(u % 100000000ull);
+    if (u < 100000000ull) {                   // up to 8 digits: 32-bit arithmetic
+        uint32_t x = (uint32_t)u;
+        int nd = digits32(x);
+        s.put8(eight_digits(x) >> (8 * (8 - nd)), nd);
+        return;
+    }
+    uint32_t c2 = (uint32_t)(u % 100000000ull);
     uint64_t q = u / 100000000ull;
-    c1 = (uint32_t)(q % 100000000ull);
-    c0 = (uint32_t)(q / 100000000ull);      // <= 922
-    ch[0] = four_digits(c0);
-    ch[1] = four_digits(c1 / 10000u); ch[2] = four_digits(c1 % 10000u);
-    ch[3] = four_digits(c2 / 10000u); ch[4] = four_digits(c2 % 10000u);
-    int nd = u < 100000000ull ? digits32((uint32_t)u)
-             : (q < 100000000ull ? 8 + digits32((uint32_t)q) : 16 + digits32(c0));
-    int skip = 20 - nd;          // leading zero digits to drop
-    int k = skip >> 2, off = skip & 3;
-    if (off) { s.put(ch[k] >> (8 * off), 4 - off); k++; }
-    for (; k < 5; k++) s.put(ch[k], 4);
+    if (q < 100000000ull) {                   // 9..16 digits
+        uint32_t x = (uint32_t)q;
+        int nd = digits32(x);
+        s.put8(eight_digits(x) >> (8 * (8 - nd)), nd);
+        s.put8(eight_digits(c2), 8);
+        return;
+    }
+    uint32_t c1 = (uint32_t)(q % 100000000ull), c0 = (uint32_t)(q / 100000000ull);  // c0 <= 922
+    int nd = digits32(c0);
+    s.put(four_digits(c0) >> (8 * (4 - nd)), nd);
+    s.put8(eight_digits(c1), 8);
+    s.put8(eight_digits(c2), 8);
+}
+
+// Length only (no digit strings built).
+__device__ __forceinline__ void emit_long(CountSink &s, int64_t v) {
+    uint64_t u = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
+    int n = v < 0;
+    if (u < 100000000ull) n += digits32((uint32_t)u);
+    else if (u < 10000000000000000ull) n += 8 + digits32((uint32_t)(u / 100000000ull));
+    else n += 16 + digits32((uint32_t)(u / 10000000000000000ull));
+    s.n += (uint64_t)n;
 }
 
 // ----------------------------------------------------------------- strings
-__device__ __forceinline__ int esc_extra(uint32_t c) {  // bytes added by escaping c
-    if (c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13) return 1;
-    return c < 0x20 ? 5 : 0;
-}
-
 template <class S> __device__ __forceinline__ void emit_esc_byte(S &s, uint32_t c, uint32_t hexa) {
     if (c >= 0x20 && c != '"' && c != '\\') { s.put_byte(c); return; }
     uint32_t e;
@@ -127,79 +209,55 @@ template <class S> __device__ __forceinline__ void emit_esc_byte(S &s, uint32_t 
     default: {
         uint32_t lo = c & 15;
         uint32_t hc = lo < 10 ? '0' + lo : hexa + lo - 10;
-        s.put(pack4("\\u00", 4), 4);
-        s.put(('0' + (c >> 4)) | (hc << 8), 2);
+        s.put8(pack8("\\u00", 4) | ((uint64_t)('0' + (c >> 4)) << 32) | ((uint64_t)hc << 40), 6);
         return;
     }
     }
     s.put('\\' | (e << 8), 2);
 }
 
-// Escaped body length of a raw UTF-8 string (without quotes).
-__device__ __forceinline__ uint64_t str_len(const uint8_t *p, uint64_t len) {
-    if (len == 0) return 0;
-    const uint8_t *a = (const uint8_t *)((uintptr_t)p & ~(uintptr_t)3);
-    const int off = (int)((uintptr_t)p & 3);
-    uint64_t extra = 0;
-    uint32_t lo = ld32(a);
-    for (uint64_t k = 0; k < len; k += 4) {
-        uint64_t rem = len - k;
-        uint32_t w = lo;
-        if (off) {
-            uint32_t hi = (off + rem > 4) ? ld32(a + 4) : 0u;
-            w = __builtin_amdgcn_alignbyte(hi, lo, off);
-            lo = hi;
-        } else if (rem > 4) {
-            lo = ld32(a + 4);
-        }
-        a += 4;
-        int m = rem < 4 ? (int)rem : 4;
-        uint32_t vm = m == 4 ? 0xFFFFFFFFu : ((1u << (8 * m)) - 1);
-        uint32_t x = (w & vm) | (0x41414141u & ~vm);
-        if (any_special(x)) {
-            for (int b = 0; b < m; b++) extra += (uint64_t)esc_extra((x >> (8 * b)) & 0xFF);
-        }
-    }
-    return len + extra;
+__device__ __forceinline__ uint32_t esc_extra(uint32_t c) {  // bytes added by escaping c
+    if (c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13) return 1;
+    return c < 0x20 ? 5 : 0;
 }
 
+template <class S> __device__ __forceinline__ void esc_bytes(S &s, uint64_t x, int m, uint32_t hexa) {
+    for (int b = 0; b < m; b++) emit_esc_byte(s, (uint32_t)(x >> (8 * b)) & 0xFF, hexa);
+}
+__device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint32_t) {
+    uint32_t e = 0;
+    for (int b = 0; b < m; b++) e += esc_extra((uint32_t)(x >> (8 * b)) & 0xFF);
+    s.n += (uint64_t)(m + e);
+}
+
+// A JSON string (quotes included) from raw UTF-8 bytes: 8 bytes per step
+// through the no-escape fast path.
 template <class S> __device__ __forceinline__ void emit_str(S &s, const uint8_t *p, uint64_t len, uint32_t hexa) {
     s.put_byte('"');
-    if (len) {
-        const uint8_t *a = (const uint8_t *)((uintptr_t)p & ~(uintptr_t)3);
-        const int off = (int)((uintptr_t)p & 3);
-        uint32_t lo = ld32(a);
-        for (uint64_t k = 0; k < len; k += 4) {
-            uint64_t rem = len - k;
-            uint32_t w = lo;
-            if (off) {
-                uint32_t hi = (off + rem > 4) ? ld32(a + 4) : 0u;
-                w = __builtin_amdgcn_alignbyte(hi, lo, off);
-                lo = hi;
-            } else if (rem > 4) {
-                lo = ld32(a + 4);
-            }
-            a += 4;
-            int m = rem < 4 ? (int)rem : 4;
-            uint32_t vm = m == 4 ? 0xFFFFFFFFu : ((1u << (8 * m)) - 1);
-            uint32_t x = (w & vm) | (0x41414141u & ~vm);
-            if (!any_special(x)) {
-                s.put(w, m);
-            } else {
-                for (int b = 0; b < m; b++) emit_esc_byte(s, (x >> (8 * b)) & 0xFF, hexa);
-            }
-        }
+    uint64_t k = 0;
+    for (; k + 8 <= len; k += 8) {
+        uint64_t x = ldu64(p + k);
+        if (!special64(x)) s.put8(x, 8);
+        else esc_bytes(s, x, 8, hexa);
+    }
+    if (k < len) {
+        int m = (int)(len - k);
+        uint64_t x = ld_tail(p + k, m);
+        uint64_t mk = (1ull << (8 * m)) - 1;
+        if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
+        else esc_bytes(s, x, m, hexa);
     }
     s.put_byte('"');
 }
 
-// The count sink only needs lengths: a specialisation avoids re-walking.
-__device__ __forceinline__ void emit_str(CountSink &s, const uint8_t *p, uint64_t len, uint32_t) {
-    s.n += 2 + str_len(p, len);
-}
-__device__ __forceinline__ void emit_long(CountSink &s, int64_t v) { s.n += (uint64_t)long_len(v); }
-
 // ------------------------------------------------------------------ record
+constexpr uint32_t NO_ITEMS = 0xFFFFFFFFu;  // list not written (null / omitted)
+
+struct RecItems {             // staged layout of one record's lists
+    uint32_t usz, tsz;        // bytes of its url / tag items (from the item scans)
+    uint32_t ustart, tstart;  // tile offsets where they start (set by emit_pet)
+};
+
 template <class S> __device__ __forceinline__ void key(S &s, bool &first) {
     if (!first) s.put_byte(',');
     first = false;
@@ -220,8 +278,27 @@ __device__ __forceinline__ void emit_sub(S &s, const EncParams &P, uint32_t fl, 
     s.put_byte('}');
 }
 
-template <bool NESTED, class S>
-__device__ __forceinline__ void emit_pet(S &s, const EncParams &P, uint64_t i) {
+// url item: `"url"` + (',' or ']' after the record's last url)
+template <class S> __device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, uint64_t u, bool last) {
+    const pj_pet_columns &c = P.c;
+    uint64_t a = c.url_off[u], b = c.url_off[u + 1];
+    emit_str(s, c.url_bytes + a, b - a, P.hexa);
+    s.put_byte(last ? ']' : ',');
+}
+
+// tag item: `{...}` + (',' or ']')
+template <class S> __device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, uint64_t g, bool last) {
+    const pj_pet_columns &c = P.c;
+    uint32_t tf = c.tag_flags ? c.tag_flags[g] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
+    uint64_t a = c.tag_name_off[g], b = c.tag_name_off[g + 1];
+    emit_sub(s, P, tf, c.tag_id[g], c.tag_name_bytes + a, b - a);
+    s.put_byte(last ? ']' : ',');
+}
+
+// One Pet.  INLINE: lists written here; otherwise their item bytes are
+// skipped (written by item threads) and their tile offsets recorded in ri.
+template <bool NESTED, bool INLINE, class S>
+__device__ __forceinline__ void emit_pet(S &s, const EncParams &P, uint64_t i, RecItems &ri) {
     const pj_pet_columns &c = P.c;
     const uint32_t fl = c.flags ? c.flags[i] : (uint32_t)PJ_PET_DEFAULT_FLAGS;
     bool first = true;
@@ -240,79 +317,203 @@ __device__ __forceinline__ void emit_pet(S &s, const EncParams &P, uint64_t i) {
         uint64_t a = c.name_off[i], b = c.name_off[i + 1];
         emit_str(s, c.name_bytes + a, b - a, P.hexa);
     } else lit(s, "\"name\":null");
-    s.put_byte(',');
     if (fl & PJ_PET_HAS_PHOTOURLS) {
-        lit(s, "\"photoUrls\":[");
-        if (NESTED && c.photo_off) {
-            uint64_t u0 = c.photo_off[i], u1 = c.photo_off[i + 1];
-            for (uint64_t u = u0; u < u1; u++) {
-                if (u > u0) s.put_byte(',');
-                uint64_t a = c.url_off[u], b = c.url_off[u + 1];
-                emit_str(s, c.url_bytes + a, b - a, P.hexa);
-            }
+        lit(s, ",\"photoUrls\":[");
+        uint64_t u0 = 0, u1 = 0;
+        if (NESTED && c.photo_off) { u0 = c.photo_off[i]; u1 = c.photo_off[i + 1]; }
+        if (u1 == u0) s.put_byte(']');
+        else if (INLINE) {
+            for (uint64_t u = u0; u < u1; u++) emit_url_item(s, P, u, u + 1 == u1);
+        } else {
+            ri.ustart = s.pos();
+            s.skip(ri.usz);
         }
-        s.put_byte(']');
-    } else lit(s, "\"photoUrls\":null");
+    } else lit(s, ",\"photoUrls\":null");
     if (NESTED && (fl & PJ_PET_HAS_TAGS)) {
         uint64_t t0 = c.tag_off ? c.tag_off[i] : 0, t1 = c.tag_off ? c.tag_off[i + 1] : 0;
         if (t1 > t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
             lit(s, ",\"tags\":[");
-            for (uint64_t t = t0; t < t1; t++) {
-                if (t > t0) s.put_byte(',');
-                uint32_t tf = c.tag_flags ? c.tag_flags[t] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
-                uint64_t a = c.tag_name_off[t], b = c.tag_name_off[t + 1];
-                emit_sub(s, P, tf, c.tag_id[t], c.tag_name_bytes + a, b - a);
+            if (t1 == t0) s.put_byte(']');
+            else if (INLINE) {
+                for (uint64_t g = t0; g < t1; g++) emit_tag_item(s, P, g, g + 1 == t1);
+            } else {
+                ri.tstart = s.pos();
+                s.skip(ri.tsz);
             }
-            s.put_byte(']');
         }
     } else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"tags\":null");
     const uint32_t st = c.status ? c.status[i] : (uint32_t)PJ_STATUS_NULL;
-    if (st == 0) lit(s, ",\"status\":\"available\"");
-    else if (st == 1) lit(s, ",\"status\":\"pending\"");
-    else if (st == 2) lit(s, ",\"status\":\"sold\"");
-    else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null");
-    s.put_byte('}');
+    if (st == 0) lit(s, ",\"status\":\"available\"}");
+    else if (st == 1) lit(s, ",\"status\":\"pending\"}");
+    else if (st == 2) lit(s, ",\"status\":\"sold\"}");
+    else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null}");
+    else s.put_byte('}');
+}
+
+// Record plus its separator: '[' or ',' before (array), '\n' or ']' after.
+template <bool NESTED, bool INLINE, class S>
+__device__ __forceinline__ void emit_rec(S &s, const EncParams &P, uint64_t i, RecItems &ri) {
+    const bool nd = P.format == PJ_FORMAT_NDJSON;
+    if (!nd) s.put_byte(i == 0 ? '[' : ',');
+    emit_pet<NESTED, INLINE>(s, P, i, ri);
+    if (nd) s.put_byte('\n');
+    else if (i == P.n - 1) s.put_byte(']');
+}
+
+// In-place exclusive scan of n u32 values in LDS (all BT threads call);
+// a[n] receives the total.
+template <int BT>
+__device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t *sh) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (n + BT - 1) / BT;
+    const uint32_t s0 = min(t * per, n), s1 = min(s0 + per, n);
+    uint64_t sum = 0;
+    for (uint32_t k = s0; k < s1; k++) sum += a[k];
+    uint64_t tot;
+    uint64_t run = block_excl_scan<BT>(sum, sh, &tot);
+    for (uint32_t k = s0; k < s1; k++) {
+        uint32_t v = a[k];
+        a[k] = (uint32_t)run;
+        run += v;
+    }
+    if (t == 0) a[n] = (uint32_t)tot;
+    __syncthreads();
 }
 
 // ------------------------------------------------------------------ kernel
-template <bool NESTED>
-__global__ __launch_bounds__(PJ_BLOCK) void k_encode(EncParams P) {
-    __shared__ uint64_t sh_scan[PJ_WAVES + 1];
-    __shared__ uint64_t sh_blk;
-    __shared__ uint64_t sh_base;
-    const int t = threadIdx.x;
-    if (t == 0) sh_blk = atomicAdd(P.ticket, 1ull);
+template <bool NESTED, int BT, int R, int TILE, int UCAP, int GCAP>
+__global__ __launch_bounds__(BT) void k_encode(EncParams P) {
+    constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE];
+    __shared__ uint32_t su[UA + 1], sg[GA + 1];      // item prefix sums (tile-relative)
+    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: item area base - su[first]
+    __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
+    __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
+    __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint64_t sh_blk, sh_base, sh_rng[4];
+    const uint32_t t = threadIdx.x;
+    const pj_pet_columns &c = P.c;
+    if (t == 0) {
+        uint64_t b = atomicAdd(P.ticket, 1ull);
+        sh_blk = b;
+        uint64_t r0 = b * R, r1 = min(r0 + R, P.n);
+        sh_rng[0] = NESTED && c.photo_off ? c.photo_off[r0] : 0;
+        sh_rng[1] = NESTED && c.photo_off ? c.photo_off[r1] : 0;
+        sh_rng[2] = NESTED && c.tag_off ? c.tag_off[r0] : 0;
+        sh_rng[3] = NESTED && c.tag_off ? c.tag_off[r1] : 0;
+    }
     __syncthreads();
     const uint64_t b = sh_blk;
-    const uint64_t i = b * PJ_BLOCK + (uint64_t)t;
-    const bool live = i < P.n;
-    const bool ndjson = P.format == PJ_FORMAT_NDJSON;
+    const uint64_t r0 = b * R;
+    const uint64_t U0 = sh_rng[0], G0 = sh_rng[2];
+    const uint64_t U = sh_rng[1] - U0, G = sh_rng[3] - G0;
+    const bool staged = !NESTED || (U <= UCAP && G <= GCAP);
+    const uint64_t i = r0 + t;
+    const bool live = t < (uint32_t)R && i < P.n;
 
+    // ---- phase 1: item lengths and their block scans
+    if (NESTED && staged) {
+        for (uint32_t k = t; k < U; k += BT) {
+            CountSink cs;
+            emit_url_item(cs, P, U0 + k, false);
+            su[k] = (uint32_t)cs.n;
+        }
+        for (uint32_t k = t; k < G; k += BT) {
+            CountSink cs;
+            emit_tag_item(cs, P, G0 + k, false);
+            sg[k] = (uint32_t)cs.n;
+        }
+        __syncthreads();
+        lds_excl_scan<BT>(su, (uint32_t)U, sh_scan);
+        lds_excl_scan<BT>(sg, (uint32_t)G, sh_scan);
+    }
+
+    // ---- phase 2: record lengths, scan, publish the aggregate
+    RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
+    uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
     uint64_t len = 0;
     if (live) {
         CountSink cs;
-        emit_pet<NESTED>(cs, P, i);
-        len = cs.n + 1;                                     // ',' / '[' / '\n'
-        if (!ndjson && i == P.n - 1) len += 1;              // closing ']'
+        if (NESTED && staged) {
+            if (c.photo_off) { ul0 = (uint32_t)(c.photo_off[i] - U0); ul1 = (uint32_t)(c.photo_off[i + 1] - U0); }
+            if (c.tag_off) { gl0 = (uint32_t)(c.tag_off[i] - G0); gl1 = (uint32_t)(c.tag_off[i + 1] - G0); }
+            ri.usz = su[ul1] - su[ul0];
+            ri.tsz = sg[gl1] - sg[gl0];
+            emit_rec<NESTED, false>(cs, P, i, ri);
+        } else {
+            emit_rec<NESTED, true>(cs, P, i, ri);
+        }
+        len = cs.n;
     }
     uint64_t agg;
-    uint64_t pre = block_excl_scan(len, sh_scan, &agg);
+    const uint64_t pre = block_excl_scan<BT>(len, sh_scan, &agg);
+    if (t == 0) lb_publish(P.state, b, agg);
+    const bool fits = staged && agg + 16 <= TILE;
+
+    if (fits && !P.count_only) {
+        // ---- phase 3: build the tile
+        if (NESTED && live) {
+            ubase[t] = ri.ustart == NO_ITEMS ? NO_ITEMS : (uint32_t)pre + ri.ustart - su[ul0];
+            gbase[t] = ri.tstart == NO_ITEMS ? NO_ITEMS : (uint32_t)pre + ri.tstart - sg[gl0];
+            uend[t] = (uint16_t)ul1;
+            gend[t] = (uint16_t)gl1;
+            for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
+            for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
+        }
+        __syncthreads();
+        if (live) {
+            LdsSink ls{tile, (uint32_t)pre};
+            RecItems r2 = ri;
+            emit_rec<NESTED, false>(ls, P, i, r2);
+        }
+        if (NESTED) {
+            for (uint32_t k = t; k < U; k += BT) {
+                uint32_t own = uown[k];
+                if (ubase[own] == NO_ITEMS) continue;
+                LdsSink ls{tile, ubase[own] + su[k]};
+                emit_url_item(ls, P, U0 + k, k + 1 == uend[own]);
+            }
+            for (uint32_t k = t; k < G; k += BT) {
+                uint32_t own = gown[k];
+                if (gbase[own] == NO_ITEMS) continue;
+                LdsSink ls{tile, gbase[own] + sg[k]};
+                emit_tag_item(ls, P, G0 + k, k + 1 == gend[own]);
+            }
+        }
+    }
+    // ---- phase 4: look-back, then copy out
     if (t < 64) {
-        uint64_t excl = lookback(P.state, b, agg);
+        uint64_t excl = lb_resolve(P.state, b, agg);
         if (t == 0) {
             sh_base = excl;
             if (b == gridDim.x - 1) *P.total = excl + agg;
         }
     }
     __syncthreads();
-    if (!live || P.count_only) return;
-    const uint64_t pos = sh_base + pre;
-    if (pos + len > P.cap) return;                           // capacity guard
-    WriteSink ws{P.out, pos, 0ull, 0};
-    if (!ndjson) ws.put_byte(i == 0 ? '[' : ',');
-    emit_pet<NESTED>(ws, P, i);
-    if (ndjson) ws.put_byte('\n');
-    else if (i == P.n - 1) ws.put_byte(']');
+    if (P.count_only) return;
+    const uint64_t base = sh_base;
+    if (fits) {
+        const uint64_t end = min(base + agg, P.cap);
+        if (base >= end) return;
+        const uint64_t s = base & 15, g0 = base - s;
+        const uint32_t nch = (uint32_t)((s + (end - base) + 15) >> 4);
+        for (uint32_t ch = t; ch < nch; ch += BT) {
+            const uint64_t g = g0 + 16ull * ch;
+            if (g >= base && g + 16 <= end) {
+                *reinterpret_cast<uint4 *>(P.out + g) = *reinterpret_cast<const uint4 *>(tile + (g - base));
+            } else {
+                for (int j = 0; j < 16; j++)
+                    if (g + j >= base && g + j < end) P.out[g + j] = tile[g + j - base];
+            }
+        }
+        return;
+    }
+    if (!live) return;
+    const uint64_t p = base + pre;
+    if (p + len > P.cap) return;
+    WriteSink ws;
+    ws.init(P.out, p, P.dummy + t);
+    emit_rec<NESTED, true>(ws, P, i, ri);
     ws.finish();
 }
 
@@ -335,12 +536,23 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
     return hipGetLastError();
 }
 
+// Workgroup shapes: threads, records, LDS tile bytes, item capacities.
+constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256, ENC_FLAT_TILE = 32 * 1024;
+constexpr int ENC_NEST_BT = 256, ENC_NEST_R = 128, ENC_NEST_TILE = 44 * 1024, ENC_NEST_UCAP = 512,
+              ENC_NEST_GCAP = 384;
+
+int pj_encode_block_records(bool nested) { return nested ? ENC_NEST_R : ENC_FLAT_R; }
+
 hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st) {
-    uint64_t g = (P.n + PJ_BLOCK - 1) / PJ_BLOCK;
-    if (nested)
-        hipLaunchKernelGGL(pj::k_encode<true>, dim3((unsigned)g), dim3(PJ_BLOCK), 0, st, P);
-    else
-        hipLaunchKernelGGL(pj::k_encode<false>, dim3((unsigned)g), dim3(PJ_BLOCK), 0, st, P);
+    if (nested) {
+        uint64_t g = (P.n + ENC_NEST_R - 1) / ENC_NEST_R;
+        hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_UCAP, ENC_NEST_GCAP>),
+                           dim3((unsigned)g), dim3(ENC_NEST_BT), 0, st, P);
+    } else {
+        uint64_t g = (P.n + ENC_FLAT_R - 1) / ENC_FLAT_R;
+        hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, 1, 1>), dim3((unsigned)g),
+                           dim3(ENC_FLAT_BT), 0, st, P);
+    }
     return hipGetLastError();
 }
 

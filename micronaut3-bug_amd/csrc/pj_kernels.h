@@ -16,6 +16,7 @@ struct EncParams {
     uint64_t *state;           // look-back words, one per block (zeroed)
     unsigned long long *ticket;// logical block counter (zeroed)
     uint64_t *total;           // encoded size (written by the last block)
+    uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)
 };
 
 struct DecParams {
@@ -44,6 +45,7 @@ enum { C_PETS = 0, C_NAMEB, C_CATB, C_URLS, C_URLB, C_TAGS, C_TAGB, C_ERRS, PJ_D
 
 hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);
 hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st);
+int pj_encode_block_records(bool nested);
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);
