@@ -359,13 +359,166 @@ void pj_decode_bounds(uint64_t len, pj_pet_columns *c) {
 
 }  // extern "C"
 
-extern "C" pj_status pj_decode_device(pj_ctx *ctx, const uint8_t *, uint64_t, pj_pet_columns *, uint64_t *,
-                                      uint8_t *, uint64_t, pj_decode_result *) {
-    pj_status s = bind(ctx);
-    return s ? s : fail(PJ_ERR_DEVICE, "decode kernels not built");
+namespace {
+
+constexpr int VLB_STRIDE_HOST = 1 + 2 * PJ_DEC_NCNT;
+
+bool dec_cols_ok(const pj_pet_columns *o) {
+    void *v[17];
+    col_ptrs(const_cast<pj_pet_columns *>(o), v);
+    for (void *x : v)
+        if (!x) return false;
+    return true;
 }
-extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *, uint64_t, pj_pet_columns *, uint64_t *,
-                                    uint8_t *, uint64_t, pj_decode_result *) {
+
+pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                      uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
     pj_status s = bind(ctx);
-    return s ? s : fail(PJ_ERR_DEVICE, "decode kernels not built");
+    if (s) return s;
+    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
+    if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
+    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    std::memset(res, 0, sizeof *res);
+    ctx->n_ev = 0;
+    const uint64_t nblk64 = (len + 63) / 64;
+    uint64_t ls_cap = len / 128 + 16;
+    for (int attempt = 0; attempt < 2; attempt++) {
+        const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
+        const uint64_t gpar = (ls_cap + pj_dec_parse_block() - 1) / pj_dec_parse_block();
+        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | state_parse gpar*stride |
+        //                     special nblk64 | line_start ls_cap | bad (bytes)
+        const uint64_t o_dummy = 16, o_sidx = 48, o_spar = o_sidx + gidx, o_spec = o_spar + gpar * VLB_STRIDE_HOST,
+                       o_ls = o_spec + nblk64, o_bad = o_ls + ls_cap;
+        const uint64_t bytes = o_bad * 8 + nblk64 + 64;
+        PJ_HIP(ctx->index.ensure(bytes));
+        uint64_t *X = static_cast<uint64_t *>(ctx->index.p);
+        DecParams P;
+        std::memset(&P, 0, sizeof P);
+        P.in = in;
+        P.len = len;
+        P.nblk64 = nblk64;
+        P.special = X + o_spec;
+        P.bad = reinterpret_cast<uint8_t *>(X + o_bad);
+        P.line_start = X + o_ls;
+        P.ls_cap = ls_cap;
+        P.n_lines = X + 2;
+        P.o = *out;
+        P.err_line = err_line;
+        P.err_code = err_code;
+        P.err_cap = err_cap;
+        P.totals = X + 4;
+        P.state_idx = X + o_sidx;
+        P.state_parse = X + o_spar;
+        P.tickets = reinterpret_cast<unsigned long long *>(X);
+        P.dummy = reinterpret_cast<uint32_t *>(X + o_dummy);
+        ctx->n_ev = 0;
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_fill_u64(X, 16, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(X + o_sidx, gidx, 0, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        if (nblk64) PJ_HIP(pj_launch_dec_index(P, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 2, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        const uint64_t lines = ctx->pinned[0];
+        if (lines + 1 > ls_cap) {          // more lines than the first guess: grow and redo
+            ls_cap = lines + 2;
+            continue;
+        }
+        P.lines = lines;
+        const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_fill_u64(X + o_spar, gp * VLB_STRIDE_HOST, 0, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        if (lines) PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+        else {
+            // no lines: the offset arrays still start with 0
+            uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
+                                  out->tag_name_off};
+            for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
+        }
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 4, PJ_DEC_NCNT * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                              ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if ((s = finish_timing(ctx))) return s;
+        const uint64_t *T = ctx->pinned;
+        res->n_lines = lines;
+        if (lines) {
+            res->n_pets = T[C_PETS];
+            res->name_bytes = T[C_NAMEB];
+            res->cat_name_bytes = T[C_CATB];
+            res->n_urls = T[C_URLS];
+            res->url_bytes = T[C_URLB];
+            res->n_tags = T[C_TAGS];
+            res->tag_name_bytes = T[C_TAGB];
+            res->n_errors = T[C_ERRS];
+        }
+        out->n_pets = std::min(res->n_pets, out->cap_pets);
+        if (res->n_errors > err_cap) return fail(PJ_ERR_CAPACITY, "error list capacity too small");
+        if (res->n_pets > out->cap_pets || res->name_bytes > out->cap_name_bytes ||
+            res->cat_name_bytes > out->cap_cat_name_bytes || res->n_urls > out->cap_urls ||
+            res->url_bytes > out->cap_url_bytes || res->n_tags > out->cap_tags ||
+            res->tag_name_bytes > out->cap_tag_name_bytes)
+            return fail(PJ_ERR_CAPACITY, "column capacity too small (sizes needed are in the result)");
+        return PJ_OK;
+    }
+    return fail(PJ_ERR_DEVICE, "line index did not converge");
+}
+
+}  // namespace
+
+extern "C" pj_status pj_decode_device(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
+                                      uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
+                                      pj_decode_result *res) {
+    return decode_impl(ctx, in, len, out, err_line, err_code, err_cap, res);
+}
+
+extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
+                                    uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
+                                    pj_decode_result *res) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
+    if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
+    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    // device staging: input, then every output column sized by the capacities
+    const uint64_t cp = out->cap_pets, cu = out->cap_urls, ct = out->cap_tags;
+    const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, out->cap_name_bytes, cp * 8, cp, (cp + 1) * 8,
+                             out->cap_cat_name_bytes, (cp + 1) * 8, (cu + 1) * 8, out->cap_url_bytes, (cp + 1) * 8,
+                             ct * 8, ct, (ct + 1) * 8, out->cap_tag_name_bytes, err_cap * 8, err_cap};
+    uint64_t off[20];
+    off[0] = align256(len + 16);
+    for (int k = 0; k < 19; k++) off[k + 1] = off[k] + align256(sz[k] + 8);
+    PJ_HIP(ctx->stage_out.ensure(off[19]));
+    uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
+    if (len) PJ_HIP(hipMemcpyAsync(D, in, len, hipMemcpyHostToDevice, ctx->stream));
+    void *dp[17];
+    for (int k = 0; k < 17; k++) dp[k] = D + off[k];
+    pj_pet_columns dc = *out;
+    set_col_ptrs(&dc, dp);
+    uint64_t *del = reinterpret_cast<uint64_t *>(D + off[17]);
+    uint8_t *dec = D + off[18];
+    s = decode_impl(ctx, D, len, &dc, err_cap ? del : nullptr, err_cap ? dec : nullptr, err_cap, res);
+    if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
+    const uint64_t np = std::min(res->n_pets, cp), nu = std::min(res->n_urls, cu), nt = std::min(res->n_tags, ct);
+    const uint64_t used[17] = {np * 8, np, np, (np + 1) * 8, std::min(res->name_bytes, out->cap_name_bytes), np * 8,
+                               np, (np + 1) * 8, std::min(res->cat_name_bytes, out->cap_cat_name_bytes),
+                               (np + 1) * 8, (nu + 1) * 8, std::min(res->url_bytes, out->cap_url_bytes),
+                               (np + 1) * 8, nt * 8, nt, (nt + 1) * 8,
+                               std::min(res->tag_name_bytes, out->cap_tag_name_bytes)};
+    void *hp[17];
+    col_ptrs(out, hp);
+    for (int k = 0; k < 17; k++)
+        if (used[k]) PJ_HIP(hipMemcpyAsync(hp[k], dp[k], used[k], hipMemcpyDeviceToHost, ctx->stream));
+    const uint64_t ne = std::min(res->n_errors, err_cap);
+    if (ne) {
+        PJ_HIP(hipMemcpyAsync(err_line, del, ne * 8, hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipMemcpyAsync(err_code, dec, ne, hipMemcpyDeviceToHost, ctx->stream));
+    }
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    out->n_pets = np;
+    return s;
 }

@@ -26,27 +26,6 @@
 
 namespace pj {
 
-// ------------------------------------------------------- memory helpers
-// Unaligned 8-byte global load (gfx950 global memory is in unaligned mode).
-__device__ __forceinline__ uint64_t ldu64(const uint8_t *p) { return *reinterpret_cast<const uint64_t *>(p); }
-
-// The n (1..7) bytes at p, touching only aligned qwords that hold some of
-// them (so never a page past the end of the buffer).
-__device__ __forceinline__ uint64_t ld_tail(const uint8_t *p, int n) {
-    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)7;
-    const int sh = (int)((uintptr_t)p & 7);
-    uint64_t v = *reinterpret_cast<const uint64_t *>(a) >> (8 * sh);
-    if (sh + n > 8) v |= *reinterpret_cast<const uint64_t *>(a + 8) << (64 - 8 * sh);
-    return v & ((1ull << (8 * n)) - 1);
-}
-
-constexpr uint64_t ONES = 0x0101010101010101ull;
-// Nonzero iff some byte of x needs an output escape (< 0x20, '"', '\\').
-__device__ __forceinline__ uint64_t special64(uint64_t x) {
-    const uint64_t q = x ^ (0x22 * ONES), b = x ^ (0x5C * ONES);
-    return (((x - 0x20 * ONES) & ~x) | ((q - ONES) & ~q) | ((b - ONES) & ~b)) & (0x80 * ONES);
-}
-
 constexpr uint64_t pack8(const char *s, int k) {
     uint64_t v = 0;
     for (int j = 0; j < k && j < 8; j++) v |= (uint64_t)(uint8_t)s[j] << (8 * j);
@@ -81,56 +60,6 @@ struct LdsSink {
     __device__ __forceinline__ void put_byte(uint32_t b) { t[o++] = (uint8_t)b; }
     __device__ __forceinline__ void skip(uint32_t k) { o += k; }
     __device__ __forceinline__ uint32_t pos() const { return o; }
-};
-
-// Direct global writes (fallback for blocks whose tile does not fit LDS).
-// Bytes gather in a 64-bit accumulator that always describes an aligned
-// output dword; full dwords are stored whole, and the first dword (shared
-// with the previous record) is diverted to a per-thread dummy slot while the
-// record's own bytes of it, and the tail bytes, are stored one by one.
-struct WriteSink {
-    uint8_t *out;
-    uint32_t *dst;
-    uint64_t ps, ps0, acc;
-    uint32_t head;
-    int nacc, lead;
-
-    __device__ __forceinline__ void init(uint8_t *o, uint64_t p, uint32_t *dummy) {
-        out = o;
-        ps = ps0 = p & ~3ull;
-        lead = nacc = (int)(p & 3);
-        acc = 0;
-        head = 0;
-        dst = lead ? dummy : reinterpret_cast<uint32_t *>(out + ps);
-    }
-    __device__ __forceinline__ void put(uint32_t w, int k) {
-        uint64_t m = (1ull << (8 * k)) - 1;
-        acc |= ((uint64_t)w & m) << (8 * nacc);
-        nacc += k;
-        if (nacc >= 4) {
-            *dst = (uint32_t)acc;
-            head = ps == ps0 ? (uint32_t)acc : head;
-            ps += 4;
-            dst = reinterpret_cast<uint32_t *>(out + ps);
-            acc >>= 32;
-            nacc -= 4;
-        }
-    }
-    __device__ __forceinline__ void put8(uint64_t x, int k) {
-        if (k > 4) { put((uint32_t)x, 4); put((uint32_t)(x >> 32), k - 4); }
-        else if (k > 0) put((uint32_t)x, k);
-    }
-    __device__ __forceinline__ void put_byte(uint32_t b) { put(b & 0xFF, 1); }
-    __device__ __forceinline__ void skip(uint32_t) {}
-    __device__ __forceinline__ uint32_t pos() const { return 0; }
-    __device__ __forceinline__ void finish() {
-        if (ps == ps0) {
-            for (int b = lead; b < nacc; b++) out[ps + b] = (uint8_t)(acc >> (8 * b));
-            return;
-        }
-        for (int b = lead; b > 0 && b < 4; b++) out[ps0 + b] = (uint8_t)(head >> (8 * b));
-        for (int b = 0; b < nacc; b++) out[ps + b] = (uint8_t)(acc >> (8 * b));
-    }
 };
 
 template <class S, int N> __device__ __forceinline__ void lit(S &s, const char (&str)[N]) {

@@ -26,7 +26,8 @@ struct DecParams {
     // index stage outputs
     uint64_t *special;         // [nblk64] unescaped quotes | backslashes
     uint8_t *bad;              // [nblk64] 1 = string-content fault in block
-    uint64_t *line_start;      // [n_lines+1]
+    uint64_t *line_start;      // [ls_cap]: line l spans [line_start[l], line_start[l+1]-1)
+    uint64_t ls_cap;
     uint64_t *n_lines;         // device scalar
     // parse stage
     pj_pet_columns o;          // outputs with capacities
@@ -38,6 +39,7 @@ struct DecParams {
     uint64_t *state_parse;     // look-back words of the parse stage, PJ_DEC_NCNT per block
     unsigned long long *tickets; // [2]
     uint64_t lines;            // n_lines as known by the host for the parse stage
+    uint32_t *dummy;           // sink for diverted shared dwords (never read)
 };
 
 // counters carried through the parse-stage scan
@@ -49,3 +51,5 @@ int pj_encode_block_records(bool nested);
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);
+int pj_dec_index_block();
+int pj_dec_parse_block();

@@ -354,3 +354,69 @@ class Codec:
         self._check(self.L.pj_encode_host(self.ctx, C.byref(s), fmt, C.c_void_p(out.ctypes.data), out.size,
                                           C.byref(n)))
         return out[: n.value].tobytes()
+
+    # ---- decode
+    def _alloc_decode(self, caps, device):
+        import torch
+        dev = f"cuda:{self.device}" if device is None else device
+        cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
+        sizes = {"id": cp, "flags": cp, "status": cp, "name_off": cp + 1, "name_bytes": caps["cap_name_bytes"],
+                 "cat_id": cp, "cat_flags": cp, "cat_name_off": cp + 1, "cat_name_bytes": caps["cap_cat_name_bytes"],
+                 "photo_off": cp + 1, "url_off": cu + 1, "url_bytes": caps["cap_url_bytes"], "tag_off": cp + 1,
+                 "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
+        tdt = {np.int64: torch.int64, np.uint8: torch.uint8, np.uint64: torch.int64}
+        arrays = {k: torch.empty(max(1, v) + 8, dtype=tdt[DTYPES[k]], device=dev) for k, v in sizes.items()}
+        return Columns(0, arrays, dict(caps), {k: 0 for k in arrays})
+
+    def decode(self, data, caps=None, err_cap=None, device=None):
+        """Decode NDJSON held in a uint8 device tensor.  Returns (columns on the
+        device trimmed to size, error line indices, error codes, DecodeResult)."""
+        import torch
+        n = data.numel()
+        caps = caps or decode_bounds(n)
+        cols = self._alloc_decode(caps, device)
+        if err_cap is None:
+            err_cap = n // 16 + 16
+        el = torch.empty(max(1, err_cap), dtype=torch.int64, device=data.device)
+        ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=data.device)
+        torch.cuda.synchronize()
+        s = cols.struct()
+        res = DecodeResult()
+        ptr = C.c_void_p(data.data_ptr()) if n else C.c_void_p(el.data_ptr())
+        rc = self.L.pj_decode_device(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()),
+                                     C.c_void_p(ec.data_ptr()), err_cap, C.byref(res))
+        self._check(rc)
+        return self._trim(cols, res), el[: res.n_errors], ec[: res.n_errors], res
+
+    @staticmethod
+    def _trim(cols, res):
+        np_, nu, nt = res.n_pets, res.n_urls, res.n_tags
+        lens = {"id": np_, "flags": np_, "status": np_, "name_off": np_ + 1, "name_bytes": res.name_bytes,
+                "cat_id": np_, "cat_flags": np_, "cat_name_off": np_ + 1, "cat_name_bytes": res.cat_name_bytes,
+                "photo_off": np_ + 1, "url_off": nu + 1, "url_bytes": res.url_bytes, "tag_off": np_ + 1,
+                "tag_id": nt, "tag_flags": nt, "tag_name_off": nt + 1, "tag_name_bytes": res.tag_name_bytes}
+        return Columns(np_, cols.arrays, dict(cols.caps), lens)
+
+    def decode_host(self, data: bytes, caps=None, err_cap=None):
+        """Decode NDJSON bytes through the host entry point; numpy results."""
+        n = len(data)
+        caps = caps or decode_bounds(n)
+        cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
+        sizes = {"id": cp, "flags": cp, "status": cp, "name_off": cp + 1, "name_bytes": caps["cap_name_bytes"],
+                 "cat_id": cp, "cat_flags": cp, "cat_name_off": cp + 1, "cat_name_bytes": caps["cap_cat_name_bytes"],
+                 "photo_off": cp + 1, "url_off": cu + 1, "url_bytes": caps["cap_url_bytes"], "tag_off": cp + 1,
+                 "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
+        arrays = {k: np.zeros(max(1, v), dtype=DTYPES[k]) for k, v in sizes.items()}
+        cols = Columns(0, arrays, dict(caps))
+        if err_cap is None:
+            err_cap = n // 16 + 16
+        el = np.zeros(max(1, err_cap), np.uint64)
+        ec = np.zeros(max(1, err_cap), np.uint8)
+        buf = np.frombuffer(data, np.uint8) if n else np.zeros(1, np.uint8)
+        s = cols.struct()
+        res = DecodeResult()
+        self._check(self.L.pj_decode_host(self.ctx, C.c_void_p(buf.ctypes.data), n, C.byref(s),
+                                          C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap,
+                                          C.byref(res)))
+        t = self._trim(cols, res).to_host()
+        return t, el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res
