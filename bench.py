@@ -66,6 +66,52 @@ def encode_workload(codec, config, n, steps, warmup):
     return cols, res
 
 
+def decode_workload(codec, n, steps, warmup):
+    """NDJSON from the nested generator, 0.1% of lines corrupted."""
+    import numpy as np
+    import torch
+    import petjson as pj
+    log(f"[bench] generating config 4, {n} records")
+    cols = pj.generate(4, n)
+    dev = cols.to_device()
+    text = codec.encode(dev, pj.FORMAT_NDJSON)
+    host = text.cpu().numpy().copy()
+    del dev, text
+    torch.cuda.empty_cache()
+    lines, codes = pj.corrupt_ndjson(host, 0xBAD, 0.001)
+    data = torch.from_numpy(host).cuda()
+    sz = cols.sizes()
+    caps = {"cap_pets": n, "cap_name_bytes": sz["name_bytes"], "cap_cat_name_bytes": sz["cat_name_bytes"],
+            "cap_urls": sz["n_urls"], "cap_url_bytes": sz["url_bytes"], "cap_tags": sz["n_tags"],
+            "cap_tag_name_bytes": sz["tag_name_bytes"]}
+    bufs = codec.decode_buffers(caps, max(16, 2 * len(lines)))
+    for _ in range(warmup):
+        codec.decode(data, out=bufs)
+    torch.cuda.synchronize()
+    ti, tp = [], []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dcols, el, ec, res = codec.decode(data, out=bufs)
+        tm = codec.timings()            # [total, fill, index, host gap, fill, parse]
+        ti.append(tm[2])
+        tp.append(tm[5])
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ok = (res.n_errors == len(lines) and np.array_equal(el.cpu().numpy().astype(np.uint64), lines)
+          and np.array_equal(ec.cpu().numpy(), codes) and res.n_pets == n - len(lines))
+    out_bytes = sum(int(dcols[k].numel()) * dcols[k].element_size() for k in pj.COLS)
+    in_bytes = int(data.numel())
+    kidx, kpar = sum(ti) / len(ti), sum(tp) / len(tp)
+    r = {"records": int(res.n_lines), "records_per_s": res.n_lines / wall, "ms_per_step": wall * 1e3,
+         "input_bytes": in_bytes, "output_bytes": out_bytes, "input_GBps": in_bytes / wall / 1e9,
+         "alg_GBps": (in_bytes + out_bytes) / wall / 1e9,
+         "alg_frac_hbm": (in_bytes + out_bytes) / wall / 1e9 / HBM_PEAK_GBPS,
+         "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
+         "kernels": {"k_dec_index_ms": kidx, "k_dec_parse_ms": kpar,
+                     "k_dec_index_GBps": in_bytes / (kidx * 1e-3) / 1e9}}
+    return r
+
+
 def cpu_baseline_encode(cols_full, n_sample, budget_s=10.0):
     """Oracle (CPU restatement) encode on a bounded sample, one thread."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -92,6 +138,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="flat", choices=["flat", "nested"])
     ap.add_argument("--records", type=int, default=10_000_000)
+    ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     a = ap.parse_args()
@@ -111,6 +158,9 @@ def main():
         workloads[("nested" if other == 3 else "flat") + "_encode"] = r
     del cols
     torch.cuda.empty_cache()
+    if not a.no_extra:
+        workloads["ndjson_decode"] = decode_workload(codec, a.decode_records, max(3, a.steps // 2), 1)
+        torch.cuda.empty_cache()
     cpu = cpu_baseline_encode({"_config": cfg}, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
     alg = head["input_bytes"] + head["output_bytes"]
     achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9

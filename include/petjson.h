@@ -149,6 +149,8 @@ typedef struct pj_decode_result {
     uint64_t n_errors;            /* invalid records                           */
     uint64_t name_bytes, cat_name_bytes, n_urls, url_bytes, n_tags,
              tag_name_bytes;      /* column sizes written (or needed)          */
+    uint64_t n_general;           /* lines read by the general (non-canonical)
+                                     parser rather than the fast path          */
 } pj_decode_result;
 
 /* ----------------------------------------------------------------- context */

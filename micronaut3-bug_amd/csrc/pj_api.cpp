@@ -361,7 +361,6 @@ void pj_decode_bounds(uint64_t len, pj_pet_columns *c) {
 
 namespace {
 
-constexpr int VLB_STRIDE_HOST = 1 + 2 * PJ_DEC_NCNT;
 
 bool dec_cols_ok(const pj_pet_columns *o) {
     void *v[17];
@@ -385,10 +384,10 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
     uint64_t ls_cap = len / 128 + 16;
     for (int attempt = 0; attempt < 2; attempt++) {
         const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
-        const uint64_t gpar = (ls_cap + pj_dec_parse_block() - 1) / pj_dec_parse_block();
-        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | state_parse gpar*stride |
-        //                     special nblk64 | line_start ls_cap | bad (bytes)
-        const uint64_t o_dummy = 16, o_sidx = 48, o_spar = o_sidx + gidx, o_spec = o_spar + gpar * VLB_STRIDE_HOST,
+        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | special nblk64 |
+        //                     line_start ls_cap | bad (bytes)
+        // header: 0-1 tickets, 2 line count, 4-11 totals, 12 general-queue length
+        const uint64_t o_dummy = 16, o_sidx = 48, o_spec = o_sidx + gidx,
                        o_ls = o_spec + nblk64, o_bad = o_ls + ls_cap;
         const uint64_t bytes = o_bad * 8 + nblk64 + 64;
         PJ_HIP(ctx->index.ensure(bytes));
@@ -409,7 +408,6 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.err_cap = err_cap;
         P.totals = X + 4;
         P.state_idx = X + o_sidx;
-        P.state_parse = X + o_spar;
         P.tickets = reinterpret_cast<unsigned long long *>(X);
         P.dummy = reinterpret_cast<uint32_t *>(X + o_dummy);
         ctx->n_ev = 0;
@@ -427,9 +425,18 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             continue;
         }
         P.lines = lines;
-        const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
+        const uint64_t lb = (uint64_t)pj_dec_parse_block();
+        const uint64_t gp = (lines + lb - 1) / lb;
+        // line-sized scratch: records | general queue | block sums
+        PJ_HIP(ctx->scan.ensure(lines * sizeof(LineRec) + lines * 8 + gp * PJ_DEC_NCNT * 8 + 1024));
+        uint8_t *Y = static_cast<uint8_t *>(ctx->scan.p);
+        P.rec = reinterpret_cast<LineRec *>(Y);
+        P.gq = reinterpret_cast<uint64_t *>(Y + align256(lines * sizeof(LineRec)));
+        P.bagg = reinterpret_cast<uint64_t *>(Y + align256(lines * sizeof(LineRec)) + align256(lines * 8));
+        P.gq_count = reinterpret_cast<unsigned long long *>(X + 12);
+        P.line_block = lb;
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(X + o_spar, gp * VLB_STRIDE_HOST, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(X + 12, 1, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
         if (lines) PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
         else {
@@ -439,11 +446,11 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
         }
         if ((s = mark(ctx))) return s;
-        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 4, PJ_DEC_NCNT * sizeof(uint64_t), hipMemcpyDeviceToHost,
-                              ctx->stream));
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 4, 9 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));
         if ((s = finish_timing(ctx))) return s;
         const uint64_t *T = ctx->pinned;
+        res->n_general = lines ? ctx->pinned[8] : 0;
         res->n_lines = lines;
         if (lines) {
             res->n_pets = T[C_PETS];

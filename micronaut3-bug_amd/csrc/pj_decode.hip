@@ -270,8 +270,15 @@ __global__ __launch_bounds__(BT) void k_dec_index(DecParams P) {
 }
 
 // =========================================================== stage 2
+// Property keys, container contexts and parser states.
 enum { K_UNKNOWN = 0, K_ID, K_CATEGORY, K_NAME, K_PHOTOURLS, K_TAGS, K_STATUS };
+enum { X_NONE = 0, X_PET, X_CAT, X_URLS, X_TAGS, X_TAG, X_SKIP };
+enum { S_VALUE = 0, S_KEY_OR_CLOSE, S_KEY, S_COLON, S_ELEM_OR_CLOSE, S_AFTER, S_DONE };
+// what a string value is read for
+enum { U_NONE = 0, U_KEY, U_NAME, U_SUBNAME, U_URL, U_STATUS, U_SKIP };
 
+// Per-line results of the validating pass (last occurrence of each
+// property), reused by the materialising pass.
 struct LineInfo {
     int64_t id, cat_id;
     uint32_t name_pos, name_len, cat_pos, cat_len, photo_pos, n_urls, url_bytes, tags_pos, n_tags, tag_bytes;
@@ -301,24 +308,144 @@ __device__ __forceinline__ uint32_t utf8_pack(uint32_t cp, int *k) {
            ((0x80u | (cp & 63)) << 24);
 }
 
-// Line parser.  SLOW validates every string byte itself; otherwise string
-// contents are trusted (stage 1 flagged none) and skipped via the bitmap.
-template <bool SLOW>
-struct LP {
-    const uint8_t *in;
-    uint64_t len;            // whole input length
-    const uint64_t *special;
-    uint64_t s0;             // absolute start of the line
-    uint32_t n;              // line length (without '\n')
-    uint32_t p;              // cursor, relative to s0
-    int depth;
-    uint64_t wlo, whi;       // 16-byte window [wp, wp+16)
-    uint32_t wp;
-
-    __device__ __forceinline__ void init(const DecParams &P, uint64_t start, uint32_t nn) {
-        in = P.in; len = P.len; special = P.special; s0 = start; n = nn; p = 0; depth = 0;
-        wp = 0xFFFFFF00u; wlo = whi = 0;
+// Escape sequence at line offset q (a backslash).  Rare, so out of line and
+// reading bytes straight from memory.
+struct Esc {
+    int err;
+    uint32_t adv;     // bytes consumed
+    uint32_t out;     // decoded UTF-8 bytes, little endian
+    int k;            // how many
+};
+__device__ __noinline__ Esc escape_at(const uint8_t *s, uint32_t n, uint32_t q) {
+    Esc r{PJ_REC_STRING, 2, 0, 1};
+    if (q + 1 >= n) return r;
+    switch (s[q + 1]) {
+    case '"': r.out = '"'; break;
+    case '\\': r.out = '\\'; break;
+    case '/': r.out = '/'; break;
+    case 'b': r.out = 8; break;
+    case 'f': r.out = 12; break;
+    case 'n': r.out = 10; break;
+    case 'r': r.out = 13; break;
+    case 't': r.out = 9; break;
+    case 'u': {
+        if (q + 6 > n) return r;
+        uint32_t cu = 0;
+        for (int j = 0; j < 4; j++) {
+            int h = hexval(s[q + 2 + j]);
+            if (h < 0) return r;
+            cu = cu * 16 + (uint32_t)h;
+        }
+        r.adv = 6;
+        if (cu >= 0xDC00 && cu <= 0xDFFF) return r;                  // lone low surrogate
+        if (cu >= 0xD800 && cu <= 0xDBFF) {                           // needs \uDC00-\uDFFF next
+            if (q + 12 > n || s[q + 6] != '\\' || s[q + 7] != 'u') return r;
+            uint32_t lo = 0;
+            for (int j = 0; j < 4; j++) {
+                int h = hexval(s[q + 8 + j]);
+                if (h < 0) return r;
+                lo = lo * 16 + (uint32_t)h;
+            }
+            if (lo < 0xDC00 || lo > 0xDFFF) return r;
+            cu = 0x10000 + ((cu - 0xD800) << 10) + (lo - 0xDC00);
+            r.adv = 12;
+        }
+        r.out = utf8_pack(cu, &r.k);
+        break;
     }
+    default: return r;
+    }
+    r.err = 0;
+    return r;
+}
+
+struct Str {
+    int err;
+    uint32_t end;     // closing quote
+    uint32_t dlen;    // decoded length
+    bool esc;         // holds escapes
+};
+// Byte-by-byte string scan with full validation (lines whose blocks stage 1
+// flagged): raw control characters, jackson's UTF-8 lead / continuation rules.
+__device__ __noinline__ Str scan_slow(const uint8_t *s, uint32_t n, uint32_t q) {
+    Str r{PJ_REC_STRING, 0, 0, false};
+    uint32_t pos = q + 1, d = 0;
+    for (;;) {
+        if (pos >= n) return r;
+        uint32_t c = s[pos];
+        if (c == '"') break;
+        if (c == '\\') {
+            Esc e = escape_at(s, n, pos);
+            if (e.err) return r;
+            d += (uint32_t)e.k;
+            pos += e.adv;
+            r.esc = true;
+            continue;
+        }
+        if (c < 0x20) return r;
+        uint32_t extra;
+        if (c < 0x80) extra = 0;
+        else if (c >= 0xC0 && c <= 0xDF) extra = 1;
+        else if (c >= 0xE0 && c <= 0xEF) extra = 2;
+        else if (c >= 0xF0 && c <= 0xF7) extra = 3;
+        else return r;
+        if (pos + 1 + extra > n) return r;
+        for (uint32_t j = 1; j <= extra; j++)
+            if ((s[pos + j] & 0xC0) != 0x80) return r;
+        d += 1 + extra;
+        pos += 1 + extra;
+    }
+    r.err = 0;
+    r.end = pos;
+    r.dlen = d;
+    return r;
+}
+
+// First 16 decoded bytes of a validated string with escapes.
+__device__ __noinline__ uint2 small_decode_esc(const uint8_t *s, uint32_t q, uint32_t end, uint32_t n, uint64_t *hi) {
+    uint64_t v[2] = {0, 0};
+    uint32_t pos = q + 1, o = 0;
+    while (pos < end && o < 16) {
+        uint32_t bytes = s[pos], adv = 1;
+        int k = 1;
+        if (bytes == '\\') {
+            Esc e = escape_at(s, n, pos);
+            bytes = e.out;
+            adv = e.adv;
+            k = e.k;
+        }
+        for (int j = 0; j < k && o < 16; j++, o++) v[o >> 3] |= (uint64_t)((bytes >> (8 * j)) & 0xFF) << (8 * (o & 7));
+        pos += adv;
+    }
+    *hi = v[1];
+    return make_uint2((uint32_t)v[0], (uint32_t)(v[0] >> 32));
+}
+
+// Is the innermost container open at nesting level d (1-based), seen at
+// cursor p, an object?  Used beyond the 64 levels the register stack holds.
+__device__ __noinline__ bool opener_at(const uint8_t *s, uint32_t p, int d) {
+    int lvl = 0;
+    bool kind = false, instr = false;
+    for (uint32_t q = 0; q < p; q++) {
+        uint32_t c = s[q];
+        if (instr) {
+            if (c == '\\') q++;
+            else if (c == '"') instr = false;
+            continue;
+        }
+        if (c == '"') instr = true;
+        else if (c == '{' || c == '[') { lvl++; if (lvl == d) kind = c == '{'; }
+        else if (c == '}' || c == ']') lvl--;
+    }
+    return kind;
+}
+
+// 16-byte window over a line for the skeleton bytes.
+struct Win {
+    const uint8_t *in;
+    uint64_t len, s0;
+    uint64_t wlo, whi;
+    uint32_t wp;
     __device__ __forceinline__ void refill(uint32_t q) {
         const uint64_t a = s0 + q;
         wp = q;
@@ -333,447 +460,31 @@ struct LP {
             }
         }
     }
-    __device__ __forceinline__ int at(uint32_t q) {   // q < n
+    __device__ __forceinline__ int at(uint32_t q) {
         if (q - wp >= 16) refill(q);
         const uint32_t d = q - wp;
         return (int)(((d < 8 ? wlo : whi) >> (8 * (d & 7))) & 0xFF);
     }
-    __device__ __forceinline__ int peek() { return p < n ? at(p) : -1; }
-    __device__ __forceinline__ void skip_ws() {
-        while (p < n) {
-            int c = at(p);
-            if (c != ' ' && c != '\t' && c != '\r') break;
-            p++;
-        }
-    }
-    // first unescaped quote or backslash at or after q (n if none)
-    __device__ __forceinline__ uint32_t next_special(uint32_t q) {
-        const uint64_t a = s0 + q, lim = s0 + n;
-        if (a >= lim) return n;
-        uint64_t wi = a >> 6;
-        uint64_t m = special[wi] & (~0ull << (a & 63));
-        while (!m) {
-            wi++;
-            if (wi * 64 >= lim) return n;
-            m = special[wi];
-        }
-        const uint64_t pos = wi * 64 + (uint64_t)__builtin_ctzll(m);
-        return pos >= lim ? n : (uint32_t)(pos - s0);
-    }
-    // escape sequence at q ('\\'): *adv bytes consumed, decoded bytes packed
-    // in *out (*k of them)
-    __device__ __forceinline__ int escape_at(uint32_t q, uint32_t *adv, uint32_t *out, int *k) {
-        if (q + 1 >= n) return PJ_REC_STRING;
-        int e = at(q + 1);
-        *k = 1;
-        *adv = 2;
-        switch (e) {
-        case '"': *out = '"'; return 0;
-        case '\\': *out = '\\'; return 0;
-        case '/': *out = '/'; return 0;
-        case 'b': *out = 8; return 0;
-        case 'f': *out = 12; return 0;
-        case 'n': *out = 10; return 0;
-        case 'r': *out = 13; return 0;
-        case 't': *out = 9; return 0;
-        case 'u': break;
-        default: return PJ_REC_STRING;
-        }
-        if (q + 6 > n) return PJ_REC_STRING;
-        uint32_t cu = 0;
-        for (int j = 0; j < 4; j++) {
-            int h = hexval(at(q + 2 + j));
-            if (h < 0) return PJ_REC_STRING;
-            cu = cu * 16 + (uint32_t)h;
-        }
-        *adv = 6;
-        if (cu >= 0xDC00 && cu <= 0xDFFF) return PJ_REC_STRING;
-        if (cu >= 0xD800 && cu <= 0xDBFF) {
-            if (q + 8 > n || at(q + 6) != '\\' || at(q + 7) != 'u') return PJ_REC_STRING;
-            if (q + 12 > n) return PJ_REC_STRING;
-            uint32_t lo = 0;
-            for (int j = 0; j < 4; j++) {
-                int h = hexval(at(q + 8 + j));
-                if (h < 0) return PJ_REC_STRING;
-                lo = lo * 16 + (uint32_t)h;
-            }
-            if (lo < 0xDC00 || lo > 0xDFFF) return PJ_REC_STRING;
-            cu = 0x10000 + ((cu - 0xD800) << 10) + (lo - 0xDC00);
-            *adv = 12;
-        }
-        *out = utf8_pack(cu, k);
-        return 0;
-    }
-    // string whose opening quote is at q: closing quote position, decoded
-    // length, whether it holds escapes
-    __device__ int str_scan(uint32_t q, uint32_t *end, uint32_t *dlen, bool *esc) {
-        uint32_t pos = q + 1, d = 0;
-        bool es = false;
-        if (SLOW) {
-            for (;;) {
-                if (pos >= n) return PJ_REC_STRING;
-                int c = at(pos);
-                if (c == '"') break;
-                if (c == '\\') {
-                    uint32_t adv, o;
-                    int k;
-                    int e = escape_at(pos, &adv, &o, &k);
-                    if (e) return e;
-                    d += (uint32_t)k;
-                    pos += adv;
-                    es = true;
-                    continue;
-                }
-                if (c < 0x20) return PJ_REC_STRING;
-                int extra;
-                if (c < 0x80) extra = 0;
-                else if (c >= 0xC0 && c <= 0xDF) extra = 1;
-                else if (c >= 0xE0 && c <= 0xEF) extra = 2;
-                else if (c >= 0xF0 && c <= 0xF7) extra = 3;
-                else return PJ_REC_STRING;
-                if (pos + 1 + (uint32_t)extra > n) return PJ_REC_STRING;
-                for (int j = 1; j <= extra; j++)
-                    if ((at(pos + j) & 0xC0) != 0x80) return PJ_REC_STRING;
-                d += 1 + (uint32_t)extra;
-                pos += 1 + (uint32_t)extra;
-            }
-        } else {
-            for (;;) {
-                uint32_t sp = next_special(pos);
-                if (sp >= n) return PJ_REC_STRING;
-                d += sp - pos;
-                if (at(sp) == '"') { pos = sp; break; }
-                uint32_t adv, o;
-                int k;
-                int e = escape_at(sp, &adv, &o, &k);
-                if (e) return e;
-                d += (uint32_t)k;
-                pos = sp + adv;
-                es = true;
-            }
-        }
-        *end = pos;
-        *dlen = d;
-        *esc = es;
-        return 0;
-    }
-    // decoded bytes of a (validated) string, first 16 of them
-    __device__ void small_decode(uint32_t q, uint32_t end, bool esc, uint64_t *lo, uint64_t *hi) {
-        uint64_t v[2] = {0, 0};
-        uint32_t pos = q + 1, o = 0;
-        while (pos < end && o < 16) {
-            int c = at(pos);
-            uint32_t bytes = (uint32_t)c, adv = 1;
-            int k = 1;
-            if (esc && c == '\\') escape_at(pos, &adv, &bytes, &k);
-            for (int j = 0; j < k && o < 16; j++, o++) v[o >> 3] |= (uint64_t)((bytes >> (8 * j)) & 0xFF) << (8 * (o & 7));
-            pos += adv;
-        }
-        *lo = v[0];
-        *hi = v[1];
-    }
-    // number grammar; *real when a fraction or exponent is present
-    __device__ int rd_number(bool *real) {
-        uint32_t q = p;
-        bool r = false;
-        if (q < n && at(q) == '-') q++;
-        if (q >= n) return PJ_REC_SYNTAX;
-        int c = at(q);
-        if (c == '0') {
-            q++;
-            if (q < n && at(q) >= '0' && at(q) <= '9') return PJ_REC_SYNTAX;
-        } else if (c >= '1' && c <= '9') {
-            while (q < n && at(q) >= '0' && at(q) <= '9') q++;
-        } else return PJ_REC_SYNTAX;
-        if (q < n && at(q) == '.') {
-            q++;
-            r = true;
-            if (q >= n || at(q) < '0' || at(q) > '9') return PJ_REC_SYNTAX;
-            while (q < n && at(q) >= '0' && at(q) <= '9') q++;
-        }
-        if (q < n && (at(q) == 'e' || at(q) == 'E')) {
-            q++;
-            r = true;
-            if (q < n && (at(q) == '+' || at(q) == '-')) q++;
-            if (q >= n || at(q) < '0' || at(q) > '9') return PJ_REC_SYNTAX;
-            while (q < n && at(q) >= '0' && at(q) <= '9') q++;
-        }
-        p = q;
-        *real = r;
-        return 0;
-    }
-    // literal or number; *kind: 0 null, 1 true, 2 false, 3 int, 4 real
-    __device__ int rd_scalar(int *kind) {
-        int c = peek();
-        if (c == '-' || (c >= '0' && c <= '9')) {
-            bool real;
-            int e = rd_number(&real);
-            *kind = real ? 4 : 3;
-            return e;
-        }
-        uint32_t L;
-        uint64_t want;
-        if (c == 'n') { L = 4; want = 0x6C6C756Eull; *kind = 0; }
-        else if (c == 't') { L = 4; want = 0x65757274ull; *kind = 1; }
-        else if (c == 'f') { L = 5; want = 0x65736C6166ull; *kind = 2; }
-        else return PJ_REC_SYNTAX;
-        if (p + L > n) return PJ_REC_SYNTAX;
-        for (uint32_t j = 0; j < L; j++)
-            if ((uint64_t)at(p + j) != ((want >> (8 * j)) & 0xFF)) return PJ_REC_SYNTAX;
-        if (p + L < n && is_ident(at(p + L))) return PJ_REC_SYNTAX;
-        p += L;
-        return 0;
-    }
-    __device__ int type_mismatch() {
-        int c = peek();
-        if (c == '"' || c == '{' || c == '[') return PJ_REC_TYPE;
-        int kind;
-        int e = rd_scalar(&kind);
-        return e ? e : PJ_REC_TYPE;
-    }
-    // null literal at the cursor? (consumes it)  1 = null, 0 = not null, <0 error
-    __device__ int rd_null_or_mismatch(int *err) {
-        int kind;
-        int e = rd_scalar(&kind);
-        if (e) { *err = e; return -1; }
-        if (kind != 0) { *err = PJ_REC_TYPE; return -1; }
-        return 1;
-    }
-    // int64 value or null
-    __device__ int rd_long(int64_t *v, bool *present) {
-        int c = peek();
-        if (c == 'n') {
-            int err = 0;
-            if (rd_null_or_mismatch(&err) < 0) return err;
-            *present = false;
-            return 0;
-        }
-        if (!(c == '-' || (c >= '0' && c <= '9'))) return type_mismatch();
-        const uint32_t start = p;
-        bool real;
-        int e = rd_number(&real);
-        if (e) return e;
-        if (real) return PJ_REC_NUMBER;
-        const bool neg = at(start) == '-';
-        const uint64_t lim = neg ? (1ull << 63) : ((1ull << 63) - 1);
-        uint64_t acc = 0;
-        for (uint32_t q = start + (neg ? 1 : 0); q < p; q++) {
-            uint64_t d = (uint64_t)(at(q) - '0');
-            if (acc > (lim - d) / 10) return PJ_REC_NUMBER;
-            acc = acc * 10 + d;
-        }
-        *v = neg ? (int64_t)(0ull - acc) : (int64_t)acc;
-        *present = true;
-        return 0;
-    }
-    __device__ int open_container() {
-        if (++depth > PJ_MAX_DEPTH) return PJ_REC_DEPTH;
-        p++;
-        skip_ws();
-        return 0;
-    }
-    // kind of the innermost container still open at local nesting level d
-    // (1-based) of a value that starts at v0: object = true.  Used beyond the
-    // 64 levels the register stack holds.
-    __device__ bool opener_at(uint32_t v0, int d) {
-        int lvl = 0;
-        bool kind = false, instr = false;
-        for (uint32_t q = v0; q < p; q++) {
-            int c = at(q);
-            if (instr) {
-                if (c == '\\') q++;
-                else if (c == '"') instr = false;
-                continue;
-            }
-            if (c == '"') instr = true;
-            else if (c == '{' || c == '[') { lvl++; if (lvl == d) kind = c == '{'; }
-            else if (c == '}' || c == ']') lvl--;
-        }
-        return kind;
-    }
-    // skip any JSON value (validated), iteratively
-    __device__ int skip_value() {
-        int c = peek();
-        if (c == '"') {
-            uint32_t end, dl;
-            bool es;
-            int e = str_scan(p, &end, &dl, &es);
-            if (e) return e;
-            p = end + 1;
-            return 0;
-        }
-        if (c != '{' && c != '[') {
-            int kind;
-            return rd_scalar(&kind);
-        }
-        const uint32_t v0 = p;
-        uint64_t stack = 0;
-        int d = 0;
-        enum { S_OPEN, S_KEY, S_VALUE, S_AFTER } state = S_OPEN;
-        for (;;) {
-            switch (state) {
-            case S_OPEN: {
-                c = peek();
-                const bool obj = c == '{';
-                if (d < 64) stack = obj ? (stack | (1ull << d)) : (stack & ~(1ull << d));
-                d++;
-                int e = open_container();
-                if (e) return e;
-                c = peek();
-                if (c == (obj ? '}' : ']')) { p++; depth--; d--; if (d == 0) return 0; state = S_AFTER; }
-                else state = obj ? S_KEY : S_VALUE;
-                break;
-            }
-            case S_KEY: {
-                skip_ws();
-                if (peek() != '"') return PJ_REC_SYNTAX;
-                uint32_t end, dl;
-                bool es;
-                int e = str_scan(p, &end, &dl, &es);
-                if (e) return e;
-                p = end + 1;
-                skip_ws();
-                if (peek() != ':') return PJ_REC_SYNTAX;
-                p++;
-                skip_ws();
-                if (p >= n) return PJ_REC_SYNTAX;
-                state = S_VALUE;
-                break;
-            }
-            case S_VALUE: {
-                skip_ws();
-                c = peek();
-                if (c < 0) return PJ_REC_SYNTAX;
-                if (c == '{' || c == '[') { state = S_OPEN; break; }
-                if (c == '"') {
-                    uint32_t end, dl;
-                    bool es;
-                    int e = str_scan(p, &end, &dl, &es);
-                    if (e) return e;
-                    p = end + 1;
-                } else {
-                    int kind;
-                    int e = rd_scalar(&kind);
-                    if (e) return e;
-                }
-                state = S_AFTER;
-                break;
-            }
-            case S_AFTER: {
-                skip_ws();
-                c = peek();
-                const bool obj = d <= 64 ? ((stack >> (d - 1)) & 1) : opener_at(v0, d);
-                if (c == ',') { p++; state = obj ? S_KEY : S_VALUE; break; }
-                if (c == (obj ? '}' : ']')) {
-                    p++;
-                    depth--;
-                    d--;
-                    if (d == 0) return 0;
-                    break;
-                }
-                return PJ_REC_SYNTAX;
-            }
-            }
-        }
-    }
-    // member loop helpers: after '{' consumed by open_container
-    //   returns 1 = a member key was read (key id in *key, cursor at value),
-    //   0 = object closed, <0 = -error
-    __device__ int first_member(int *key, bool *more) {
-        if (peek() == '}') { p++; depth--; *more = false; return 0; }
-        *more = true;
-        return read_key(key);
-    }
-    __device__ int next_member(int *key, bool *more) {
-        skip_ws();
-        int c = peek();
-        if (c == ',') { p++; *more = true; return read_key(key); }
-        if (c == '}') { p++; depth--; *more = false; return 0; }
-        return PJ_REC_SYNTAX;
-    }
-    __device__ int read_key(int *key) {
-        skip_ws();
-        if (peek() != '"') return PJ_REC_SYNTAX;
-        uint32_t end, dl;
-        bool es;
-        int e = str_scan(p, &end, &dl, &es);
-        if (e) return e;
-        *key = K_UNKNOWN;
-        if (dl == 2 || dl == 4 || dl == 6 || dl == 8 || dl == 9) {
-            uint64_t lo, hi;
-            small_decode(p, end, es, &lo, &hi);
-            if (dl == 2 && lo == 0x6469ull) *key = K_ID;                                   // id
-            else if (dl == 8 && lo == 0x79726F6765746163ull) *key = K_CATEGORY;            // category
-            else if (dl == 4 && lo == 0x656D616Eull) *key = K_NAME;                        // name
-            else if (dl == 9 && lo == 0x6C72556F746F6870ull && hi == 0x73ull) *key = K_PHOTOURLS;  // photoUrls
-            else if (dl == 4 && lo == 0x73676174ull) *key = K_TAGS;                        // tags
-            else if (dl == 6 && lo == 0x737574617473ull) *key = K_STATUS;                  // status
-        }
-        p = end + 1;
-        skip_ws();
-        if (peek() != ':') return PJ_REC_SYNTAX;
-        p++;
-        skip_ws();
-        if (p >= n) return PJ_REC_SYNTAX;
-        return 0;
-    }
-    // string property: string or null
-    __device__ int rd_str_prop(bool *present, uint32_t *pos, uint32_t *dlen, bool *esc) {
-        int c = peek();
-        if (c == '"') {
-            uint32_t end;
-            int e = str_scan(p, &end, dlen, esc);
-            if (e) return e;
-            *pos = p;
-            *present = true;
-            p = end + 1;
-            return 0;
-        }
-        if (c == 'n') {
-            int err = 0;
-            if (rd_null_or_mismatch(&err) < 0) return err;
-            *present = false;
-            return 0;
-        }
-        return type_mismatch();
-    }
-    // Category / Tag object (cursor at '{'): last id / name win
-    __device__ int rd_sub(int64_t *id, uint8_t *fl, uint32_t *name_len) {
-        int e = open_container();
-        if (e) return e;
-        *id = 0;
-        *fl = 0;
-        *name_len = 0;
-        int key;
-        bool more;
-        e = first_member(&key, &more);
-        while (!e && more) {
-            if (key == K_ID) {
-                int64_t v = 0;
-                bool pr;
-                e = rd_long(&v, &pr);
-                if (e) return e;
-                *id = pr ? v : 0;
-                *fl = pr ? (*fl | PJ_SUB_HAS_ID) : (*fl & ~PJ_SUB_HAS_ID);
-            } else if (key == K_NAME) {
-                bool pr;
-                uint32_t pos, dl;
-                bool es;
-                e = rd_str_prop(&pr, &pos, &dl, &es);
-                if (e) return e;
-                *name_len = pr ? dl : 0;
-                *fl = pr ? (*fl | PJ_SUB_HAS_NAME) : (*fl & ~PJ_SUB_HAS_NAME);
-            } else {
-                e = skip_value();
-                if (e) return e;
-            }
-            e = next_member(&key, &more);
-        }
-        return e;
-    }
+};
 
-    // ---- validating pass over the whole line
-    __device__ int parse(LineInfo &L) {
+// One pass over one line.  write == false validates and measures (returns
+// the PJ_REC_* code and fills L); write == true materialises a line the
+// first pass found valid, at the offsets pos[].  Strings are skipped through
+// the specials bitmap unless `slow`.  One string-scan site, one copy site
+// and one scalar site keep the whole machine in registers.
+__device__ __forceinline__ int run_line(const DecParams &P, uint64_t s0, uint32_t n, bool slow, bool write,
+                                        LineInfo &L, const uint64_t *pos) {
+    const uint8_t *s = P.in + s0;
+    Win W{P.in, P.len, s0, 0, 0, 0xFFFFFF00u};
+    uint32_t p = 0;
+#define PEEK() (p < n ? W.at(p) : -1)
+#define SKIP_WS()                                                \
+    while (p < n) {                                              \
+        const int c_ = W.at(p);                                  \
+        if (c_ != ' ' && c_ != '\t' && c_ != '\r') break;        \
+        p++;                                                     \
+    }
+    if (!write) {
         L.has_id = L.has_cat = L.has_name = L.has_photo = L.has_tags = 0;
         L.id = L.cat_id = 0;
         L.cat_flags = 0;
@@ -781,412 +492,934 @@ struct LP {
         L.name_len = L.cat_len = L.n_urls = L.url_bytes = L.n_tags = L.tag_bytes = 0;
         L.name_pos = L.cat_pos = L.photo_pos = L.tags_pos = 0;
         L.name_esc = 0;
-        skip_ws();
-        if (p >= n) return PJ_REC_EMPTY;
-        if (peek() != '{') return type_mismatch();
-        int e = open_container();
-        if (e) return e;
-        int key;
-        bool more;
-        e = first_member(&key, &more);
-        while (!e && more) {
-            const int c = peek();
-            switch (key) {
-            case K_ID: {
-                int64_t v = 0;
-                bool pr = false;
-                e = rd_long(&v, &pr);
-                L.has_id = pr;
-                L.id = pr ? v : 0;
-                break;
-            }
-            case K_CATEGORY:
-                if (c == '{') {
-                    L.has_cat = 1;
-                    L.cat_pos = p;
-                    e = rd_sub(&L.cat_id, &L.cat_flags, &L.cat_len);
-                } else if (c == 'n') {
-                    int err = 0;
-                    if (rd_null_or_mismatch(&err) < 0) e = err;
-                    else { L.has_cat = 0; L.cat_id = 0; L.cat_flags = 0; L.cat_len = 0; }
-                } else e = type_mismatch();
-                break;
-            case K_NAME: {
-                bool pr = false, es = false;
-                uint32_t pos = 0, dl = 0;
-                e = rd_str_prop(&pr, &pos, &dl, &es);
-                L.has_name = pr;
-                L.name_pos = pos;
-                L.name_len = pr ? dl : 0;
-                L.name_esc = es;
-                break;
-            }
-            case K_PHOTOURLS:
-                if (c == '[') {
-                    L.has_photo = 1;
-                    L.photo_pos = p;
-                    L.n_urls = 0;
-                    L.url_bytes = 0;
-                    e = open_container();
-                    if (e) break;
-                    if (peek() == ']') { p++; depth--; break; }
-                    for (;;) {
-                        skip_ws();
-                        if (peek() != '"') { e = p >= n ? PJ_REC_SYNTAX : type_mismatch(); break; }
-                        uint32_t end, dl;
-                        bool es;
-                        e = str_scan(p, &end, &dl, &es);
-                        if (e) break;
-                        p = end + 1;
-                        L.n_urls++;
-                        L.url_bytes += dl;
-                        skip_ws();
-                        int d = peek();
-                        if (d == ',') { p++; continue; }
-                        if (d == ']') { p++; depth--; break; }
-                        e = PJ_REC_SYNTAX;
-                        break;
-                    }
-                } else if (c == 'n') {
-                    int err = 0;
-                    if (rd_null_or_mismatch(&err) < 0) e = err;
-                    else { L.has_photo = 0; L.n_urls = 0; L.url_bytes = 0; }
-                } else e = type_mismatch();
-                break;
-            case K_TAGS:
-                if (c == '[') {
-                    L.has_tags = 1;
-                    L.tags_pos = p;
-                    L.n_tags = 0;
-                    L.tag_bytes = 0;
-                    e = open_container();
-                    if (e) break;
-                    if (peek() == ']') { p++; depth--; break; }
-                    for (;;) {
-                        skip_ws();
-                        if (peek() != '{') { e = p >= n ? PJ_REC_SYNTAX : type_mismatch(); break; }
-                        int64_t tid;
-                        uint8_t tfl;
-                        uint32_t tl;
-                        e = rd_sub(&tid, &tfl, &tl);
-                        if (e) break;
-                        L.n_tags++;
-                        L.tag_bytes += tl;
-                        skip_ws();
-                        int d = peek();
-                        if (d == ',') { p++; continue; }
-                        if (d == ']') { p++; depth--; break; }
-                        e = PJ_REC_SYNTAX;
-                        break;
-                    }
-                } else if (c == 'n') {
-                    int err = 0;
-                    if (rd_null_or_mismatch(&err) < 0) e = err;
-                    else { L.has_tags = 0; L.n_tags = 0; L.tag_bytes = 0; }
-                } else e = type_mismatch();
-                break;
-            case K_STATUS: {
-                bool pr = false, es = false;
-                uint32_t pos = 0, dl = 0;
-                e = rd_str_prop(&pr, &pos, &dl, &es);
-                if (e) break;
-                if (!pr) { L.status = PJ_STATUS_NULL; break; }
-                uint64_t lo = 0, hi = 0;
-                if (dl == 9 || dl == 7 || dl == 4) {
-                    uint32_t end = p - 1;   // closing quote
-                    small_decode(pos, end, es, &lo, &hi);
-                }
-                if (dl == 9 && lo == 0x6C62616C69617661ull && hi == 0x65ull) L.status = PJ_STATUS_AVAILABLE;
-                else if (dl == 7 && lo == 0x676E69646E6570ull) L.status = PJ_STATUS_PENDING;
-                else if (dl == 4 && lo == 0x646C6F73ull) L.status = PJ_STATUS_SOLD;
-                else e = PJ_REC_BAD_STATUS;
-                break;
-            }
-            default:
-                e = skip_value();
-            }
-            if (e) break;
-            e = next_member(&key, &more);
-        }
-        if (e) return e;
-        if (!L.has_name) return PJ_REC_MISSING_NAME;
-        if (!L.has_photo) return PJ_REC_MISSING_PHOTOURLS;
-        skip_ws();
-        if (p < n) return PJ_REC_SYNTAX;
-        return 0;
     }
+    SKIP_WS();
+    if (p >= n) return PJ_REC_EMPTY;
+    int depth = 0;
+    uint64_t stk = 0;           // bit d-1: container at depth d is an object
+    uint32_t sem = 0;           // 4 bits per depth 1..3: X_* context
+    int state = S_VALUE, k1 = K_UNKNOWN, k2 = K_UNKNOWN;
+    int64_t sub_id = 0;         // Category / Tag being read
+    uint32_t sub_fl = 0, sub_len = 0, sub_q = 0;
+    bool sub_esc = false;
+    uint32_t cat_q = 0;         // '{' of the category being read
+    bool last_urls = false, last_tags = false;
+    const pj_pet_columns &o = P.o;
+    uint64_t u_idx = write ? pos[C_URLS] : 0, u_b = write ? pos[C_URLB] : 0;
+    uint64_t g_idx = write ? pos[C_TAGS] : 0, g_b = write ? pos[C_TAGB] : 0;
 
-    // ---- materialisation helpers (line known valid)
-    // copy the decoded string whose opening quote is at q into ws
-    __device__ void copy_str(uint32_t q, WriteSink &ws) {
-        uint32_t end, dl;
-        bool es;
-        str_scan(q, &end, &dl, &es);
-        uint32_t pos = q + 1;
-        if (!es) {
-            const uint8_t *src = in + s0 + pos;
-            uint32_t L = end - pos, k = 0;
-            for (; k + 8 <= L; k += 8) ws.put8(ldu64(src + k), 8);
-            if (k < L) ws.put8(ld_tail(src + k, (int)(L - k)), (int)(L - k));
-            return;
-        }
-        while (pos < end) {
-            int c = at(pos);
-            if (c == '\\') {
-                uint32_t adv, o;
-                int k;
-                escape_at(pos, &adv, &o, &k);
-                ws.put(o, k);
-                pos += adv;
-            } else {
-                ws.put_byte((uint32_t)c);
-                pos++;
+    for (;;) {
+        SKIP_WS();
+        int c = PEEK();
+        if (state == S_DONE) return c < 0 ? 0 : PJ_REC_SYNTAX;
+        const int ctx = depth == 0 ? X_NONE : depth <= 3 ? (int)((sem >> (4 * (depth - 1))) & 15) : X_SKIP;
+        // ---- decide what this token is for
+        int use = U_NONE;          // string use
+        int push = X_NONE;         // container to open
+        bool close = false, scalar = false;
+        // value rules
+        bool v_any = false, v_null = false, v_long = false;
+        int v_obj = X_NONE, v_arr = X_NONE, v_str = U_NONE;
+        switch (state) {
+        case S_KEY_OR_CLOSE:
+            if (c == '}') { close = true; break; }
+            [[fallthrough]];
+        case S_KEY:
+            if (c != '"') return PJ_REC_SYNTAX;
+            use = U_KEY;
+            break;
+        case S_COLON:
+            if (c != ':') return PJ_REC_SYNTAX;
+            p++;
+            SKIP_WS();
+            if (p >= n) return PJ_REC_SYNTAX;
+            state = S_VALUE;
+            continue;
+        case S_ELEM_OR_CLOSE:
+            if (c == ']') { close = true; break; }
+            [[fallthrough]];
+        case S_VALUE:
+            if (c < 0) return PJ_REC_SYNTAX;
+            if (ctx == X_NONE) v_obj = X_PET;
+            else if (ctx == X_PET) {
+                switch (k1) {
+                case K_ID: v_long = v_null = true; break;
+                case K_CATEGORY: v_obj = X_CAT; v_null = true; break;
+                case K_NAME: v_str = U_NAME; v_null = true; break;
+                case K_PHOTOURLS: v_arr = X_URLS; v_null = true; break;
+                case K_TAGS: v_arr = X_TAGS; v_null = true; break;
+                case K_STATUS: v_str = U_STATUS; v_null = true; break;
+                default: v_any = true;
+                }
+            } else if (ctx == X_CAT || ctx == X_TAG) {
+                if (k2 == K_ID) v_long = v_null = true;
+                else if (k2 == K_NAME) { v_str = U_SUBNAME; v_null = true; }
+                else v_any = true;
+            } else if (ctx == X_URLS) v_str = U_URL;
+            else if (ctx == X_TAGS) v_obj = X_TAG;
+            else v_any = true;
+            if (c == '{') {
+                if (v_any) push = X_SKIP;
+                else if (v_obj) push = v_obj;
+                else return PJ_REC_TYPE;
+            } else if (c == '[') {
+                if (v_any) push = X_SKIP;
+                else if (v_arr) push = v_arr;
+                else return PJ_REC_TYPE;
+            } else if (c == '"') {
+                if (v_any) use = U_SKIP;
+                else if (v_str) use = v_str;
+                else return PJ_REC_TYPE;
+            } else scalar = true;
+            break;
+        case S_AFTER: {
+            const bool obj = depth <= 64 ? ((stk >> (depth - 1)) & 1) : opener_at(s, p, depth);
+            if (c == ',') {
+                p++;
+                state = obj ? S_KEY : S_VALUE;
+                continue;
             }
+            if (c == (obj ? '}' : ']')) { close = true; break; }
+            return PJ_REC_SYNTAX;
+        }
+        }
+        // ---- strings (the one scan site)
+        if (use) {
+            Str r;
+            if (slow) r = scan_slow(s, n, p);
+            else {
+                r.err = 0;
+                r.esc = false;
+                uint32_t q = p + 1, d = 0;
+                for (;;) {
+                    // next unescaped quote or backslash at or after q
+                    const uint64_t a = s0 + q, lim = s0 + n;
+                    uint32_t sp = n;
+                    if (a < lim) {
+                        uint64_t wi = a >> 6;
+                        uint64_t m = P.special[wi] & (~0ull << (a & 63));
+                        while (!m && (wi + 1) * 64 < lim) m = P.special[++wi];
+                        if (m) {
+                            const uint64_t at = wi * 64 + (uint64_t)__builtin_ctzll(m);
+                            if (at < lim) sp = (uint32_t)(at - s0);
+                        }
+                    }
+                    if (sp >= n) { r.err = PJ_REC_STRING; break; }
+                    d += sp - q;
+                    if (s[sp] == '"') { r.end = sp; break; }
+                    Esc e = escape_at(s, n, sp);
+                    if (e.err) { r.err = e.err; break; }
+                    d += (uint32_t)e.k;
+                    q = sp + e.adv;
+                    r.esc = true;
+                }
+                r.dlen = d;
+            }
+            if (r.err) return r.err;
+            const uint32_t q0 = p;
+            p = r.end + 1;
+            uint64_t lo = 0, hi = 0;
+            if ((use == U_KEY || use == U_STATUS) && r.dlen <= 9) {
+                if (!r.esc) {
+                    // raw bytes of the (short) string, read in two safe halves
+                    uint32_t L1 = r.dlen < 8 ? r.dlen : 8;
+                    if (L1) lo = L1 == 8 ? ldu64(s + q0 + 1) : ld_tail(s + q0 + 1, (int)L1);
+                    if (r.dlen > 8) hi = ld_tail(s + q0 + 9, (int)(r.dlen - 8));
+                } else {
+                    uint2 l2 = small_decode_esc(s, q0, r.end, n, &hi);
+                    lo = (uint64_t)l2.x | ((uint64_t)l2.y << 32);
+                }
+            }
+            switch (use) {
+            case U_KEY: {
+                int kid = K_UNKNOWN;
+                const uint32_t dl = r.dlen;
+                if (dl == 2 && lo == 0x6469ull) kid = K_ID;                                        // id
+                else if (dl == 8 && lo == 0x79726F6765746163ull) kid = K_CATEGORY;                 // category
+                else if (dl == 4 && lo == 0x656D616Eull) kid = K_NAME;                             // name
+                else if (dl == 9 && lo == 0x6C72556F746F6870ull && hi == 0x73ull) kid = K_PHOTOURLS;  // photoUrls
+                else if (dl == 4 && lo == 0x73676174ull) kid = K_TAGS;                             // tags
+                else if (dl == 6 && lo == 0x737574617473ull) kid = K_STATUS;                       // status
+                if (ctx == X_PET) k1 = kid;
+                else k2 = kid;
+                state = S_COLON;
+                continue;
+            }
+            case U_NAME:
+                if (!write) {
+                    L.has_name = 1;
+                    L.name_pos = q0;
+                    L.name_len = r.dlen;
+                    L.name_esc = r.esc;
+                }
+                break;
+            case U_SUBNAME:
+                sub_fl |= PJ_SUB_HAS_NAME;
+                sub_len = r.dlen;
+                sub_q = q0;
+                sub_esc = r.esc;
+                break;
+            case U_URL:
+                if (!write) {
+                    L.n_urls++;
+                    L.url_bytes += r.dlen;
+                }
+                break;
+            case U_STATUS: {
+                uint8_t st;
+                if (r.dlen == 9 && lo == 0x6C62616C69617661ull && hi == 0x65ull) st = PJ_STATUS_AVAILABLE;
+                else if (r.dlen == 7 && lo == 0x676E69646E6570ull) st = PJ_STATUS_PENDING;
+                else if (r.dlen == 4 && lo == 0x646C6F73ull) st = PJ_STATUS_SOLD;
+                else return PJ_REC_BAD_STATUS;   // the enum's @JsonCreator rejects it
+                if (!write) L.status = st;
+                break;
+            }
+            default: break;
+            }
+            // the one copy site: urls are copied as they are met
+            if (write && use == U_URL && last_urls) {
+                if (r.dlen && u_b + r.dlen <= o.cap_url_bytes) {
+                    WriteSink ws;
+                    ws.init(o.url_bytes, u_b, P.dummy);
+                    if (!r.esc) {
+                        const uint8_t *src = s + q0 + 1;
+                        uint32_t k = 0;
+                        for (; k + 8 <= r.dlen; k += 8) ws.put8(ldu64(src + k), 8);
+                        if (k < r.dlen) ws.put8(ld_tail(src + k, (int)(r.dlen - k)), (int)(r.dlen - k));
+                    } else {
+                        for (uint32_t q = q0 + 1; q < r.end;) {
+                            uint32_t c2 = s[q];
+                            if (c2 == '\\') {
+                                Esc e = escape_at(s, n, q);
+                                ws.put(e.out, e.k);
+                                q += e.adv;
+                            } else {
+                                ws.put_byte(c2);
+                                q++;
+                            }
+                        }
+                    }
+                    ws.finish();
+                }
+                u_b += r.dlen;
+                u_idx++;
+                if (u_idx <= o.cap_urls) o.url_off[u_idx] = u_b;
+            }
+            state = S_AFTER;
+            continue;
+        }
+        // ---- scalars (the one scalar site)
+        if (scalar) {
+            const uint32_t t0 = p;
+            int kind = -1;       // 0 null, 1 true, 2 false, 3 int, 4 real
+            if (c == '-' || (c >= '0' && c <= '9')) {
+                uint32_t q = p;
+                bool real = false;
+                if (W.at(q) == '-') q++;
+                if (q >= n) return PJ_REC_SYNTAX;
+                int d = W.at(q);
+                if (d == '0') {
+                    q++;
+                    if (q < n && W.at(q) >= '0' && W.at(q) <= '9') return PJ_REC_SYNTAX;   // leading zero
+                } else if (d >= '1' && d <= '9') {
+                    while (q < n && W.at(q) >= '0' && W.at(q) <= '9') q++;
+                } else return PJ_REC_SYNTAX;
+                if (q < n && W.at(q) == '.') {
+                    q++;
+                    real = true;
+                    if (q >= n || W.at(q) < '0' || W.at(q) > '9') return PJ_REC_SYNTAX;
+                    while (q < n && W.at(q) >= '0' && W.at(q) <= '9') q++;
+                }
+                if (q < n && (W.at(q) == 'e' || W.at(q) == 'E')) {
+                    q++;
+                    real = true;
+                    if (q < n && (W.at(q) == '+' || W.at(q) == '-')) q++;
+                    if (q >= n || W.at(q) < '0' || W.at(q) > '9') return PJ_REC_SYNTAX;
+                    while (q < n && W.at(q) >= '0' && W.at(q) <= '9') q++;
+                }
+                p = q;
+                kind = real ? 4 : 3;
+            } else {
+                uint32_t Ln;
+                uint64_t want;
+                if (c == 'n') { Ln = 4; want = 0x6C6C756Eull; kind = 0; }
+                else if (c == 't') { Ln = 4; want = 0x65757274ull; kind = 1; }
+                else if (c == 'f') { Ln = 5; want = 0x65736C6166ull; kind = 2; }
+                else return PJ_REC_SYNTAX;
+                if (p + Ln > n) return PJ_REC_SYNTAX;
+                for (uint32_t j = 0; j < Ln; j++)
+                    if ((uint64_t)W.at(p + j) != ((want >> (8 * j)) & 0xFF)) return PJ_REC_SYNTAX;
+                if (p + Ln < n && is_ident(W.at(p + Ln))) return PJ_REC_SYNTAX;
+                p += Ln;
+            }
+            if (!v_any) {
+                if (kind == 0 && v_null) {
+                    // null: the property is absent
+                    if (ctx == X_PET) {
+                        if (!write) {
+                            if (k1 == K_ID) { L.has_id = 0; L.id = 0; }
+                            else if (k1 == K_CATEGORY) { L.has_cat = 0; L.cat_id = 0; L.cat_flags = 0; L.cat_len = 0; }
+                            else if (k1 == K_NAME) L.has_name = 0;
+                            else if (k1 == K_PHOTOURLS) { L.has_photo = 0; L.n_urls = 0; L.url_bytes = 0; }
+                            else if (k1 == K_TAGS) { L.has_tags = 0; L.n_tags = 0; L.tag_bytes = 0; }
+                            else if (k1 == K_STATUS) L.status = PJ_STATUS_NULL;
+                        }
+                    } else if (k2 == K_ID) { sub_fl &= ~PJ_SUB_HAS_ID; sub_id = 0; }
+                    else { sub_fl &= ~PJ_SUB_HAS_NAME; sub_len = 0; }
+                } else if (v_long && kind == 4) return PJ_REC_NUMBER;
+                else if (v_long && kind == 3) {
+                    const bool neg = W.at(t0) == '-';
+                    const uint64_t lim = neg ? (1ull << 63) : ((1ull << 63) - 1);
+                    uint64_t acc = 0;
+                    for (uint32_t q = t0 + (neg ? 1 : 0); q < p; q++) {
+                        const uint64_t dg = (uint64_t)(W.at(q) - '0');
+                        if (acc > (lim - dg) / 10) return PJ_REC_NUMBER;
+                        acc = acc * 10 + dg;
+                    }
+                    const int64_t v = neg ? (int64_t)(0ull - acc) : (int64_t)acc;
+                    if (ctx == X_PET) {
+                        if (!write) { L.has_id = 1; L.id = v; }
+                    } else { sub_fl |= PJ_SUB_HAS_ID; sub_id = v; }
+                } else return PJ_REC_TYPE;
+            }
+            state = S_AFTER;
+            continue;
+        }
+        // ---- open a container
+        if (push) {
+            if (++depth > PJ_MAX_DEPTH) return PJ_REC_DEPTH;
+            const bool obj = c == '{';
+            if (depth <= 64) stk = obj ? (stk | (1ull << (depth - 1))) : (stk & ~(1ull << (depth - 1)));
+            if (depth <= 3) sem = (sem & ~(15u << (4 * (depth - 1)))) | ((uint32_t)push << (4 * (depth - 1)));
+            if (push == X_CAT) {
+                cat_q = p;
+                if (!write) { L.has_cat = 1; L.cat_pos = p; }
+                sub_id = 0; sub_fl = 0; sub_len = 0; sub_q = 0; sub_esc = false;
+            } else if (push == X_TAG) {
+                sub_id = 0; sub_fl = 0; sub_len = 0; sub_q = 0; sub_esc = false;
+            } else if (push == X_URLS) {
+                if (!write) { L.has_photo = 1; L.photo_pos = p; L.n_urls = 0; L.url_bytes = 0; }
+                else last_urls = p == L.photo_pos;
+            } else if (push == X_TAGS) {
+                if (!write) { L.has_tags = 1; L.tags_pos = p; L.n_tags = 0; L.tag_bytes = 0; }
+                else last_tags = p == L.tags_pos;
+            }
+            p++;
+            state = obj ? S_KEY_OR_CLOSE : S_ELEM_OR_CLOSE;
+            continue;
+        }
+        // ---- close a container
+        if (close) {
+            p++;
+            // the one sub-string copy site: category / tag names and the pet name
+            uint32_t cq = 0, clen = 0;
+            bool cesc = false;
+            uint8_t *cdst = nullptr;
+            uint64_t coff = 0, ccap = 0;
+            if (ctx == X_CAT) {
+                if (!write) {
+                    L.cat_id = sub_id;
+                    L.cat_flags = (uint8_t)sub_fl;
+                    L.cat_len = (sub_fl & PJ_SUB_HAS_NAME) ? sub_len : 0;
+                } else if (cat_q == L.cat_pos && (sub_fl & PJ_SUB_HAS_NAME)) {
+                    cq = sub_q; clen = sub_len; cesc = sub_esc;
+                    cdst = o.cat_name_bytes; coff = pos[C_CATB]; ccap = o.cap_cat_name_bytes;
+                }
+            } else if (ctx == X_TAG) {
+                const uint32_t tl = (sub_fl & PJ_SUB_HAS_NAME) ? sub_len : 0;
+                if (!write) {
+                    L.n_tags++;
+                    L.tag_bytes += tl;
+                } else if (last_tags) {
+                    if (g_idx < o.cap_tags) {
+                        o.tag_id[g_idx] = sub_id;
+                        o.tag_flags[g_idx] = (uint8_t)sub_fl;
+                    }
+                    if (tl) { cq = sub_q; clen = tl; cesc = sub_esc; cdst = o.tag_name_bytes; coff = g_b; ccap = o.cap_tag_name_bytes; }
+                    g_b += tl;
+                    g_idx++;
+                    if (g_idx <= o.cap_tags) o.tag_name_off[g_idx] = g_b;
+                }
+            } else if (ctx == X_PET) {
+                if (!write) {
+                    if (!L.has_name) return PJ_REC_MISSING_NAME;       // required (petstore.json:873-876)
+                    if (!L.has_photo) return PJ_REC_MISSING_PHOTOURLS;
+                } else {
+                    const uint64_t row = pos[C_PETS];
+                    if (row < o.cap_pets) {
+                        o.id[row] = L.id;
+                        o.flags[row] = (uint8_t)((L.has_id ? PJ_PET_HAS_ID : 0) | (L.has_cat ? PJ_PET_HAS_CATEGORY : 0) |
+                                                 PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS |
+                                                 (L.has_tags ? PJ_PET_HAS_TAGS : 0));
+                        o.status[row] = L.status;
+                        o.cat_id[row] = L.cat_id;
+                        o.cat_flags[row] = L.cat_flags;
+                        o.name_off[row + 1] = pos[C_NAMEB] + L.name_len;
+                        o.cat_name_off[row + 1] = pos[C_CATB] + L.cat_len;
+                        o.photo_off[row + 1] = pos[C_URLS] + L.n_urls;
+                        o.tag_off[row + 1] = pos[C_TAGS] + L.n_tags;
+                    }
+                    if (L.name_len) {
+                        cq = L.name_pos; clen = L.name_len; cesc = L.name_esc;
+                        cdst = o.name_bytes; coff = pos[C_NAMEB]; ccap = o.cap_name_bytes;
+                    }
+                }
+            }
+            if (cdst && coff + clen <= ccap) {
+                WriteSink ws;
+                ws.init(cdst, coff, P.dummy);
+                if (!cesc) {
+                    const uint8_t *src = s + cq + 1;
+                    uint32_t k = 0;
+                    for (; k + 8 <= clen; k += 8) ws.put8(ldu64(src + k), 8);
+                    if (k < clen) ws.put8(ld_tail(src + k, (int)(clen - k)), (int)(clen - k));
+                } else {
+                    for (uint32_t q = cq + 1; s[q] != '"';) {
+                        uint32_t c2 = s[q];
+                        if (c2 == '\\') {
+                            Esc e = escape_at(s, n, q);
+                            ws.put(e.out, e.k);
+                            q += e.adv;
+                        } else {
+                            ws.put_byte(c2);
+                            q++;
+                        }
+                    }
+                }
+                ws.finish();
+            }
+            depth--;
+            state = depth == 0 ? S_DONE : S_AFTER;
+            continue;
         }
     }
-    // position of the opening quote of the last "name" of the object at q
-    __device__ uint32_t last_name_of(uint32_t q) {
-        p = q;
-        open_container();
-        int key;
-        bool more;
-        uint32_t last = 0;
-        int e = first_member(&key, &more);
-        while (!e && more) {            // every step advances p or stops
-            if (key == K_NAME && peek() == '"') last = p;
-            if (skip_value()) break;
-            e = next_member(&key, &more);
+#undef PEEK
+#undef SKIP_WS
+}
+
+// ---------------------------------------------------------------- line records
+// The 8 scanned counters of a line.
+__device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
+    const bool ok = r.code == 0;
+    v[C_PETS] = ok;
+    v[C_NAMEB] = ok ? r.name_len : 0;
+    v[C_CATB] = ok ? r.cat_len : 0;
+    v[C_URLS] = ok ? r.n_urls : 0;
+    v[C_URLB] = ok ? r.url_bytes : 0;
+    v[C_TAGS] = ok ? r.n_tags : 0;
+    v[C_TAGB] = ok ? r.tag_bytes : 0;
+    v[C_ERRS] = !ok;
+}
+
+// ---------------------------------------------------------------- fast path
+// Straight-line parser for lines shaped like encoder output: no whitespace,
+// properties in schema order (id, category, name, photoUrls, tags, status;
+// Category / Tag: id, name), no nulls, no unknown keys, integer ids.
+// Anything else returns PJ_BAIL and the line goes through run_line.  Errors
+// it does return (status not in the enum, id out of range, broken string,
+// missing required property) are the first error of the line, exactly as
+// run_line reports them.
+constexpr int PJ_BAIL = -1;
+
+struct FLine {
+    const uint8_t *s;        // line start
+    const uint64_t *special;
+    uint64_t s0, len;        // absolute line start, input length
+    uint32_t n;
+    // 8 bytes at q (bytes past the end of the input read as 0)
+    __device__ __forceinline__ uint64_t ld8(uint32_t q) const {
+        const uint64_t a = s0 + q;
+        if (a + 8 <= len) return ldu64(s + q);
+        uint64_t v = 0;
+        for (uint32_t j = 0; j < 8 && a + j < len; j++) v |= (uint64_t)s[q + j] << (8 * j);
+        return v;
+    }
+    __device__ __forceinline__ int at(uint32_t q) const { return q < n ? (int)s[q] : -1; }
+    __device__ __forceinline__ uint32_t next_special(uint32_t q) const {
+        const uint64_t a = s0 + q, lim = s0 + n;
+        if (a >= lim) return n;
+        uint64_t wi = a >> 6;
+        uint64_t m = special[wi] & (~0ull << (a & 63));
+        while (!m && (wi + 1) * 64 < lim) m = special[++wi];
+        if (!m) return n;
+        const uint64_t at = wi * 64 + (uint64_t)__builtin_ctzll(m);
+        return at < lim ? (uint32_t)(at - s0) : n;
+    }
+    // string whose first content byte is at q (opening quote at q-1)
+    __device__ __forceinline__ Str str(uint32_t q) const {
+        Str r{0, 0, 0, false};
+        uint32_t d = 0;
+        for (;;) {
+            const uint32_t sp = next_special(q);
+            if (sp >= n) { r.err = PJ_REC_STRING; return r; }
+            d += sp - q;
+            if (s[sp] == '"') { r.end = sp; break; }
+            Esc e = escape_at(s, n, sp);
+            if (e.err) { r.err = e.err; return r; }
+            d += (uint32_t)e.k;
+            q = sp + e.adv;
+            r.esc = true;
         }
-        return last;
+        r.dlen = d;
+        return r;
+    }
+    // copy the decoded string (content from q, described by r) to dst+off
+    __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst, uint64_t off, uint32_t *dummy) const {
+        WriteSink ws;
+        ws.init(dst, off, dummy);
+        if (!r.esc) {
+            const uint8_t *src = s + q;
+            uint32_t k = 0;
+            for (; k + 8 <= r.dlen; k += 8) ws.put8(ldu64(src + k), 8);
+            if (k < r.dlen) ws.put8(ld_tail(src + k, (int)(r.dlen - k)), (int)(r.dlen - k));
+        } else {
+            for (uint32_t x = q; x < r.end;) {
+                const uint32_t c = s[x];
+                if (c == '\\') {
+                    Esc e = escape_at(s, n, x);
+                    ws.put(e.out, e.k);
+                    x += e.adv;
+                } else {
+                    ws.put_byte(c);
+                    x++;
+                }
+            }
+        }
+        ws.finish();
     }
 };
 
-// ---- vector look-back over PJ_DEC_NCNT counters
-// per block: [flag][agg x NC][inc x NC]
-constexpr int VLB_STRIDE = 1 + 2 * PJ_DEC_NCNT;
-
-__device__ __forceinline__ void vlb_publish(uint64_t *st, uint64_t b, const uint64_t *agg, int lane) {
-    uint64_t *s = st + b * VLB_STRIDE;
-    if (lane < PJ_DEC_NCNT) lb_store(&s[1 + lane], agg[lane]);
-    if (b == 0 && lane < PJ_DEC_NCNT) lb_store(&s[1 + PJ_DEC_NCNT + lane], agg[lane]);
-    __threadfence();
-    if (lane == 0) lb_store(&s[0], b == 0 ? 2 : 1);
+// bit 7 of each byte set iff that byte is not an ASCII digit
+__device__ __forceinline__ uint64_t nondigit8(uint64_t x) {
+    const uint64_t m7 = 0x7F7F7F7F7F7F7F7Full;
+    const uint64_t ge0 = ((x & m7) + 0x5050505050505050ull) | x;   // >= '0' (or >= 0x80)
+    const uint64_t ge9 = ((x & m7) + 0x4646464646464646ull) | x;   // >= ':' (or >= 0x80)
+    return (~ge0 | ge9) & 0x8080808080808080ull;
 }
 
-// one full wave; returns the exclusive prefix in excl[] (all lanes)
-__device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint64_t *agg, uint64_t *excl) {
-    const int l = lane_id();
-    for (int k = 0; k < PJ_DEC_NCNT; k++) excl[k] = 0;
-    if (b == 0) return;
-    int64_t j = (int64_t)b - 1;
-    for (;;) {
-        int64_t idx = j - l;
-        uint64_t f = idx >= 0 ? lb_load(&st[idx * VLB_STRIDE]) : 2;
-        uint64_t notready = __ballot(f == 0);
-        uint64_t isp = __ballot(f == 2);
-        int fp = isp ? __builtin_ctzll(isp) : 64;
-        uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1);
-        if (notready & need) { __builtin_amdgcn_s_sleep(1); continue; }
-        __threadfence();
-        const bool use = l <= fp && idx >= 0;
-        const uint64_t *src = st + (idx >= 0 ? idx : 0) * VLB_STRIDE + (f == 2 ? 1 + PJ_DEC_NCNT : 1);
-#pragma unroll
-        for (int k = 0; k < PJ_DEC_NCNT; k++) excl[k] += wave_sum(use ? lb_load(&src[k]) : 0);
-        if (fp < 64) break;
-        j -= 64;
+// value of m (1..8) ASCII digits packed little endian in x (first digit low)
+__device__ __forceinline__ uint64_t digits8(uint64_t x, int m) {
+    uint64_t y = x - 0x3030303030303030ull;
+    if (m < 8) y <<= 8 * (8 - m);
+    y = (y * 10 + (y >> 8)) & 0x00FF00FF00FF00FFull;
+    y = (y * 100 + (y >> 16)) & 0x0000FFFF0000FFFFull;
+    return (y * 10000 + (y >> 32)) & 0xFFFFFFFFull;
+}
+
+// Canonical Long at p: -?(0|[1-9][0-9]*) followed by ',' or '}'.  Returns 0,
+// PJ_REC_NUMBER (out of int64 range) or PJ_BAIL; the value only when VAL.
+template <bool VAL>
+__device__ __forceinline__ int fnum(const FLine &F, uint32_t &p, int64_t &v) {
+    uint32_t q = p;
+    const bool neg = F.at(q) == '-';
+    q += neg;
+    uint32_t k = 0;
+    uint64_t c0 = 0, c1 = 0, c2 = 0;
+    {
+        c0 = F.ld8(q);
+        uint64_t nd = nondigit8(c0);
+        k = nd ? (uint32_t)(__builtin_ctzll(nd) >> 3) : 8;
+        if (k == 8) {
+            c1 = F.ld8(q + 8);
+            nd = nondigit8(c1);
+            uint32_t k1 = nd ? (uint32_t)(__builtin_ctzll(nd) >> 3) : 8;
+            k += k1;
+            if (k1 == 8) {
+                c2 = F.ld8(q + 16);
+                nd = nondigit8(c2);
+                k += nd ? (uint32_t)(__builtin_ctzll(nd) >> 3) : 8;
+            }
+        }
     }
-    uint64_t *s = st + b * VLB_STRIDE;
-    if (l < PJ_DEC_NCNT) {
-        uint64_t v = 0;
-#pragma unroll
-        for (int k = 0; k < PJ_DEC_NCNT; k++) v = k == l ? excl[k] + agg[k] : v;
-        lb_store(&s[1 + PJ_DEC_NCNT + l], v);
+    if (k == 0 || q + k > F.n) return PJ_BAIL;
+    if ((c0 & 0xFF) == '0' && k > 1) return PJ_BAIL;            // leading zero: general rules
+    const int nx = F.at(q + k);
+    if (nx != ',' && nx != '}') return PJ_BAIL;                  // fraction, exponent, space...
+    if (k > 19) return PJ_REC_NUMBER;
+    if (k == 19) {                                               // compare with 9223372036854775807/8
+        const uint64_t a = __builtin_bswap64(c0), b = __builtin_bswap64(c1);
+        const uint32_t c = (uint32_t)((c2 & 0xFF) << 16 | ((c2 >> 8) & 0xFF) << 8 | ((c2 >> 16) & 0xFF));
+        const uint64_t A = __builtin_bswap64(pack8("92233720", 8)), B = __builtin_bswap64(pack8("36854775", 8));
+        const uint32_t Cl = neg ? ('8' << 16 | '0' << 8 | '8') : ('8' << 16 | '0' << 8 | '7');
+        if (a > A || (a == A && (b > B || (b == B && c > Cl)))) return PJ_REC_NUMBER;
     }
-    __threadfence();
-    if (l == 0) lb_store(&s[0], 2);
+    if (VAL) {
+        uint64_t acc;
+        if (k <= 8) acc = digits8(c0, (int)k);
+        else if (k <= 16) {
+            uint64_t p10 = 1;
+            for (uint32_t j = 0; j < k - 8; j++) p10 *= 10;
+            acc = digits8(c0, 8) * p10 + digits8(c1, (int)(k - 8));
+        } else {
+            uint64_t p10 = 1;
+            for (uint32_t j = 0; j < k - 16; j++) p10 *= 10;
+            acc = (digits8(c0, 8) * 100000000ull + digits8(c1, 8)) * p10 + digits8(c2, (int)(k - 16));
+        }
+        v = neg ? (int64_t)(0ull - acc) : (int64_t)acc;
+    }
+    p = q + k;
+    return 0;
 }
 
-template <bool SLOW>
-__device__ __forceinline__ int parse_line(const DecParams &P, uint64_t s, uint32_t n, LineInfo &L) {
-    LP<SLOW> lp;
-    lp.init(P, s, n);
-    return lp.parse(L);
+// 8-byte key prefixes (opening quote included)
+constexpr uint64_t KP_ID = pack8("\"id\":", 5), KP_ID_MASK = 0xFFFFFFFFFFull;   // "id":
+constexpr uint64_t KP_CATEGORY = pack8("\"categor", 8), KP_NAME = pack8("\"name\":\"", 8),
+                   KP_PHOTO = pack8("\"photoUr", 8), KP_TAGS = pack8("\"tags\":[", 8),
+                   KP_STATUS = pack8("\"status\"", 8);
+
+// Category / Tag body after '{': optional "id":N, then optional "name":"S",
+// then '}'.
+template <bool WRITE>
+__device__ __forceinline__ int fsub(const FLine &F, uint32_t &p, int64_t &id, uint32_t &fl, uint32_t &nq, Str &nr) {
+    fl = 0;
+    id = 0;
+    uint64_t k8 = F.ld8(p);
+    if ((k8 & KP_ID_MASK) == pack8("\"id\":", 5) && p + 5 <= F.n) {
+        p += 5;
+        int e = fnum<WRITE>(F, p, id);
+        if (e) return e;
+        fl |= PJ_SUB_HAS_ID;
+        if (F.at(p) == ',') {
+            p++;
+            k8 = F.ld8(p);
+            if (k8 != KP_NAME || p + 8 > F.n) return PJ_BAIL;
+        }
+    }
+    if (k8 == KP_NAME && p + 8 <= F.n && !(fl & PJ_SUB_HAS_NAME)) {
+        p += 8;
+        nq = p;
+        nr = F.str(p);
+        if (nr.err) return nr.err;
+        p = nr.end + 1;
+        fl |= PJ_SUB_HAS_NAME;
+    }
+    if (F.at(p) != '}') return PJ_BAIL;
+    p++;
+    return 0;
 }
 
-template <bool SLOW>
-__device__ void write_line(const DecParams &P, uint64_t s, uint32_t n, const LineInfo &L, const uint64_t *pos) {
+template <bool WRITE>
+__device__ __forceinline__ int fline(const DecParams &P, uint64_t s0, uint32_t n, LineRec &R, const uint64_t *pos) {
+    const FLine F{P.in + s0, P.special, s0, P.len, n};
     const pj_pet_columns &o = P.o;
-    LP<SLOW> lp;
-    lp.init(P, s, n);
-    const uint64_t row = pos[C_PETS];
-    const uint64_t nb = pos[C_NAMEB], cb = pos[C_CATB], u0 = pos[C_URLS], ub = pos[C_URLB], g0 = pos[C_TAGS],
-                   tb = pos[C_TAGB];
-    if (row < o.cap_pets) {
-        o.id[row] = L.id;
-        o.flags[row] = (uint8_t)((L.has_id ? PJ_PET_HAS_ID : 0) | (L.has_cat ? PJ_PET_HAS_CATEGORY : 0) |
-                                 PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS | (L.has_tags ? PJ_PET_HAS_TAGS : 0));
-        o.status[row] = L.status;
-        o.cat_id[row] = L.cat_id;
-        o.cat_flags[row] = L.cat_flags;
-        o.name_off[row + 1] = nb + L.name_len;
-        o.cat_name_off[row + 1] = cb + L.cat_len;
-        o.photo_off[row + 1] = u0 + L.n_urls;
-        o.tag_off[row + 1] = g0 + L.n_tags;
-    }
-    if (L.name_len && nb + L.name_len <= o.cap_name_bytes) {
-        WriteSink ws;
-        ws.init(o.name_bytes, nb, P.dummy);
-        lp.copy_str(L.name_pos, ws);
-        ws.finish();
-    }
-    if (L.has_cat && L.cat_len && cb + L.cat_len <= o.cap_cat_name_bytes) {
-        uint32_t q = lp.last_name_of(L.cat_pos);
-        WriteSink ws;
-        ws.init(o.cat_name_bytes, cb, P.dummy);
-        lp.copy_str(q, ws);
-        ws.finish();
-    }
-    if (L.has_photo && L.n_urls) {
-        lp.p = L.photo_pos;
-        lp.open_container();
-        uint64_t u = u0, b = ub;
+    if (n == 0) return PJ_REC_EMPTY;
+    if (F.at(0) != '{') return PJ_BAIL;
+    uint32_t p = 1;
+    uint32_t flags = 0;
+    uint8_t status = PJ_STATUS_NULL;
+    int64_t id = 0, cat_id = 0;
+    uint32_t cat_fl = 0, name_len = 0, cat_len = 0, n_urls = 0, url_bytes = 0, n_tags = 0, tag_bytes = 0;
+    int slot = 0;                    // next schema slot allowed
+    if (F.at(p) != '}') {
         for (;;) {
-            lp.skip_ws();
-            const uint32_t q = lp.p;
-            uint32_t end, dl;
-            bool es;
-            lp.str_scan(q, &end, &dl, &es);
-            if (b + dl <= o.cap_url_bytes && dl) {
-                WriteSink ws;
-                ws.init(o.url_bytes, b, P.dummy);
-                lp.copy_str(q, ws);
-                ws.finish();
+            const uint64_t k8 = F.ld8(p);
+            int key, klen;
+            if ((k8 & KP_ID_MASK) == KP_ID) { key = 0; klen = 5; }
+            else if (k8 == KP_CATEGORY && (F.ld8(p + 8) & 0xFFFFFFFFull) == pack8("y\":{", 4)) { key = 1; klen = 11; }
+            else if (k8 == KP_NAME) { key = 2; klen = 7; }
+            else if (k8 == KP_PHOTO && (F.ld8(p + 8) & 0xFFFFFFFFFFull) == pack8("ls\":[", 5)) { key = 3; klen = 12; }
+            else if (k8 == KP_TAGS) { key = 4; klen = 7; }
+            else if (k8 == KP_STATUS && (F.ld8(p + 8) & 0xFFFFull) == pack8(":\"", 2)) { key = 5; klen = 9; }
+            else return PJ_BAIL;
+            if (key < slot || p + (uint32_t)klen >= n) return PJ_BAIL;
+            slot = key + 1;
+            p += (uint32_t)klen;
+            switch (key) {
+            case 0: {                                             // id
+                int e = fnum<WRITE>(F, p, id);
+                if (e) return e;
+                flags |= PJ_PET_HAS_ID;
+                break;
             }
-            b += dl;
-            u++;
-            if (u <= o.cap_urls) o.url_off[u] = b;
-            lp.p = end + 1;
-            lp.skip_ws();
-            if (lp.peek() == ',') { lp.p++; continue; }
-            break;
+            case 1: {                                             // category {
+                p++;
+                uint32_t nq = 0;
+                Str nr{0, 0, 0, false};
+                int e = fsub<WRITE>(F, p, cat_id, cat_fl, nq, nr);
+                if (e) return e;
+                flags |= PJ_PET_HAS_CATEGORY;
+                cat_len = (cat_fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+                if (WRITE && cat_len && pos[C_CATB] + cat_len <= o.cap_cat_name_bytes)
+                    F.copy(nq, nr, o.cat_name_bytes, pos[C_CATB], P.dummy);
+                break;
+            }
+            case 2: {                                             // name "
+                const uint32_t q = p + 1;
+                Str r = F.str(q);
+                if (r.err) return r.err;
+                p = r.end + 1;
+                flags |= PJ_PET_HAS_NAME;
+                name_len = r.dlen;
+                if (WRITE && r.dlen && pos[C_NAMEB] + r.dlen <= o.cap_name_bytes)
+                    F.copy(q, r, o.name_bytes, pos[C_NAMEB], P.dummy);
+                break;
+            }
+            case 3: {                                             // photoUrls [
+                flags |= PJ_PET_HAS_PHOTOURLS;
+                p++;
+                uint64_t u = WRITE ? pos[C_URLS] : 0, ub = WRITE ? pos[C_URLB] : 0;
+                if (F.at(p) == ']') { p++; break; }
+                for (;;) {
+                    if (F.at(p) != '"') return PJ_BAIL;
+                    const uint32_t q = p + 1;
+                    Str r = F.str(q);
+                    if (r.err) return r.err;
+                    p = r.end + 1;
+                    n_urls++;
+                    url_bytes += r.dlen;
+                    if (WRITE) {
+                        if (r.dlen && ub + r.dlen <= o.cap_url_bytes) F.copy(q, r, o.url_bytes, ub, P.dummy);
+                        ub += r.dlen;
+                        u++;
+                        if (u <= o.cap_urls) o.url_off[u] = ub;
+                    }
+                    const int c = F.at(p++);
+                    if (c == ',') continue;
+                    if (c == ']') break;
+                    return PJ_BAIL;
+                }
+                break;
+            }
+            case 4: {                                             // tags [
+                flags |= PJ_PET_HAS_TAGS;
+                p++;
+                uint64_t g = WRITE ? pos[C_TAGS] : 0, gb = WRITE ? pos[C_TAGB] : 0;
+                if (F.at(p) == ']') { p++; break; }
+                for (;;) {
+                    if (F.at(p) != '{') return PJ_BAIL;
+                    p++;
+                    int64_t tid;
+                    uint32_t tfl, nq = 0;
+                    Str nr{0, 0, 0, false};
+                    int e = fsub<WRITE>(F, p, tid, tfl, nq, nr);
+                    if (e) return e;
+                    const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+                    n_tags++;
+                    tag_bytes += tl;
+                    if (WRITE) {
+                        if (g < o.cap_tags) { o.tag_id[g] = tid; o.tag_flags[g] = (uint8_t)tfl; }
+                        if (tl && gb + tl <= o.cap_tag_name_bytes) F.copy(nq, nr, o.tag_name_bytes, gb, P.dummy);
+                        gb += tl;
+                        g++;
+                        if (g <= o.cap_tags) o.tag_name_off[g] = gb;
+                    }
+                    const int c = F.at(p++);
+                    if (c == ',') continue;
+                    if (c == ']') break;
+                    return PJ_BAIL;
+                }
+                break;
+            }
+            default: {                                            // status "
+                const uint32_t q = p + 1;
+                Str r = F.str(q);
+                if (r.err) return r.err;
+                p = r.end + 1;
+                if (r.esc) return PJ_BAIL;
+                const uint64_t x = F.ld8(q), y = F.ld8(q + 8) & 0xFF;
+                if (r.dlen == 9 && x == pack8("availabl", 8) && y == 'e') status = PJ_STATUS_AVAILABLE;
+                else if (r.dlen == 7 && (x & 0xFFFFFFFFFFFFFFull) == pack8("pending", 7)) status = PJ_STATUS_PENDING;
+                else if (r.dlen == 4 && (x & 0xFFFFFFFFull) == pack8("sold", 4)) status = PJ_STATUS_SOLD;
+                else return PJ_REC_BAD_STATUS;                    // the enum's @JsonCreator rejects it
+            }
+            }
+            const int c = F.at(p);
+            if (c == ',') { p++; continue; }
+            if (c == '}') break;
+            return PJ_BAIL;
         }
     }
-    if (L.has_tags && L.n_tags) {
-        lp.p = L.tags_pos;
-        lp.open_container();
-        uint64_t g = g0, b = tb;
-        for (;;) {
-            lp.skip_ws();
-            const uint32_t q = lp.p;
-            int64_t tid;
-            uint8_t tfl;
-            uint32_t tl;
-            lp.rd_sub(&tid, &tfl, &tl);
-            const uint32_t after = lp.p;
-            if (g < o.cap_tags) {
-                o.tag_id[g] = tid;
-                o.tag_flags[g] = tfl;
-            }
-            if (tl && b + tl <= o.cap_tag_name_bytes) {
-                uint32_t nq = lp.last_name_of(q);
-                WriteSink ws;
-                ws.init(o.tag_name_bytes, b, P.dummy);
-                lp.copy_str(nq, ws);
-                ws.finish();
-            }
-            b += tl;
-            g++;
-            if (g <= o.cap_tags) o.tag_name_off[g] = b;
-            lp.p = after;
-            lp.skip_ws();
-            if (lp.peek() == ',') { lp.p++; continue; }
-            break;
+    if (p + 1 != n) return PJ_BAIL;                               // trailing bytes: general rules
+    if (!(flags & PJ_PET_HAS_NAME)) return PJ_REC_MISSING_NAME;   // required (petstore.json:873-876)
+    if (!(flags & PJ_PET_HAS_PHOTOURLS)) return PJ_REC_MISSING_PHOTOURLS;
+    if (!WRITE) {
+        R.name_len = name_len; R.cat_len = cat_len; R.n_urls = n_urls; R.url_bytes = url_bytes;
+        R.n_tags = n_tags; R.tag_bytes = tag_bytes;
+    } else {
+        const uint64_t row = pos[C_PETS];
+        if (row < o.cap_pets) {
+            o.id[row] = id;
+            o.flags[row] = (uint8_t)flags;
+            o.status[row] = status;
+            o.cat_id[row] = cat_id;
+            o.cat_flags[row] = (uint8_t)cat_fl;
+            o.name_off[row + 1] = pos[C_NAMEB] + name_len;
+            o.cat_name_off[row + 1] = pos[C_CATB] + cat_len;
+            o.photo_off[row + 1] = pos[C_URLS] + n_urls;
+            o.tag_off[row + 1] = pos[C_TAGS] + n_tags;
         }
+    }
+    return 0;
+}
+
+__device__ __forceinline__ bool line_bounds(const DecParams &P, uint64_t l, uint64_t &s, uint32_t &n) {
+    s = P.line_start[l];
+    const uint64_t e = P.line_start[l + 1] - 1;
+    n = (uint32_t)(e - s);
+    bool slow = false;
+    if (n)
+        for (uint64_t k = s >> 6; k <= (e - 1) >> 6; k++) slow |= P.bad[k] != 0;
+    return slow;
+}
+
+// ---------------------------------------------------------------- kernels
+// Count: one thread per line, fast path only; non-canonical lines queued.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_dec_count(DecParams P) {
+    __shared__ uint64_t sh[BT / 64][PJ_DEC_NCNT];
+    const uint32_t t = threadIdx.x;
+    const uint64_t l = (uint64_t)blockIdx.x * BT + t;
+    LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (l < P.lines) {
+        uint64_t s;
+        uint32_t n;
+        const bool slow = line_bounds(P, l, s, n);
+        int code = slow ? PJ_BAIL : fline<false>(P, s, n, r, nullptr);
+        if (code == PJ_BAIL) {
+            r.general = 1;
+            P.gq[atomicAdd(P.gq_count, 1ull)] = l;
+        } else {
+            r.code = (uint32_t)code;
+            if (code) r.name_len = r.cat_len = r.n_urls = r.url_bytes = r.n_tags = r.tag_bytes = 0;
+            rec_counts(r, v);
+        }
+        P.rec[l] = r;
+    }
+    const int w = t >> 6, ln = t & 63;
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++) {
+        const uint64_t x = wave_sum(v[k]);
+        if (ln == 0) sh[w][k] = x;
+    }
+    __syncthreads();
+    if (t < PJ_DEC_NCNT) {
+        uint64_t x = 0;
+        for (int k = 0; k < BT / 64; k++) x += sh[k][t];
+        P.bagg[blockIdx.x * PJ_DEC_NCNT + t] = x;
     }
 }
 
-template <int BT>
-__global__ __launch_bounds__(BT) void k_dec_parse(DecParams P) {
-    __shared__ uint64_t sh_scan[BT / 64];
-    __shared__ uint64_t sh_blk;
-    __shared__ uint64_t sh_base[PJ_DEC_NCNT];
+// General count: the queued lines through run_line; adds them to their
+// block sums.
+__global__ __launch_bounds__(256) void k_dec_gcount(DecParams P) {
+    const uint64_t cnt = *P.gq_count;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < cnt; i += (uint64_t)gridDim.x * 256) {
+        const uint64_t l = P.gq[i];
+        uint64_t s;
+        uint32_t n;
+        const bool slow = line_bounds(P, l, s, n);
+        LineInfo L;
+        const int code = run_line(P, s, n, slow, false, L, nullptr);
+        LineRec r{0, 0, 0, 0, 0, 0, (uint32_t)code, 1};
+        if (!code) {
+            r.name_len = L.name_len;
+            r.cat_len = L.has_cat ? L.cat_len : 0;
+            r.n_urls = L.n_urls;
+            r.url_bytes = L.url_bytes;
+            r.n_tags = L.n_tags;
+            r.tag_bytes = L.tag_bytes;
+        }
+        P.rec[l] = r;
+        uint64_t v[PJ_DEC_NCNT];
+        rec_counts(r, v);
+        unsigned long long *ba = reinterpret_cast<unsigned long long *>(P.bagg + (l / P.line_block) * PJ_DEC_NCNT);
+        for (int k = 0; k < PJ_DEC_NCNT; k++)
+            if (v[k]) atomicAdd(&ba[k], (unsigned long long)v[k]);
+    }
+}
+
+// Exclusive scan of the per-block sums (one workgroup); totals at the end.
+__global__ __launch_bounds__(1024) void k_dec_bscan(DecParams P, uint64_t nblocks) {
+    __shared__ uint64_t sh[16];
     const uint32_t t = threadIdx.x;
-    if (t == 0) sh_blk = atomicAdd(&P.tickets[1], 1ull);
-    __syncthreads();
-    const uint64_t b = sh_blk;
-    const uint64_t l = b * BT + t;
+    const uint64_t per = (nblocks + 1023) / 1024;
+    const uint64_t b0 = min((uint64_t)t * per, nblocks), b1 = min(b0 + per, nblocks);
+    for (int k = 0; k < PJ_DEC_NCNT; k++) {
+        uint64_t sum = 0;
+        for (uint64_t b = b0; b < b1; b++) sum += P.bagg[b * PJ_DEC_NCNT + k];
+        uint64_t tot;
+        uint64_t run = block_excl_scan<1024>(sum, sh, &tot);
+        for (uint64_t b = b0; b < b1; b++) {
+            const uint64_t x = P.bagg[b * PJ_DEC_NCNT + k];
+            P.bagg[b * PJ_DEC_NCNT + k] = run;
+            run += x;
+        }
+        if (t == 0) P.totals[k] = tot;
+    }
+}
+
+// Write: one thread per line; fast lines materialised here, errors listed.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_dec_write(DecParams P) {
+    __shared__ uint64_t sh_scan[BT / 64];
+    const uint32_t t = threadIdx.x;
+    const uint64_t l = (uint64_t)blockIdx.x * BT + t;
     const bool live = l < P.lines;
-    LineInfo L;
-    int code = 0;
-    uint64_t s = 0;
-    uint32_t n = 0;
-    bool slow = false;
+    LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) {
-        s = P.line_start[l];
-        const uint64_t e = P.line_start[l + 1] - 1;
-        n = (uint32_t)(e - s);
-        if (n) {
-            for (uint64_t k = s >> 6; k <= (e - 1) >> 6; k++) slow |= P.bad[k] != 0;
-        }
-        code = slow ? parse_line<true>(P, s, n, L) : parse_line<false>(P, s, n, L);
+        r = P.rec[l];
+        rec_counts(r, v);
     }
-    uint64_t v[PJ_DEC_NCNT], pre[PJ_DEC_NCNT], agg[PJ_DEC_NCNT];
-    const bool ok = live && code == 0;
-    v[C_PETS] = ok;
-    v[C_NAMEB] = ok ? L.name_len : 0;
-    v[C_CATB] = ok && L.has_cat ? L.cat_len : 0;
-    v[C_URLS] = ok ? L.n_urls : 0;
-    v[C_URLB] = ok ? L.url_bytes : 0;
-    v[C_TAGS] = ok ? L.n_tags : 0;
-    v[C_TAGB] = ok ? L.tag_bytes : 0;
-    v[C_ERRS] = live && code != 0;
+    uint64_t pos[PJ_DEC_NCNT];
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) pre[k] = block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
-    if (t < 64) {
-        vlb_publish(P.state_parse, b, agg, (int)t);
-        uint64_t excl[PJ_DEC_NCNT];
-        vlb_resolve(P.state_parse, b, agg, excl);
-        if (t < PJ_DEC_NCNT) {
-            uint64_t x = 0;
-#pragma unroll
-            for (int k = 0; k < PJ_DEC_NCNT; k++) x = k == (int)t ? excl[k] : x;
-            sh_base[t] = x;
-        }
-        if (b == gridDim.x - 1 && t < PJ_DEC_NCNT) {
-            uint64_t x = 0;
-#pragma unroll
-            for (int k = 0; k < PJ_DEC_NCNT; k++) x = k == (int)t ? excl[k] + agg[k] : x;
-            P.totals[t] = x;
-        }
+    for (int k = 0; k < PJ_DEC_NCNT; k++) {
+        uint64_t agg;
+        pos[k] = block_excl_scan<BT>(v[k], sh_scan, &agg) + P.bagg[blockIdx.x * PJ_DEC_NCNT + k];
     }
-    __syncthreads();
-    if (b == 0 && t == 0) {
+    if (blockIdx.x == 0 && t == 0) {
         const pj_pet_columns &o = P.o;
         o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
         o.url_off[0] = 0; o.tag_name_off[0] = 0;
     }
     if (!live) return;
-    if (code) {
-        uint64_t e = sh_base[C_ERRS] + pre[C_ERRS];
+    if (r.code) {
+        const uint64_t e = pos[C_ERRS];
         if (e < P.err_cap) {
             P.err_line[e] = l;
-            P.err_code[e] = (uint8_t)code;
+            P.err_code[e] = (uint8_t)r.code;
         }
         return;
     }
-    uint64_t pos[PJ_DEC_NCNT];
-#pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = sh_base[k] + pre[k];
-    if (slow) write_line<true>(P, s, n, L, pos);
-    else write_line<false>(P, s, n, L, pos);
+    if (r.general) return;                    // k_dec_gwrite
+    uint64_t s;
+    uint32_t n;
+    line_bounds(P, l, s, n);
+    LineRec dummy;
+    fline<true>(P, s, n, dummy, pos);
+}
+
+// General write: queued valid lines through run_line; their offsets are the
+// block's base plus the counts of the lines before them in the block.
+__global__ __launch_bounds__(256) void k_dec_gwrite(DecParams P) {
+    const uint64_t cnt = *P.gq_count;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < cnt; i += (uint64_t)gridDim.x * 256) {
+        const uint64_t l = P.gq[i];
+        if (P.rec[l].code) continue;
+        const uint64_t blk = l / P.line_block;
+        uint64_t pos[PJ_DEC_NCNT];
+        for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = P.bagg[blk * PJ_DEC_NCNT + k];
+        for (uint64_t m = blk * P.line_block; m < l; m++) {
+            uint64_t v[PJ_DEC_NCNT];
+            rec_counts(P.rec[m], v);
+            for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += v[k];
+        }
+        uint64_t s;
+        uint32_t n;
+        const bool slow = line_bounds(P, l, s, n);
+        LineInfo L;
+        run_line(P, s, n, slow, false, L, nullptr);
+        run_line(P, s, n, slow, true, L, pos);
+    }
 }
 
 }  // namespace pj
 
-constexpr int DEC_IDX_BT = 256, DEC_PARSE_BT = 256;
+constexpr int DEC_IDX_BT = 256, DEC_LINE_BT = 256, DEC_GEN_GRID = 512;
 
 int pj_dec_index_block() { return DEC_IDX_BT; }
-int pj_dec_parse_block() { return DEC_PARSE_BT; }
+int pj_dec_parse_block() { return DEC_LINE_BT; }
 
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     uint64_t g = (P.nblk64 + DEC_IDX_BT - 1) / DEC_IDX_BT;
@@ -1195,7 +1428,11 @@ hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
 }
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
-    uint64_t g = (P.lines + DEC_PARSE_BT - 1) / DEC_PARSE_BT;
-    hipLaunchKernelGGL(pj::k_dec_parse<DEC_PARSE_BT>, dim3((unsigned)g), dim3(DEC_PARSE_BT), 0, st, P);
+    const uint64_t g = (P.lines + DEC_LINE_BT - 1) / DEC_LINE_BT;
+    hipLaunchKernelGGL(pj::k_dec_count<DEC_LINE_BT>, dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
+    hipLaunchKernelGGL(pj::k_dec_gcount, dim3(DEC_GEN_GRID), dim3(256), 0, st, P);
+    hipLaunchKernelGGL(pj::k_dec_bscan, dim3(1), dim3(1024), 0, st, P, g);
+    hipLaunchKernelGGL(pj::k_dec_write<DEC_LINE_BT>, dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
+    hipLaunchKernelGGL(pj::k_dec_gwrite, dim3(DEC_GEN_GRID), dim3(256), 0, st, P);
     return hipGetLastError();
 }

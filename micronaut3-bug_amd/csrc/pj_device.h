@@ -136,6 +136,13 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p 4-byte aligne
     return *reinterpret_cast<const uint32_t *>(p);
 }
 
+// Compile-time packing of up to 8 literal bytes (little endian).
+constexpr uint64_t pack8(const char *s, int k) {
+    uint64_t v = 0;
+    for (int j = 0; j < k && j < 8; j++) v |= (uint64_t)(uint8_t)s[j] << (8 * j);
+    return v;
+}
+
 // Compile-time packing of up to 4 literal bytes (little endian).
 constexpr uint32_t pack4(const char *s, int k) {
     return (k > 0 ? (uint32_t)(uint8_t)s[0] : 0u) | (k > 1 ? (uint32_t)(uint8_t)s[1] << 8 : 0u) |

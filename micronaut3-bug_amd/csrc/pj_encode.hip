@@ -26,12 +26,6 @@
 
 namespace pj {
 
-constexpr uint64_t pack8(const char *s, int k) {
-    uint64_t v = 0;
-    for (int j = 0; j < k && j < 8; j++) v |= (uint64_t)(uint8_t)s[j] << (8 * j);
-    return v;
-}
-
 // ------------------------------------------------------------------ sinks
 // Every sink offers put(w, k) (k <= 4 bytes of w), put8(x, k) (k <= 8),
 // put_byte, skip(k) and pos().

@@ -19,6 +19,14 @@ struct EncParams {
     uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)
 };
 
+// What the decode counting kernels learn about each line, read back by the
+// writers (32 bytes per line).
+struct LineRec {
+    uint32_t name_len, cat_len, n_urls, url_bytes, n_tags, tag_bytes;
+    uint32_t code;      // PJ_REC_* (general lines: set by the general count kernel)
+    uint32_t general;   // 1: the line is read by the general parser
+};
+
 struct DecParams {
     const uint8_t *in;
     uint64_t len;
@@ -40,6 +48,12 @@ struct DecParams {
     unsigned long long *tickets; // [2]
     uint64_t lines;            // n_lines as known by the host for the parse stage
     uint32_t *dummy;           // sink for diverted shared dwords (never read)
+    // stage 2 (sized by the line count)
+    LineRec *rec;              // [lines]
+    uint64_t *gq;              // [lines] queue of lines for the general parser
+    unsigned long long *gq_count;
+    uint64_t *bagg;            // [line blocks][PJ_DEC_NCNT] sums, then exclusive prefixes
+    uint64_t line_block;       // lines per block of the line kernels
 };
 
 // counters carried through the parse-stage scan

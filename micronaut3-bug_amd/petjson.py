@@ -59,7 +59,7 @@ class Options(C.Structure):
 
 class DecodeResult(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in ("n_lines", "n_pets", "n_errors", "name_bytes", "cat_name_bytes",
-                                          "n_urls", "url_bytes", "n_tags", "tag_name_bytes")]
+                                          "n_urls", "url_bytes", "n_tags", "tag_name_bytes", "n_general")]
 
 
 class PetJsonError(RuntimeError):
@@ -368,17 +368,28 @@ class Codec:
         arrays = {k: torch.empty(max(1, v) + 8, dtype=tdt[DTYPES[k]], device=dev) for k, v in sizes.items()}
         return Columns(0, arrays, dict(caps), {k: 0 for k in arrays})
 
-    def decode(self, data, caps=None, err_cap=None, device=None):
+    def decode_buffers(self, caps, err_cap, device=None):
+        """Preallocated outputs for decode(..., out=...): (columns, err lines, err codes)."""
+        import torch
+        cols = self._alloc_decode(caps, device)
+        dev = cols.arrays["id"].device
+        el = torch.empty(max(1, err_cap), dtype=torch.int64, device=dev)
+        ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=dev)
+        return cols, el, ec
+
+    def decode(self, data, caps=None, err_cap=None, device=None, out=None):
         """Decode NDJSON held in a uint8 device tensor.  Returns (columns on the
-        device trimmed to size, error line indices, error codes, DecodeResult)."""
+        device trimmed to size, error line indices, error codes, DecodeResult).
+        `out` = decode_buffers(...) reuses preallocated outputs."""
         import torch
         n = data.numel()
-        caps = caps or decode_bounds(n)
-        cols = self._alloc_decode(caps, device)
-        if err_cap is None:
-            err_cap = n // 16 + 16
-        el = torch.empty(max(1, err_cap), dtype=torch.int64, device=data.device)
-        ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=data.device)
+        if out is None:
+            caps = caps or decode_bounds(n)
+            if err_cap is None:
+                err_cap = n // 16 + 16
+            out = self.decode_buffers(caps, err_cap, device)
+        cols, el, ec = out
+        err_cap = el.numel() if err_cap is None else err_cap
         torch.cuda.synchronize()
         s = cols.struct()
         res = DecodeResult()
