@@ -141,7 +141,19 @@ def main():
     ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device-to-device copy of BYTES (4x), to scale rocprof "
+                         "FETCH_SIZE / WRITE_SIZE readings")
     a = ap.parse_args()
+    if a.calibrate_copy:
+        import torch
+        src = torch.ones(a.calibrate_copy, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": a.calibrate_copy}))
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {a.gpus}); this codec's sharding is described "
               f"in DESIGN.md and no multi-GPU figure is produced.", file=sys.stderr)
@@ -164,6 +176,10 @@ def main():
     cpu = cpu_baseline_encode({"_config": cfg}, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
     alg = head["input_bytes"] + head["output_bytes"]
     achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "k_encode_traffic.json")
+    if os.path.exists(tf) and a.records == 10_000_000:
+        traffic = json.load(open(tf)).get(a.workload + "_encode", {}).get("traffic")
     line = {
         "metric": METRIC,
         "value": head["records_per_s"],
@@ -183,7 +199,7 @@ def main():
         "output_GBps": head["output_GBps"],
         "output_frac_hbm": head["output_frac_hbm"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBPS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "kernel": "k_encode", "kernel_ms": head["kernel_ms"],
                      "alg_bytes_per_launch": alg},
         "cpu_baseline": cpu,

@@ -88,6 +88,13 @@ def load_lib():
         p = lib_path()
         if not os.path.exists(p):
             raise FileNotFoundError(f"{p} missing: run __graft_entry__.build() (no CPU fallback exists)")
+        # torch bundles its own HIP runtime under the same soname as
+        # /opt/rocm's; whichever loads first is the one both use, and torch
+        # only finds the GPU through its own.  So torch is loaded first.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(p)
         vp, u64, i32 = C.c_void_p, C.c_uint64, C.c_int
         L.pj_create.restype = vp
