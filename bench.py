@@ -88,27 +88,30 @@ def decode_workload(codec, n, steps, warmup):
     for _ in range(warmup):
         codec.decode(data, out=bufs)
     torch.cuda.synchronize()
-    ti, tp = [], []
+    ti, tp, te = [], [], []
     t0 = time.perf_counter()
     for _ in range(steps):
         dcols, el, ec, res = codec.decode(data, out=bufs)
-        tm = codec.timings()            # [total, fill, index, host gap, fill, parse]
+        tm = codec.timings()            # [total, fill, k_dec_lines, host gap, fill, k_dec_block, k_dec_errcode]
         ti.append(tm[2])
         tp.append(tm[5])
+        te.append(tm[6])
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     ok = (res.n_errors == len(lines) and np.array_equal(el.cpu().numpy().astype(np.uint64), lines)
           and np.array_equal(ec.cpu().numpy(), codes) and res.n_pets == n - len(lines))
     out_bytes = sum(int(dcols[k].numel()) * dcols[k].element_size() for k in pj.COLS)
     in_bytes = int(data.numel())
-    kidx, kpar = sum(ti) / len(ti), sum(tp) / len(tp)
+    kidx, kpar, kerr = sum(ti) / len(ti), sum(tp) / len(tp), sum(te) / len(te)
     r = {"records": int(res.n_lines), "records_per_s": res.n_lines / wall, "ms_per_step": wall * 1e3,
          "input_bytes": in_bytes, "output_bytes": out_bytes, "input_GBps": in_bytes / wall / 1e9,
          "alg_GBps": (in_bytes + out_bytes) / wall / 1e9,
          "alg_frac_hbm": (in_bytes + out_bytes) / wall / 1e9 / HBM_PEAK_GBPS,
          "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
-         "kernels": {"k_dec_index_ms": kidx, "k_dec_parse_ms": kpar,
-                     "k_dec_index_GBps": in_bytes / (kidx * 1e-3) / 1e9}}
+         "lines_general_parser": int(res.n_general),
+         "kernels": {"k_dec_lines_ms": kidx, "k_dec_block_ms": kpar, "k_dec_errcode_ms": kerr,
+                     "k_dec_lines_GBps": in_bytes / (kidx * 1e-3) / 1e9,
+                     "k_dec_block_alg_GBps": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9}}
     return r
 
 

@@ -362,6 +362,8 @@ void pj_decode_bounds(uint64_t len, pj_pet_columns *c) {
 namespace {
 
 
+constexpr uint64_t VLB_WORDS = PJ_DEC_NCNT;   // vector look-back words per line block
+
 bool dec_cols_ok(const pj_pet_columns *o) {
     void *v[17];
     col_ptrs(const_cast<pj_pet_columns *>(o), v);
@@ -384,21 +386,17 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
     uint64_t ls_cap = len / 128 + 16;
     for (int attempt = 0; attempt < 2; attempt++) {
         const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
-        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | special nblk64 |
-        //                     line_start ls_cap | bad (bytes)
-        // header: 0-1 tickets, 2 line count, 4-11 totals, 12 general-queue length
-        const uint64_t o_dummy = 16, o_sidx = 48, o_spec = o_sidx + gidx,
-                       o_ls = o_spec + nblk64, o_bad = o_ls + ls_cap;
-        const uint64_t bytes = o_bad * 8 + nblk64 + 64;
-        PJ_HIP(ctx->index.ensure(bytes));
+        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | line_start ls_cap
+        // header: 0-1 tickets, 2 line count, 4-11 totals, 12 lines off the fast path,
+        //         13 deferred error-code queue length
+        const uint64_t o_dummy = 16, o_sidx = 48, o_ls = o_sidx + gidx;
+        PJ_HIP(ctx->index.ensure((o_ls + ls_cap) * 8 + 64));
         uint64_t *X = static_cast<uint64_t *>(ctx->index.p);
         DecParams P;
         std::memset(&P, 0, sizeof P);
         P.in = in;
         P.len = len;
         P.nblk64 = nblk64;
-        P.special = X + o_spec;
-        P.bad = reinterpret_cast<uint8_t *>(X + o_bad);
         P.line_start = X + o_ls;
         P.ls_cap = ls_cap;
         P.n_lines = X + 2;
@@ -410,6 +408,7 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.state_idx = X + o_sidx;
         P.tickets = reinterpret_cast<unsigned long long *>(X);
         P.dummy = reinterpret_cast<uint32_t *>(X + o_dummy);
+        P.gq_count = reinterpret_cast<unsigned long long *>(X + 12);
         ctx->n_ev = 0;
         if ((s = mark(ctx))) return s;
         PJ_HIP(pj_launch_fill_u64(X, 16, 0, ctx->stream));
@@ -425,21 +424,20 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             continue;
         }
         P.lines = lines;
-        const uint64_t lb = (uint64_t)pj_dec_parse_block();
-        const uint64_t gp = (lines + lb - 1) / lb;
-        // line-sized scratch: records | general queue | block sums
-        PJ_HIP(ctx->scan.ensure(lines * sizeof(LineRec) + lines * 8 + gp * PJ_DEC_NCNT * 8 + 1024));
-        uint8_t *Y = static_cast<uint8_t *>(ctx->scan.p);
-        P.rec = reinterpret_cast<LineRec *>(Y);
-        P.gq = reinterpret_cast<uint64_t *>(Y + align256(lines * sizeof(LineRec)));
-        P.bagg = reinterpret_cast<uint64_t *>(Y + align256(lines * sizeof(LineRec)) + align256(lines * 8));
-        P.gq_count = reinterpret_cast<unsigned long long *>(X + 12);
-        P.line_block = lb;
+        const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
+        // scan buffer: vector look-back words, then the deferred error-code queue
+        PJ_HIP(ctx->scan.ensure((gp * VLB_WORDS + lines + 8) * 8));
+        P.state_parse = static_cast<uint64_t *>(ctx->scan.p);
+        P.dq = P.state_parse + gp * VLB_WORDS;
+        P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(X + 12, 1, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
-        if (lines) PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
-        else {
+        if (lines) {
+            PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
+        } else {
             // no lines: the offset arrays still start with 0
             uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
                                   out->tag_name_off};

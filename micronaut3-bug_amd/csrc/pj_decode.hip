@@ -41,6 +41,9 @@ __device__ __forceinline__ uint32_t lt_bytes4(uint32_t x, uint32_t c) {
     return (((z >> 7) * 0x00204081u) >> 21) & 0xFu;
 }
 
+// bit i set iff bit 7 of byte i of m is set (m holds only bits 7, 15, 23, 31)
+__device__ __forceinline__ uint32_t movemask4(uint32_t m) { return (((m >> 7) * 0x00204081u) >> 21) & 0xFu; }
+
 __device__ __forceinline__ uint64_t prefix_xor(uint64_t x) {
     x ^= x << 1; x ^= x << 2; x ^= x << 4; x ^= x << 8; x ^= x << 16; x ^= x << 32;
     return x;
@@ -81,39 +84,10 @@ __device__ __forceinline__ uint64_t block_excl_scan_idx(uint64_t v, uint64_t *sh
     return idx_combine(before, excl);
 }
 
-// look-back with idx_combine (one full wave); values must fit LB_VAL.
-__device__ __forceinline__ uint64_t lb_resolve_idx(uint64_t *state, uint64_t b, uint64_t agg) {
-    const int l = lane_id();
-    if (b == 0) return 0;
-    uint64_t excl = 0;
-    int64_t j = (int64_t)b - 1;
-    for (;;) {
-        int64_t idx = j - l;
-        uint64_t s = idx >= 0 ? lb_load(&state[idx]) : LB_PRE;
-        uint32_t fl = (uint32_t)(s >> 62);
-        uint64_t notready = __ballot(fl == 0);
-        uint64_t isp = __ballot(fl == 2);
-        int fp = isp ? __builtin_ctzll(isp) : 64;
-        uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1);
-        if (notready & need) { __builtin_amdgcn_s_sleep(1); continue; }
-        // ordered reduction: higher lanes are earlier blocks
-        uint64_t v = l <= fp ? (s & LB_VAL) : 0;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            uint64_t o = shfl_u64(v, (l + d) & 63);
-            if (l + d < 64) v = idx_combine(o, v);
-        }
-        v = shfl_u64(v, 0);
-        excl = idx_combine(v, excl);
-        if (fp < 64) break;
-        j -= 64;
-    }
-    if (l == 0) lb_store(&state[b], LB_PRE | idx_combine(excl, agg));
-    return excl;
-}
-
+// Stage 1, k_dec_lines: one thread per 64-byte block; exact newline mask,
+// block scan + decoupled look-back of newline counts -> line starts.
 template <int BT>
-__global__ __launch_bounds__(BT) void k_dec_index(DecParams P) {
+__global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_blk, sh_pre;
     const uint32_t t = threadIdx.x;
@@ -123,152 +97,49 @@ __global__ __launch_bounds__(BT) void k_dec_index(DecParams P) {
     const uint64_t blk = b * BT + t;
     const bool live = blk < P.nblk64;
     const uint64_t st = blk * 64;
-    const uint8_t *in = P.in;
-
-    uint32_t w[16];
-    if (live && st + 64 <= P.len) {
-        const uint4 *q = reinterpret_cast<const uint4 *>(in + st);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint4 v = q[k];
-            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
-        }
-    } else {
-#pragma unroll
-        for (int k = 0; k < 16; k++) w[k] = 0x20202020u;
-        if (live) {
-            for (uint32_t j = 0; st + j < P.len; j++) {
-                uint32_t sh = 8 * (j & 3);
-                w[j >> 2] = (w[j >> 2] & ~(0xFFu << sh)) | ((uint32_t)in[st + j] << sh);
-            }
-        }
-    }
-    // ---- byte classes
-    uint64_t Q = 0, Bm = 0, C = 0, N = 0;
-    uint32_t anyb = 0, anyc = 0, anyh = 0;
-#pragma unroll
-    for (int k = 0; k < 16; k++) {
-        const uint32_t x = w[k];
-        Q |= (uint64_t)zero_bytes4(x ^ 0x22222222u) << (4 * k);
-        anyb |= any_zero(x ^ 0x5C5C5C5Cu);
-        anyc |= any_lt20(x);
-        anyh |= x & 0x80808080u;
-    }
-    if (anyb) {
-#pragma unroll
-        for (int k = 0; k < 16; k++) Bm |= (uint64_t)zero_bytes4(w[k] ^ 0x5C5C5C5Cu) << (4 * k);
-    }
-    if (anyc) {
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            C |= (uint64_t)lt_bytes4(w[k], 0x20) << (4 * k);
-            N |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
-        }
-    }
-    // UTF-8 structure (jackson: leads C0-DF / E0-EF / F0-F7, 10xxxxxx continuations)
-    uint64_t u8err = 0, expect_in = 0;
-    uint32_t bs_run = 0;
-    if (live && st > 0) {
-        // bytes just before the block: backslash run parity and pending continuations
-        uint64_t a = st >= 8 ? st - 8 : 0;
-        uint64_t prev = 0;
-        for (uint64_t j = a; j < st; j++) prev |= (uint64_t)in[j] << (8 * (j - a + 8 - (st - a)));
-        // prev holds the (up to) 8 bytes before st, the byte at st-1 in bits 63:56
-        for (int k = 7; k >= 0 && ((prev >> (8 * k)) & 0xFF) == '\\' && (uint64_t)(8 - k) <= st; k--) bs_run++;
-        if (bs_run == 8) {
-            uint64_t q = st - 8;
-            while (q > 0 && in[q - 1] == '\\') { bs_run++; q--; }
-        }
-        uint32_t b1 = (uint32_t)(prev >> 56) & 0xFF, b2 = (uint32_t)(prev >> 48) & 0xFF, b3 = (uint32_t)(prev >> 40) & 0xFF;
-        if (st >= 1) {
-            if (b1 >= 0xC0 && b1 <= 0xDF) expect_in |= 1;
-            else if (b1 >= 0xE0 && b1 <= 0xEF) expect_in |= 3;
-            else if (b1 >= 0xF0 && b1 <= 0xF7) expect_in |= 7;
-        }
-        if (st >= 2) {
-            if (b2 >= 0xE0 && b2 <= 0xEF) expect_in |= 1;
-            else if (b2 >= 0xF0 && b2 <= 0xF7) expect_in |= 3;
-        }
-        if (st >= 3 && b3 >= 0xF0 && b3 <= 0xF7) expect_in |= 1;
-    }
-    if (anyh | expect_in) {
-        uint64_t cont = 0, l2 = 0, l3 = 0, l4 = 0, badl = 0;
-        for (int j = 0; j < 64; j++) {
-            uint32_t c = (w[j >> 2] >> (8 * (j & 3))) & 0xFF;
-            uint64_t bit = 1ull << j;
-            if (c < 0x80) continue;
-            if (c < 0xC0) cont |= bit;
-            else if (c < 0xE0) l2 |= bit;
-            else if (c < 0xF0) l3 |= bit;
-            else if (c < 0xF8) l4 |= bit;
-            else badl |= bit;
-        }
-        uint64_t expect = (l2 << 1) | (l3 << 1) | (l3 << 2) | (l4 << 1) | (l4 << 2) | (l4 << 3) | expect_in;
-        u8err = (cont ^ expect) | badl;
-    }
-    // ---- escapes: position e after a backslash run is escaped iff the run
-    // (including its part before the block) has odd length
-    uint64_t E = 0;
-    const bool c_odd = bs_run & 1;
-    if (Bm) {
-        constexpr uint64_t EVEN = 0x5555555555555555ull, ODD = ~EVEN;
-        uint64_t rs = Bm & ~(Bm << 1);
-        uint64_t rs_e = rs & EVEN, rs_o = rs & ODD;
-        if (c_odd && (Bm & 1)) { rs_e &= ~1ull; rs_o |= 1ull; }
-        E = (((Bm + rs_e) & ~Bm) & ODD) | (((Bm + rs_o) & ~Bm) & EVEN);
-    }
-    if (c_odd && !(Bm & 1)) E |= 1ull;
-    const uint64_t Qu = Q & ~E;
-    // ---- block summary for the scan
-    uint64_t summ = 0;
+    uint64_t N = 0;
     if (live) {
-        uint64_t par;
-        if (N) {
-            int last = 63 - __builtin_clzll(N);
-            uint64_t above = last == 63 ? 0 : (Qu >> (last + 1));
-            par = __builtin_popcountll(above) & 1;
-        } else par = __builtin_popcountll(Qu) & 1;
-        summ = ((uint64_t)__builtin_popcountll(N) << 2) | (N ? 2 : 0) | par;
+        if (st + 64 <= P.len) {
+            const uint4 *q = reinterpret_cast<const uint4 *>(P.in + st);
+            uint32_t w[16];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint4 v = q[k];
+                w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+            }
+            uint32_t any = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) any |= any_zero(w[k] ^ 0x0A0A0A0Au);
+            if (any) {
+#pragma unroll
+                for (int k = 0; k < 16; k++) N |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
+            }
+        } else {
+            for (uint32_t j = 0; st + j < P.len; j++) N |= (uint64_t)(P.in[st + j] == '\n') << j;
+        }
     }
     uint64_t agg;
-    const uint64_t pre_in = block_excl_scan_idx<BT>(summ, sh_scan, &agg);
-    if (t == 0) lb_store(&P.state_idx[b], (b == 0 ? LB_PRE : LB_AGG) | agg);
+    const uint64_t pre = block_excl_scan<BT>((uint64_t)__builtin_popcountll(N), sh_scan, &agg);
+    if (t == 0) lb_publish(P.state_idx, b, agg);
     if (t < 64) {
-        uint64_t e = lb_resolve_idx(P.state_idx, b, agg);
+        const uint64_t e = lb_resolve(P.state_idx, b, agg);
         if (t == 0) sh_pre = e;
     }
     __syncthreads();
     if (!live) return;
-    const uint64_t carry = idx_combine(sh_pre, pre_in);
-    const uint64_t lines_before = carry >> 2;
-    const uint64_t cin = carry & 1;                 // in a string at block start
-    // ---- in-string mask with resets after newlines
-    uint64_t x = prefix_xor(Qu) ^ (cin ? ~0ull : 0ull);
+    uint64_t li = sh_pre + pre;
     for (uint64_t m = N; m; m &= m - 1) {
-        int p = __builtin_ctzll(m);
-        if ((x >> p) & 1) x ^= p == 63 ? 0ull : (~0ull << (p + 1));
-    }
-    const uint64_t inS = x;
-    const uint64_t near = inS | (inS << 1) | cin;
-    const uint64_t bad = (C & inS) | (u8err & near);
-    P.special[blk] = Bm | Qu;
-    P.bad[blk] = bad ? 1 : 0;
-    // ---- line index
-    uint64_t li = lines_before;
-    for (uint64_t m = N; m; m &= m - 1) {
-        int p = __builtin_ctzll(m);
         li++;
-        if (li < P.ls_cap) P.line_start[li] = st + (uint64_t)p + 1;
+        if (li < P.ls_cap) P.line_start[li] = st + (uint64_t)__builtin_ctzll(m) + 1;
     }
     if (blk == 0) P.line_start[0] = 0;
     if (blk == P.nblk64 - 1) {
-        uint32_t lastb = (w[((P.len - 1) & 63) >> 2] >> (8 * ((P.len - 1) & 3))) & 0xFF;
-        uint64_t nl = li + (lastb != '\n' ? 1 : 0);
-        if (lastb != '\n' && nl < P.ls_cap) P.line_start[nl] = P.len + 1;
+        const bool open = P.in[P.len - 1] != '\n';      // last line without '\n'
+        const uint64_t nl = li + (open ? 1 : 0);
+        if (open && nl < P.ls_cap) P.line_start[nl] = P.len + 1;
         *P.n_lines = nl;
     }
 }
-
 // =========================================================== stage 2
 // Property keys, container contexts and parser states.
 enum { K_UNKNOWN = 0, K_ID, K_CATEGORY, K_NAME, K_PHOTOURLS, K_TAGS, K_STATUS };
@@ -440,6 +311,14 @@ __device__ __noinline__ bool opener_at(const uint8_t *s, uint32_t p, int d) {
     return kind;
 }
 
+// Where a line's bytes live: the LDS tile of its workgroup (with the tile's
+// specials bitmap) or global memory (no bitmap: the byte-by-byte path).
+struct Src {
+    const uint8_t *in;
+    uint64_t len;
+    const uint64_t *special;
+};
+
 // 16-byte window over a line for the skeleton bytes.
 struct Win {
     const uint8_t *in;
@@ -472,10 +351,10 @@ struct Win {
 // first pass found valid, at the offsets pos[].  Strings are skipped through
 // the specials bitmap unless `slow`.  One string-scan site, one copy site
 // and one scalar site keep the whole machine in registers.
-__device__ __forceinline__ int run_line(const DecParams &P, uint64_t s0, uint32_t n, bool slow, bool write,
-                                        LineInfo &L, const uint64_t *pos) {
-    const uint8_t *s = P.in + s0;
-    Win W{P.in, P.len, s0, 0, 0, 0xFFFFFF00u};
+__device__ __forceinline__ int run_line(const DecParams &P, const Src &S, uint64_t s0, uint32_t n, bool slow,
+                                        bool write, LineInfo &L, const uint64_t *pos) {
+    const uint8_t *s = S.in + s0;
+    Win W{S.in, S.len, s0, 0, 0, 0xFFFFFF00u};
     uint32_t p = 0;
 #define PEEK() (p < n ? W.at(p) : -1)
 #define SKIP_WS()                                                \
@@ -597,8 +476,8 @@ __device__ __forceinline__ int run_line(const DecParams &P, uint64_t s0, uint32_
                     uint32_t sp = n;
                     if (a < lim) {
                         uint64_t wi = a >> 6;
-                        uint64_t m = P.special[wi] & (~0ull << (a & 63));
-                        while (!m && (wi + 1) * 64 < lim) m = P.special[++wi];
+                        uint64_t m = S.special[wi] & (~0ull << (a & 63));
+                        while (!m && (wi + 1) * 64 < lim) m = S.special[++wi];
                         if (m) {
                             const uint64_t at = wi * 64 + (uint64_t)__builtin_ctzll(m);
                             if (at < lim) sp = (uint32_t)(at - s0);
@@ -758,10 +637,12 @@ __device__ __forceinline__ int run_line(const DecParams &P, uint64_t s0, uint32_
                     if (ctx == X_PET) {
                         if (!write) {
                             if (k1 == K_ID) { L.has_id = 0; L.id = 0; }
-                            else if (k1 == K_CATEGORY) { L.has_cat = 0; L.cat_id = 0; L.cat_flags = 0; L.cat_len = 0; }
-                            else if (k1 == K_NAME) L.has_name = 0;
-                            else if (k1 == K_PHOTOURLS) { L.has_photo = 0; L.n_urls = 0; L.url_bytes = 0; }
-                            else if (k1 == K_TAGS) { L.has_tags = 0; L.n_tags = 0; L.tag_bytes = 0; }
+                            // a later null also forgets where an earlier value
+                            // was, so the writing pass copies nothing of it
+                            else if (k1 == K_CATEGORY) { L.has_cat = 0; L.cat_id = 0; L.cat_flags = 0; L.cat_len = 0; L.cat_pos = 0; }
+                            else if (k1 == K_NAME) { L.has_name = 0; L.name_len = 0; }
+                            else if (k1 == K_PHOTOURLS) { L.has_photo = 0; L.n_urls = 0; L.url_bytes = 0; L.photo_pos = 0; }
+                            else if (k1 == K_TAGS) { L.has_tags = 0; L.n_tags = 0; L.tag_bytes = 0; L.tags_pos = 0; }
                             else if (k1 == K_STATUS) L.status = PJ_STATUS_NULL;
                         }
                     } else if (k2 == K_ID) { sub_fl &= ~PJ_SUB_HAS_ID; sub_id = 0; }
@@ -964,25 +845,22 @@ struct FLine {
         return r;
     }
     // copy the decoded string (content from q, described by r) to dst+off
-    __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst, uint64_t off, uint32_t *dummy) const {
-        WriteSink ws;
-        ws.init(dst, off, dummy);
+    __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst, uint64_t off, uint32_t *) const {
         if (!r.esc) {
-            const uint8_t *src = s + q;
-            uint32_t k = 0;
-            for (; k + 8 <= r.dlen; k += 8) ws.put8(ldu64(src + k), 8);
-            if (k < r.dlen) ws.put8(ld_tail(src + k, (int)(r.dlen - k)), (int)(r.dlen - k));
-        } else {
-            for (uint32_t x = q; x < r.end;) {
-                const uint32_t c = s[x];
-                if (c == '\\') {
-                    Esc e = escape_at(s, n, x);
-                    ws.put(e.out, e.k);
-                    x += e.adv;
-                } else {
-                    ws.put_byte(c);
-                    x++;
-                }
+            copy_exact(dst + off, s + q, r.dlen);
+            return;
+        }
+        StoreSink ws;
+        ws.init(dst + off);
+        for (uint32_t x = q; x < r.end;) {
+            const uint32_t c = s[x];
+            if (c == '\\') {
+                const Esc e = escape_at(s, n, x);
+                ws.put(e.out, e.k);
+                x += e.adv;
+            } else {
+                ws.put(c, 1);
+                x++;
             }
         }
         ws.finish();
@@ -1098,9 +976,84 @@ __device__ __forceinline__ int fsub(const FLine &F, uint32_t &p, int64_t &id, ui
     return 0;
 }
 
+// Does the 8-byte prefix at a key start belong to one of the Pet keys as the
+// encoder writes them?
+__device__ __forceinline__ bool known8(uint64_t k8) {
+    return ((k8 & KP_ID_MASK) == KP_ID) | (k8 == KP_CATEGORY) | (k8 == KP_NAME) | (k8 == KP_PHOTO) | (k8 == KP_TAGS) |
+           (k8 == KP_STATUS);
+}
+
+// An unknown property at p: its key, ':' and a string, integer or literal
+// value are skipped, as serde skips properties the bean does not declare.
+// Keys with escapes, known keys in another shape, nested values and
+// anything irregular return PJ_BAIL.  Returns (new p) << 32 | code.
+__device__ __noinline__ uint64_t fskip(const FLine &F, uint32_t p) {
+    constexpr uint64_t BAIL = (uint32_t)PJ_BAIL;
+    if (F.at(p) != '"') return BAIL;
+    const Str k = F.str(p + 1);
+    if (k.err) return (uint32_t)k.err;
+    if (k.esc) return BAIL;
+    const uint64_t x = F.ld8(p + 1), x2 = F.ld8(p + 9) & 0xFF;
+    const uint32_t L = k.dlen;
+    if ((L == 2 && (x & 0xFFFFull) == pack8("id", 2)) || (L == 8 && x == pack8("category", 8)) ||
+        (L == 4 && (x & 0xFFFFFFFFull) == pack8("name", 4)) || (L == 9 && x == pack8("photoUrl", 8) && x2 == 's') ||
+        (L == 4 && (x & 0xFFFFFFFFull) == pack8("tags", 4)) || (L == 6 && (x & 0xFFFFFFFFFFFFull) == pack8("status", 6)))
+        return BAIL;
+    p = k.end + 1;
+    if (F.at(p) != ':') return BAIL;
+    p++;
+    const int c = F.at(p);
+    if (c == '"') {
+        const Str v = F.str(p + 1);
+        if (v.err) return (uint32_t)v.err;
+        p = v.end + 1;
+    } else if (c == '-' || (c >= '0' && c <= '9')) {
+        uint32_t q = p + (c == '-'), d = 0;
+        for (int i = 0; i < 3; i++) {
+            const uint64_t nd = nondigit8(F.ld8(q + d));
+            const uint32_t m = nd ? (uint32_t)(__builtin_ctzll(nd) >> 3) : 8;
+            d += m;
+            if (m < 8) break;
+        }
+        if (d == 0 || d >= 24 || q + d > F.n) return BAIL;
+        if (F.at(q) == '0' && d > 1) return BAIL;
+        p = q + d;
+    } else {
+        const uint64_t w = F.ld8(p);
+        if ((w & 0xFFFFFFFFull) == pack8("true", 4) || (w & 0xFFFFFFFFull) == pack8("null", 4)) p += 4;
+        else if ((w & 0xFFFFFFFFFFull) == pack8("false", 5)) p += 5;
+        else return BAIL;
+    }
+    if (p > F.n) return BAIL;
+    return (uint64_t)p << 32;
+}
+
+// Separator after a property value: ',' loads the next key prefix, '}' ends
+// the object; anything else is not canonical.
+#define FL_SEP()                                                    \
+    {                                                               \
+        const int c_ = F.at(p);                                     \
+        if (c_ == ',') { p++; k8 = F.ld8(p); }                      \
+        else if (c_ == '}') more = false;                           \
+        else return PJ_BAIL;                                        \
+    }
+
+// Unknown properties before the next key.
+#define FL_UNKNOWN()                                                \
+    while (more && !known8(k8)) {                                   \
+        const uint64_t r_ = fskip(F, p);                            \
+        if ((uint32_t)r_) return (int)(uint32_t)r_;                 \
+        p = (uint32_t)(r_ >> 32);                                   \
+        FL_SEP();                                                   \
+    }
+
+// The properties are tried in schema order, each at most once, as straight
+// code: the lanes of a wave then walk the same instruction stream whatever
+// subset of properties their lines hold.
 template <bool WRITE>
-__device__ __forceinline__ int fline(const DecParams &P, uint64_t s0, uint32_t n, LineRec &R, const uint64_t *pos) {
-    const FLine F{P.in + s0, P.special, s0, P.len, n};
+__device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t s0, uint32_t n, LineRec &R,
+                                     const uint64_t *pos) {
+    const FLine F{S.in + s0, S.special, s0, S.len, n};
     const pj_pet_columns &o = P.o;
     if (n == 0) return PJ_REC_EMPTY;
     if (F.at(0) != '{') return PJ_BAIL;
@@ -1109,126 +1062,123 @@ __device__ __forceinline__ int fline(const DecParams &P, uint64_t s0, uint32_t n
     uint8_t status = PJ_STATUS_NULL;
     int64_t id = 0, cat_id = 0;
     uint32_t cat_fl = 0, name_len = 0, cat_len = 0, n_urls = 0, url_bytes = 0, n_tags = 0, tag_bytes = 0;
-    int slot = 0;                    // next schema slot allowed
-    if (F.at(p) != '}') {
-        for (;;) {
-            const uint64_t k8 = F.ld8(p);
-            int key, klen;
-            if ((k8 & KP_ID_MASK) == KP_ID) { key = 0; klen = 5; }
-            else if (k8 == KP_CATEGORY && (F.ld8(p + 8) & 0xFFFFFFFFull) == pack8("y\":{", 4)) { key = 1; klen = 11; }
-            else if (k8 == KP_NAME) { key = 2; klen = 7; }
-            else if (k8 == KP_PHOTO && (F.ld8(p + 8) & 0xFFFFFFFFFFull) == pack8("ls\":[", 5)) { key = 3; klen = 12; }
-            else if (k8 == KP_TAGS) { key = 4; klen = 7; }
-            else if (k8 == KP_STATUS && (F.ld8(p + 8) & 0xFFFFull) == pack8(":\"", 2)) { key = 5; klen = 9; }
-            else return PJ_BAIL;
-            if (key < slot || p + (uint32_t)klen >= n) return PJ_BAIL;
-            slot = key + 1;
-            p += (uint32_t)klen;
-            switch (key) {
-            case 0: {                                             // id
-                int e = fnum<WRITE>(F, p, id);
-                if (e) return e;
-                flags |= PJ_PET_HAS_ID;
-                break;
-            }
-            case 1: {                                             // category {
-                p++;
-                uint32_t nq = 0;
-                Str nr{0, 0, 0, false};
-                int e = fsub<WRITE>(F, p, cat_id, cat_fl, nq, nr);
-                if (e) return e;
-                flags |= PJ_PET_HAS_CATEGORY;
-                cat_len = (cat_fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
-                if (WRITE && cat_len && pos[C_CATB] + cat_len <= o.cap_cat_name_bytes)
-                    F.copy(nq, nr, o.cat_name_bytes, pos[C_CATB], P.dummy);
-                break;
-            }
-            case 2: {                                             // name "
-                const uint32_t q = p + 1;
-                Str r = F.str(q);
-                if (r.err) return r.err;
-                p = r.end + 1;
-                flags |= PJ_PET_HAS_NAME;
-                name_len = r.dlen;
-                if (WRITE && r.dlen && pos[C_NAMEB] + r.dlen <= o.cap_name_bytes)
-                    F.copy(q, r, o.name_bytes, pos[C_NAMEB], P.dummy);
-                break;
-            }
-            case 3: {                                             // photoUrls [
-                flags |= PJ_PET_HAS_PHOTOURLS;
-                p++;
-                uint64_t u = WRITE ? pos[C_URLS] : 0, ub = WRITE ? pos[C_URLB] : 0;
-                if (F.at(p) == ']') { p++; break; }
-                for (;;) {
-                    if (F.at(p) != '"') return PJ_BAIL;
-                    const uint32_t q = p + 1;
-                    Str r = F.str(q);
-                    if (r.err) return r.err;
-                    p = r.end + 1;
-                    n_urls++;
-                    url_bytes += r.dlen;
-                    if (WRITE) {
-                        if (r.dlen && ub + r.dlen <= o.cap_url_bytes) F.copy(q, r, o.url_bytes, ub, P.dummy);
-                        ub += r.dlen;
-                        u++;
-                        if (u <= o.cap_urls) o.url_off[u] = ub;
-                    }
-                    const int c = F.at(p++);
-                    if (c == ',') continue;
-                    if (c == ']') break;
-                    return PJ_BAIL;
-                }
-                break;
-            }
-            case 4: {                                             // tags [
-                flags |= PJ_PET_HAS_TAGS;
-                p++;
-                uint64_t g = WRITE ? pos[C_TAGS] : 0, gb = WRITE ? pos[C_TAGB] : 0;
-                if (F.at(p) == ']') { p++; break; }
-                for (;;) {
-                    if (F.at(p) != '{') return PJ_BAIL;
-                    p++;
-                    int64_t tid;
-                    uint32_t tfl, nq = 0;
-                    Str nr{0, 0, 0, false};
-                    int e = fsub<WRITE>(F, p, tid, tfl, nq, nr);
-                    if (e) return e;
-                    const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
-                    n_tags++;
-                    tag_bytes += tl;
-                    if (WRITE) {
-                        if (g < o.cap_tags) { o.tag_id[g] = tid; o.tag_flags[g] = (uint8_t)tfl; }
-                        if (tl && gb + tl <= o.cap_tag_name_bytes) F.copy(nq, nr, o.tag_name_bytes, gb, P.dummy);
-                        gb += tl;
-                        g++;
-                        if (g <= o.cap_tags) o.tag_name_off[g] = gb;
-                    }
-                    const int c = F.at(p++);
-                    if (c == ',') continue;
-                    if (c == ']') break;
-                    return PJ_BAIL;
-                }
-                break;
-            }
-            default: {                                            // status "
-                const uint32_t q = p + 1;
-                Str r = F.str(q);
-                if (r.err) return r.err;
-                p = r.end + 1;
-                if (r.esc) return PJ_BAIL;
-                const uint64_t x = F.ld8(q), y = F.ld8(q + 8) & 0xFF;
-                if (r.dlen == 9 && x == pack8("availabl", 8) && y == 'e') status = PJ_STATUS_AVAILABLE;
-                else if (r.dlen == 7 && (x & 0xFFFFFFFFFFFFFFull) == pack8("pending", 7)) status = PJ_STATUS_PENDING;
-                else if (r.dlen == 4 && (x & 0xFFFFFFFFull) == pack8("sold", 4)) status = PJ_STATUS_SOLD;
-                else return PJ_REC_BAD_STATUS;                    // the enum's @JsonCreator rejects it
-            }
-            }
-            const int c = F.at(p);
-            if (c == ',') { p++; continue; }
-            if (c == '}') break;
-            return PJ_BAIL;
-        }
+    bool more = F.at(p) != '}';
+    uint64_t k8 = more ? F.ld8(p) : 0;
+    FL_UNKNOWN();
+    // id
+    if (more && (k8 & KP_ID_MASK) == KP_ID) {
+        p += 5;
+        const int e = fnum<WRITE>(F, p, id);
+        if (e) return e;
+        flags |= PJ_PET_HAS_ID;
+        FL_SEP();
     }
+    FL_UNKNOWN();
+    // category
+    if (more && k8 == KP_CATEGORY && (F.ld8(p + 8) & 0xFFFFFFFFull) == pack8("y\":{", 4)) {
+        p += 12;
+        uint32_t nq = 0;
+        Str nr{0, 0, 0, false};
+        const int e = fsub<WRITE>(F, p, cat_id, cat_fl, nq, nr);
+        if (e) return e;
+        flags |= PJ_PET_HAS_CATEGORY;
+        cat_len = (cat_fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+        if (WRITE && cat_len && pos[C_CATB] + cat_len <= o.cap_cat_name_bytes)
+            F.copy(nq, nr, o.cat_name_bytes, pos[C_CATB], P.dummy);
+        FL_SEP();
+    }
+    FL_UNKNOWN();
+    // name
+    if (more && k8 == KP_NAME) {
+        const uint32_t q = p + 8;
+        const Str r = F.str(q);
+        if (r.err) return r.err;
+        p = r.end + 1;
+        flags |= PJ_PET_HAS_NAME;
+        name_len = r.dlen;
+        if (WRITE && r.dlen && pos[C_NAMEB] + r.dlen <= o.cap_name_bytes)
+            F.copy(q, r, o.name_bytes, pos[C_NAMEB], P.dummy);
+        FL_SEP();
+    }
+    FL_UNKNOWN();
+    // photoUrls
+    if (more && k8 == KP_PHOTO && (F.ld8(p + 8) & 0xFFFFFFFFFFull) == pack8("ls\":[", 5)) {
+        p += 13;
+        flags |= PJ_PET_HAS_PHOTOURLS;
+        uint64_t u = WRITE ? pos[C_URLS] : 0, ub = WRITE ? pos[C_URLB] : 0;
+        if (F.at(p) == ']') p++;
+        else {
+            for (;;) {
+                if (F.at(p) != '"') return PJ_BAIL;
+                const uint32_t q = p + 1;
+                const Str r = F.str(q);
+                if (r.err) return r.err;
+                p = r.end + 1;
+                n_urls++;
+                url_bytes += r.dlen;
+                if (WRITE) {
+                    if (r.dlen && ub + r.dlen <= o.cap_url_bytes) F.copy(q, r, o.url_bytes, ub, P.dummy);
+                    ub += r.dlen;
+                    u++;
+                    if (u <= o.cap_urls) o.url_off[u] = ub;
+                }
+                const int c = F.at(p++);
+                if (c == ']') break;
+                if (c != ',') return PJ_BAIL;
+            }
+        }
+        FL_SEP();
+    }
+    FL_UNKNOWN();
+    // tags
+    if (more && k8 == KP_TAGS) {
+        p += 8;
+        flags |= PJ_PET_HAS_TAGS;
+        uint64_t g = WRITE ? pos[C_TAGS] : 0, gb = WRITE ? pos[C_TAGB] : 0;
+        if (F.at(p) == ']') p++;
+        else {
+            for (;;) {
+                if (F.at(p) != '{') return PJ_BAIL;
+                p++;
+                int64_t tid;
+                uint32_t tfl, nq = 0;
+                Str nr{0, 0, 0, false};
+                const int e = fsub<WRITE>(F, p, tid, tfl, nq, nr);
+                if (e) return e;
+                const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+                n_tags++;
+                tag_bytes += tl;
+                if (WRITE) {
+                    if (g < o.cap_tags) { o.tag_id[g] = tid; o.tag_flags[g] = (uint8_t)tfl; }
+                    if (tl && gb + tl <= o.cap_tag_name_bytes) F.copy(nq, nr, o.tag_name_bytes, gb, P.dummy);
+                    gb += tl;
+                    g++;
+                    if (g <= o.cap_tags) o.tag_name_off[g] = gb;
+                }
+                const int c = F.at(p++);
+                if (c == ']') break;
+                if (c != ',') return PJ_BAIL;
+            }
+        }
+        FL_SEP();
+    }
+    FL_UNKNOWN();
+    // status
+    if (more && k8 == KP_STATUS && (F.ld8(p + 8) & 0xFFFFull) == pack8(":\"", 2)) {
+        const uint32_t q = p + 10;
+        const Str r = F.str(q);
+        if (r.err) return r.err;
+        p = r.end + 1;
+        if (r.esc) return PJ_BAIL;
+        const uint64_t x = F.ld8(q), y = F.ld8(q + 8) & 0xFF;
+        if (r.dlen == 9 && x == pack8("availabl", 8) && y == 'e') status = PJ_STATUS_AVAILABLE;
+        else if (r.dlen == 7 && (x & 0xFFFFFFFFFFFFFFull) == pack8("pending", 7)) status = PJ_STATUS_PENDING;
+        else if (r.dlen == 4 && (x & 0xFFFFFFFFull) == pack8("sold", 4)) status = PJ_STATUS_SOLD;
+        else return PJ_REC_BAD_STATUS;                            // the enum's @JsonCreator rejects it
+        FL_SEP();
+    }
+    FL_UNKNOWN();
+    if (more) return PJ_BAIL;                                     // repeated or out-of-order key
     if (p + 1 != n) return PJ_BAIL;                               // trailing bytes: general rules
     if (!(flags & PJ_PET_HAS_NAME)) return PJ_REC_MISSING_NAME;   // required (petstore.json:873-876)
     if (!(flags & PJ_PET_HAS_PHOTOURLS)) return PJ_REC_MISSING_PHOTOURLS;
@@ -1251,188 +1201,465 @@ __device__ __forceinline__ int fline(const DecParams &P, uint64_t s0, uint32_t n
     }
     return 0;
 }
+#undef FL_SEP
+#undef FL_UNKNOWN
 
-__device__ __forceinline__ bool line_bounds(const DecParams &P, uint64_t l, uint64_t &s, uint32_t &n) {
-    s = P.line_start[l];
-    const uint64_t e = P.line_start[l + 1] - 1;
-    n = (uint32_t)(e - s);
-    bool slow = false;
-    if (n)
-        for (uint64_t k = s >> 6; k <= (e - 1) >> 6; k++) slow |= P.bad[k] != 0;
-    return slow;
+// ---------------------------------------------------------------- tile bitmaps
+// Build, for the nw 64-byte words of an LDS tile that starts at a line
+// start (or whose first line starts after a newline inside it), the specials
+// bitmap (unescaped quotes | backslashes) and a per-word flag for raw control
+// characters or malformed UTF-8 inside strings.  Each thread owns a
+// contiguous run of words; the in-string carry between runs comes from a
+// block scan of (newline seen, quote parity).
+template <int BT>
+__device__ __forceinline__ void tile_bitmaps(const uint8_t *tile, uint32_t nw, uint64_t *spec, uint64_t *qu,
+                                             uint64_t *sh) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t per = (nw + BT - 1) / BT;
+    const uint32_t w0 = min(t * per, nw), w1 = min(w0 + per, nw);
+    // pass 1: masks, escapes, per-run summary
+    uint64_t summ = 0;
+    for (uint32_t w = w0; w < w1; w++) {
+        const uint4 *q4 = reinterpret_cast<const uint4 *>(tile + 64 * w);
+        uint32_t x[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 v = q4[k];
+            x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+        }
+        uint64_t Q = 0, B = 0, N = 0;
+        uint32_t anyb = 0, anyn = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            Q |= (uint64_t)zero_bytes4(x[k] ^ 0x22222222u) << (4 * k);
+            anyb |= any_zero(x[k] ^ 0x5C5C5C5Cu);
+            anyn |= any_zero(x[k] ^ 0x0A0A0A0Au);
+        }
+        if (anyb) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) B |= (uint64_t)zero_bytes4(x[k] ^ 0x5C5C5C5Cu) << (4 * k);
+        }
+        if (anyn) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) N |= (uint64_t)zero_bytes4(x[k] ^ 0x0A0A0A0Au) << (4 * k);
+        }
+        // backslash run ending just before the word (within the tile)
+        uint32_t run = 0;
+        for (uint32_t j = 64 * w; j > 0 && tile[j - 1] == '\\'; j--) run++;
+        uint64_t E = 0;
+        if (B) {
+            constexpr uint64_t EVEN = 0x5555555555555555ull, ODD = ~EVEN;
+            const uint64_t rs = B & ~(B << 1);
+            uint64_t rs_e = rs & EVEN, rs_o = rs & ODD;
+            if ((run & 1) && (B & 1)) { rs_e &= ~1ull; rs_o |= 1ull; }
+            E = (((B + rs_e) & ~B) & ODD) | (((B + rs_o) & ~B) & EVEN);
+        }
+        if ((run & 1) && !(B & 1)) E |= 1ull;
+        const uint64_t Qu = Q & ~E;
+        spec[w] = B | Qu;
+        qu[w] = N;                                      // newline mask until pass 2, then bad bytes
+        uint64_t par;
+        if (N) {
+            const int last = 63 - __builtin_clzll(N);
+            par = last == 63 ? 0 : (__builtin_popcountll(Qu >> (last + 1)) & 1);
+        } else par = __builtin_popcountll(Qu) & 1;
+        summ = idx_combine(summ, (N ? 2ull : 0ull) | par);
+    }
+    uint64_t tot;
+    const uint64_t carry0 = block_excl_scan_idx<BT>(summ, sh, &tot);
+    // pass 2: in-string mask, faults inside strings
+    uint64_t cin = carry0 & 1;
+    for (uint32_t w = w0; w < w1; w++) {
+        const uint64_t Qu = spec[w], N = qu[w];
+        const uint32_t *x32 = reinterpret_cast<const uint32_t *>(tile + 64 * w);
+        // Qu currently holds B | Qu: strip backslashes again (B bits are never quotes)
+        uint64_t Bq = 0;
+        uint32_t anyc = 0, anyh = 0;
+        uint32_t x[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            x[k] = x32[k];
+            anyc |= any_lt20(x[k]);
+            anyh |= x[k] & 0x80808080u;
+            Bq |= (uint64_t)zero_bytes4(x[k] ^ 0x22222222u) << (4 * k);
+        }
+        const uint64_t Quq = Qu & Bq;                   // the unescaped quotes
+        uint64_t s = prefix_xor(Quq) ^ (cin ? ~0ull : 0ull);
+        for (uint64_t m = N; m; m &= m - 1) {
+            const int p = __builtin_ctzll(m);
+            if ((s >> p) & 1) s ^= p == 63 ? 0ull : (~0ull << (p + 1));
+        }
+        uint64_t bad = 0;
+        if (anyc) {
+            uint64_t C = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) C |= (uint64_t)lt_bytes4(x[k], 0x20) << (4 * k);
+            bad |= C & s;
+        }
+        uint64_t expect_in = 0;
+        if (w > 0) {
+            const uint32_t b1 = tile[64 * w - 1], b2 = w * 64 >= 2 ? tile[64 * w - 2] : 0,
+                           b3 = w * 64 >= 3 ? tile[64 * w - 3] : 0;
+            if (b1 >= 0xC0 && b1 <= 0xDF) expect_in |= 1;
+            else if (b1 >= 0xE0 && b1 <= 0xEF) expect_in |= 3;
+            else if (b1 >= 0xF0 && b1 <= 0xF7) expect_in |= 7;
+            if (b2 >= 0xE0 && b2 <= 0xEF) expect_in |= 1;
+            else if (b2 >= 0xF0 && b2 <= 0xF7) expect_in |= 3;
+            if (b3 >= 0xF0 && b3 <= 0xF7) expect_in |= 1;
+        }
+        if (anyh | expect_in) {
+            // byte classes of UTF-8, four bytes at a time: each class test
+            // lines the relevant bit of every byte up at bit 7
+            uint64_t cont = 0, l2 = 0, l3 = 0, l4 = 0, badl = 0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const uint32_t v = x[k];
+                const uint32_t h7 = v & 0x80808080u, h6 = (v << 1) & 0x80808080u, h5 = (v << 2) & 0x80808080u,
+                               h4 = (v << 3) & 0x80808080u, h3 = (v << 4) & 0x80808080u;
+                const uint32_t hh = h7 & h6, hhh = hh & h5, hhhh = hhh & h4;
+                cont |= (uint64_t)movemask4(h7 & ~h6) << (4 * k);
+                l2 |= (uint64_t)movemask4(hh & ~h5) << (4 * k);
+                l3 |= (uint64_t)movemask4(hhh & ~h4) << (4 * k);
+                l4 |= (uint64_t)movemask4(hhhh & ~h3) << (4 * k);
+                badl |= (uint64_t)movemask4(hhhh & h3) << (4 * k);
+            }
+            const uint64_t expect = (l2 << 1) | (l3 << 1) | (l3 << 2) | (l4 << 1) | (l4 << 2) | (l4 << 3) | expect_in;
+            bad |= ((cont ^ expect) | badl) & (s | (s << 1) | cin);
+        }
+        qu[w] = bad;                                    // the newline mask is no longer needed
+        cin = (N >> 63) ? 0 : (s >> 63);               // a newline in the last byte resets
+    }
 }
 
-// ---------------------------------------------------------------- kernels
-// Count: one thread per line, fast path only; non-canonical lines queued.
-template <int BT>
-__global__ __launch_bounds__(BT) void k_dec_count(DecParams P) {
-    __shared__ uint64_t sh[BT / 64][PJ_DEC_NCNT];
-    const uint32_t t = threadIdx.x;
-    const uint64_t l = (uint64_t)blockIdx.x * BT + t;
-    LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
-    uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (l < P.lines) {
-        uint64_t s;
-        uint32_t n;
-        const bool slow = line_bounds(P, l, s, n);
-        int code = slow ? PJ_BAIL : fline<false>(P, s, n, r, nullptr);
-        if (code == PJ_BAIL) {
-            r.general = 1;
-            P.gq[atomicAdd(P.gq_count, 1ull)] = l;
-        } else {
-            r.code = (uint32_t)code;
-            if (code) r.name_len = r.cat_len = r.n_urls = r.url_bytes = r.n_tags = r.tag_bytes = 0;
-            rec_counts(r, v);
-        }
-        P.rec[l] = r;
-    }
-    const int w = t >> 6, ln = t & 63;
+// ---------------------------------------------------------------- vector look-back
+// Per block PJ_DEC_NCNT words, one per counter, each holding its flag in the
+// top two bits (LB_AGG: block aggregate, LB_PRE: inclusive prefix) and the
+// value below, so a single load gives a consistent (flag, value) pair and a
+// look-back window costs one round trip.  The counters resolve
+// independently: a word may already hold its inclusive prefix while another
+// word of the same block still holds the aggregate.
+constexpr int VLB_STRIDE = PJ_DEC_NCNT;
+constexpr uint64_t VLB_VAL = (1ull << 62) - 1;
+
+__device__ __forceinline__ void vlb_publish(uint64_t *st, uint64_t b, const uint64_t *agg, int lane) {
+    if (lane < PJ_DEC_NCNT) {
+        uint64_t v = 0;
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) {
-        const uint64_t x = wave_sum(v[k]);
-        if (ln == 0) sh[w][k] = x;
+        for (int k = 0; k < PJ_DEC_NCNT; k++) v = k == lane ? agg[k] : v;
+        lb_store(&st[b * VLB_STRIDE + lane], (b == 0 ? LB_PRE : LB_AGG) | v);
+    }
+}
+
+// one full wave; returns the exclusive prefixes in excl[] (all lanes) and
+// publishes the inclusive ones
+__device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint64_t *agg, uint64_t *excl) {
+    const int l = lane_id();
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++) excl[k] = 0;
+    if (b == 0) return;
+    uint32_t open = (1u << PJ_DEC_NCNT) - 1;            // counters still walking back
+    int64_t j = (int64_t)b - 1;
+#ifdef PJ_DEC_PROF
+    uint32_t n_win = 0, n_spin = 0;
+#endif
+    while (open) {
+#ifdef PJ_DEC_PROF
+        n_win++;
+#endif
+        const int64_t idx = j - l;
+        uint64_t w[PJ_DEC_NCNT];
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) w[k] = idx >= 0 ? lb_load(&st[idx * VLB_STRIDE + k]) : LB_PRE;
+        bool wait = false;
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) {
+            if (!((open >> k) & 1)) continue;
+            const uint64_t isp = __ballot((w[k] >> 62) == 2);
+            const int fp = isp ? __builtin_ctzll(isp) : 64;
+            const uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1);
+            wait |= (__ballot((w[k] >> 62) == 0) & need) != 0;
+        }
+        if (wait) {
+#ifdef PJ_DEC_PROF
+            n_spin++;
+#endif
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) {
+            if (!((open >> k) & 1)) continue;
+            const uint64_t isp = __ballot((w[k] >> 62) == 2);
+            const int fp = isp ? __builtin_ctzll(isp) : 64;
+            excl[k] += wave_sum(l <= fp ? (w[k] & VLB_VAL) : 0);
+            if (fp < 64) open &= ~(1u << k);
+        }
+        j -= 64;
+    }
+    if (l < PJ_DEC_NCNT) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) v = k == l ? excl[k] + agg[k] : v;
+        lb_store(&st[b * VLB_STRIDE + l], LB_PRE | v);
+    }
+#ifdef PJ_DEC_PROF
+    if (l == 0) excl[0] |= ((uint64_t)n_win << 40) | ((uint64_t)n_spin << 50);
+#endif
+}
+
+// ---------------------------------------------------------------- stage 2 kernel
+// One workgroup per BT consecutive lines, one line per thread.  The lines'
+// bytes are loaded once into an LDS tile (coalesced 16-byte loads), the
+// bitmaps are built in LDS, and every line is classified:
+//   * a raw control character or malformed UTF-8 inside one of its strings
+//     makes it invalid whatever else it holds; its error slot is reserved
+//     here and k_dec_errcode later finds which error comes first;
+//   * otherwise the canonical fast path validates and measures it, and
+//     lines it does not recognise go through the general parser.
+// A block scan plus a vector look-back over 8 counters gives the rows / byte
+// offsets, and a second walk over the tile writes the columns.  A block
+// whose bytes exceed the tile reads its lines from global memory with the
+// byte-by-byte general parser.
+template <int BT, int TILE>
+__global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
+    __shared__ uint64_t spec[TILE / 64 + 1];
+    __shared__ uint64_t badm[TILE / 64 + 1];
+    __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint64_t sh_blk, sh_a0, sh_g0, sh_g1, sh_base[PJ_DEC_NCNT];
+    const uint32_t t = threadIdx.x;
+    if (t == 0) {
+        const uint64_t b = atomicAdd(&P.tickets[1], 1ull);
+        sh_blk = b;
+        const uint64_t l0 = b * BT, l1 = min(l0 + BT, P.lines);
+        const uint64_t g0 = P.line_start[l0];
+        sh_a0 = g0 & ~15ull;
+        sh_g0 = g0;
+        sh_g1 = min(P.line_start[l1], P.len);
     }
     __syncthreads();
-    if (t < PJ_DEC_NCNT) {
-        uint64_t x = 0;
-        for (int k = 0; k < BT / 64; k++) x += sh[k][t];
-        P.bagg[blockIdx.x * PJ_DEC_NCNT + t] = x;
-    }
-}
-
-// General count: the queued lines through run_line; adds them to their
-// block sums.
-__global__ __launch_bounds__(256) void k_dec_gcount(DecParams P) {
-    const uint64_t cnt = *P.gq_count;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < cnt; i += (uint64_t)gridDim.x * 256) {
-        const uint64_t l = P.gq[i];
-        uint64_t s;
-        uint32_t n;
-        const bool slow = line_bounds(P, l, s, n);
-        LineInfo L;
-        const int code = run_line(P, s, n, slow, false, L, nullptr);
-        LineRec r{0, 0, 0, 0, 0, 0, (uint32_t)code, 1};
-        if (!code) {
-            r.name_len = L.name_len;
-            r.cat_len = L.has_cat ? L.cat_len : 0;
-            r.n_urls = L.n_urls;
-            r.url_bytes = L.url_bytes;
-            r.n_tags = L.n_tags;
-            r.tag_bytes = L.tag_bytes;
-        }
-        P.rec[l] = r;
-        uint64_t v[PJ_DEC_NCNT];
-        rec_counts(r, v);
-        unsigned long long *ba = reinterpret_cast<unsigned long long *>(P.bagg + (l / P.line_block) * PJ_DEC_NCNT);
-        for (int k = 0; k < PJ_DEC_NCNT; k++)
-            if (v[k]) atomicAdd(&ba[k], (unsigned long long)v[k]);
-    }
-}
-
-// Exclusive scan of the per-block sums (one workgroup); totals at the end.
-__global__ __launch_bounds__(1024) void k_dec_bscan(DecParams P, uint64_t nblocks) {
-    __shared__ uint64_t sh[16];
-    const uint32_t t = threadIdx.x;
-    const uint64_t per = (nblocks + 1023) / 1024;
-    const uint64_t b0 = min((uint64_t)t * per, nblocks), b1 = min(b0 + per, nblocks);
-    for (int k = 0; k < PJ_DEC_NCNT; k++) {
-        uint64_t sum = 0;
-        for (uint64_t b = b0; b < b1; b++) sum += P.bagg[b * PJ_DEC_NCNT + k];
-        uint64_t tot;
-        uint64_t run = block_excl_scan<1024>(sum, sh, &tot);
-        for (uint64_t b = b0; b < b1; b++) {
-            const uint64_t x = P.bagg[b * PJ_DEC_NCNT + k];
-            P.bagg[b * PJ_DEC_NCNT + k] = run;
-            run += x;
-        }
-        if (t == 0) P.totals[k] = tot;
-    }
-}
-
-// Write: one thread per line; fast lines materialised here, errors listed.
-template <int BT>
-__global__ __launch_bounds__(BT) void k_dec_write(DecParams P) {
-    __shared__ uint64_t sh_scan[BT / 64];
-    const uint32_t t = threadIdx.x;
-    const uint64_t l = (uint64_t)blockIdx.x * BT + t;
+    const uint64_t b = sh_blk;
+#ifdef PJ_DEC_PROF
+#define PROF(k) if (t == 0) P.err_line[P.err_cap - 1 - (b * 6 + (k))] = wall_clock64();
+#else
+#define PROF(k)
+#endif
+    PROF(0);
+    const uint64_t l = b * BT + t;
     const bool live = l < P.lines;
-    LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
-    uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint64_t a0 = sh_a0, g0 = sh_g0, g1 = sh_g1;
+    const uint64_t tb = g1 - a0;
+    const bool fits = tb <= TILE;
+    const uint32_t nw = fits ? (uint32_t)((tb + 63) >> 6) : 0;
+    Src S;
+    uint64_t s0 = 0;
+    uint32_t n = 0;
     if (live) {
-        r = P.rec[l];
-        rec_counts(r, v);
+        const uint64_t gs = P.line_start[l];
+        n = (uint32_t)(P.line_start[l + 1] - 1 - gs);
+        s0 = fits ? gs - a0 : gs;
     }
-    uint64_t pos[PJ_DEC_NCNT];
+    if (fits) {
+        // 16-byte chunks, 4 in flight per thread; the tile is padded with
+        // zeros to whole 64-byte words and the previous line's bytes in the
+        // first chunk are cleared (no line reads them, and zeros keep them
+        // out of the string state)
+        const uint32_t nch = (uint32_t)((tb + 15) >> 4), nall = nw * 4;
+        for (uint32_t c0 = t; c0 < nall; c0 += 4 * BT) {
+            uint4 v[4];
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) {
-        uint64_t agg;
-        pos[k] = block_excl_scan<BT>(v[k], sh_scan, &agg) + P.bagg[blockIdx.x * PJ_DEC_NCNT + k];
+            for (int u = 0; u < 4; u++) {
+                const uint32_t c = c0 + u * BT;
+                const uint64_t g = a0 + 16ull * c;
+                v[u] = make_uint4(0, 0, 0, 0);
+                if (c < nch) {
+                    if (g + 16 <= P.len) v[u] = *reinterpret_cast<const uint4 *>(P.in + g);
+                    else {
+                        uint32_t w[4] = {0, 0, 0, 0};
+                        for (uint32_t j = 0; j < 16 && g + j < P.len; j++) w[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
+                        v[u] = make_uint4(w[0], w[1], w[2], w[3]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t c = c0 + u * BT;
+                if (c >= nall) break;
+                if (c == 0 && a0 < g0) {
+                    const uint32_t lead = (uint32_t)(g0 - a0);
+                    uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int clr = (int)lead - 4 * k;      // bytes of dword k to clear
+                        if (clr >= 4) w[k] = 0;
+                        else if (clr > 0) w[k] &= ~0u << (8 * clr);
+                    }
+                    v[u] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+                reinterpret_cast<uint4 *>(tile)[c] = v[u];
+            }
+        }
+        __syncthreads();
+#ifdef PJ_DEC_STOP
+        if (PJ_DEC_STOP <= 1) { if (t == 0 && tile[t * 7] == 77) P.dummy[0] = 1; return; }
+#endif
+        PROF(1);
+        tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+        __syncthreads();
+        PROF(2);
+        S = Src{tile, tb, spec};
+#ifdef PJ_DEC_STOP
+        if (PJ_DEC_STOP <= 2) { if (t == 0 && badm[0] == 77) P.dummy[0] = 1; return; }
+#endif
+    } else {
+        S = Src{P.in, P.len, nullptr};
     }
-    if (blockIdx.x == 0 && t == 0) {
+    // a bad byte anywhere in the line, its newline included
+    bool bad = false;
+    if (live && fits) {
+        const uint64_t e = s0 + n;
+        for (uint64_t k = s0 >> 6; k <= (e >> 6) && k < nw; k++) {
+            uint64_t m = badm[k];
+            if (k == (s0 >> 6)) m &= ~0ull << (s0 & 63);
+            if (k == (e >> 6)) m &= (e & 63) == 63 ? ~0ull : ((2ull << (e & 63)) - 1);
+            bad |= m != 0;
+        }
+    }
+    // ---- pass 0: validate and measure
+    LineInfo L;
+    LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+    int code = 0;
+    bool general = live && !fits;
+    if (live && fits) {
+        if (bad) code = PJ_REC_STRING;              // provisional: k_dec_errcode settles it
+        else {
+            code = fline<false>(P, S, s0, n, r, nullptr);
+            if (code == PJ_BAIL) general = true;
+        }
+    }
+    if (general) {
+        code = run_line(P, S, s0, n, !fits, false, L, nullptr);
+        if (!code) {
+            r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
+            r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
+        }
+        atomicAdd(P.gq_count, 1ull);                // diagnostics: lines off the fast path
+    }
+    r.code = live ? (uint32_t)code : 0;
+#ifdef PJ_DEC_STOP
+    if (PJ_DEC_STOP <= 3) { if (r.name_len == 12345 && code == 7) P.dummy[0] = 1; return; }
+#endif
+    uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (live) rec_counts(r, v);
+    PROF(3);
+    uint64_t pos[PJ_DEC_NCNT], agg[PJ_DEC_NCNT];
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
+    if (t < 64) {
+        vlb_publish(P.state_parse, b, agg, (int)t);
+        uint64_t excl[PJ_DEC_NCNT];
+        vlb_resolve(P.state_parse, b, agg, excl);
+#ifdef PJ_DEC_PROF
+        if (t == 0) P.err_line[P.err_cap - 1 - (gridDim.x * 6 + b)] = excl[0] >> 40;
+        excl[0] &= (1ull << 40) - 1;
+#endif
+        if (t < PJ_DEC_NCNT) {
+            uint64_t x = 0, y = 0;
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) {
+                x = k == (int)t ? excl[k] : x;
+                y = k == (int)t ? excl[k] + agg[k] : y;
+            }
+            sh_base[t] = x;
+            if (b == gridDim.x - 1) P.totals[t] = y;
+        }
+    }
+    __syncthreads();
+    PROF(4);
+    if (b == 0 && t == 0) {
         const pj_pet_columns &o = P.o;
         o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
         o.url_off[0] = 0; o.tag_name_off[0] = 0;
     }
     if (!live) return;
-    if (r.code) {
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += sh_base[k];
+    if (code) {
         const uint64_t e = pos[C_ERRS];
         if (e < P.err_cap) {
             P.err_line[e] = l;
-            P.err_code[e] = (uint8_t)r.code;
+            P.err_code[e] = (uint8_t)code;
+            if (bad) P.dq[atomicAdd(P.dq_count, 1ull)] = e;
         }
         return;
     }
-    if (r.general) return;                    // k_dec_gwrite
-    uint64_t s;
-    uint32_t n;
-    line_bounds(P, l, s, n);
-    LineRec dummy;
-    fline<true>(P, s, n, dummy, pos);
+    // ---- pass 1: materialise
+#ifdef PJ_DEC_STOP
+    if (PJ_DEC_STOP <= 4) return;
+#endif
+    if (!general) fline<true>(P, S, s0, n, r, pos);
+    else run_line(P, S, s0, n, !fits, true, L, pos);
+#ifdef PJ_DEC_PROF
+    __syncthreads();
+    PROF(5);
+#endif
 }
 
-// General write: queued valid lines through run_line; their offsets are the
-// block's base plus the counts of the lines before them in the block.
-__global__ __launch_bounds__(256) void k_dec_gwrite(DecParams P) {
-    const uint64_t cnt = *P.gq_count;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < cnt; i += (uint64_t)gridDim.x * 256) {
-        const uint64_t l = P.gq[i];
-        if (P.rec[l].code) continue;
-        const uint64_t blk = l / P.line_block;
-        uint64_t pos[PJ_DEC_NCNT];
-        for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = P.bagg[blk * PJ_DEC_NCNT + k];
-        for (uint64_t m = blk * P.line_block; m < l; m++) {
-            uint64_t v[PJ_DEC_NCNT];
-            rec_counts(P.rec[m], v);
-            for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += v[k];
+// ---------------------------------------------------------------- error codes
+// Lines found invalid from the bitmaps alone: the code of the first error
+// reading left to right comes from the byte-by-byte general parser.  One
+// workgroup per queued line at a time (grid-stride over the queue, whose
+// length every thread reads after the parse kernel has finished); lines up to
+// ERR_STAGE bytes are staged in LDS.
+template <int BT, int ERR_STAGE>
+__global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t buf[ERR_STAGE + 16];
+    const uint64_t cnt = *P.dq_count;
+    for (uint64_t i = blockIdx.x; i < cnt; i += gridDim.x) {
+        const uint64_t e = P.dq[i];
+        const uint64_t l = P.err_line[e];
+        const uint64_t gs = P.line_start[l];
+        const uint32_t n = (uint32_t)(P.line_start[l + 1] - 1 - gs);
+        const bool staged = n <= ERR_STAGE;
+        if (staged)
+            for (uint32_t j = threadIdx.x; j < n; j += BT) buf[j] = P.in[gs + j];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            LineInfo L;
+            const Src S = staged ? Src{buf, n, nullptr} : Src{P.in, P.len, nullptr};
+            const int code = run_line(P, S, staged ? 0 : gs, n, true, false, L, nullptr);
+            P.err_code[e] = (uint8_t)code;
         }
-        uint64_t s;
-        uint32_t n;
-        const bool slow = line_bounds(P, l, s, n);
-        LineInfo L;
-        run_line(P, s, n, slow, false, L, nullptr);
-        run_line(P, s, n, slow, true, L, pos);
+        __syncthreads();
     }
 }
 
 }  // namespace pj
 
-constexpr int DEC_IDX_BT = 256, DEC_LINE_BT = 256, DEC_GEN_GRID = 512;
+#ifndef PJ_DEC_LINE_BT
+#define PJ_DEC_LINE_BT 128
+#endif
+#ifndef PJ_DEC_TILE_KB
+#define PJ_DEC_TILE_KB 40
+#endif
+constexpr int DEC_IDX_BT = 256, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
 
 int pj_dec_index_block() { return DEC_IDX_BT; }
 int pj_dec_parse_block() { return DEC_LINE_BT; }
 
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     uint64_t g = (P.nblk64 + DEC_IDX_BT - 1) / DEC_IDX_BT;
-    hipLaunchKernelGGL(pj::k_dec_index<DEC_IDX_BT>, dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);
+    hipLaunchKernelGGL(pj::k_dec_lines<DEC_IDX_BT>, dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);
+    return hipGetLastError();
+}
+
+hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
+    hipLaunchKernelGGL((pj::k_dec_errcode<64, 8192>), dim3(1024), dim3(64), 0, st, P);
     return hipGetLastError();
 }
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.lines + DEC_LINE_BT - 1) / DEC_LINE_BT;
-    hipLaunchKernelGGL(pj::k_dec_count<DEC_LINE_BT>, dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
-    hipLaunchKernelGGL(pj::k_dec_gcount, dim3(DEC_GEN_GRID), dim3(256), 0, st, P);
-    hipLaunchKernelGGL(pj::k_dec_bscan, dim3(1), dim3(1024), 0, st, P, g);
-    hipLaunchKernelGGL(pj::k_dec_write<DEC_LINE_BT>, dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
-    hipLaunchKernelGGL(pj::k_dec_gwrite, dim3(DEC_GEN_GRID), dim3(256), 0, st, P);
+    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
     return hipGetLastError();
 }

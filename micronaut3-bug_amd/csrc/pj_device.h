@@ -175,6 +175,50 @@ __device__ __forceinline__ uint64_t special64(uint64_t x) {
 // output dword; full dwords are stored whole, and the first dword (shared
 // with the previous record) is diverted to a per-thread dummy slot while the
 // record's own bytes of it, and the tail bytes, are stored one by one.
+// Exact-size stores at any byte address (gfx950 runs global memory in
+// unaligned mode; bytes outside [p, p+n) are never written, so neighbouring
+// writers need no coordination).
+__device__ __forceinline__ void stu64(uint8_t *p, uint64_t v) { *reinterpret_cast<uint64_t *>(p) = v; }
+__device__ __forceinline__ void stu32(uint8_t *p, uint32_t v) { *reinterpret_cast<uint32_t *>(p) = v; }
+__device__ __forceinline__ void stu16(uint8_t *p, uint32_t v) { *reinterpret_cast<uint16_t *>(p) = (uint16_t)v; }
+// the low n (0..7) bytes of v
+__device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
+    if (n & 4) { stu32(p, (uint32_t)v); p += 4; v >>= 32; }
+    if (n & 2) { stu16(p, (uint32_t)v); p += 2; v >>= 16; }
+    if (n & 1) *p = (uint8_t)v;
+}
+// n bytes from src (LDS or global, readable up to 8 bytes past the end) to dst
+__device__ __forceinline__ void copy_exact(uint8_t *dst, const uint8_t *src, uint32_t n) {
+    uint32_t k = 0;
+    for (; k + 16 <= n; k += 16) {
+        const uint64_t a = ldu64(src + k), b = ldu64(src + k + 8);
+        stu64(dst + k, a);
+        stu64(dst + k + 8, b);
+    }
+    if (n - k >= 8) { stu64(dst + k, ldu64(src + k)); k += 8; }
+    if (k < n) st_tail(dst + k, ldu64(src + k), n - k);
+}
+// Byte-stream writer for decoded (unescaped) strings: 8-byte stores at any
+// address, exact tail.
+struct StoreSink {
+    uint8_t *p;
+    uint64_t acc;
+    uint32_t nacc;
+    __device__ __forceinline__ void init(uint8_t *dst) { p = dst; acc = 0; nacc = 0; }
+    __device__ __forceinline__ void put(uint32_t w, int k) {     // k (1..4) bytes of w
+        const uint64_t v = (uint64_t)w & ((1ull << (8 * k)) - 1);
+        acc |= v << (8 * nacc);
+        const uint32_t tot = nacc + (uint32_t)k;
+        if (tot >= 8) {
+            stu64(p, acc);
+            p += 8;
+            acc = nacc ? v >> (8 * (8 - nacc)) : 0;
+            nacc = tot - 8;
+        } else nacc = tot;
+    }
+    __device__ __forceinline__ void finish() { st_tail(p, acc, nacc); }
+};
+
 struct WriteSink {
     uint8_t *out;
     uint32_t *dst;

@@ -31,9 +31,7 @@ struct DecParams {
     const uint8_t *in;
     uint64_t len;
     uint64_t nblk64;           // number of 64-byte blocks
-    // index stage outputs
-    uint64_t *special;         // [nblk64] unescaped quotes | backslashes
-    uint8_t *bad;              // [nblk64] 1 = string-content fault in block
+    // line index
     uint64_t *line_start;      // [ls_cap]: line l spans [line_start[l], line_start[l+1]-1)
     uint64_t ls_cap;
     uint64_t *n_lines;         // device scalar
@@ -43,17 +41,16 @@ struct DecParams {
     uint8_t *err_code;
     uint64_t err_cap;
     uint64_t *totals;          // [PJ_DEC_NCNT] column totals (written by last block)
-    uint64_t *state_idx;       // look-back words of the index stage
-    uint64_t *state_parse;     // look-back words of the parse stage, PJ_DEC_NCNT per block
+    uint64_t *state_idx;       // look-back words of the line-index stage, one per block
+    uint64_t *state_parse;     // vector look-back words of the parse stage, per line block
     unsigned long long *tickets; // [2]
     uint64_t lines;            // n_lines as known by the host for the parse stage
     uint32_t *dummy;           // sink for diverted shared dwords (never read)
-    // stage 2 (sized by the line count)
-    LineRec *rec;              // [lines]
-    uint64_t *gq;              // [lines] queue of lines for the general parser
-    unsigned long long *gq_count;
-    uint64_t *bagg;            // [line blocks][PJ_DEC_NCNT] sums, then exclusive prefixes
-    uint64_t line_block;       // lines per block of the line kernels
+    unsigned long long *gq_count;   // lines read by the general parser (diagnostic)
+    // error slots whose code is settled by k_dec_errcode (lines known to be
+    // invalid from the bitmaps alone)
+    uint64_t *dq;
+    unsigned long long *dq_count;
 };
 
 // counters carried through the parse-stage scan
@@ -65,5 +62,6 @@ int pj_encode_block_records(bool nested);
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);
+hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st);
 int pj_dec_index_block();
 int pj_dec_parse_block();

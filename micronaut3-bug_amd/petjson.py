@@ -78,7 +78,8 @@ EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "p
 
 
 def lib_path() -> str:
-    return os.path.join(PKG_DIR, "libpetjson.so")
+    """The in-tree library, or the file named by $PETJSON_LIB."""
+    return os.environ.get("PETJSON_LIB") or os.path.join(PKG_DIR, "libpetjson.so")
 
 
 def load_lib():

@@ -155,3 +155,75 @@ def test_decode_capacity_error(codec):
     with pytest.raises(pj.PetJsonError) as ei:
         gpu_decode(codec, text, caps=caps)
     assert ei.value.status == pj.PJ_ERR_CAPACITY
+
+
+def test_decode_in_string_carry_reset_at_word_edge(codec):
+    """A line ending inside an unterminated string, whose newline falls on
+    every possible byte of a 64-byte word, followed by a line whose only
+    fault (a stray UTF-8 continuation byte in a key) sits inside a string:
+    the in-string state must restart at the newline."""
+    victim = b'{"id":1,"catego\xa9y":{"id":2},"name":"x","photoUrls":[],"status":"sold","x":tru}'
+    lines = []
+    for k in range(0, 130):
+        lines.append(b'{"name":"' + b"a" * k)          # unterminated string
+        lines.append(victim)
+    data = b"\n".join(lines) + b"\n"
+    for shift in (0, 1, 9):
+        assert_same(gpu_decode(codec, data, shift=shift), orc.decode(data))
+
+
+def _insert_unknown(rnd, line: bytes) -> bytes:
+    """Insert properties the Pet does not declare (and, now and then, known
+    keys in a non-canonical shape) before a random top-level key."""
+    vals = [b'"v"', b'""', b'"a\\"b\\u00e9"', b'0', b'-17', b'123456789012345678901234', b'true', b'false',
+            b'null', b'1.5', b'{"a":1}', b'[1,2]', b'"\\q"', b'01', b'tru', b'"open']
+    keys = [b'"x"', b'"idx"', b'"nam"', b'"names"', b'"category2"', b'"statusX"', b'"n\\u0061me"', b'"id"',
+            b'"tags"', b'"\xc3\xa9"']
+    # top-level key starts: after '{' or ',' at depth 1, outside strings
+    starts, depth, instr, esc = [], 0, False, False
+    for i, c in enumerate(line):
+        if instr:
+            if esc: esc = False
+            elif c == 0x5C: esc = True
+            elif c == 0x22: instr = False
+            continue
+        if c == 0x22:
+            if depth == 1 and line[i - 1] in (0x7B, 0x2C): starts.append(i)
+            instr = True
+        elif c in (0x7B, 0x5B): depth += 1
+        elif c in (0x7D, 0x5D): depth -= 1
+    if not starts:
+        return line
+    at = rnd.choice(starts + [len(line) - 1])
+    prop = rnd.choice(keys) + b":" + rnd.choice(vals)
+    if at == len(line) - 1:
+        return line[:at] + (b"," if line[at - 1] != 0x7B else b"") + prop + line[at:]
+    return line[:at] + prop + b"," + line[at:]
+
+
+def test_decode_unknown_properties_match_oracle(codec):
+    rnd = random.Random(77)
+    cols = pj.generate(3, 6000)
+    lines = orc.encode(cols, pj.FORMAT_NDJSON).split(b"\n")[:-1]
+    out = []
+    for ln in lines:
+        for _ in range(rnd.choice([0, 1, 1, 2, 3])):
+            ln = _insert_unknown(rnd, ln)
+        out.append(ln)
+    data = b"\n".join(out) + b"\n"
+    ref = orc.decode(data)
+    assert ref[3].n_pets > 2000 and ref[3].n_errors > 200
+    for shift in (0, 5):
+        assert_same(gpu_decode(codec, data, shift=shift), ref)
+
+
+def test_decode_null_after_value_writes_nothing(codec):
+    """A property set and then nulled later in the line is absent: the
+    writing pass must not copy the earlier value into the next record's
+    slots."""
+    lines = [b'{"name":"a","photoUrls":["u"],"tags":[{"id":1,"name":"t"}],"tags":null}',
+             b'{"name":"b","photoUrls":[],"category":{"id":2,"name":"c"},"category":null}',
+             b'{"name":"c","photoUrls":["x"],"photoUrls":null}',
+             b'{"name":"d","photoUrls":["v"],"tags":[{"id":3,"name":"s"}],"category":{"id":4,"name":"k"}}']
+    data = b"\n".join(lines * 50) + b"\n"
+    assert_same(gpu_decode(codec, data), orc.decode(data))
