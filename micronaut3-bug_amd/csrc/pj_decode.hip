@@ -311,6 +311,12 @@ __device__ __noinline__ bool opener_at(const uint8_t *s, uint32_t p, int d) {
     return kind;
 }
 
+// A value every lane holds alike, moved to scalar registers.
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return (uint64_t)hi << 32 | lo;
+}
+
 // Where a line's bytes live: the LDS tile of its workgroup (with the tile's
 // specials bitmap) or global memory (no bitmap: the byte-by-byte path).
 struct Src {
@@ -803,28 +809,22 @@ __device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
 constexpr int PJ_BAIL = -1;
 
 struct FLine {
-    const uint8_t *s;        // line start
-    const uint64_t *special;
-    uint64_t s0, len;        // absolute line start, input length
-    uint32_t n;
-    // 8 bytes at q (bytes past the end of the input read as 0)
-    __device__ __forceinline__ uint64_t ld8(uint32_t q) const {
-        const uint64_t a = s0 + q;
-        if (a + 8 <= len) return ldu64(s + q);
-        uint64_t v = 0;
-        for (uint32_t j = 0; j < 8 && a + j < len; j++) v |= (uint64_t)s[q + j] << (8 * j);
-        return v;
-    }
+    const uint8_t *s;        // the line's first byte in the LDS tile
+    const uint64_t *special; // the tile's specials bitmap
+    uint32_t s0, n;          // tile offset and length of the line
+    // 8 bytes at q: the tile is zero-padded 64 bytes past its data, so any
+    // q up to n + 32 may be read without a check
+    __device__ __forceinline__ uint64_t ld8(uint32_t q) const { return ldu64(s + q); }
     __device__ __forceinline__ int at(uint32_t q) const { return q < n ? (int)s[q] : -1; }
     __device__ __forceinline__ uint32_t next_special(uint32_t q) const {
-        const uint64_t a = s0 + q, lim = s0 + n;
+        const uint32_t a = s0 + q, lim = s0 + n;
         if (a >= lim) return n;
-        uint64_t wi = a >> 6;
+        uint32_t wi = a >> 6;
         uint64_t m = special[wi] & (~0ull << (a & 63));
         while (!m && (wi + 1) * 64 < lim) m = special[++wi];
         if (!m) return n;
-        const uint64_t at = wi * 64 + (uint64_t)__builtin_ctzll(m);
-        return at < lim ? (uint32_t)(at - s0) : n;
+        const uint32_t at = wi * 64 + (uint32_t)__builtin_ctzll(m);
+        return at < lim ? at - s0 : n;
     }
     // string whose first content byte is at q (opening quote at q-1)
     __device__ __forceinline__ Str str(uint32_t q) const {
@@ -844,14 +844,14 @@ struct FLine {
         r.dlen = d;
         return r;
     }
-    // copy the decoded string (content from q, described by r) to dst+off
-    __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst, uint64_t off, uint32_t *) const {
+    // copy the decoded string (content from q, described by r) to dst
+    __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst) const {
         if (!r.esc) {
-            copy_exact(dst + off, s + q, r.dlen);
+            copy_exact(dst, s + q, r.dlen);
             return;
         }
         StoreSink ws;
-        ws.init(dst + off);
+        ws.init(dst);
         for (uint32_t x = q; x < r.end;) {
             const uint32_t c = s[x];
             if (c == '\\') {
@@ -865,6 +865,18 @@ struct FLine {
         }
         ws.finish();
     }
+};
+
+// One workgroup's slice of every output column: the pointers are already
+// advanced to the block's first row / byte / item, and the b_* fields are the
+// absolute offsets those slices start at (what the offset arrays hold).
+struct BlockCols {
+    int64_t *id, *cat_id, *tag_id;
+    uint8_t *flags, *status, *cat_flags, *tag_flags;
+    uint64_t *name_off, *cat_name_off, *photo_off, *tag_off;     // entry row + 1
+    uint64_t *url_off, *tag_name_off;                            // entry item + 1
+    uint8_t *name, *cat_name, *url, *tag_name;
+    uint64_t b_name, b_cat, b_urls, b_url, b_tags, b_tag;
 };
 
 // bit 7 of each byte set iff that byte is not an ASCII digit
@@ -1050,11 +1062,11 @@ __device__ __noinline__ uint64_t fskip(const FLine &F, uint32_t p) {
 // The properties are tried in schema order, each at most once, as straight
 // code: the lanes of a wave then walk the same instruction stream whatever
 // subset of properties their lines hold.
+// Pass 0 (WRITE false) validates and measures into R; pass 1 writes the
+// record at the line's offsets rel[] inside the block's column slices W.
 template <bool WRITE>
-__device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t s0, uint32_t n, LineRec &R,
-                                     const uint64_t *pos) {
-    const FLine F{S.in + s0, S.special, s0, S.len, n};
-    const pj_pet_columns &o = P.o;
+__device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols *W, const uint32_t *rel) {
+    const uint32_t n = F.n;
     if (n == 0) return PJ_REC_EMPTY;
     if (F.at(0) != '{') return PJ_BAIL;
     uint32_t p = 1;
@@ -1083,8 +1095,7 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
         if (e) return e;
         flags |= PJ_PET_HAS_CATEGORY;
         cat_len = (cat_fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
-        if (WRITE && cat_len && pos[C_CATB] + cat_len <= o.cap_cat_name_bytes)
-            F.copy(nq, nr, o.cat_name_bytes, pos[C_CATB], P.dummy);
+        if (WRITE && cat_len) F.copy(nq, nr, W->cat_name + rel[C_CATB]);
         FL_SEP();
     }
     FL_UNKNOWN();
@@ -1096,8 +1107,7 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
         p = r.end + 1;
         flags |= PJ_PET_HAS_NAME;
         name_len = r.dlen;
-        if (WRITE && r.dlen && pos[C_NAMEB] + r.dlen <= o.cap_name_bytes)
-            F.copy(q, r, o.name_bytes, pos[C_NAMEB], P.dummy);
+        if (WRITE && r.dlen) F.copy(q, r, W->name + rel[C_NAMEB]);
         FL_SEP();
     }
     FL_UNKNOWN();
@@ -1105,7 +1115,7 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
     if (more && k8 == KP_PHOTO && (F.ld8(p + 8) & 0xFFFFFFFFFFull) == pack8("ls\":[", 5)) {
         p += 13;
         flags |= PJ_PET_HAS_PHOTOURLS;
-        uint64_t u = WRITE ? pos[C_URLS] : 0, ub = WRITE ? pos[C_URLB] : 0;
+        uint32_t u = WRITE ? rel[C_URLS] : 0, ub = WRITE ? rel[C_URLB] : 0;
         if (F.at(p) == ']') p++;
         else {
             for (;;) {
@@ -1117,10 +1127,10 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
                 n_urls++;
                 url_bytes += r.dlen;
                 if (WRITE) {
-                    if (r.dlen && ub + r.dlen <= o.cap_url_bytes) F.copy(q, r, o.url_bytes, ub, P.dummy);
+                    if (r.dlen) F.copy(q, r, W->url + ub);
                     ub += r.dlen;
+                    W->url_off[u] = W->b_url + ub;
                     u++;
-                    if (u <= o.cap_urls) o.url_off[u] = ub;
                 }
                 const int c = F.at(p++);
                 if (c == ']') break;
@@ -1134,7 +1144,7 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
     if (more && k8 == KP_TAGS) {
         p += 8;
         flags |= PJ_PET_HAS_TAGS;
-        uint64_t g = WRITE ? pos[C_TAGS] : 0, gb = WRITE ? pos[C_TAGB] : 0;
+        uint32_t g = WRITE ? rel[C_TAGS] : 0, gb = WRITE ? rel[C_TAGB] : 0;
         if (F.at(p) == ']') p++;
         else {
             for (;;) {
@@ -1149,11 +1159,12 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
                 n_tags++;
                 tag_bytes += tl;
                 if (WRITE) {
-                    if (g < o.cap_tags) { o.tag_id[g] = tid; o.tag_flags[g] = (uint8_t)tfl; }
-                    if (tl && gb + tl <= o.cap_tag_name_bytes) F.copy(nq, nr, o.tag_name_bytes, gb, P.dummy);
+                    W->tag_id[g] = tid;
+                    W->tag_flags[g] = (uint8_t)tfl;
+                    if (tl) F.copy(nq, nr, W->tag_name + gb);
                     gb += tl;
+                    W->tag_name_off[g] = W->b_tag + gb;
                     g++;
-                    if (g <= o.cap_tags) o.tag_name_off[g] = gb;
                 }
                 const int c = F.at(p++);
                 if (c == ']') break;
@@ -1186,18 +1197,16 @@ __device__ __forceinline__ int fline(const DecParams &P, const Src &S, uint64_t 
         R.name_len = name_len; R.cat_len = cat_len; R.n_urls = n_urls; R.url_bytes = url_bytes;
         R.n_tags = n_tags; R.tag_bytes = tag_bytes;
     } else {
-        const uint64_t row = pos[C_PETS];
-        if (row < o.cap_pets) {
-            o.id[row] = id;
-            o.flags[row] = (uint8_t)flags;
-            o.status[row] = status;
-            o.cat_id[row] = cat_id;
-            o.cat_flags[row] = (uint8_t)cat_fl;
-            o.name_off[row + 1] = pos[C_NAMEB] + name_len;
-            o.cat_name_off[row + 1] = pos[C_CATB] + cat_len;
-            o.photo_off[row + 1] = pos[C_URLS] + n_urls;
-            o.tag_off[row + 1] = pos[C_TAGS] + n_tags;
-        }
+        const uint32_t row = rel[C_PETS];
+        W->id[row] = id;
+        W->flags[row] = (uint8_t)flags;
+        W->status[row] = status;
+        W->cat_id[row] = cat_id;
+        W->cat_flags[row] = (uint8_t)cat_fl;
+        W->name_off[row] = W->b_name + rel[C_NAMEB] + name_len;
+        W->cat_name_off[row] = W->b_cat + rel[C_CATB] + cat_len;
+        W->photo_off[row] = W->b_urls + rel[C_URLS] + n_urls;
+        W->tag_off[row] = W->b_tags + rel[C_TAGS] + n_tags;
     }
     return 0;
 }
@@ -1499,6 +1508,7 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
                 reinterpret_cast<uint4 *>(tile)[c] = v[u];
             }
         }
+        if (t < 4) reinterpret_cast<uint4 *>(tile)[nall + t] = make_uint4(0, 0, 0, 0);   // 64 zero bytes past the data
         __syncthreads();
 #ifdef PJ_DEC_STOP
         if (PJ_DEC_STOP <= 1) { if (t == 0 && tile[t * 7] == 77) P.dummy[0] = 1; return; }
@@ -1526,6 +1536,7 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         }
     }
     // ---- pass 0: validate and measure
+    const FLine F{tile + s0, spec, (uint32_t)s0, n};
     LineInfo L;
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
@@ -1533,7 +1544,7 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
     if (live && fits) {
         if (bad) code = PJ_REC_STRING;              // provisional: k_dec_errcode settles it
         else {
-            code = fline<false>(P, S, s0, n, r, nullptr);
+            code = fline<false>(F, r, nullptr, nullptr);
             if (code == PJ_BAIL) general = true;
         }
     }
@@ -1576,16 +1587,17 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
     }
     __syncthreads();
     PROF(4);
+    const pj_pet_columns &o = P.o;
     if (b == 0 && t == 0) {
-        const pj_pet_columns &o = P.o;
         o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
         o.url_off[0] = 0; o.tag_name_off[0] = 0;
     }
     if (!live) return;
+    uint64_t base[PJ_DEC_NCNT];
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += sh_base[k];
+    for (int k = 0; k < PJ_DEC_NCNT; k++) base[k] = uniform_u64(sh_base[k]);
     if (code) {
-        const uint64_t e = pos[C_ERRS];
+        const uint64_t e = base[C_ERRS] + pos[C_ERRS];
         if (e < P.err_cap) {
             P.err_line[e] = l;
             P.err_code[e] = (uint8_t)code;
@@ -1593,12 +1605,38 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         }
         return;
     }
-    // ---- pass 1: materialise
+    // ---- pass 1: materialise.  One capacity check per block: a block
+    // whose slice of some column would not fit writes nothing (the call then
+    // reports PJ_ERR_CAPACITY).
+    const bool room = base[C_PETS] + agg[C_PETS] <= o.cap_pets && base[C_NAMEB] + agg[C_NAMEB] <= o.cap_name_bytes &&
+                      base[C_CATB] + agg[C_CATB] <= o.cap_cat_name_bytes && base[C_URLS] + agg[C_URLS] <= o.cap_urls &&
+                      base[C_URLB] + agg[C_URLB] <= o.cap_url_bytes && base[C_TAGS] + agg[C_TAGS] <= o.cap_tags &&
+                      base[C_TAGB] + agg[C_TAGB] <= o.cap_tag_name_bytes;
 #ifdef PJ_DEC_STOP
     if (PJ_DEC_STOP <= 4) return;
 #endif
-    if (!general) fline<true>(P, S, s0, n, r, pos);
-    else run_line(P, S, s0, n, !fits, true, L, pos);
+    if (!room) return;
+    if (!general) {
+        BlockCols W;
+        W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
+        W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
+        W.name_off = o.name_off + base[C_PETS] + 1; W.cat_name_off = o.cat_name_off + base[C_PETS] + 1;
+        W.photo_off = o.photo_off + base[C_PETS] + 1; W.tag_off = o.tag_off + base[C_PETS] + 1;
+        W.url_off = o.url_off + base[C_URLS] + 1; W.tag_name_off = o.tag_name_off + base[C_TAGS] + 1;
+        W.tag_id = o.tag_id + base[C_TAGS]; W.tag_flags = o.tag_flags + base[C_TAGS];
+        W.name = o.name_bytes + base[C_NAMEB]; W.cat_name = o.cat_name_bytes + base[C_CATB];
+        W.url = o.url_bytes + base[C_URLB]; W.tag_name = o.tag_name_bytes + base[C_TAGB];
+        W.b_name = base[C_NAMEB]; W.b_cat = base[C_CATB]; W.b_urls = base[C_URLS]; W.b_url = base[C_URLB];
+        W.b_tags = base[C_TAGS]; W.b_tag = base[C_TAGB];
+        uint32_t rel[PJ_DEC_NCNT];
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
+        fline<true>(F, r, &W, rel);
+    } else {
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += base[k];
+        run_line(P, S, s0, n, !fits, true, L, pos);
+    }
 #ifdef PJ_DEC_PROF
     __syncthreads();
     PROF(5);
