@@ -139,7 +139,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="flat", choices=["flat", "nested"])
+    ap.add_argument("--workload", default="flat", choices=["flat", "nested", "decode"],
+                    help="headline workload; 'decode' runs only the NDJSON decode (for profiling)")
     ap.add_argument("--records", type=int, default=10_000_000)
     ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
@@ -164,6 +165,10 @@ def main():
     import torch
     import petjson as pj
     codec = pj.Codec(0)
+    if a.workload == "decode":
+        print(json.dumps({"ndjson_decode": decode_workload(codec, a.decode_records, a.steps, a.warmup)}), flush=True)
+        codec.close()
+        return
     cfg = 2 if a.workload == "flat" else 3
     cols, head = encode_workload(codec, cfg, a.records, a.steps, a.warmup)
     workloads = {a.workload + "_encode": head}

@@ -52,7 +52,7 @@ struct DevBuf {
     }
 };
 
-constexpr int MAX_EV = 6;
+constexpr int MAX_EV = 10;
 
 inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 

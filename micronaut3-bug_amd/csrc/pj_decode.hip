@@ -84,9 +84,10 @@ __device__ __forceinline__ uint64_t block_excl_scan_idx(uint64_t v, uint64_t *sh
     return idx_combine(before, excl);
 }
 
-// Stage 1, k_dec_lines: one thread per 64-byte block; exact newline mask,
-// block scan + decoupled look-back of newline counts -> line starts.
-template <int BT>
+// Stage 1, k_dec_lines: each thread owns R consecutive 64-byte words;
+// exact newline masks, block scan + decoupled look-back of newline counts ->
+// line starts.
+template <int BT, int R>
 __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_blk, sh_pre;
@@ -94,51 +95,60 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     if (t == 0) sh_blk = atomicAdd(&P.tickets[0], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
-    const uint64_t blk = b * BT + t;
-    const bool live = blk < P.nblk64;
-    const uint64_t st = blk * 64;
-    uint64_t N = 0;
-    if (live) {
-        if (st + 64 <= P.len) {
-            const uint4 *q = reinterpret_cast<const uint4 *>(P.in + st);
-            uint32_t w[16];
+    const uint64_t w0 = (b * BT + t) * R;             // first word of this thread
+    uint64_t N[R];
+    uint32_t cnt = 0;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint4 v = q[k];
-                w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+    for (int r = 0; r < R; r++) {
+        const uint64_t wd = w0 + r, st = wd * 64;
+        uint64_t m = 0;
+        if (wd < P.nblk64) {
+            if (st + 64 <= P.len) {
+                const uint4 *q = reinterpret_cast<const uint4 *>(P.in + st);
+                uint32_t w[16];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint4 v = q[k];
+                    w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+                }
+                uint32_t any = 0;
+#pragma unroll
+                for (int k = 0; k < 16; k++) any |= any_zero(w[k] ^ 0x0A0A0A0Au);
+                if (any) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) m |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
+                }
+            } else {
+                for (uint32_t j = 0; st + j < P.len; j++) m |= (uint64_t)(P.in[st + j] == '\n') << j;
             }
-            uint32_t any = 0;
-#pragma unroll
-            for (int k = 0; k < 16; k++) any |= any_zero(w[k] ^ 0x0A0A0A0Au);
-            if (any) {
-#pragma unroll
-                for (int k = 0; k < 16; k++) N |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
-            }
-        } else {
-            for (uint32_t j = 0; st + j < P.len; j++) N |= (uint64_t)(P.in[st + j] == '\n') << j;
         }
+        N[r] = m;
+        cnt += (uint32_t)__builtin_popcountll(m);
     }
     uint64_t agg;
-    const uint64_t pre = block_excl_scan<BT>((uint64_t)__builtin_popcountll(N), sh_scan, &agg);
+    const uint64_t pre = block_excl_scan<BT>((uint64_t)cnt, sh_scan, &agg);
     if (t == 0) lb_publish(P.state_idx, b, agg);
     if (t < 64) {
         const uint64_t e = lb_resolve(P.state_idx, b, agg);
         if (t == 0) sh_pre = e;
     }
     __syncthreads();
-    if (!live) return;
     uint64_t li = sh_pre + pre;
-    for (uint64_t m = N; m; m &= m - 1) {
-        li++;
-        if (li < P.ls_cap) P.line_start[li] = st + (uint64_t)__builtin_ctzll(m) + 1;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint64_t st = (w0 + r) * 64;
+        for (uint64_t m = N[r]; m; m &= m - 1) {
+            li++;
+            if (li < P.ls_cap) P.line_start[li] = st + (uint64_t)__builtin_ctzll(m) + 1;
+        }
+        if (w0 + r == P.nblk64 - 1) {
+            const bool open = P.in[P.len - 1] != '\n';  // last line without '\n'
+            const uint64_t nl = li + (open ? 1 : 0);
+            if (open && nl < P.ls_cap) P.line_start[nl] = P.len + 1;
+            *P.n_lines = nl;
+        }
     }
-    if (blk == 0) P.line_start[0] = 0;
-    if (blk == P.nblk64 - 1) {
-        const bool open = P.in[P.len - 1] != '\n';      // last line without '\n'
-        const uint64_t nl = li + (open ? 1 : 0);
-        if (open && nl < P.ls_cap) P.line_start[nl] = P.len + 1;
-        *P.n_lines = nl;
-    }
+    if (b == 0 && t == 0) P.line_start[0] = 0;
 }
 // =========================================================== stage 2
 // Property keys, container contexts and parser states.
@@ -1631,7 +1641,11 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
         for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
+#ifdef PJ_DEC_P1PARSE
+        if (fline<false>(F, r, nullptr, nullptr) == 99) P.dummy[0] = rel[0];
+#else
         fline<true>(F, r, &W, rel);
+#endif
     } else {
 #pragma unroll
         for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += base[k];
@@ -1680,19 +1694,19 @@ __global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
 #ifndef PJ_DEC_TILE_KB
 #define PJ_DEC_TILE_KB 40
 #endif
-constexpr int DEC_IDX_BT = 256, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
+constexpr int DEC_IDX_BT = 256, DEC_IDX_R = 4, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
 
-int pj_dec_index_block() { return DEC_IDX_BT; }
+int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
 int pj_dec_parse_block() { return DEC_LINE_BT; }
 
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
-    uint64_t g = (P.nblk64 + DEC_IDX_BT - 1) / DEC_IDX_BT;
-    hipLaunchKernelGGL(pj::k_dec_lines<DEC_IDX_BT>, dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);
+    const uint64_t g = (P.nblk64 + DEC_IDX_BT * DEC_IDX_R - 1) / (DEC_IDX_BT * DEC_IDX_R);
+    hipLaunchKernelGGL((pj::k_dec_lines<DEC_IDX_BT, DEC_IDX_R>), dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);
     return hipGetLastError();
 }
 
 hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
-    hipLaunchKernelGGL((pj::k_dec_errcode<64, 8192>), dim3(1024), dim3(64), 0, st, P);
+    hipLaunchKernelGGL((pj::k_dec_errcode<64, 8192>), dim3(8192), dim3(64), 0, st, P);
     return hipGetLastError();
 }
 

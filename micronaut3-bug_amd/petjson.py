@@ -325,8 +325,8 @@ class Codec:
         self._check(self.L.pj_set_options(self.ctx, C.byref(o)))
 
     def timings(self):
-        buf = (C.c_float * 8)()
-        k = self.L.pj_last_timings(self.ctx, buf, 8)
+        buf = (C.c_float * 16)()
+        k = self.L.pj_last_timings(self.ctx, buf, 16)
         return [buf[i] for i in range(k)]
 
     # ---- encode
