@@ -176,6 +176,47 @@ template <class S> __device__ __forceinline__ void emit_str(S &s, const uint8_t 
 // ------------------------------------------------------------------ record
 constexpr uint32_t NO_ITEMS = 0xFFFFFFFFu;  // list not written (null / omitted)
 
+// Where string bytes are read from: the workgroup's LDS copy of its slice of
+// each byte column, or the columns in global memory.  Byte a (absolute
+// offset) of the name column is at name[a - nb], and so on.
+struct ColSrc {
+    const uint8_t *name, *cat, *url, *tag;
+    uint64_t nb, cb, ub, tb;
+};
+
+// One record's scalar fields, loaded once and kept in registers across the
+// measuring and writing passes.
+struct RecVals {
+    uint32_t fl, cf, st;
+    int64_t id, cat_id;
+    uint64_t na, nb, ca, cb, u0, u1, t0, t1;
+};
+
+template <bool NESTED>
+__device__ __forceinline__ RecVals load_rec(const EncParams &P, uint64_t i) {
+    const pj_pet_columns &c = P.c;
+    RecVals v;
+    v.fl = c.flags ? c.flags[i] : (uint32_t)PJ_PET_DEFAULT_FLAGS;
+    v.st = c.status ? c.status[i] : (uint32_t)PJ_STATUS_NULL;
+    v.id = c.id ? c.id[i] : 0;
+    v.na = c.name_off[i];
+    v.nb = c.name_off[i + 1];
+    v.cf = PJ_SUB_DEFAULT_FLAGS;
+    v.cat_id = 0;
+    v.ca = v.cb = v.u0 = v.u1 = v.t0 = v.t1 = 0;
+    if (NESTED) {
+        if (c.cat_id) {
+            v.cat_id = c.cat_id[i];
+            if (c.cat_flags) v.cf = c.cat_flags[i];
+            v.ca = c.cat_name_off[i];
+            v.cb = c.cat_name_off[i + 1];
+        }
+        if (c.photo_off) { v.u0 = c.photo_off[i]; v.u1 = c.photo_off[i + 1]; }
+        if (c.tag_off) { v.t0 = c.tag_off[i]; v.t1 = c.tag_off[i + 1]; }
+    }
+    return v;
+}
+
 struct RecItems {             // staged layout of one record's lists
     uint32_t usz, tsz;        // bytes of its url / tag items (from the item scans)
     uint32_t ustart, tstart;  // tile offsets where they start (set by emit_pet)
@@ -202,70 +243,68 @@ __device__ __forceinline__ void emit_sub(S &s, const EncParams &P, uint32_t fl, 
 }
 
 // url item: `"url"` + (',' or ']' after the record's last url)
-template <class S> __device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, uint64_t u, bool last) {
+template <class S>
+__device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, const ColSrc &X, uint64_t u, bool last) {
     const pj_pet_columns &c = P.c;
-    uint64_t a = c.url_off[u], b = c.url_off[u + 1];
-    emit_str(s, c.url_bytes + a, b - a, P.hexa);
+    const uint64_t a = c.url_off[u], b = c.url_off[u + 1];
+    emit_str(s, X.url + (a - X.ub), b - a, P.hexa);
     s.put_byte(last ? ']' : ',');
 }
 
 // tag item: `{...}` + (',' or ']')
-template <class S> __device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, uint64_t g, bool last) {
+template <class S>
+__device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, const ColSrc &X, uint64_t g, bool last) {
     const pj_pet_columns &c = P.c;
-    uint32_t tf = c.tag_flags ? c.tag_flags[g] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
-    uint64_t a = c.tag_name_off[g], b = c.tag_name_off[g + 1];
-    emit_sub(s, P, tf, c.tag_id[g], c.tag_name_bytes + a, b - a);
+    const uint32_t tf = c.tag_flags ? c.tag_flags[g] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
+    const uint64_t a = c.tag_name_off[g], b = c.tag_name_off[g + 1];
+    emit_sub(s, P, tf, c.tag_id[g], X.tag + (a - X.tb), b - a);
     s.put_byte(last ? ']' : ',');
 }
 
 // One Pet.  INLINE: lists written here; otherwise their item bytes are
 // skipped (written by item threads) and their tile offsets recorded in ri.
 template <bool NESTED, bool INLINE, class S>
-__device__ __forceinline__ void emit_pet(S &s, const EncParams &P, uint64_t i, RecItems &ri) {
+__device__ __forceinline__ void emit_pet(S &s, const EncParams &P, const ColSrc &X, const RecVals &v, RecItems &ri) {
     const pj_pet_columns &c = P.c;
-    const uint32_t fl = c.flags ? c.flags[i] : (uint32_t)PJ_PET_DEFAULT_FLAGS;
+    const uint32_t fl = v.fl;
     bool first = true;
     s.put_byte('{');
-    if (fl & PJ_PET_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, c.id[i]); }
+    if (fl & PJ_PET_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, v.id); }
     else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
     if (NESTED && (fl & PJ_PET_HAS_CATEGORY) && c.cat_id) {
         key(s, first); lit(s, "\"category\":");
-        uint32_t cf = c.cat_flags ? c.cat_flags[i] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
-        uint64_t a = c.cat_name_off[i], b = c.cat_name_off[i + 1];
-        emit_sub(s, P, cf, c.cat_id[i], c.cat_name_bytes + a, b - a);
+        emit_sub(s, P, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
     } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"category\":null"); }
     key(s, first);
     if (fl & PJ_PET_HAS_NAME) {
         lit(s, "\"name\":");
-        uint64_t a = c.name_off[i], b = c.name_off[i + 1];
-        emit_str(s, c.name_bytes + a, b - a, P.hexa);
+        emit_str(s, X.name + (v.na - X.nb), v.nb - v.na, P.hexa);
     } else lit(s, "\"name\":null");
     if (fl & PJ_PET_HAS_PHOTOURLS) {
         lit(s, ",\"photoUrls\":[");
-        uint64_t u0 = 0, u1 = 0;
-        if (NESTED && c.photo_off) { u0 = c.photo_off[i]; u1 = c.photo_off[i + 1]; }
+        const uint64_t u0 = v.u0, u1 = v.u1;
         if (u1 == u0) s.put_byte(']');
         else if (INLINE) {
-            for (uint64_t u = u0; u < u1; u++) emit_url_item(s, P, u, u + 1 == u1);
+            for (uint64_t u = u0; u < u1; u++) emit_url_item(s, P, X, u, u + 1 == u1);
         } else {
             ri.ustart = s.pos();
             s.skip(ri.usz);
         }
     } else lit(s, ",\"photoUrls\":null");
     if (NESTED && (fl & PJ_PET_HAS_TAGS)) {
-        uint64_t t0 = c.tag_off ? c.tag_off[i] : 0, t1 = c.tag_off ? c.tag_off[i + 1] : 0;
+        const uint64_t t0 = v.t0, t1 = v.t1;
         if (t1 > t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
             lit(s, ",\"tags\":[");
             if (t1 == t0) s.put_byte(']');
             else if (INLINE) {
-                for (uint64_t g = t0; g < t1; g++) emit_tag_item(s, P, g, g + 1 == t1);
+                for (uint64_t g = t0; g < t1; g++) emit_tag_item(s, P, X, g, g + 1 == t1);
             } else {
                 ri.tstart = s.pos();
                 s.skip(ri.tsz);
             }
         }
     } else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"tags\":null");
-    const uint32_t st = c.status ? c.status[i] : (uint32_t)PJ_STATUS_NULL;
+    const uint32_t st = v.st;
     if (st == 0) lit(s, ",\"status\":\"available\"}");
     else if (st == 1) lit(s, ",\"status\":\"pending\"}");
     else if (st == 2) lit(s, ",\"status\":\"sold\"}");
@@ -275,10 +314,11 @@ __device__ __forceinline__ void emit_pet(S &s, const EncParams &P, uint64_t i, R
 
 // Record plus its separator: '[' or ',' before (array), '\n' or ']' after.
 template <bool NESTED, bool INLINE, class S>
-__device__ __forceinline__ void emit_rec(S &s, const EncParams &P, uint64_t i, RecItems &ri) {
+__device__ __forceinline__ void emit_rec(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v,
+                                         RecItems &ri) {
     const bool nd = P.format == PJ_FORMAT_NDJSON;
     if (!nd) s.put_byte(i == 0 ? '[' : ',');
-    emit_pet<NESTED, INLINE>(s, P, i, ri);
+    emit_pet<NESTED, INLINE>(s, P, X, v, ri);
     if (nd) s.put_byte('\n');
     else if (i == P.n - 1) s.put_byte(']');
 }
@@ -304,80 +344,151 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 }
 
 // ------------------------------------------------------------------ kernel
-template <bool NESTED, int BT, int R, int TILE, int UCAP, int GCAP>
+// Per workgroup: R records.  Fast blocks stage the string bytes of their
+// records (names, category names, urls, tag names: one contiguous slice of
+// each byte column) into LDS with 16-byte loads, measure and build the
+// output tile from there, and copy the tile out with aligned 16-byte stores.
+// Blocks whose slices, lists or output do not fit write each record from one
+// thread, reading global memory.
+template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP>
 __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t inb[INCAP];  // staged input slices
     __shared__ uint32_t su[UA + 1], sg[GA + 1];      // item prefix sums (tile-relative)
-    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: item area base - su[first]
+    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: item area base - su[first] (mod 2^32)
+    __shared__ uint8_t uon[RA], gon[RA];              // per record: its url / tag items are written
     __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
     __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
     __shared__ uint64_t sh_scan[BT / 64];
-    __shared__ uint64_t sh_blk, sh_base, sh_rng[4];
+    __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4];
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
     if (t == 0) {
-        uint64_t b = atomicAdd(P.ticket, 1ull);
+        const uint64_t b = atomicAdd(P.ticket, 1ull);
         sh_blk = b;
-        uint64_t r0 = b * R, r1 = min(r0 + R, P.n);
-        sh_rng[0] = NESTED && c.photo_off ? c.photo_off[r0] : 0;
-        sh_rng[1] = NESTED && c.photo_off ? c.photo_off[r1] : 0;
-        sh_rng[2] = NESTED && c.tag_off ? c.tag_off[r0] : 0;
-        sh_rng[3] = NESTED && c.tag_off ? c.tag_off[r1] : 0;
+        const uint64_t r0 = b * R, r1 = min(r0 + R, P.n);
+        const bool pu = NESTED && c.photo_off, pt = NESTED && c.tag_off;
+        const uint64_t u0 = pu ? c.photo_off[r0] : 0, u1 = pu ? c.photo_off[r1] : 0;
+        const uint64_t g0 = pt ? c.tag_off[r0] : 0, g1 = pt ? c.tag_off[r1] : 0;
+        sh_rng[0] = u0; sh_rng[1] = u1; sh_rng[2] = g0; sh_rng[3] = g1;
+        // byte slices: names, category names, urls, tag names
+        sh_lo[0] = c.name_off[r0]; sh_hi[0] = c.name_off[r1];
+        const bool pc = NESTED && c.cat_id && c.cat_name_off;
+        sh_lo[1] = pc ? c.cat_name_off[r0] : 0; sh_hi[1] = pc ? c.cat_name_off[r1] : 0;
+        sh_lo[2] = u1 > u0 ? c.url_off[u0] : 0; sh_hi[2] = u1 > u0 ? c.url_off[u1] : 0;
+        sh_lo[3] = g1 > g0 ? c.tag_name_off[g0] : 0; sh_hi[3] = g1 > g0 ? c.tag_name_off[g1] : 0;
     }
     __syncthreads();
     const uint64_t b = sh_blk;
+#ifdef PJ_ENC_PROF
+#define EPROF(k) if (t == 0 && !P.count_only && P.out) reinterpret_cast<uint64_t *>(P.out + P.cap)[-1 - (int64_t)(b * 6 + (k))] = wall_clock64();
+#else
+#define EPROF(k)
+#endif
+    EPROF(0);
     const uint64_t r0 = b * R;
     const uint64_t U0 = sh_rng[0], G0 = sh_rng[2];
     const uint64_t U = sh_rng[1] - U0, G = sh_rng[3] - G0;
-    const bool staged = !NESTED || (U <= UCAP && G <= GCAP);
     const uint64_t i = r0 + t;
     const bool live = t < (uint32_t)R && i < P.n;
-
-    // ---- phase 1: item lengths and their block scans
-    if (NESTED && staged) {
-        for (uint32_t k = t; k < U; k += BT) {
-            CountSink cs;
-            emit_url_item(cs, P, U0 + k, false);
-            su[k] = (uint32_t)cs.n;
-        }
-        for (uint32_t k = t; k < G; k += BT) {
-            CountSink cs;
-            emit_tag_item(cs, P, G0 + k, false);
-            sg[k] = (uint32_t)cs.n;
-        }
-        __syncthreads();
-        lds_excl_scan<BT>(su, (uint32_t)U, sh_scan);
-        lds_excl_scan<BT>(sg, (uint32_t)G, sh_scan);
+    RecVals rv{};
+    if (live) rv = load_rec<NESTED>(P, i);
+    // staged slices: 16-byte aligned chunk ranges, laid end to end in inb
+    uint64_t lo16[4];
+    uint32_t nch[4], off[5];
+    off[0] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        lo16[k] = sh_lo[k] & ~15ull;
+        const uint64_t hi16 = (sh_hi[k] + 15) & ~15ull;
+        nch[k] = sh_hi[k] > sh_lo[k] ? (uint32_t)min((hi16 - lo16[k]) >> 4, (uint64_t)INCAP) : 0;
+        off[k + 1] = off[k] + 16 * nch[k];
     }
+    const bool fast = off[4] <= INCAP && (!NESTED || (U <= UCAP && G <= GCAP));
+    const ColSrc XG{c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes, 0, 0, 0, 0};
+    const ColSrc XL{inb + off[0], inb + off[1], inb + off[2], inb + off[3], lo16[0], lo16[1], lo16[2], lo16[3]};
+    const uint8_t *srcs[4] = {c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes};
 
-    // ---- phase 2: record lengths, scan, publish the aggregate
     RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
     uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
     uint64_t len = 0;
-    if (live) {
-        CountSink cs;
-        if (NESTED && staged) {
-            if (c.photo_off) { ul0 = (uint32_t)(c.photo_off[i] - U0); ul1 = (uint32_t)(c.photo_off[i + 1] - U0); }
-            if (c.tag_off) { gl0 = (uint32_t)(c.tag_off[i] - G0); gl1 = (uint32_t)(c.tag_off[i + 1] - G0); }
-            ri.usz = su[ul1] - su[ul0];
-            ri.tsz = sg[gl1] - sg[gl0];
-            emit_rec<NESTED, false>(cs, P, i, ri);
-        } else {
-            emit_rec<NESTED, true>(cs, P, i, ri);
+    if (fast) {
+        // ---- phase 0: stage the input slices (4 loads in flight per thread)
+        const uint32_t tot = off[4] >> 4;
+        for (uint32_t j0 = t; j0 < tot; j0 += 4 * BT) {
+            uint4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t j = j0 + u * BT;
+                v[u] = make_uint4(0, 0, 0, 0);
+                if (j < tot) {
+                    const uint32_t byte = 16 * j;
+                    const int k = byte >= off[1] ? (byte >= off[2] ? (byte >= off[3] ? 3 : 2) : 1) : 0;
+                    const uint8_t *g = (k == 0 ? srcs[0] : k == 1 ? srcs[1] : k == 2 ? srcs[2] : srcs[3]) +
+                                       ((k == 0 ? lo16[0] : k == 1 ? lo16[1] : k == 2 ? lo16[2] : lo16[3]) +
+                                        (byte - (k == 0 ? off[0] : k == 1 ? off[1] : k == 2 ? off[2] : off[3])));
+                    v[u] = *reinterpret_cast<const uint4 *>(g);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t j = j0 + u * BT;
+                if (j < tot) reinterpret_cast<uint4 *>(inb)[j] = v[u];
+            }
         }
+        __syncthreads();
+        EPROF(1);
+        // ---- phase 1: item lengths and their block scans
+        if (NESTED) {
+            for (uint32_t k = t; k < U; k += BT) {
+                CountSink cs;
+                emit_url_item(cs, P, XL, U0 + k, false);
+                su[k] = (uint32_t)cs.n;
+            }
+            for (uint32_t k = t; k < G; k += BT) {
+                CountSink cs;
+                emit_tag_item(cs, P, XL, G0 + k, false);
+                sg[k] = (uint32_t)cs.n;
+            }
+            __syncthreads();
+            lds_excl_scan<BT>(su, (uint32_t)U, sh_scan);
+            lds_excl_scan<BT>(sg, (uint32_t)G, sh_scan);
+        }
+        EPROF(2);
+        // ---- phase 2: record lengths
+        if (live) {
+            CountSink cs;
+            if (NESTED) {
+                if (c.photo_off) { ul0 = (uint32_t)(rv.u0 - U0); ul1 = (uint32_t)(rv.u1 - U0); }
+                if (c.tag_off) { gl0 = (uint32_t)(rv.t0 - G0); gl1 = (uint32_t)(rv.t1 - G0); }
+                ri.usz = su[ul1] - su[ul0];
+                ri.tsz = sg[gl1] - sg[gl0];
+            }
+            emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
+            len = cs.n;
+        }
+    } else if (live) {
+        CountSink cs;
+        emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
         len = cs.n;
     }
+    // ---- block scan, publish the aggregate
     uint64_t agg;
     const uint64_t pre = block_excl_scan<BT>(len, sh_scan, &agg);
     if (t == 0) lb_publish(P.state, b, agg);
-    const bool fits = staged && agg + 16 <= TILE;
+    const bool fits = fast && agg + 16 <= TILE;
+    EPROF(3);
 
     if (fits && !P.count_only) {
         // ---- phase 3: build the tile
         if (NESTED && live) {
-            ubase[t] = ri.ustart == NO_ITEMS ? NO_ITEMS : (uint32_t)pre + ri.ustart - su[ul0];
-            gbase[t] = ri.tstart == NO_ITEMS ? NO_ITEMS : (uint32_t)pre + ri.tstart - sg[gl0];
+            // the bases wrap modulo 2^32 (any value is valid), so whether a
+            // record's items are written is kept apart from them
+            uon[t] = ri.ustart != NO_ITEMS;
+            gon[t] = ri.tstart != NO_ITEMS;
+            ubase[t] = (uint32_t)pre + ri.ustart - su[ul0];
+            gbase[t] = (uint32_t)pre + ri.tstart - sg[gl0];
             uend[t] = (uint16_t)ul1;
             gend[t] = (uint16_t)gl1;
             for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
@@ -387,26 +498,27 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
         if (live) {
             LdsSink ls{tile, (uint32_t)pre};
             RecItems r2 = ri;
-            emit_rec<NESTED, false>(ls, P, i, r2);
+            emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
         }
         if (NESTED) {
             for (uint32_t k = t; k < U; k += BT) {
-                uint32_t own = uown[k];
-                if (ubase[own] == NO_ITEMS) continue;
+                const uint32_t own = uown[k];
+                if (!uon[own]) continue;
                 LdsSink ls{tile, ubase[own] + su[k]};
-                emit_url_item(ls, P, U0 + k, k + 1 == uend[own]);
+                emit_url_item(ls, P, XL, U0 + k, k + 1 == uend[own]);
             }
             for (uint32_t k = t; k < G; k += BT) {
-                uint32_t own = gown[k];
-                if (gbase[own] == NO_ITEMS) continue;
+                const uint32_t own = gown[k];
+                if (!gon[own]) continue;
                 LdsSink ls{tile, gbase[own] + sg[k]};
-                emit_tag_item(ls, P, G0 + k, k + 1 == gend[own]);
+                emit_tag_item(ls, P, XL, G0 + k, k + 1 == gend[own]);
             }
         }
     }
+    EPROF(4);
     // ---- phase 4: look-back, then copy out
     if (t < 64) {
-        uint64_t excl = lb_resolve(P.state, b, agg);
+        const uint64_t excl = lb_resolve(P.state, b, agg);
         if (t == 0) {
             sh_base = excl;
             if (b == gridDim.x - 1) *P.total = excl + agg;
@@ -419,8 +531,8 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
         const uint64_t end = min(base + agg, P.cap);
         if (base >= end) return;
         const uint64_t s = base & 15, g0 = base - s;
-        const uint32_t nch = (uint32_t)((s + (end - base) + 15) >> 4);
-        for (uint32_t ch = t; ch < nch; ch += BT) {
+        const uint32_t nc = (uint32_t)((s + (end - base) + 15) >> 4);
+        for (uint32_t ch = t; ch < nc; ch += BT) {
             const uint64_t g = g0 + 16ull * ch;
             if (g >= base && g + 16 <= end) {
                 *reinterpret_cast<uint4 *>(P.out + g) = *reinterpret_cast<const uint4 *>(tile + (g - base));
@@ -429,6 +541,10 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
                     if (g + j >= base && g + j < end) P.out[g + j] = tile[g + j - base];
             }
         }
+#ifdef PJ_ENC_PROF
+        __syncthreads();
+        EPROF(5);
+#endif
         return;
     }
     if (!live) return;
@@ -436,7 +552,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     if (p + len > P.cap) return;
     WriteSink ws;
     ws.init(P.out, p, P.dummy + t);
-    emit_rec<NESTED, true>(ws, P, i, ri);
+    emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
     ws.finish();
 }
 
@@ -459,21 +575,25 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
     return hipGetLastError();
 }
 
+#ifndef PJ_ENC_NEST_R
+#define PJ_ENC_NEST_R 96
+#endif
 // Workgroup shapes: threads, records, LDS tile bytes, item capacities.
-constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256, ENC_FLAT_TILE = 32 * 1024;
-constexpr int ENC_NEST_BT = 256, ENC_NEST_R = 128, ENC_NEST_TILE = 44 * 1024, ENC_NEST_UCAP = 512,
-              ENC_NEST_GCAP = 384;
+constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256, ENC_FLAT_TILE = 28 * 1024, ENC_FLAT_IN = 8 * 1024;
+constexpr int ENC_NEST_BT = 256, ENC_NEST_R = PJ_ENC_NEST_R, ENC_NEST_TILE = 30 * 1024 + 512, ENC_NEST_IN = 14 * 1024,
+              ENC_NEST_UCAP = 320, ENC_NEST_GCAP = 256;
 
 int pj_encode_block_records(bool nested) { return nested ? ENC_NEST_R : ENC_FLAT_R; }
 
 hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st) {
     if (nested) {
         uint64_t g = (P.n + ENC_NEST_R - 1) / ENC_NEST_R;
-        hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_UCAP, ENC_NEST_GCAP>),
+        hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
+                                         ENC_NEST_GCAP>),
                            dim3((unsigned)g), dim3(ENC_NEST_BT), 0, st, P);
     } else {
         uint64_t g = (P.n + ENC_FLAT_R - 1) / ENC_FLAT_R;
-        hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, 1, 1>), dim3((unsigned)g),
+        hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1>), dim3((unsigned)g),
                            dim3(ENC_FLAT_BT), 0, st, P);
     }
     return hipGetLastError();

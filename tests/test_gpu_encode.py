@@ -113,3 +113,46 @@ def test_encode_full_size_matches_oracle(codec, config):
     ref = orc.encode(cols, pj.FORMAT_ARRAY)
     assert gpu.size == len(ref)
     assert hashlib.sha256(gpu.tobytes()).hexdigest() == hashlib.sha256(ref).hexdigest()
+
+
+def _wrap_case(R, lists):
+    """Records where, at the start of every R-record block, a record that owns
+    list items but has that list nulled is followed by one that writes its
+    list, with item lengths chosen so that the second record's item base
+    (tile offset minus the items before it, modulo 2^32) is 0xFFFFFFFF."""
+    from model import Pet, Tag, StatusEnum
+    key = "photoUrls" if lists == "urls" else "tags"
+    flag = pj.PET_HAS_PHOTOURLS if lists == "urls" else pj.PET_HAS_TAGS
+
+    def build(fill):
+        pets = [Pet(name="p", photo_urls=["u"], id=j, status=StatusEnum.SOLD) for j in range(2 * R)]
+        for k in (0, R):
+            if lists == "urls":
+                pets[k] = Pet(name="a", photo_urls=["x" * fill], id=k)
+                pets[k + 1] = Pet(name="b", photo_urls=["u"], id=k + 1)
+            else:
+                pets[k] = Pet(name="a", photo_urls=[], tags=[Tag(name="x" * fill)], id=k)
+                pets[k + 1] = Pet(name="b", photo_urls=[], tags=[Tag(id=1, name="t")], id=k + 1)
+        cols = to_columns(pets)
+        for k in (0, R):
+            cols.arrays["flags"][k] &= ~np.uint8(flag)
+        return cols
+
+    cols = build(1)
+    recs = orc.encode(cols, pj.FORMAT_NDJSON).split(b"\n")
+    pre = len(recs[0]) + 1                          # the block's first record with its separator
+    ustart = 1 + recs[1].index(b'"' + key.encode() + b'":[') + len(key) + 4
+    item_overhead = 3 if lists == "urls" else len(b'{"name":""},')
+    fill = pre + ustart + 1 - item_overhead
+    assert fill > 0
+    return build(fill)
+
+
+@pytest.mark.parametrize("lists", ["urls", "tags"])
+def test_encode_item_base_wrap(codec, lists):
+    """Regression: an item base equal to the no-items sentinel must still be
+    written (whatever the records-per-block of the build)."""
+    for R in (32, 48, 64, 80, 96, 112, 128, 160, 192, 256):
+        cols = _wrap_case(R, lists)
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt), (R, lists, fmt)
