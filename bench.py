@@ -115,23 +115,72 @@ def decode_workload(codec, n, steps, warmup):
     return r
 
 
-def cpu_baseline_encode(cols_full, n_sample, budget_s=10.0):
-    """Oracle (CPU restatement) encode on a bounded sample, one thread."""
+def _timed(fn, budget_s, threads):
+    """Run fn repeatedly on `threads` host threads for about budget_s seconds
+    (the oracle's ctypes calls release the GIL); returns (calls, seconds)."""
+    import threading
+    fn()                            # warm: library load, first-touch allocations
+    counts = [0] * threads
+    t0 = time.perf_counter()
+
+    def work(k):
+        while time.perf_counter() - t0 < budget_s:
+            fn()
+            counts[k] += 1
+
+    ts = [threading.Thread(target=work, args=(k,)) for k in range(threads)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join()
+    return sum(counts), time.perf_counter() - t0
+
+
+def host_cores():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))       # the GPU box's CPU share is 16 cores
+
+
+def cpu_baseline_encode(config, n_sample, budget_s=10.0):
+    """Oracle (C restatement) encode of a bounded sample of the same
+    configuration: one thread, then every host core (one sample per thread)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_py as orc
     import petjson as pj
-    sample = pj.generate(cols_full["_config"], n_sample) if isinstance(cols_full, dict) else None
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        orc.encode(sample, pj.FORMAT_ARRAY)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": n_sample * reps / el, "unit": "records/s", "cores": 1, "kind": "port",
-            "sample": f"{n_sample} records of the same configuration, encoded {reps}x in {el:.1f}s "
-                      f"by oracle/pj_oracle.c (C restatement of the serde/Jackson rules; the reference is "
-                      f"Java and no JVM is available)"}
+    sample = pj.generate(config, n_sample)
+    fn = lambda: orc.encode(sample, pj.FORMAT_ARRAY)
+    r1, e1 = _timed(fn, budget_s / 2, 1)
+    cores = host_cores()
+    rn, en = _timed(fn, budget_s / 2, cores)
+    return {"value": n_sample * rn / en, "unit": "records/s", "cores": cores, "kind": "port",
+            "single_thread_value": n_sample * r1 / e1,
+            "sample": f"{n_sample} records of the same configuration, encoded by oracle/pj_oracle.c (C restatement "
+                      f"of the serde/Jackson rules; the reference is Java and no JVM is available): {r1}x on 1 thread "
+                      f"in {e1:.1f}s, {rn}x over {cores} threads in {en:.1f}s"}
+
+
+def cpu_baseline_decode(n_sample, budget_s=10.0):
+    """Oracle decode of a bounded sample of the decode workload (config 4
+    generator, NDJSON, 0.1% corrupted): one thread, then every host core."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import numpy as np
+    import oracle_py as orc
+    import petjson as pj
+    cols = pj.generate(4, n_sample)
+    text = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), dtype=np.uint8).copy()
+    pj.corrupt_ndjson(text, 0xBAD, 0.001)
+    data = text.tobytes()
+    fn = lambda: orc.decode(data)
+    r1, e1 = _timed(fn, budget_s / 2, 1)
+    cores = host_cores()
+    rn, en = _timed(fn, budget_s / 2, cores)
+    return {"value": n_sample * rn / en, "unit": "records/s", "cores": cores, "kind": "port",
+            "single_thread_value": n_sample * r1 / e1,
+            "sample": f"{n_sample} NDJSON lines ({len(data)} bytes) of the decode workload, decoded by "
+                      f"oracle/pj_oracle.c: {r1}x on 1 thread in {e1:.1f}s, {rn}x over {cores} threads in {en:.1f}s"}
 
 
 def main():
@@ -170,7 +219,8 @@ def main():
     import petjson as pj
     codec = pj.Codec(0)
     if a.workload == "decode":
-        print(json.dumps({"ndjson_decode": decode_workload(codec, a.decode_records, a.steps, a.warmup)}), flush=True)
+        print(json.dumps({"ndjson_decode": decode_workload(codec, a.decode_records, a.steps, a.warmup),
+                          "cpu_baseline_decode": cpu_baseline_decode(20_000, a.cpu_budget)}), flush=True)
         codec.close()
         return
     cfg = 2 if a.workload == "flat" else 3
@@ -185,7 +235,8 @@ def main():
     if not a.no_extra and a.with_decode:
         workloads["ndjson_decode"] = decode_workload(codec, a.decode_records, max(3, a.steps // 2), 1)
         torch.cuda.empty_cache()
-    cpu = cpu_baseline_encode({"_config": cfg}, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
+    cpu = cpu_baseline_encode(cfg, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
+    cpu_dec = cpu_baseline_decode(20_000, a.cpu_budget) if not a.no_extra else None
     alg = head["input_bytes"] + head["output_bytes"]
     achieved = alg / (head["kernel_ms"] * 1e-3) / 1e9
     traffic = None
@@ -215,6 +266,7 @@ def main():
                      "kernel": "k_encode", "kernel_ms": head["kernel_ms"],
                      "alg_bytes_per_launch": alg},
         "cpu_baseline": cpu,
+        "cpu_baseline_decode": cpu_dec,
         "workloads": workloads,
     }
     print(json.dumps(line), flush=True)
