@@ -528,23 +528,59 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     if (P.count_only) return;
     const uint64_t base = sh_base;
     if (fits) {
+        // Global chunk c covers [g0 + 16c, g0 + 16c + 16), which is tile bytes
+        // [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
+        // head of word c, joined with one funnel shift.  Whole chunks leave
+        // with one aligned 16-byte store; the block's first and last chunks
+        // (shared with the neighbouring blocks) with exact 8/4/2/1-byte stores.
         const uint64_t end = min(base + agg, P.cap);
         if (base >= end) return;
-        const uint64_t s = base & 15, g0 = base - s;
+        const uint32_t s = (uint32_t)(base & 15);
+        const uint64_t g0 = base - s;
         const uint32_t nc = (uint32_t)((s + (end - base) + 15) >> 4);
-        for (uint32_t ch = t; ch < nc; ch += BT) {
-            const uint64_t g = g0 + 16ull * ch;
-            if (g >= base && g + 16 <= end) {
-                *reinterpret_cast<uint4 *>(P.out + g) = *reinterpret_cast<const uint4 *>(tile + (g - base));
-            } else {
-                for (int j = 0; j < 16; j++)
-                    if (g + j >= base && g + j < end) P.out[g + j] = tile[g + j - base];
+        const uint4 *W = reinterpret_cast<const uint4 *>(tile);
+        constexpr int U = 4;
+        for (uint32_t c0 = t; c0 < nc; c0 += U * BT) {
+            unsigned __int128 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint32_t c = c0 + u * BT;
+                v[u] = 0;
+                if (c < nc) {
+                    const uint4 hi4 = W[c];
+                    const unsigned __int128 hi = (unsigned __int128)(((uint64_t)hi4.w << 32) | hi4.z) << 64 |
+                                                 (((uint64_t)hi4.y << 32) | hi4.x);
+                    if (s == 0) v[u] = hi;
+                    else {
+                        unsigned __int128 lo = 0;
+                        if (c > 0) {
+                            const uint4 lo4 = W[c - 1];
+                            lo = (unsigned __int128)(((uint64_t)lo4.w << 32) | lo4.z) << 64 |
+                                 (((uint64_t)lo4.y << 32) | lo4.x);
+                        }
+                        v[u] = (lo >> (8 * (16 - s))) | (hi << (8 * s));
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const uint32_t c = c0 + u * BT;
+                if (c >= nc) break;
+                const uint64_t g = g0 + 16ull * c;
+                const uint64_t lo = g > base ? g : base, hi = g + 16 < end ? g + 16 : end;
+                const unsigned __int128 x = v[u];
+                if (lo == g && hi == g + 16) {
+                    *reinterpret_cast<uint4 *>(P.out + g) =
+                        make_uint4((uint32_t)x, (uint32_t)(x >> 32), (uint32_t)(x >> 64), (uint32_t)(x >> 96));
+                } else {
+                    unsigned __int128 y = x >> (8 * (uint32_t)(lo - g));
+                    uint32_t n = (uint32_t)(hi - lo);
+                    uint8_t *q = P.out + lo;
+                    if (n & 8) { *reinterpret_cast<uint64_t *>(q) = (uint64_t)y; q += 8; y >>= 64; }
+                    st_tail(q, (uint64_t)y, n & 7);
+                }
             }
         }
-#ifdef PJ_ENC_PROF
-        __syncthreads();
-        EPROF(5);
-#endif
         return;
     }
     if (!live) return;
