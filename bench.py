@@ -144,6 +144,38 @@ def host_cores():
     return max(1, min(n, 16))       # the GPU box's CPU share is 16 cores
 
 
+def skew_workload(codec, n, steps, warmup, with_decode):
+    """2M records with log-normal names (1% of 8-16 KiB names and
+    200 tags, 30% escape-heavy UTF-8): NDJSON encode, and with with_decode the
+    round trip back to columns, checked bit-exact."""
+    import numpy as np
+    import torch
+    import petjson as pj
+    log(f"[bench] generating config 5, {n} records")
+    cols = pj.generate(5, n)
+    dev = cols.to_device()
+    in_bytes = col_bytes(cols)
+    out_bytes, wall, kms, out = run_encode(codec, dev, pj.FORMAT_NDJSON, steps, warmup)
+    r = {"records": n, "records_per_s": n / wall, "ms_per_step": wall * 1e3, "input_bytes": in_bytes,
+         "output_bytes": out_bytes, "kernel_ms": kms,
+         "kernel_alg_GBps": (in_bytes + out_bytes) / (kms * 1e-3) / 1e9}
+    if with_decode:
+        text = out[:out_bytes]
+        res = None
+        t0 = time.perf_counter()
+        for _ in range(max(1, steps // 2)):
+            dcols, el, ec, res = codec.decode(text)
+        torch.cuda.synchronize()
+        dwall = (time.perf_counter() - t0) / max(1, steps // 2)
+        h = dcols.to_host()
+        same = res.n_errors == 0 and all(np.array_equal(h[k], cols[k]) for k in pj.COLS if cols[k] is not None)
+        r.update({"decode_ms_per_step": dwall * 1e3, "roundtrip_bit_exact": bool(same),
+                  "decode_alg_GBps": (out_bytes + in_bytes) / dwall / 1e9})
+    del dev, out
+    torch.cuda.empty_cache()
+    return r
+
+
 def cpu_baseline_encode(config, n_sample, budget_s=10.0):
     """Oracle (C restatement) encode of a bounded sample of the same
     configuration: one thread, then every host core (one sample per thread)."""
@@ -232,6 +264,9 @@ def main():
         workloads[("nested" if other == 3 else "flat") + "_encode"] = r
     del cols
     torch.cuda.empty_cache()
+    if not a.no_extra:
+        workloads["skew_encode"] = skew_workload(codec, 2_000_000, max(3, a.steps // 2), 1, a.with_decode)
+        torch.cuda.empty_cache()
     if not a.no_extra and a.with_decode:
         workloads["ndjson_decode"] = decode_workload(codec, a.decode_records, max(3, a.steps // 2), 1)
         torch.cuda.empty_cache()
