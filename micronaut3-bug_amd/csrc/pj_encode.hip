@@ -261,12 +261,16 @@ __device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, const Co
     s.put_byte(last ? ']' : ',');
 }
 
-// One Pet.  INLINE: lists written here; otherwise their item bytes are
-// skipped (written by item threads) and their tile offsets recorded in ri.
-template <bool NESTED, bool INLINE, class S>
-__device__ __forceinline__ void emit_pet(S &s, const EncParams &P, const ColSrc &X, const RecVals &v, RecItems &ri) {
+// The pieces of one record, in order: head (separator, '{', id, category,
+// the name key), the name string, the photoUrls opener, the url items, the
+// tags opener, the tag items, tail (status, '}', terminator).  Which pieces
+// are present follows from the flags and the inclusion mode; emit_rec and
+// the cooperative path for large records both assemble records from them.
+template <bool NESTED, class S>
+__device__ __forceinline__ void rec_head(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v) {
     const pj_pet_columns &c = P.c;
     const uint32_t fl = v.fl;
+    if (P.format != PJ_FORMAT_NDJSON) s.put_byte(i == 0 ? '[' : ',');
     bool first = true;
     s.put_byte('{');
     if (fl & PJ_PET_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, v.id); }
@@ -276,51 +280,219 @@ __device__ __forceinline__ void emit_pet(S &s, const EncParams &P, const ColSrc 
         emit_sub(s, P, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
     } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"category\":null"); }
     key(s, first);
-    if (fl & PJ_PET_HAS_NAME) {
-        lit(s, "\"name\":");
-        emit_str(s, X.name + (v.na - X.nb), v.nb - v.na, P.hexa);
-    } else lit(s, "\"name\":null");
-    if (fl & PJ_PET_HAS_PHOTOURLS) {
+    if (fl & PJ_PET_HAS_NAME) lit(s, "\"name\":");
+    else lit(s, "\"name\":null");
+}
+
+template <class S> __device__ __forceinline__ void rec_urls_open(S &s, const RecVals &v) {
+    if (v.fl & PJ_PET_HAS_PHOTOURLS) {
         lit(s, ",\"photoUrls\":[");
-        const uint64_t u0 = v.u0, u1 = v.u1;
-        if (u1 == u0) s.put_byte(']');
-        else if (INLINE) {
-            for (uint64_t u = u0; u < u1; u++) emit_url_item(s, P, X, u, u + 1 == u1);
-        } else {
-            ri.ustart = s.pos();
-            s.skip(ri.usz);
-        }
+        if (v.u1 == v.u0) s.put_byte(']');
     } else lit(s, ",\"photoUrls\":null");
-    if (NESTED && (fl & PJ_PET_HAS_TAGS)) {
-        const uint64_t t0 = v.t0, t1 = v.t1;
-        if (t1 > t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
+}
+
+template <bool NESTED, class S> __device__ __forceinline__ void rec_tags_open(S &s, const EncParams &P, const RecVals &v) {
+    if (NESTED && (v.fl & PJ_PET_HAS_TAGS)) {
+        if (v.t1 > v.t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
             lit(s, ",\"tags\":[");
-            if (t1 == t0) s.put_byte(']');
-            else if (INLINE) {
-                for (uint64_t g = t0; g < t1; g++) emit_tag_item(s, P, X, g, g + 1 == t1);
-            } else {
-                ri.tstart = s.pos();
-                s.skip(ri.tsz);
-            }
+            if (v.t1 == v.t0) s.put_byte(']');
         }
     } else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"tags\":null");
+}
+
+template <class S> __device__ __forceinline__ void rec_tail(S &s, const EncParams &P, uint64_t i, const RecVals &v) {
     const uint32_t st = v.st;
     if (st == 0) lit(s, ",\"status\":\"available\"}");
     else if (st == 1) lit(s, ",\"status\":\"pending\"}");
     else if (st == 2) lit(s, ",\"status\":\"sold\"}");
     else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null}");
     else s.put_byte('}');
+    if (P.format == PJ_FORMAT_NDJSON) s.put_byte('\n');
+    else if (i == P.n - 1) s.put_byte(']');
 }
 
-// Record plus its separator: '[' or ',' before (array), '\n' or ']' after.
+__device__ __forceinline__ bool rec_has_urls(const RecVals &v) { return (v.fl & PJ_PET_HAS_PHOTOURLS) && v.u1 > v.u0; }
+template <bool NESTED> __device__ __forceinline__ bool rec_has_tags(const RecVals &v) {
+    return NESTED && (v.fl & PJ_PET_HAS_TAGS) && v.t1 > v.t0;
+}
+
+// One record plus its separators: '[' or ',' before (array), '\n' or ']'
+// after.  INLINE: lists written here; otherwise their item bytes are
+// skipped (written by item threads) and their tile offsets recorded in ri.
 template <bool NESTED, bool INLINE, class S>
 __device__ __forceinline__ void emit_rec(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v,
                                          RecItems &ri) {
-    const bool nd = P.format == PJ_FORMAT_NDJSON;
-    if (!nd) s.put_byte(i == 0 ? '[' : ',');
-    emit_pet<NESTED, INLINE>(s, P, X, v, ri);
-    if (nd) s.put_byte('\n');
-    else if (i == P.n - 1) s.put_byte(']');
+    rec_head<NESTED>(s, P, X, i, v);
+    if (v.fl & PJ_PET_HAS_NAME) emit_str(s, X.name + (v.na - X.nb), v.nb - v.na, P.hexa);
+    rec_urls_open(s, v);
+    if (rec_has_urls(v)) {
+        if (INLINE) {
+            for (uint64_t u = v.u0; u < v.u1; u++) emit_url_item(s, P, X, u, u + 1 == v.u1);
+        } else {
+            ri.ustart = s.pos();
+            s.skip(ri.usz);
+        }
+    }
+    rec_tags_open<NESTED>(s, P, v);
+    if (rec_has_tags<NESTED>(v)) {
+        if (INLINE) {
+            for (uint64_t g = v.t0; g < v.t1; g++) emit_tag_item(s, P, X, g, g + 1 == v.t1);
+        } else {
+            ri.tstart = s.pos();
+            s.skip(ri.tsz);
+        }
+    }
+    rec_tail(s, P, i, v);
+}
+
+// ---------------------------------------------------- large records, cooperatively
+// Exact bytes at any global address: 8-byte stores, exact tail.
+struct XSink {
+    uint8_t *p;
+    uint64_t acc;
+    uint32_t nacc;
+    __device__ __forceinline__ void put4(uint32_t w, int k) {
+        const uint64_t v = (uint64_t)w & ((1ull << (8 * k)) - 1);
+        acc |= v << (8 * nacc);
+        const uint32_t tot = nacc + (uint32_t)k;
+        if (tot >= 8) {
+            stu64(p, acc);
+            p += 8;
+            acc = nacc ? v >> (8 * (8 - nacc)) : 0;
+            nacc = tot - 8;
+        } else nacc = tot;
+    }
+    __device__ __forceinline__ void put8(uint64_t x, int k) {
+        if (k > 4) { put4((uint32_t)x, 4); put4((uint32_t)(x >> 32), k - 4); }
+        else if (k > 0) put4((uint32_t)x, k);
+    }
+    __device__ __forceinline__ void put(uint32_t w, int k) { put8(w, k); }
+    __device__ __forceinline__ void put_byte(uint32_t b) { put4(b & 0xFF, 1); }
+    __device__ __forceinline__ void skip(uint32_t) {}
+    __device__ __forceinline__ uint32_t pos() const { return 0; }
+    __device__ __forceinline__ void finish() { st_tail(p, acc, nacc); }
+};
+
+// Escaped bytes of p[0, len) without quotes, 8 bytes per step.
+template <class S> __device__ __forceinline__ void esc_run(S &s, const uint8_t *p, uint64_t len, uint32_t hexa) {
+    uint64_t k = 0;
+    for (; k + 8 <= len; k += 8) {
+        const uint64_t x = ldu64(p + k);
+        if (!special64(x)) s.put8(x, 8);
+        else esc_bytes(s, x, 8, hexa);
+    }
+    if (k < len) {
+        const int m = (int)(len - k);
+        const uint64_t x = ld_tail(p + k, m), mk = (1ull << (8 * m)) - 1;
+        if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
+        else esc_bytes(s, x, m, hexa);
+    }
+}
+
+// A JSON string (quotes included) of len bytes, measured (out == nullptr) or
+// written at out by the whole workgroup: each thread escapes one slice and a
+// block scan places the slices.  Returns its length (every thread).
+template <int BT>
+__device__ __forceinline__ uint64_t coop_str(const EncParams &P, uint8_t *out, const uint8_t *p, uint64_t len, uint64_t *sh) {
+    const uint32_t t = threadIdx.x;
+    const uint64_t per = ((len + BT - 1) / BT + 7) & ~7ull;
+    const uint64_t a = min((uint64_t)t * per, len), b = min(a + per, len);
+    CountSink cs;
+    esc_run(cs, p + a, b - a, P.hexa);
+    uint64_t tot;
+    const uint64_t off = block_excl_scan<BT>(cs.n, sh, &tot);
+    if (out) {
+        if (t == 0) { out[0] = '"'; out[1 + tot] = '"'; }
+        XSink xs{out + 1 + off, 0, 0};
+        esc_run(xs, p + a, b - a, P.hexa);
+        xs.finish();
+    }
+    return tot + 2;
+}
+
+// The url (URLS) or tag items [g0, g1) of one record, measured or written at
+// out by the whole workgroup, BT items per round.  Returns their length.
+template <int BT, bool URLS>
+__device__ __forceinline__ uint64_t coop_items(const EncParams &P, uint8_t *out, uint64_t g0, uint64_t g1, uint64_t *sh) {
+    const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
+    uint64_t run = 0;
+    for (uint64_t r = g0; r < g1; r += BT) {
+        const uint64_t g = r + threadIdx.x;
+        CountSink cs;
+        if (g < g1) {
+            if (URLS) emit_url_item(cs, P, XG, g, g + 1 == g1);
+            else emit_tag_item(cs, P, XG, g, g + 1 == g1);
+        }
+        uint64_t tot;
+        const uint64_t off = block_excl_scan<BT>(cs.n, sh, &tot);
+        if (out && g < g1) {
+            XSink xs{out + run + off, 0, 0};
+            if (URLS) emit_url_item(xs, P, XG, g, g + 1 == g1);
+            else emit_tag_item(xs, P, XG, g, g + 1 == g1);
+            xs.finish();
+        }
+        run += tot;
+    }
+    return run;
+}
+
+// One record measured (out == nullptr) or written at out by the whole
+// workgroup: the fixed pieces by thread 0, the name and the lists
+// cooperatively.  Every thread passes the same record.  Returns its length.
+template <bool NESTED, int BT>
+__device__ __forceinline__ uint64_t coop_rec(const EncParams &P, uint8_t *out, uint64_t i, const RecVals &v, uint64_t *sh,
+                             uint64_t *sh_len) {
+    const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
+    const uint32_t t = threadIdx.x;
+    uint64_t pos = 0;
+    // head
+    if (t == 0) {
+        CountSink cs;
+        rec_head<NESTED>(cs, P, XG, i, v);
+        *sh_len = cs.n;
+        if (out) { XSink xs{out, 0, 0}; rec_head<NESTED>(xs, P, XG, i, v); xs.finish(); }
+    }
+    __syncthreads();
+    pos += *sh_len;
+    __syncthreads();
+    if (v.fl & PJ_PET_HAS_NAME) pos += coop_str<BT>(P, out ? out + pos : nullptr, P.c.name_bytes + v.na, v.nb - v.na, sh);
+    if (t == 0) {
+        CountSink cs;
+        rec_urls_open(cs, v);
+        *sh_len = cs.n;
+        if (out) { XSink xs{out + pos, 0, 0}; rec_urls_open(xs, v); xs.finish(); }
+    }
+    __syncthreads();
+    pos += *sh_len;
+    __syncthreads();
+    if (rec_has_urls(v)) pos += coop_items<BT, true>(P, out ? out + pos : nullptr, v.u0, v.u1, sh);
+    if (t == 0) {
+        CountSink cs;
+        rec_tags_open<NESTED>(cs, P, v);
+        *sh_len = cs.n;
+        if (out) { XSink xs{out + pos, 0, 0}; rec_tags_open<NESTED>(xs, P, v); xs.finish(); }
+    }
+    __syncthreads();
+    pos += *sh_len;
+    __syncthreads();
+    if (rec_has_tags<NESTED>(v)) pos += coop_items<BT, false>(P, out ? out + pos : nullptr, v.t0, v.t1, sh);
+    if (t == 0) {
+        CountSink cs;
+        rec_tail(cs, P, i, v);
+        *sh_len = cs.n;
+        if (out) { XSink xs{out + pos, 0, 0}; rec_tail(xs, P, i, v); xs.finish(); }
+    }
+    __syncthreads();
+    pos += *sh_len;
+    __syncthreads();
+    return pos;
+}
+
+// A record handled cooperatively when its workgroup is on the fallback
+// path: a long name or a long list.
+constexpr uint64_t BIG_STR = 512, BIG_ITEMS = 16;
+template <bool NESTED> __device__ __forceinline__ bool rec_big(const RecVals &v) {
+    return v.nb - v.na > BIG_STR || (NESTED && (v.u1 - v.u0 > BIG_ITEMS || v.t1 - v.t0 > BIG_ITEMS));
 }
 
 // In-place exclusive scan of n u32 values in LDS (all BT threads call);
@@ -349,7 +521,10 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 // each byte column) into LDS with 16-byte loads, measure and build the
 // output tile from there, and copy the tile out with aligned 16-byte stores.
 // Blocks whose slices, lists or output do not fit write each record from one
-// thread, reading global memory.
+// thread, reading global memory, except records with a long name or a long
+// list, which the whole workgroup measures and writes (slices of the string
+// escaped in parallel and placed by a block scan, items spread over the
+// threads), so one skewed record does not hold its workgroup for long.
 template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP>
 __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
@@ -361,7 +536,9 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
     __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
     __shared__ uint64_t sh_scan[BT / 64];
-    __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4];
+    __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4], sh_len;
+    __shared__ uint32_t sh_nbig;
+    static_assert(3 * R * 4 <= TILE, "the fallback path keeps its large-record list in the tile");
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
     if (t == 0) {
@@ -468,10 +645,27 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
             emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
             len = cs.n;
         }
-    } else if (live) {
-        CountSink cs;
-        emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
-        len = cs.n;
+    } else {
+        // fallback block: records measured from global memory, one thread
+        // each, except large ones, which the whole workgroup measures
+        uint32_t *big = reinterpret_cast<uint32_t *>(tile);     // the tile is unused on this path
+        const bool isbig = live && rec_big<NESTED>(rv);
+        if (live && !isbig) {
+            CountSink cs;
+            emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
+            len = cs.n;
+        }
+        if (t == 0) sh_nbig = 0;
+        __syncthreads();
+        if (isbig) big[atomicAdd(&sh_nbig, 1u)] = t;
+        __syncthreads();
+        const uint32_t nbig = sh_nbig;
+        for (uint32_t k = 0; k < nbig; k++) {
+            const uint32_t r = big[k];
+            const RecVals bv = load_rec<NESTED>(P, r0 + r);
+            const uint64_t L = coop_rec<NESTED, BT>(P, nullptr, r0 + r, bv, sh_scan, &sh_len);
+            if (t == r) len = L;
+        }
     }
     // ---- block scan, publish the aggregate
     uint64_t agg;
@@ -583,13 +777,32 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
         }
         return;
     }
-    if (!live) return;
-    const uint64_t p = base + pre;
-    if (p + len > P.cap) return;
-    WriteSink ws;
-    ws.init(P.out, p, P.dummy + t);
-    emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
-    ws.finish();
+    // fallback: one thread per record writes straight to global memory;
+    // large records are written by the whole workgroup
+    uint32_t *big = reinterpret_cast<uint32_t *>(tile), *bpre = big + R, *blen = bpre + R;
+    if (t == 0) sh_nbig = 0;
+    __syncthreads();
+    const bool isbig = live && rec_big<NESTED>(rv);
+    if (isbig) {
+        const uint32_t k = atomicAdd(&sh_nbig, 1u);
+        big[k] = t;
+        bpre[k] = (uint32_t)pre;
+        blen[k] = (uint32_t)len;
+    }
+    __syncthreads();
+    if (live && !isbig && base + pre + len <= P.cap) {
+        WriteSink ws;
+        ws.init(P.out, base + pre, P.dummy + t);
+        emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
+        ws.finish();
+    }
+    const uint32_t nbig = sh_nbig;
+    for (uint32_t k = 0; k < nbig; k++) {
+        const uint64_t p = base + bpre[k];
+        if (p + blen[k] > P.cap) continue;
+        const RecVals bv = load_rec<NESTED>(P, r0 + big[k]);
+        coop_rec<NESTED, BT>(P, P.out + p, r0 + big[k], bv, sh_scan, &sh_len);
+    }
 }
 
 __global__ void k_fill_u64(uint64_t *p, uint64_t n, uint64_t v) {
