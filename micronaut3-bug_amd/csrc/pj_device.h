@@ -156,8 +156,13 @@ __device__ __forceinline__ uint64_t ldu64(const uint8_t *p) { return *reinterpre
 // The n (1..7) bytes at p, touching only aligned qwords that hold some of
 // them (so never a page past the end of the buffer).
 __device__ __forceinline__ uint64_t ld_tail(const uint8_t *p, int n) {
+    // The aligned address is formed as an integer on purpose: written as
+    // pointer arithmetic (p - (p & 7)) on a generic pointer, the compiler may
+    // fold a constant into the flat load's immediate offset and leave a base
+    // address below the start of the LDS aperture when the bytes sit at LDS
+    // offset 0, which the hardware rejects as an aperture violation.
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)7;
     const int sh = (int)((uintptr_t)p & 7);
-    const uint8_t *a = p - sh;                  // pointer arithmetic keeps the address space
     uint64_t v = *reinterpret_cast<const uint64_t *>(a) >> (8 * sh);
     if (sh + n > 8) v |= *reinterpret_cast<const uint64_t *>(a + 8) << (64 - 8 * sh);
     return v & ((1ull << (8 * n)) - 1);

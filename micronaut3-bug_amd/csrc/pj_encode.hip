@@ -165,7 +165,16 @@ template <class S> __device__ __forceinline__ void emit_str(S &s, const uint8_t 
     }
     if (k < len) {
         int m = (int)(len - k);
-        uint64_t x = ld_tail(p + k, m);
+        // staged slices in LDS are padded to 16-byte chunks (and LDS reads past
+        // the allocation return zeros), so one 8-byte read serves; global
+        // memory takes the aligned reads that never touch another page
+#if defined(__HIP_DEVICE_COMPILE__)
+        uint64_t x = __builtin_amdgcn_is_shared((const void *)(p + k))
+                         ? ldu64(p + k) & ((1ull << (8 * m)) - 1)
+                         : ld_tail(p + k, m);
+#else
+        uint64_t x = ld_tail(p + k, m);               // host pass: never executed
+#endif
         uint64_t mk = (1ull << (8 * m)) - 1;
         if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
         else esc_bytes(s, x, m, hexa);
