@@ -225,10 +225,7 @@ def main():
     ap.add_argument("--records", type=int, default=10_000_000)
     ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
-    ap.add_argument("--with-decode", action="store_true",
-                    help="also run the NDJSON decode after the encode workloads (off by default: that "
-                         "sequence ended once in a GPU memory-aperture fault whose cause is not found; "
-                         "--workload decode runs the decode alone)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode workloads")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (4x), to scale rocprof "
@@ -265,9 +262,9 @@ def main():
     del cols
     torch.cuda.empty_cache()
     if not a.no_extra:
-        workloads["skew_encode"] = skew_workload(codec, 2_000_000, max(3, a.steps // 2), 1, a.with_decode)
+        workloads["skew_encode"] = skew_workload(codec, 2_000_000, max(3, a.steps // 2), 1, not a.no_decode)
         torch.cuda.empty_cache()
-    if not a.no_extra and a.with_decode:
+    if not a.no_extra and not a.no_decode:
         workloads["ndjson_decode"] = decode_workload(codec, a.decode_records, max(3, a.steps // 2), 1)
         torch.cuda.empty_cache()
     cpu = cpu_baseline_encode(cfg, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
