@@ -1378,13 +1378,7 @@ __device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint
     if (b == 0) return;
     uint32_t open = (1u << PJ_DEC_NCNT) - 1;            // counters still walking back
     int64_t j = (int64_t)b - 1;
-#ifdef PJ_DEC_PROF
-    uint32_t n_win = 0, n_spin = 0;
-#endif
     while (open) {
-#ifdef PJ_DEC_PROF
-        n_win++;
-#endif
         const int64_t idx = j - l;
         uint64_t w[PJ_DEC_NCNT];
 #pragma unroll
@@ -1399,9 +1393,6 @@ __device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint
             wait |= (__ballot((w[k] >> 62) == 0) & need) != 0;
         }
         if (wait) {
-#ifdef PJ_DEC_PROF
-            n_spin++;
-#endif
             __builtin_amdgcn_s_sleep(1);
             continue;
         }
@@ -1421,158 +1412,177 @@ __device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint
         for (int k = 0; k < PJ_DEC_NCNT; k++) v = k == l ? excl[k] + agg[k] : v;
         lb_store(&st[b * VLB_STRIDE + l], LB_PRE | v);
     }
-#ifdef PJ_DEC_PROF
-    if (l == 0) excl[0] |= ((uint64_t)n_win << 40) | ((uint64_t)n_spin << 50);
-#endif
 }
 
 // ---------------------------------------------------------------- stage 2 kernel
-// One workgroup per BT consecutive lines, one line per thread.  The lines'
-// bytes are loaded once into an LDS tile (coalesced 16-byte loads), the
-// bitmaps are built in LDS, and every line is classified:
-//   * a raw control character or malformed UTF-8 inside one of its strings
-//     makes it invalid whatever else it holds; its error slot is reserved
-//     here and k_dec_errcode later finds which error comes first;
-//   * otherwise the canonical fast path validates and measures it, and
-//     lines it does not recognise go through the general parser.
-// A block scan plus a vector look-back over 8 counters gives the rows / byte
-// offsets, and a second walk over the tile writes the columns.  A block
-// whose bytes exceed the tile reads its lines from global memory with the
-// byte-by-byte general parser.
+// Tile bytes [a0, a0 + tb) of the input into LDS with 16-byte loads (4 in
+// flight per thread), zero-padded to whole 64-byte words plus 64 bytes; the
+// previous line's bytes in the first chunk (before g0) are cleared: no line
+// reads them, and zeros keep them out of the string state.  All threads.
+template <int BT>
+__device__ __forceinline__ void load_tile(const DecParams &P, uint8_t *tile, uint64_t a0, uint64_t g0, uint64_t tb,
+                                          uint32_t nw) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t nch = (uint32_t)((tb + 15) >> 4), nall = nw * 4;
+    for (uint32_t c0 = t; c0 < nall; c0 += 4 * BT) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t c = c0 + u * BT;
+            const uint64_t g = a0 + 16ull * c;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (c < nch) {
+                if (g + 16 <= P.len) v[u] = *reinterpret_cast<const uint4 *>(P.in + g);
+                else {
+                    uint32_t w[4] = {0, 0, 0, 0};
+                    for (uint32_t j = 0; j < 16 && g + j < P.len; j++) w[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
+                    v[u] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t c = c0 + u * BT;
+            if (c >= nall) break;
+            if (c == 0 && a0 < g0) {
+                const uint32_t lead = (uint32_t)(g0 - a0);
+                uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int clr = (int)lead - 4 * k;      // bytes of dword k to clear
+                    if (clr >= 4) w[k] = 0;
+                    else if (clr > 0) w[k] &= ~0u << (8 * clr);
+                }
+                v[u] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+            reinterpret_cast<uint4 *>(tile)[c] = v[u];
+        }
+    }
+    if (t < 4) reinterpret_cast<uint4 *>(tile)[nall + t] = make_uint4(0, 0, 0, 0);
+}
+
+// A bad byte anywhere in the line at tile offset s0 (its newline included).
+__device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint32_t s0, uint32_t n) {
+    const uint32_t e = s0 + n;
+    bool bad = false;
+    for (uint32_t k = s0 >> 6; k <= (e >> 6) && k < nw; k++) {
+        uint64_t m = badm[k];
+        if (k == (s0 >> 6)) m &= ~0ull << (s0 & 63);
+        if (k == (e >> 6)) m &= (e & 63) == 63 ? ~0ull : ((2ull << (e & 63)) - 1);
+        bad |= m != 0;
+    }
+    return bad;
+}
+
+// One workgroup per BT consecutive lines, one line per thread, in a single
+// pass over the input:
+//   * the block's lines are cut into sub-tiles: maximal runs whose bytes fit
+//     the LDS tile (normally one); each sub-tile is loaded with coalesced
+//     16-byte loads and its bitmaps are built in LDS.  A single line longer
+//     than the tile is read from global memory by the byte-by-byte parser;
+//   * per line: a raw control character or malformed UTF-8 inside one of its
+//     strings makes it invalid whatever else it holds (its error slot is
+//     reserved here and k_dec_errcode later finds which error comes first);
+//     otherwise the canonical fast path validates and measures it, and lines
+//     it does not recognise go through the general parser;
+//   * block scans plus a vector look-back over 8 counters give the rows /
+//     byte offsets, and a second walk over the sub-tiles (reloaded only when
+//     there were several) writes the columns.
 template <int BT, int TILE>
 __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t spec[TILE / 64 + 1];
     __shared__ uint64_t badm[TILE / 64 + 1];
     __shared__ uint64_t sh_scan[BT / 64];
-    __shared__ uint64_t sh_blk, sh_a0, sh_g0, sh_g1, sh_base[PJ_DEC_NCNT];
+    __shared__ uint64_t sh_ls[BT + 1];              // the block's line starts, then its end
+    __shared__ uint16_t sh_sub[BT + 1];             // sub-tile boundaries (block-local line indices)
+    __shared__ uint32_t sh_nsub;
+    __shared__ uint64_t sh_blk, sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
-    if (t == 0) {
-        const uint64_t b = atomicAdd(&P.tickets[1], 1ull);
-        sh_blk = b;
-        const uint64_t l0 = b * BT, l1 = min(l0 + BT, P.lines);
-        const uint64_t g0 = P.line_start[l0];
-        sh_a0 = g0 & ~15ull;
-        sh_g0 = g0;
-        sh_g1 = min(P.line_start[l1], P.len);
-    }
+    if (t == 0) sh_blk = atomicAdd(&P.tickets[1], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
-#ifdef PJ_DEC_PROF
-#define PROF(k) if (t == 0) P.err_line[P.err_cap - 1 - (b * 6 + (k))] = wall_clock64();
-#else
-#define PROF(k)
-#endif
-    PROF(0);
-    const uint64_t l = b * BT + t;
-    const bool live = l < P.lines;
-    const uint64_t a0 = sh_a0, g0 = sh_g0, g1 = sh_g1;
-    const uint64_t tb = g1 - a0;
-    const bool fits = tb <= TILE;
-    const uint32_t nw = fits ? (uint32_t)((tb + 63) >> 6) : 0;
-    Src S;
-    uint64_t s0 = 0;
+    const uint64_t l0 = b * BT;
+    const uint32_t cnt = (uint32_t)min((uint64_t)BT, P.lines - l0);
+    const uint64_t l = l0 + t;
+    const bool live = t < cnt;
+    if (t < cnt) sh_ls[t] = P.line_start[l0 + t];
+    if (t == 0) sh_ls[cnt] = P.line_start[l0 + cnt];  // the end of the last line (cnt may equal BT)
+    __syncthreads();
+    if (t == 0) {
+        uint32_t j = 0;
+        if (min(sh_ls[cnt], P.len) - (sh_ls[0] & ~15ull) <= TILE) sh_sub[j++] = 0;
+        else {
+            for (uint32_t k = 0; k < cnt;) {
+                sh_sub[j++] = (uint16_t)k;
+                const uint64_t a = sh_ls[k] & ~15ull;
+                uint32_t k2 = k + 1;
+                while (k2 < cnt && min(sh_ls[k2 + 1], P.len) - a <= TILE) k2++;
+                k = k2;
+            }
+        }
+        sh_sub[j] = (uint16_t)cnt;
+        sh_nsub = j;
+    }
+    __syncthreads();
+    const uint32_t nsub = sh_nsub;
+    uint64_t gs = 0;
     uint32_t n = 0;
     if (live) {
-        const uint64_t gs = P.line_start[l];
-        n = (uint32_t)(P.line_start[l + 1] - 1 - gs);
-        s0 = fits ? gs - a0 : gs;
+        gs = sh_ls[t];
+        n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
     }
-    if (fits) {
-        // 16-byte chunks, 4 in flight per thread; the tile is padded with
-        // zeros to whole 64-byte words and the previous line's bytes in the
-        // first chunk are cleared (no line reads them, and zeros keep them
-        // out of the string state)
-        const uint32_t nch = (uint32_t)((tb + 15) >> 4), nall = nw * 4;
-        for (uint32_t c0 = t; c0 < nall; c0 += 4 * BT) {
-            uint4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t c = c0 + u * BT;
-                const uint64_t g = a0 + 16ull * c;
-                v[u] = make_uint4(0, 0, 0, 0);
-                if (c < nch) {
-                    if (g + 16 <= P.len) v[u] = *reinterpret_cast<const uint4 *>(P.in + g);
-                    else {
-                        uint32_t w[4] = {0, 0, 0, 0};
-                        for (uint32_t j = 0; j < 16 && g + j < P.len; j++) w[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
-                        v[u] = make_uint4(w[0], w[1], w[2], w[3]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t c = c0 + u * BT;
-                if (c >= nall) break;
-                if (c == 0 && a0 < g0) {
-                    const uint32_t lead = (uint32_t)(g0 - a0);
-                    uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const int clr = (int)lead - 4 * k;      // bytes of dword k to clear
-                        if (clr >= 4) w[k] = 0;
-                        else if (clr > 0) w[k] &= ~0u << (8 * clr);
-                    }
-                    v[u] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
-                reinterpret_cast<uint4 *>(tile)[c] = v[u];
-            }
-        }
-        if (t < 4) reinterpret_cast<uint4 *>(tile)[nall + t] = make_uint4(0, 0, 0, 0);   // 64 zero bytes past the data
-        __syncthreads();
-#ifdef PJ_DEC_STOP
-        if (PJ_DEC_STOP <= 1) { if (t == 0 && tile[t * 7] == 77) P.dummy[0] = 1; return; }
-#endif
-        PROF(1);
-        tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
-        __syncthreads();
-        PROF(2);
-        S = Src{tile, tb, spec};
-#ifdef PJ_DEC_STOP
-        if (PJ_DEC_STOP <= 2) { if (t == 0 && badm[0] == 77) P.dummy[0] = 1; return; }
-#endif
-    } else {
-        S = Src{P.in, P.len, nullptr};
-    }
-    // a bad byte anywhere in the line, its newline included
-    bool bad = false;
-    if (live && fits) {
-        const uint64_t e = s0 + n;
-        for (uint64_t k = s0 >> 6; k <= (e >> 6) && k < nw; k++) {
-            uint64_t m = badm[k];
-            if (k == (s0 >> 6)) m &= ~0ull << (s0 & 63);
-            if (k == (e >> 6)) m &= (e & 63) == 63 ? ~0ull : ((2ull << (e & 63)) - 1);
-            bad |= m != 0;
-        }
-    }
-    // ---- pass 0: validate and measure
-    const FLine F{tile + s0, spec, (uint32_t)s0, n};
+    // ---- pass 0: validate and measure, sub-tile by sub-tile
     LineInfo L;
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
-    bool general = live && !fits;
-    if (live && fits) {
-        if (bad) code = PJ_REC_STRING;              // provisional: k_dec_errcode settles it
-        else {
-            code = fline<false>(F, r, nullptr, nullptr);
-            if (code == PJ_BAIL) general = true;
+    bool general = false, bad = false, over = false;
+    uint32_t s0 = 0;                                // tile offset of this thread's line
+    uint64_t ta0 = 0, ttb = 0;                      // its sub-tile
+    for (uint32_t j = 0; j < nsub; j++) {
+        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
+        const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
+        const bool sub_over = tb > TILE;            // one line, longer than the tile
+        const bool mine = live && t >= ka && t < kb;
+        bool need_gen = false;
+        if (!sub_over) {
+            const uint32_t nw = (uint32_t)((tb + 63) >> 6);
+            load_tile<BT>(P, tile, a0, g0, tb, nw);
+            __syncthreads();
+            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+            __syncthreads();
+            if (mine) {
+                s0 = (uint32_t)(gs - a0);
+                ta0 = a0;
+                ttb = tb;
+                bad = line_bad(badm, nw, s0, n);
+                if (bad) code = PJ_REC_STRING;      // provisional: k_dec_errcode settles it
+                else {
+                    const FLine F{tile + s0, spec, s0, n};
+                    code = fline<false>(F, r, nullptr, nullptr);
+                    need_gen = code == PJ_BAIL;
+                }
+            }
+        } else if (mine) {
+            over = true;
+            need_gen = true;
         }
-    }
-    if (general) {
-        code = run_line(P, S, s0, n, !fits, false, L, nullptr);
-        if (!code) {
-            r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
-            r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
+        if (need_gen) {
+            general = true;
+            const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, tb, spec};
+            code = run_line(P, S, over ? gs : s0, n, over, false, L, nullptr);
+            if (!code) {
+                r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
+                r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
+            }
+            atomicAdd(P.gq_count, 1ull);            // diagnostics: lines off the fast path
         }
-        atomicAdd(P.gq_count, 1ull);                // diagnostics: lines off the fast path
+        __syncthreads();                            // the tile is reused by the next sub-tile
     }
     r.code = live ? (uint32_t)code : 0;
-#ifdef PJ_DEC_STOP
-    if (PJ_DEC_STOP <= 3) { if (r.name_len == 12345 && code == 7) P.dummy[0] = 1; return; }
-#endif
+    // ---- scans and look-back
     uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) rec_counts(r, v);
-    PROF(3);
     uint64_t pos[PJ_DEC_NCNT], agg[PJ_DEC_NCNT];
 #pragma unroll
     for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
@@ -1580,10 +1590,6 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         vlb_publish(P.state_parse, b, agg, (int)t);
         uint64_t excl[PJ_DEC_NCNT];
         vlb_resolve(P.state_parse, b, agg, excl);
-#ifdef PJ_DEC_PROF
-        if (t == 0) P.err_line[P.err_cap - 1 - (gridDim.x * 6 + b)] = excl[0] >> 40;
-        excl[0] &= (1ull << 40) - 1;
-#endif
         if (t < PJ_DEC_NCNT) {
             uint64_t x = 0, y = 0;
 #pragma unroll
@@ -1596,24 +1602,21 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         }
     }
     __syncthreads();
-    PROF(4);
     const pj_pet_columns &o = P.o;
     if (b == 0 && t == 0) {
         o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
         o.url_off[0] = 0; o.tag_name_off[0] = 0;
     }
-    if (!live) return;
     uint64_t base[PJ_DEC_NCNT];
 #pragma unroll
     for (int k = 0; k < PJ_DEC_NCNT; k++) base[k] = uniform_u64(sh_base[k]);
-    if (code) {
+    if (live && code) {
         const uint64_t e = base[C_ERRS] + pos[C_ERRS];
         if (e < P.err_cap) {
             P.err_line[e] = l;
             P.err_code[e] = (uint8_t)code;
             if (bad) P.dq[atomicAdd(P.dq_count, 1ull)] = e;
         }
-        return;
     }
     // ---- pass 1: materialise.  One capacity check per block: a block
     // whose slice of some column would not fit writes nothing (the call then
@@ -1622,39 +1625,48 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
                       base[C_CATB] + agg[C_CATB] <= o.cap_cat_name_bytes && base[C_URLS] + agg[C_URLS] <= o.cap_urls &&
                       base[C_URLB] + agg[C_URLB] <= o.cap_url_bytes && base[C_TAGS] + agg[C_TAGS] <= o.cap_tags &&
                       base[C_TAGB] + agg[C_TAGB] <= o.cap_tag_name_bytes;
-#ifdef PJ_DEC_STOP
-    if (PJ_DEC_STOP <= 4) return;
-#endif
     if (!room) return;
-    if (!general) {
-        BlockCols W;
-        W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
-        W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
-        W.name_off = o.name_off + base[C_PETS] + 1; W.cat_name_off = o.cat_name_off + base[C_PETS] + 1;
-        W.photo_off = o.photo_off + base[C_PETS] + 1; W.tag_off = o.tag_off + base[C_PETS] + 1;
-        W.url_off = o.url_off + base[C_URLS] + 1; W.tag_name_off = o.tag_name_off + base[C_TAGS] + 1;
-        W.tag_id = o.tag_id + base[C_TAGS]; W.tag_flags = o.tag_flags + base[C_TAGS];
-        W.name = o.name_bytes + base[C_NAMEB]; W.cat_name = o.cat_name_bytes + base[C_CATB];
-        W.url = o.url_bytes + base[C_URLB]; W.tag_name = o.tag_name_bytes + base[C_TAGB];
-        W.b_name = base[C_NAMEB]; W.b_cat = base[C_CATB]; W.b_urls = base[C_URLS]; W.b_url = base[C_URLB];
-        W.b_tags = base[C_TAGS]; W.b_tag = base[C_TAGB];
-        uint32_t rel[PJ_DEC_NCNT];
+    BlockCols W;
+    W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
+    W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
+    W.name_off = o.name_off + base[C_PETS] + 1; W.cat_name_off = o.cat_name_off + base[C_PETS] + 1;
+    W.photo_off = o.photo_off + base[C_PETS] + 1; W.tag_off = o.tag_off + base[C_PETS] + 1;
+    W.url_off = o.url_off + base[C_URLS] + 1; W.tag_name_off = o.tag_name_off + base[C_TAGS] + 1;
+    W.tag_id = o.tag_id + base[C_TAGS]; W.tag_flags = o.tag_flags + base[C_TAGS];
+    W.name = o.name_bytes + base[C_NAMEB]; W.cat_name = o.cat_name_bytes + base[C_CATB];
+    W.url = o.url_bytes + base[C_URLB]; W.tag_name = o.tag_name_bytes + base[C_TAGB];
+    W.b_name = base[C_NAMEB]; W.b_cat = base[C_CATB]; W.b_urls = base[C_URLS]; W.b_url = base[C_URLB];
+    W.b_tags = base[C_TAGS]; W.b_tag = base[C_TAGB];
+    const bool writer = live && code == 0;
+    for (uint32_t j = 0; j < nsub; j++) {
+        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
+        const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
+        const bool sub_over = tb > TILE;
+        if (nsub > 1 && !sub_over) {                // a single sub-tile is still in LDS
+            const uint32_t nw = (uint32_t)((tb + 63) >> 6);
+            load_tile<BT>(P, tile, a0, g0, tb, nw);
+            __syncthreads();
+            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+            __syncthreads();
+        }
+        if (writer && t >= ka && t < kb) {
+            if (!general) {
+                uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
-        for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
-#ifdef PJ_DEC_P1PARSE
-        if (fline<false>(F, r, nullptr, nullptr) == 99) P.dummy[0] = rel[0];
-#else
-        fline<true>(F, r, &W, rel);
-#endif
-    } else {
+                for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
+                const FLine F{tile + s0, spec, s0, n};
+                fline<true>(F, r, &W, rel);
+            } else {
+                uint64_t gp[PJ_DEC_NCNT];
 #pragma unroll
-        for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] += base[k];
-        run_line(P, S, s0, n, !fits, true, L, pos);
+                for (int k = 0; k < PJ_DEC_NCNT; k++) gp[k] = pos[k] + base[k];
+                const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, ttb, spec};
+                run_line(P, S, over ? gs : s0, n, over, true, L, gp);
+            }
+        }
+        if (nsub > 1) __syncthreads();
     }
-#ifdef PJ_DEC_PROF
-    __syncthreads();
-    PROF(5);
-#endif
+    (void)ta0;
 }
 
 // ---------------------------------------------------------------- error codes

@@ -229,8 +229,6 @@ def test_decode_null_after_value_writes_nothing(codec):
     assert_same(gpu_decode(codec, data), orc.decode(data))
 
 
-@pytest.mark.skip(reason="the sub-tile decode this covers faulted on the GPU (an illegal memory access on "
-                         "its first run) and was taken out; blocks over the tile use the global-memory parser")
 def test_decode_blocks_over_the_tile(codec):
     """Blocks of lines whose bytes exceed one LDS tile are cut into several
     sub-tiles (and single lines longer than the tile read from global
