@@ -860,20 +860,23 @@ struct FLine {
             copy_exact(dst, s + q, r.dlen);
             return;
         }
-        StoreSink ws;
-        ws.init(dst);
-        for (uint32_t x = q; x < r.end;) {
-            const uint32_t c = s[x];
-            if (c == '\\') {
-                const Esc e = escape_at(s, n, x);
-                ws.put(e.out, e.k);
-                x += e.adv;
-            } else {
-                ws.put(c, 1);
-                x++;
+        // runs between escapes go out whole; the specials bitmap finds the
+        // next backslash (or the closing quote) in a few word reads
+        uint8_t *d = dst;
+        uint32_t x = q;
+        for (;;) {
+            const uint32_t sp = next_special(x);
+            const uint32_t stop = sp < r.end ? sp : r.end;
+            if (stop > x) {
+                copy_exact(d, s + x, stop - x);
+                d += stop - x;
             }
+            if (stop >= r.end) break;
+            const Esc e = escape_at(s, n, stop);
+            st_tail(d, e.out, (uint32_t)e.k);
+            d += e.k;
+            x = stop + e.adv;
         }
-        ws.finish();
     }
 };
 
