@@ -818,10 +818,49 @@ __device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
 // run_line reports them.
 constexpr int PJ_BAIL = -1;
 
-struct FLine {
+// bit k set iff byte k of x equals c
+__device__ __forceinline__ uint32_t eq_mask8(uint64_t x, uint32_t c) {
+    const uint64_t t = x ^ (c * 0x0101010101010101ull), m7 = 0x7F7F7F7F7F7F7F7Full;
+    const uint64_t z = ~(((t & m7) + m7) | t) & 0x8080808080808080ull;
+    return (uint32_t)(((z >> 7) * 0x0102040810204080ull) >> 56);
+}
+// Characters escaped by a backslash in a 64-byte word with backslash mask
+// bs, given whether its first byte is escaped (cin); *cout tells the same of
+// the next word's first byte.  Backslash runs pair up from their start.
+__device__ __forceinline__ uint64_t escaped64(uint64_t bs, uint32_t cin, uint32_t *cout) {
+    constexpr uint64_t EVEN = 0x5555555555555555ull;
+    bs &= ~(uint64_t)cin;
+    const uint64_t follows = (bs << 1) | cin;
+    const uint64_t odd_starts = bs & ~EVEN & ~follows;
+    uint64_t even_seq;
+    *cout = __builtin_add_overflow(odd_starts, bs, &even_seq) ? 1u : 0u;
+    return (EVEN ^ (even_seq << 1)) & follows;
+}
+// Four hex digits (bytes 0..3 of x) as a code unit, or -1.
+__device__ __forceinline__ int hex4(uint32_t x) {
+    uint32_t cu = 0;
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int h = hexval((int)((x >> (8 * j)) & 0xFF));
+        ok &= h >= 0;
+        cu = cu * 16 + (uint32_t)(h & 15);
+    }
+    return ok ? (int)cu : -1;
+}
+
+// One line of an LDS tile as the fast path reads it.  With COOP false one
+// thread owns the line.  With COOP true the 64 lanes of a wave hold the same
+// line and walk its structure in step (every decision is taken on the same
+// bytes, so the wave never diverges); strings that are long or hold escapes
+// are then measured and copied lane-parallel, 4 KiB per step, and only the
+// first lane performs the scalar column stores.
+template <bool COOP>
+struct FLineT {
     const uint8_t *s;        // the line's first byte in the LDS tile
     const uint64_t *special; // the tile's specials bitmap
     uint32_t s0, n;          // tile offset and length of the line
+    __device__ __forceinline__ bool lead() const { return !COOP || lane_id() == 0; }
     // 8 bytes at q: the tile is zero-padded 64 bytes past its data, so any
     // q up to n + 32 may be read without a check
     __device__ __forceinline__ uint64_t ld8(uint32_t q) const { return ldu64(s + q); }
@@ -836,8 +875,58 @@ struct FLine {
         const uint32_t at = wi * 64 + (uint32_t)__builtin_ctzll(m);
         return at < lim ? at - s0 : n;
     }
+    // the first special at or after q within the next two bitmap words, else n
+    __device__ __forceinline__ uint32_t near_special(uint32_t q) const {
+        const uint32_t a = s0 + q, lim = s0 + n;
+        if (a >= lim) return n;
+        const uint32_t wi = a >> 6;
+        uint64_t m = special[wi] & (~0ull << (a & 63));
+        uint32_t at = wi * 64 + (uint32_t)__builtin_ctzll(m);
+        if (!m) {
+            if ((wi + 1) * 64 >= lim) return n;
+            m = special[wi + 1];
+            if (!m) return n;
+            at = (wi + 1) * 64 + (uint32_t)__builtin_ctzll(m);
+        }
+        return at < lim ? at - s0 : n;
+    }
+    // Escape at q (a backslash).  The two-byte forms and a \uXXXX outside the
+    // surrogate range are decoded from one 8-byte read; surrogates and
+    // malformed escapes go to escape_at.
+    __device__ __forceinline__ Esc esc(uint32_t q) const {
+        const uint64_t w = ld8(q);
+        const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
+        Esc r{0, 2, 0, 1};
+        if (c == 'u') {
+            if (q + 6 <= n) {
+                const int cu = hex4((uint32_t)(w >> 16));
+                if (cu >= 0 && (cu < 0xD800 || cu > 0xDFFF)) {
+                    r.adv = 6;
+                    r.out = utf8_pack((uint32_t)cu, &r.k);
+                    return r;
+                }
+            }
+            return escape_at(s, n, q);
+        }
+        if (q + 1 >= n) return escape_at(s, n, q);
+        switch (c) {
+        case '"': case '\\': case '/': r.out = c; break;
+        case 'b': r.out = 8; break;
+        case 'f': r.out = 12; break;
+        case 'n': r.out = 10; break;
+        case 'r': r.out = 13; break;
+        case 't': r.out = 9; break;
+        default: return escape_at(s, n, q);
+        }
+        return r;
+    }
     // string whose first content byte is at q (opening quote at q-1)
     __device__ __forceinline__ Str str(uint32_t q) const {
+        if (COOP) {
+            const uint32_t sp = near_special(q);
+            if (sp < n && s[sp] == '"') return Str{0, sp, sp - q, false};
+            return wave_str<false>(q, nullptr);
+        }
         Str r{0, 0, 0, false};
         uint32_t d = 0;
         for (;;) {
@@ -845,7 +934,7 @@ struct FLine {
             if (sp >= n) { r.err = PJ_REC_STRING; return r; }
             d += sp - q;
             if (s[sp] == '"') { r.end = sp; break; }
-            Esc e = escape_at(s, n, sp);
+            Esc e = esc(sp);
             if (e.err) { r.err = e.err; return r; }
             d += (uint32_t)e.k;
             q = sp + e.adv;
@@ -856,6 +945,13 @@ struct FLine {
     }
     // copy the decoded string (content from q, described by r) to dst
     __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst) const {
+        if (COOP) {
+            if (r.esc) wave_str<true>(q, dst);
+            else
+                for (uint32_t k = 16u * (uint32_t)lane_id(); k < r.dlen; k += 1024)
+                    copy_exact(dst + k, s + q + k, min(16u, r.dlen - k));
+            return;
+        }
         if (!r.esc) {
             copy_exact(dst, s + q, r.dlen);
             return;
@@ -872,13 +968,169 @@ struct FLine {
                 d += stop - x;
             }
             if (stop >= r.end) break;
-            const Esc e = escape_at(s, n, stop);
+            const Esc e = esc(stop);
             st_tail(d, e.out, (uint32_t)e.k);
             d += e.k;
             x = stop + e.adv;
         }
     }
+
+    // Lane-parallel string walk (COOP only; all 64 lanes, uniform q).  Lane l
+    // owns tile word w0 + l of each 64-word step.  Per word: the backslash
+    // mask from its bytes, the escaped characters from a wave scan of the
+    // backslash-run carry, the closing quote as the first unescaped quote of
+    // the wave.  Each lane then decodes the escapes that start in its word;
+    // an escape reaching into the next word (at most 11 bytes) is handed on
+    // so that lane starts after it.  Any malformed escape, or no closing
+    // quote, is PJ_REC_STRING, the code the serial walk gives.  With WRITE
+    // the decoded bytes go to dst at each lane's offset (a wave scan).
+    template <bool WRITE>
+    __device__ __forceinline__ Str wave_str(uint32_t q, uint8_t *dst) const {
+        const int l = lane_id();
+        const uint8_t *tile = s - s0;
+        const uint32_t a = s0 + q, lim = s0 + n;
+        Str res{0, 0, 0, false};
+        uint32_t ecarry = 0;         // the first byte of this step is escaped
+        uint32_t reach_in = a;       // bytes before this are taken by an escape of the previous step
+        uint32_t d = 0;              // decoded bytes so far
+        bool any_esc = false;
+        for (uint32_t w0 = a >> 6;; w0 += 64) {
+            const uint32_t ws = (w0 + (uint32_t)l) * 64;
+            const bool act = ws < lim;
+            uint64_t bs = 0, qt = 0;
+            if (act) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) bs |= (uint64_t)eq_mask8(ldu64(tile + ws + 8 * j), '\\') << (8 * j);
+                qt = special[ws >> 6] & ~bs;
+                uint64_t m = ~0ull;
+                if (ws < a) m <<= (a - ws);
+                if (lim - ws < 64) m &= (1ull << (lim - ws)) - 1;
+                bs &= m;
+                qt &= m;
+            }
+            // backslash-run carry across the wave: compose c -> cout maps
+            uint32_t c0, c1;
+            const uint64_t e0 = escaped64(bs, 0, &c0), e1 = escaped64(bs, 1, &c1);
+            uint32_t F = c0 | (c1 << 1);
+#pragma unroll
+            for (int dd = 1; dd < 64; dd <<= 1) {
+                const uint32_t G = (uint32_t)__shfl_up((int)F, (unsigned)dd, 64);
+                if (l >= dd) F = ((F >> (G & 1)) & 1) | (((F >> ((G >> 1) & 1)) & 1) << 1);
+            }
+            const uint32_t Fp = (uint32_t)__shfl_up((int)F, 1u, 64);
+            const uint32_t cin = l == 0 ? ecarry : ((Fp >> ecarry) & 1);
+            uint64_t starts = bs & ~(cin ? e1 : e0);
+            // closing quote
+            const uint64_t qb = __ballot(qt != 0);
+            const int E = qb ? __builtin_ctzll(qb) : 64;
+            const uint32_t qpos = (uint32_t)__shfl((int)(ws + (uint32_t)__builtin_ctzll(qt | (1ull << 63))), E & 63, 64);
+            const uint32_t hi = qb ? qpos : ws + 64;          // this lane's bytes end here (exclusive)
+            if (l > E) starts = 0;
+            if (l == E) starts &= (1ull << (qpos & 63)) - 1;
+            const bool mine = l <= E && act;
+            // how far the last escape of this word reaches
+            uint32_t reach = 0;
+            if (starts) {
+                const uint32_t p = ws + 63 - (uint32_t)__builtin_clzll(starts);
+                const uint64_t w = ldu64(tile + p);
+                const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
+                uint32_t adv = 2;
+                if (c == 'u') {
+                    const int cu = hex4((uint32_t)(w >> 16));
+                    adv = (cu >= 0xD800 && cu <= 0xDBFF) ? 12 : 6;
+                }
+                reach = p + adv;
+            }
+            const uint32_t rprev = (uint32_t)__shfl_up((int)reach, 1u, 64);
+            uint32_t x = ws < a ? a : ws;
+            const uint32_t from = l == 0 ? reach_in : rprev;
+            if (from > x) x = from;
+            // decode this lane's escapes: count pass, then (WRITE) store pass
+            bool err = false;
+            uint32_t dl = 0;
+            const uint32_t end = min(hi, ws + 64);
+            {
+                uint32_t y = x;
+                uint64_t m = starts;
+                while (m) {
+                    const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
+                    m &= m - 1;
+                    if (p < y) continue;                     // the low half of a pair decoded before
+                    dl += p - y;
+                    const Esc e = wesc(p, err);
+                    dl += (uint32_t)e.k;
+                    y = p + e.adv;
+                }
+                if (y < end) dl += end - y;
+            }
+            if (!mine) { dl = 0; err = false; }
+            const uint32_t off = (uint32_t)(wave_incl_scan(dl) - dl);
+            if (WRITE && mine && !__ballot(err)) {
+                uint8_t *o = dst + d + off;
+                uint32_t y = x;
+                uint64_t m = starts;
+                while (m) {
+                    const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
+                    m &= m - 1;
+                    if (p < y) continue;
+                    if (p > y) { copy_exact(o, tile + y, p - y); o += p - y; }
+                    bool e2 = false;
+                    const Esc e = wesc(p, e2);
+                    st_tail(o, e.out, (uint32_t)e.k);
+                    o += e.k;
+                    y = p + e.adv;
+                }
+                if (y < end) copy_exact(o, tile + y, end - y);
+            }
+            if (__ballot(err)) { res.err = PJ_REC_STRING; return res; }
+            any_esc |= __ballot(starts != 0) != 0;
+            d += (uint32_t)wave_sum(dl);
+            if (qb) {
+                res.end = qpos - s0;
+                res.dlen = d;
+                res.esc = any_esc;
+                return res;
+            }
+            if ((w0 + 64) * 64 >= lim) { res.err = PJ_REC_STRING; return res; }   // no closing quote
+            ecarry = (uint32_t)__shfl((int)((F >> ecarry) & 1), 63, 64);
+            reach_in = (uint32_t)__shfl((int)reach, 63, 64);
+        }
+    }
+    // Escape at tile offset p for the lane-parallel walk: err is set for a
+    // malformed escape, a lone surrogate or a pair that does not close.
+    __device__ __forceinline__ Esc wesc(uint32_t p, bool &err) const {
+        const uint8_t *tile = s - s0;
+        const uint64_t w = ldu64(tile + p);
+        const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
+        Esc r{0, 2, 0, 1};
+        if (c == 'u') {
+            const int cu = hex4((uint32_t)(w >> 16));
+            r.adv = 6;
+            if (cu < 0 || (cu >= 0xDC00 && cu <= 0xDFFF)) { err = true; return r; }
+            if (cu >= 0xD800) {
+                const uint64_t w2 = ldu64(tile + p + 6);
+                const int lo = hex4((uint32_t)(w2 >> 16));
+                if ((w2 & 0xFFFF) != ('\\' | ('u' << 8)) || lo < 0xDC00 || lo > 0xDFFF) { err = true; return r; }
+                r.adv = 12;
+                r.out = utf8_pack(0x10000 + (((uint32_t)cu - 0xD800) << 10) + ((uint32_t)lo - 0xDC00), &r.k);
+                return r;
+            }
+            r.out = utf8_pack((uint32_t)cu, &r.k);
+            return r;
+        }
+        switch (c) {
+        case '"': case '\\': case '/': r.out = c; break;
+        case 'b': r.out = 8; break;
+        case 'f': r.out = 12; break;
+        case 'n': r.out = 10; break;
+        case 'r': r.out = 13; break;
+        case 't': r.out = 9; break;
+        default: err = true;
+        }
+        return r;
+    }
 };
+using FLine = FLineT<false>;
 
 // One workgroup's slice of every output column: the pointers are already
 // advanced to the block's first row / byte / item, and the b_* fields are the
@@ -911,8 +1163,8 @@ __device__ __forceinline__ uint64_t digits8(uint64_t x, int m) {
 
 // Canonical Long at p: -?(0|[1-9][0-9]*) followed by ',' or '}'.  Returns 0,
 // PJ_REC_NUMBER (out of int64 range) or PJ_BAIL; the value only when VAL.
-template <bool VAL>
-__device__ __forceinline__ int fnum(const FLine &F, uint32_t &p, int64_t &v) {
+template <bool VAL, class FL>
+__device__ __forceinline__ int fnum(const FL &F, uint32_t &p, int64_t &v) {
     uint32_t q = p;
     const bool neg = F.at(q) == '-';
     q += neg;
@@ -972,8 +1224,8 @@ constexpr uint64_t KP_CATEGORY = pack8("\"categor", 8), KP_NAME = pack8("\"name\
 
 // Category / Tag body after '{': optional "id":N, then optional "name":"S",
 // then '}'.
-template <bool WRITE>
-__device__ __forceinline__ int fsub(const FLine &F, uint32_t &p, int64_t &id, uint32_t &fl, uint32_t &nq, Str &nr) {
+template <bool WRITE, class FL>
+__device__ __forceinline__ int fsub(const FL &F, uint32_t &p, int64_t &id, uint32_t &fl, uint32_t &nq, Str &nr) {
     fl = 0;
     id = 0;
     uint64_t k8 = F.ld8(p);
@@ -1012,7 +1264,8 @@ __device__ __forceinline__ bool known8(uint64_t k8) {
 // value are skipped, as serde skips properties the bean does not declare.
 // Keys with escapes, known keys in another shape, nested values and
 // anything irregular return PJ_BAIL.  Returns (new p) << 32 | code.
-__device__ __noinline__ uint64_t fskip(const FLine &F, uint32_t p) {
+template <class FL>
+__device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
     constexpr uint64_t BAIL = (uint32_t)PJ_BAIL;
     if (F.at(p) != '"') return BAIL;
     const Str k = F.str(p + 1);
@@ -1077,8 +1330,8 @@ __device__ __noinline__ uint64_t fskip(const FLine &F, uint32_t p) {
 // subset of properties their lines hold.
 // Pass 0 (WRITE false) validates and measures into R; pass 1 writes the
 // record at the line's offsets rel[] inside the block's column slices W.
-template <bool WRITE>
-__device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols *W, const uint32_t *rel) {
+template <bool WRITE, class FL>
+__device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W, const uint32_t *rel) {
     const uint32_t n = F.n;
     if (n == 0) return PJ_REC_EMPTY;
     if (F.at(0) != '{') return PJ_BAIL;
@@ -1142,7 +1395,7 @@ __device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols
                 if (WRITE) {
                     if (r.dlen) F.copy(q, r, W->url + ub);
                     ub += r.dlen;
-                    W->url_off[u] = W->b_url + ub;
+                    if (F.lead()) W->url_off[u] = W->b_url + ub;
                     u++;
                 }
                 const int c = F.at(p++);
@@ -1172,11 +1425,13 @@ __device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols
                 n_tags++;
                 tag_bytes += tl;
                 if (WRITE) {
-                    W->tag_id[g] = tid;
-                    W->tag_flags[g] = (uint8_t)tfl;
+                    if (F.lead()) {
+                        W->tag_id[g] = tid;
+                        W->tag_flags[g] = (uint8_t)tfl;
+                        W->tag_name_off[g] = W->b_tag + gb + tl;
+                    }
                     if (tl) F.copy(nq, nr, W->tag_name + gb);
                     gb += tl;
-                    W->tag_name_off[g] = W->b_tag + gb;
                     g++;
                 }
                 const int c = F.at(p++);
@@ -1209,7 +1464,7 @@ __device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols
     if (!WRITE) {
         R.name_len = name_len; R.cat_len = cat_len; R.n_urls = n_urls; R.url_bytes = url_bytes;
         R.n_tags = n_tags; R.tag_bytes = tag_bytes;
-    } else {
+    } else if (F.lead()) {
         const uint32_t row = rel[C_PETS];
         W->id[row] = id;
         W->flags[row] = (uint8_t)flags;
@@ -1225,6 +1480,15 @@ __device__ __forceinline__ int fline(const FLine &F, LineRec &R, const BlockCols
 }
 #undef FL_SEP
 #undef FL_UNKNOWN
+
+// The wave-cooperative reading of one long line, out of line so that its
+// registers do not add to those of the per-thread path.
+template <bool WRITE>
+__device__ __noinline__ int fline_wave(const uint8_t *tile, const uint64_t *spec, uint32_t s0, uint32_t n, LineRec &R,
+                                       const BlockCols *W, const uint32_t *rel) {
+    const FLineT<true> F{tile + s0, spec, s0, n};
+    return fline<WRITE>(F, R, W, rel);
+}
 
 // ---------------------------------------------------------------- tile bitmaps
 // Build, for the nw 64-byte words of an LDS tile that starts at a line
@@ -1491,8 +1755,8 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //   * block scans plus a vector look-back over 8 counters give the rows /
 //     byte offsets, and a second walk over the sub-tiles (reloaded only when
 //     there were several) writes the columns.
-template <int BT, int TILE>
-__global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
+template <int BT, int TILE, int LONG>
+__global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t spec[TILE / 64 + 1];
     __shared__ uint64_t badm[TILE / 64 + 1];
@@ -1535,6 +1799,7 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
         gs = sh_ls[t];
         n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
     }
+    const bool longl = n > (uint32_t)LONG;
     // ---- pass 0: validate and measure, sub-tile by sub-tile
     LineInfo L;
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
@@ -1560,10 +1825,22 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
                 ttb = tb;
                 bad = line_bad(badm, nw, s0, n);
                 if (bad) code = PJ_REC_STRING;      // provisional: k_dec_errcode settles it
-                else {
+                else if (!longl) {
                     const FLine F{tile + s0, spec, s0, n};
                     code = fline<false>(F, r, nullptr, nullptr);
                     need_gen = code == PJ_BAIL;
+                }
+            }
+            // long lines: the wave of the owning thread reads them together
+            for (uint64_t m = __ballot(mine && !bad && longl); m; m &= m - 1) {
+                const int k = __builtin_ctzll(m);
+                const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
+                LineRec rr{0, 0, 0, 0, 0, 0, 0, 0};
+                const int cc = fline_wave<false>(tile, spec, ks0, kn, rr, nullptr, nullptr);
+                if (lane_id() == k) {
+                    r = rr;
+                    code = cc;
+                    need_gen = cc == PJ_BAIL;
                 }
             }
         } else if (mine) {
@@ -1652,7 +1929,16 @@ __global__ __launch_bounds__(BT) void k_dec_block(DecParams P) {
             tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
             __syncthreads();
         }
-        if (writer && t >= ka && t < kb) {
+        const bool wmine = writer && t >= ka && t < kb;
+        for (uint64_t m = __ballot(wmine && !general && longl); m; m &= m - 1) {
+            const int k = __builtin_ctzll(m);
+            uint32_t rel[PJ_DEC_NCNT];
+#pragma unroll
+            for (int c = 0; c < PJ_DEC_NCNT; c++) rel[c] = (uint32_t)__shfl((int)(uint32_t)pos[c], k, 64);
+            const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
+            fline_wave<true>(tile, spec, ks0, kn, r, &W, rel);
+        }
+        if (wmine && !(longl && !general)) {
             if (!general) {
                 uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
@@ -1709,6 +1995,10 @@ __global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
 #ifndef PJ_DEC_TILE_KB
 #define PJ_DEC_TILE_KB 40
 #endif
+#ifndef PJ_DEC_LONG
+#define PJ_DEC_LONG 1024
+#endif
+constexpr int DEC_LONG = PJ_DEC_LONG;
 constexpr int DEC_IDX_BT = 256, DEC_IDX_R = 4, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
 
 int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
@@ -1727,6 +2017,6 @@ hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.lines + DEC_LINE_BT - 1) / DEC_LINE_BT;
-    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
+    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
     return hipGetLastError();
 }

@@ -247,3 +247,46 @@ def test_decode_blocks_over_the_tile(codec):
     big = [b'{"name":"' + b"x" * k + b'","photoUrls":[]}' for k in (40_900, 40_960, 41_000, 20_000, 39_000)]
     data2 = b"\n".join(big * 3) + b"\n"
     assert_same(gpu_decode(codec, data2), orc.decode(data2))
+
+
+def _long_name(rnd, length, errors=False):
+    frags = ["a", "b", "\\\\", "\\\"", "\\n", "\\t", "\\/", "\\u00e9", "\\u20AC", "\\u0001", "\\ud83d\\ude00",
+             "\\\\\\\\\\\\", "é", "\U0001F600", "€"]
+    bad = ["\\x", "\\u12G4", "\\ud800x", "\\udc00", "\\ud800\\u0041", "\\u00", "\\ud83d\\ud83d"]
+    out, n = [], 0
+    while n < length:
+        f = rnd.choice(frags) if rnd.random() < 0.5 else "x" * rnd.randrange(1, 70)
+        out.append(f)
+        n += len(f.encode())
+    if errors:
+        out.insert(rnd.randrange(len(out) + 1), rnd.choice(bad))
+    return "".join(out)
+
+
+def test_decode_long_lines_wave_parallel(codec):
+    """Lines longer than the per-thread limit are read by a whole wave, with
+    long strings decoded lane-parallel: escapes, backslash runs and
+    surrogate pairs at every offset around 64-byte words and 4 KiB steps,
+    malformed escapes inside long strings, long URLs and tag names, and
+    mutated long lines, against the oracle."""
+    rnd = random.Random(99)
+    lines = []
+    for i in range(400):
+        name = _long_name(rnd, rnd.choice([1100, 2000, 4090, 4100, 8200, 12000]), errors=i % 7 == 3)
+        urls = ",".join('"%s"' % _long_name(rnd, rnd.randrange(10, 3000)) for _ in range(rnd.randrange(0, 3)))
+        tags = ",".join('{"id":%d,"name":"%s"}' % (rnd.randrange(-9, 10**12), _long_name(rnd, rnd.randrange(1, 900)))
+                        for _ in range(rnd.randrange(0, 40)))
+        line = '{"id":%d,"name":"%s","photoUrls":[%s],"tags":[%s],"status":"sold"}' % (i, name, urls, tags)
+        lines.append(line.encode())
+    # backslash runs and pairs that end exactly at a word or step edge
+    for pad in range(1100, 1100 + 130):
+        for frag in ("\\\\", "\\\\\\\"", "\\ud83d\\ude00", "\\u00e9", "\\\""):
+            lines.append(('{"name":"%s%s%s","photoUrls":[]}' % ("y" * pad, frag, "z" * 3000)).encode())
+    for pad in range(4096 - 80, 4096 + 20, 3):
+        lines.append(('{"name":"%s\\\\\\"\\ud83d\\ude00q","photoUrls":[]}' % ("y" * pad)).encode())
+    mut = [_mutate(rnd, rnd.choice(lines[:400])) for _ in range(300)]
+    data = b"\n".join(lines + mut + [b'{"name":"' + b"w" * 5000]) + b"\n"
+    ref = orc.decode(data)
+    assert ref[3].n_errors > 40
+    for shift in (0, 11):
+        assert_same(gpu_decode(codec, data, shift=shift), ref)
