@@ -167,10 +167,8 @@ struct LineInfo {
 };
 
 __device__ __forceinline__ int hexval(int c) {
-    if (c >= '0' && c <= '9') return c - '0';
-    if (c >= 'a' && c <= 'f') return c - 'a' + 10;
-    if (c >= 'A' && c <= 'F') return c - 'A' + 10;
-    return -1;
+    const uint32_t d = (uint32_t)c - '0', a = ((uint32_t)c | 0x20) - 'a';  // 'A'-'F' fold onto 'a'-'f'
+    return d < 10 ? (int)d : a < 6 ? (int)a + 10 : -1;
 }
 __device__ __forceinline__ bool is_ident(int c) {
     return (c >= 'a' && c <= 'z') || (c >= 'A' && c <= 'Z') || (c >= '0' && c <= '9') || c == '_' || c == '$' ||
@@ -857,13 +855,14 @@ __device__ __forceinline__ int hex4(uint32_t x) {
 // first lane performs the scalar column stores.
 template <bool COOP>
 struct FLineT {
-    const uint8_t *s;        // the line's first byte in the LDS tile
-    const uint64_t *special; // the tile's specials bitmap
+    static constexpr bool coop = COOP;
+    const PJ_LDS uint8_t *s;        // the line's first byte in the LDS tile
+    const PJ_LDS uint64_t *special; // the tile's specials bitmap
     uint32_t s0, n;          // tile offset and length of the line
     __device__ __forceinline__ bool lead() const { return !COOP || lane_id() == 0; }
     // 8 bytes at q: the tile is zero-padded 64 bytes past its data, so any
     // q up to n + 32 may be read without a check
-    __device__ __forceinline__ uint64_t ld8(uint32_t q) const { return ldu64(s + q); }
+    __device__ __forceinline__ uint64_t ld8(uint32_t q) const { return lds_u64(s + q); }
     __device__ __forceinline__ int at(uint32_t q) const { return q < n ? (int)s[q] : -1; }
     __device__ __forceinline__ uint32_t next_special(uint32_t q) const {
         const uint32_t a = s0 + q, lim = s0 + n;
@@ -893,8 +892,9 @@ struct FLineT {
     // Escape at q (a backslash).  The two-byte forms and a \uXXXX outside the
     // surrogate range are decoded from one 8-byte read; surrogates and
     // malformed escapes go to escape_at.
-    __device__ __forceinline__ Esc esc(uint32_t q) const {
-        const uint64_t w = ld8(q);
+    __device__ __forceinline__ Esc esc(uint32_t q) const { return esc_w(q, ld8(q)); }
+    // the same, given w = the 8 bytes at q
+    __device__ __forceinline__ Esc esc_w(uint32_t q, uint64_t w) const {
         const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
         Esc r{0, 2, 0, 1};
         if (c == 'u') {
@@ -906,9 +906,9 @@ struct FLineT {
                     return r;
                 }
             }
-            return escape_at(s, n, q);
+            return escape_at((const uint8_t *)s, n, q);
         }
-        if (q + 1 >= n) return escape_at(s, n, q);
+        if (q + 1 >= n) return escape_at((const uint8_t *)s, n, q);
         switch (c) {
         case '"': case '\\': case '/': r.out = c; break;
         case 'b': r.out = 8; break;
@@ -916,7 +916,7 @@ struct FLineT {
         case 'n': r.out = 10; break;
         case 'r': r.out = 13; break;
         case 't': r.out = 9; break;
-        default: return escape_at(s, n, q);
+        default: return escape_at((const uint8_t *)s, n, q);
         }
         return r;
     }
@@ -927,18 +927,37 @@ struct FLineT {
             if (sp < n && s[sp] == '"') return Str{0, sp, sp - q, false};
             return wave_str<false>(q, nullptr);
         }
+        // The current specials word stays in a register while escapes follow
+        // each other inside it, and the 8 bytes read at each special serve
+        // both to tell a quote from a backslash and to decode the escape.
         Str r{0, 0, 0, false};
-        uint32_t d = 0;
+        const uint32_t lim = s0 + n;
+        uint32_t a = s0 + q;
+        if (a >= lim) { r.err = PJ_REC_STRING; return r; }
+        uint32_t wi = a >> 6, d = 0;
+        uint64_t m = special[wi] & (~0ull << (a & 63));
         for (;;) {
-            const uint32_t sp = next_special(q);
-            if (sp >= n) { r.err = PJ_REC_STRING; return r; }
+            while (!m) {
+                if ((wi + 1) * 64 >= lim) { r.err = PJ_REC_STRING; return r; }
+                m = special[++wi];
+            }
+            const uint32_t at = wi * 64 + (uint32_t)__builtin_ctzll(m);
+            if (at >= lim) { r.err = PJ_REC_STRING; return r; }
+            const uint32_t sp = at - s0;
+            const uint64_t w = ld8(sp);
             d += sp - q;
-            if (s[sp] == '"') { r.end = sp; break; }
-            Esc e = esc(sp);
+            if ((w & 0xFF) == '"') { r.end = sp; break; }
+            const Esc e = esc_w(sp, w);
             if (e.err) { r.err = e.err; return r; }
             d += (uint32_t)e.k;
             q = sp + e.adv;
             r.esc = true;
+            a = s0 + q;
+            if (a >= lim) { r.err = PJ_REC_STRING; return r; }
+            if ((a >> 6) != wi) {
+                wi = a >> 6;
+                m = special[wi] & (~0ull << (a & 63));
+            } else m &= ~0ull << (a & 63);
         }
         r.dlen = d;
         return r;
@@ -949,22 +968,24 @@ struct FLineT {
             if (r.esc) wave_str<true>(q, dst);
             else
                 for (uint32_t k = 16u * (uint32_t)lane_id(); k < r.dlen; k += 1024)
-                    copy_exact(dst + k, s + q + k, min(16u, r.dlen - k));
+                    copy_from_lds(dst + k, s + q + k, min(16u, r.dlen - k));
             return;
         }
         if (!r.esc) {
-            copy_exact(dst, s + q, r.dlen);
+            copy_from_lds(dst, s + q, r.dlen);
             return;
         }
         // runs between escapes go out whole; the specials bitmap finds the
         // next backslash (or the closing quote) in a few word reads
         uint8_t *d = dst;
         uint32_t x = q;
+        uint32_t wi = (s0 + x) >> 6;
+        uint64_t m = special[wi] & (~0ull << ((s0 + x) & 63));
         for (;;) {
-            const uint32_t sp = next_special(x);
-            const uint32_t stop = sp < r.end ? sp : r.end;
+            while (!m) m = special[++wi];                  // the closing quote bounds the walk
+            const uint32_t stop = min(wi * 64 + (uint32_t)__builtin_ctzll(m) - s0, r.end);
             if (stop > x) {
-                copy_exact(d, s + x, stop - x);
+                copy_from_lds(d, s + x, stop - x);
                 d += stop - x;
             }
             if (stop >= r.end) break;
@@ -972,6 +993,11 @@ struct FLineT {
             st_tail(d, e.out, (uint32_t)e.k);
             d += e.k;
             x = stop + e.adv;
+            const uint32_t a = s0 + x;
+            if ((a >> 6) != wi) {
+                wi = a >> 6;
+                m = special[wi] & (~0ull << (a & 63));
+            } else m &= ~0ull << (a & 63);
         }
     }
 
@@ -979,28 +1005,46 @@ struct FLineT {
     // owns tile word w0 + l of each 64-word step.  Per word: the backslash
     // mask from its bytes, the escaped characters from a wave scan of the
     // backslash-run carry, the closing quote as the first unescaped quote of
-    // the wave.  Each lane then decodes the escapes that start in its word;
-    // an escape reaching into the next word (at most 11 bytes) is handed on
-    // so that lane starts after it.  Any malformed escape, or no closing
-    // quote, is PJ_REC_STRING, the code the serial walk gives.  With WRITE
-    // the decoded bytes go to dst at each lane's offset (a wave scan).
+    // the wave.  Each escape drops its leading bytes and keeps as many bytes
+    // as it decodes to (a simple escape drops the backslash and keeps the
+    // escaped character; \uXXXX drops 6 - k and keeps k; a surrogate pair
+    // drops 8 and keeps 4), so a lane's output is its word compacted by a
+    // keep mask: the decoded length is a popcount.  An escape reaching into
+    // the next word hands on how far its dropped bytes go.  \u escapes are
+    // decoded in a loop of their own, simple ones only checked, so lanes
+    // that meet different kinds do not run each other's code.  Any malformed
+    // escape, or no closing quote, is PJ_REC_STRING, the code the serial
+    // walk gives.  With WRITE (called only on a string that str() accepted)
+    // each escape's decoded bytes are first stored in place over its kept
+    // bytes in the tile, which no later reader of the line looks at, and the
+    // compacted words go to dst at each lane's offset (a wave scan).
     template <bool WRITE>
     __device__ __forceinline__ Str wave_str(uint32_t q, uint8_t *dst) const {
         const int l = lane_id();
-        const uint8_t *tile = s - s0;
+        const PJ_LDS uint8_t *tile = s - s0;
+        PJ_LDS uint8_t *wt = (PJ_LDS uint8_t *)(s - s0);
         const uint32_t a = s0 + q, lim = s0 + n;
         Str res{0, 0, 0, false};
         uint32_t ecarry = 0;         // the first byte of this step is escaped
-        uint32_t reach_in = a;       // bytes before this are taken by an escape of the previous step
+        uint32_t drop_in = a;        // bytes before this are dropped by an escape of the previous step
         uint32_t d = 0;              // decoded bytes so far
         bool any_esc = false;
         for (uint32_t w0 = a >> 6;; w0 += 64) {
             const uint32_t ws = (w0 + (uint32_t)l) * 64;
             const bool act = ws < lim;
-            uint64_t bs = 0, qt = 0;
+            uint64_t xs[8];
+            uint64_t bs = 0, qt = 0, ub = 0;
+            uint32_t nb = 0;         // the byte after the word
+#pragma unroll
+            for (int j = 0; j < 8; j++) xs[j] = 0;
             if (act) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) bs |= (uint64_t)eq_mask8(ldu64(tile + ws + 8 * j), '\\') << (8 * j);
+                for (int j = 0; j < 8; j++) {
+                    xs[j] = lds_u64(tile + ws + 8 * j);
+                    bs |= (uint64_t)eq_mask8(xs[j], '\\') << (8 * j);
+                    ub |= (uint64_t)eq_mask8(xs[j], 'u') << (8 * j);
+                }
+                nb = tile[ws + 64];
                 qt = special[ws >> 6] & ~bs;
                 uint64_t m = ~0ull;
                 if (ws < a) m <<= (a - ws);
@@ -1028,61 +1072,109 @@ struct FLineT {
             if (l > E) starts = 0;
             if (l == E) starts &= (1ull << (qpos & 63)) - 1;
             const bool mine = l <= E && act;
-            // how far the last escape of this word reaches
-            uint32_t reach = 0;
+            // how far the dropped bytes of this word's last escape reach
+            uint32_t drop = 0;
             if (starts) {
                 const uint32_t p = ws + 63 - (uint32_t)__builtin_clzll(starts);
-                const uint64_t w = ldu64(tile + p);
-                const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
-                uint32_t adv = 2;
-                if (c == 'u') {
-                    const int cu = hex4((uint32_t)(w >> 16));
-                    adv = (cu >= 0xD800 && cu <= 0xDBFF) ? 12 : 6;
+                const uint64_t w = lds_u64(tile + p);
+                const int cu = hex4((uint32_t)(w >> 16));
+                drop = p + 1;
+                if (((w >> 8) & 0xFF) == 'u') {
+                    drop = cu >= 0xD800 && cu <= 0xDBFF ? p + 8                 // pair: 12 bytes, keeps 4
+                         : cu >= 0xDC00 && cu <= 0xDFFF ? p + 2                 // low half: pair began at p - 6
+                         : p + 6 - (cu < 0x80 ? 1 : cu < 0x800 ? 2 : 3);
                 }
-                reach = p + adv;
             }
-            const uint32_t rprev = (uint32_t)__shfl_up((int)reach, 1u, 64);
+            const uint32_t dprev = (uint32_t)__shfl_up((int)drop, 1u, 64);
             uint32_t x = ws < a ? a : ws;
-            const uint32_t from = l == 0 ? reach_in : rprev;
+            const uint32_t from = l == 0 ? drop_in : dprev;
             if (from > x) x = from;
-            // decode this lane's escapes: count pass, then (WRITE) store pass
-            bool err = false;
-            uint32_t dl = 0;
             const uint32_t end = min(hi, ws + 64);
+            uint64_t keep = 0;
+            if (mine && x < end) {
+                keep = ~0ull << (x - ws);
+                if (end - ws < 64) keep &= (1ull << (end - ws)) - 1;
+            }
+            starts &= keep;
+            const uint64_t nu = (ub >> 1) | ((uint64_t)(nb == 'u') << 63);
+            const uint64_t su = starts & nu, ss = starts & ~nu;
+            bool err = false;
+            uint64_t dropm = ss;                        // a simple escape drops its backslash
+            // \u escapes
             {
                 uint32_t y = x;
-                uint64_t m = starts;
-                while (m) {
+                for (uint64_t m = su; m; m &= m - 1) {
                     const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
-                    m &= m - 1;
-                    if (p < y) continue;                     // the low half of a pair decoded before
-                    dl += p - y;
-                    const Esc e = wesc(p, err);
-                    dl += (uint32_t)e.k;
-                    y = p + e.adv;
+                    if (p < y) continue;                    // the low half of a pair
+                    const uint64_t w = lds_u64(tile + p), w2 = lds_u64(tile + p + 6);
+                    const int cu = hex4((uint32_t)(w >> 16)), lo = hex4((uint32_t)(w2 >> 16));
+                    const bool hs = cu >= 0xD800 && cu <= 0xDBFF, ls = cu >= 0xDC00 && cu <= 0xDFFF;
+                    const bool pair = hs && (w2 & 0xFFFF) == ('\\' | ('u' << 8)) && lo >= 0xDC00 && lo <= 0xDFFF;
+                    err |= cu < 0 || ls || (hs && !pair);
+                    const uint32_t cp =
+                        pair ? 0x10000 + (((uint32_t)cu - 0xD800) << 10) + ((uint32_t)lo - 0xDC00) : (uint32_t)cu;
+                    const uint32_t k = cp < 0x80 ? 1 : cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+                    const uint32_t adv = pair ? 12 : 6, dr = adv - k, b = p - ws;
+                    dropm |= (b + dr >= 64 ? ~0ull : ((1ull << (b + dr)) - 1)) & (~0ull << b);
+                    if (WRITE) {
+                        int kk;
+                        const uint32_t u8 = utf8_pack(cp, &kk);
+                        for (uint32_t i = 0; i < k; i++) wt[p + dr + i] = (uint8_t)(u8 >> (8 * i));
+                    }
+                    y = p + adv;
                 }
-                if (y < end) dl += end - y;
             }
-            if (!mine) { dl = 0; err = false; }
-            const uint32_t off = (uint32_t)(wave_incl_scan(dl) - dl);
-            if (WRITE && mine && !__ballot(err)) {
-                uint8_t *o = dst + d + off;
-                uint32_t y = x;
-                uint64_t m = starts;
-                while (m) {
-                    const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
-                    m &= m - 1;
-                    if (p < y) continue;
-                    if (p > y) { copy_exact(o, tile + y, p - y); o += p - y; }
-                    bool e2 = false;
-                    const Esc e = wesc(p, e2);
-                    st_tail(o, e.out, (uint32_t)e.k);
-                    o += e.k;
-                    y = p + e.adv;
+            // simple escapes: the escaped character must be one of "\/bfnrt
+            // (WRITE: decoded in place)
+            for (uint64_t m = ss; m; m &= m - 1) {
+                const uint32_t i = (uint32_t)__builtin_ctzll(m) + 1;
+                uint64_t qw = xs[0];
+#pragma unroll
+                for (int j = 1; j < 8; j++) qw = (i >> 3) == (uint32_t)j ? xs[j] : qw;
+                const uint32_t c = i == 64 ? nb : (uint32_t)(qw >> (8 * (i & 7))) & 0xFF;
+                if (!WRITE) {
+                    constexpr uint64_t LO = (1ull << '"') | (1ull << '/');
+                    constexpr uint64_t HI = (1ull << ('\\' - 64)) | (1ull << ('b' - 64)) | (1ull << ('f' - 64)) |
+                                            (1ull << ('n' - 64)) | (1ull << ('r' - 64)) | (1ull << ('t' - 64));
+                    err |= c >= 128 || !(((c < 64 ? LO : HI) >> (c & 63)) & 1);
+                } else if (c >= 'b') {
+                    uint32_t o = 8;                         // 'b'
+                    o = c == 'f' ? 12u : o;
+                    o = c == 'n' ? 10u : o;
+                    o = c == 'r' ? 13u : o;
+                    o = c == 't' ? 9u : o;
+                    wt[ws + i] = (uint8_t)o;
                 }
-                if (y < end) copy_exact(o, tile + y, end - y);
             }
+            const uint64_t km = keep & ~dropm;
+            const uint32_t dl = mine ? (uint32_t)__builtin_popcountll(km) : 0u;
+            if (!mine) err = false;
             if (__ballot(err)) { res.err = PJ_REC_STRING; return res; }
+            const uint32_t off = (uint32_t)(wave_incl_scan(dl) - dl);
+            if (WRITE && dl) {
+                StoreSink o;
+                o.init(dst + d + off);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t kb = (uint32_t)(km >> (8 * j)) & 0xFF;
+                    if (!kb) continue;
+                    const uint64_t v = lds_u64(tile + ws + 8 * j);   // after the in-place decoding
+                    if (kb == 0xFF) {
+                        o.put8(v, 8);
+                        continue;
+                    }
+                    uint64_t cv = 0;
+                    uint32_t cn = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const bool kp = (kb >> i) & 1;
+                        cv |= kp ? ((v >> (8 * i)) & 0xFF) << (8 * cn) : 0ull;
+                        cn += kp;
+                    }
+                    o.put8(cv, cn);
+                }
+                o.finish();
+            }
             any_esc |= __ballot(starts != 0) != 0;
             d += (uint32_t)wave_sum(dl);
             if (qb) {
@@ -1093,41 +1185,8 @@ struct FLineT {
             }
             if ((w0 + 64) * 64 >= lim) { res.err = PJ_REC_STRING; return res; }   // no closing quote
             ecarry = (uint32_t)__shfl((int)((F >> ecarry) & 1), 63, 64);
-            reach_in = (uint32_t)__shfl((int)reach, 63, 64);
+            drop_in = (uint32_t)__shfl((int)drop, 63, 64);
         }
-    }
-    // Escape at tile offset p for the lane-parallel walk: err is set for a
-    // malformed escape, a lone surrogate or a pair that does not close.
-    __device__ __forceinline__ Esc wesc(uint32_t p, bool &err) const {
-        const uint8_t *tile = s - s0;
-        const uint64_t w = ldu64(tile + p);
-        const uint32_t c = (uint32_t)(w >> 8) & 0xFF;
-        Esc r{0, 2, 0, 1};
-        if (c == 'u') {
-            const int cu = hex4((uint32_t)(w >> 16));
-            r.adv = 6;
-            if (cu < 0 || (cu >= 0xDC00 && cu <= 0xDFFF)) { err = true; return r; }
-            if (cu >= 0xD800) {
-                const uint64_t w2 = ldu64(tile + p + 6);
-                const int lo = hex4((uint32_t)(w2 >> 16));
-                if ((w2 & 0xFFFF) != ('\\' | ('u' << 8)) || lo < 0xDC00 || lo > 0xDFFF) { err = true; return r; }
-                r.adv = 12;
-                r.out = utf8_pack(0x10000 + (((uint32_t)cu - 0xD800) << 10) + ((uint32_t)lo - 0xDC00), &r.k);
-                return r;
-            }
-            r.out = utf8_pack((uint32_t)cu, &r.k);
-            return r;
-        }
-        switch (c) {
-        case '"': case '\\': case '/': r.out = c; break;
-        case 'b': r.out = 8; break;
-        case 'f': r.out = 12; break;
-        case 'n': r.out = 10; break;
-        case 'r': r.out = 13; break;
-        case 't': r.out = 9; break;
-        default: err = true;
-        }
-        return r;
     }
 };
 using FLine = FLineT<false>;
@@ -1251,6 +1310,104 @@ __device__ __forceinline__ int fsub(const FL &F, uint32_t &p, int64_t &id, uint3
     if (F.at(p) != '}') return PJ_BAIL;
     p++;
     return 0;
+}
+
+// Lane-parallel reading of a tags array (COOP lines) whose first element
+// starts at p (a '{').  Lane l owns tile word w0 + l of each 64-word step; the
+// '{' bytes outside strings (string state from the parity of unescaped
+// quotes since p) are the element starts, and each lane reads the elements
+// that start in its word with the per-thread parser, in order.  An element
+// that reads cleanly and is followed by ",{" hands over to the next start,
+// which is therefore the next element; the first lane that meets ']', an
+// error or anything else decides the array, and lanes after it are ignored.
+// Elements are validated exactly as the serial loop validates them, so the
+// code returned is the one it would return.  On success p is past ']' and
+// cnt / bytes hold the number of tags and their name bytes; with WRITE the
+// tags are stored from block-relative index g0 / name byte gb0.
+template <bool WRITE>
+__device__ __forceinline__ int wave_tags(const FLineT<true> &F, uint32_t &p, uint32_t &cnt, uint32_t &bytes,
+                                         const BlockCols *W, uint32_t g0, uint32_t gb0) {
+    const int l = lane_id();
+    const FLine L{F.s, F.special, F.s0, F.n};
+    const PJ_LDS uint8_t *tile = F.s - F.s0;
+    const uint32_t a = F.s0 + p, lim = F.s0 + F.n;
+    uint32_t par = 0;                     // inside a string at the start of this step
+    uint32_t c_done = 0, b_done = 0;      // tags and name bytes of earlier steps
+    for (uint32_t w0 = a >> 6;; w0 += 64) {
+        const uint32_t ws = (w0 + (uint32_t)l) * 64;
+        uint64_t qt = 0, lb = 0;
+        if (ws < lim) {
+            uint64_t bs = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint64_t x = lds_u64(tile + ws + 8 * j);
+                bs |= (uint64_t)eq_mask8(x, '\\') << (8 * j);
+                lb |= (uint64_t)eq_mask8(x, '{') << (8 * j);
+            }
+            qt = F.special[ws >> 6] & ~bs;
+            uint64_t m = ~0ull;
+            if (ws < a) m <<= (a - ws);
+            if (lim - ws < 64) m &= (1ull << (lim - ws)) - 1;
+            qt &= m;
+            lb &= m;
+        }
+        const uint64_t pb = __ballot(__builtin_popcountll(qt) & 1);
+        const uint32_t before = (par ^ (uint32_t)__builtin_popcountll(pb & ((1ull << l) - 1))) & 1;
+        const uint64_t instr = prefix_xor(qt) ^ (before ? ~0ull : 0ull);
+        const uint64_t cand = lb & ~instr;
+        // read this lane's elements
+        uint32_t lc = 0, lbytes = 0, pend = 0;
+        int stop = 0, scode = 0;          // stop: 1 ']' after a clean element, 2 the array fails
+        for (uint64_t m = cand; m; m &= m - 1) {
+            uint32_t q = ws + (uint32_t)__builtin_ctzll(m) - F.s0 + 1;
+            int64_t id;
+            uint32_t fl, nq = 0;
+            Str nr{0, 0, 0, false};
+            const int e = fsub<false>(L, q, id, fl, nq, nr);
+            if (e) { stop = 2; scode = e; break; }
+            lc++;
+            lbytes += (fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+            const int c = L.at(q);
+            if (c == ']') { stop = 1; pend = q + 1; break; }
+            if (c != ',' || L.at(q + 1) != '{') { stop = 2; scode = PJ_BAIL; break; }
+        }
+        const uint64_t sb = __ballot(stop != 0);
+        const int S = sb ? __builtin_ctzll(sb) : 64;
+        if (l > S) { lc = 0; lbytes = 0; }
+        if (sb) {
+            const int st = __shfl(stop, S, 64);
+            if (st == 2) return __shfl(scode, S, 64);
+        }
+        const uint32_t oc = (uint32_t)(wave_incl_scan(lc) - lc), ob = (uint32_t)(wave_incl_scan(lbytes) - lbytes);
+        if (WRITE && l <= S && lc) {
+            uint32_t gi = g0 + c_done + oc, bi = gb0 + b_done + ob;
+            uint64_t m = cand;
+            for (uint32_t k = 0; k < lc; k++, m &= m - 1) {
+                uint32_t q = ws + (uint32_t)__builtin_ctzll(m) - F.s0 + 1;
+                int64_t id;
+                uint32_t fl, nq = 0;
+                Str nr{0, 0, 0, false};
+                fsub<true>(L, q, id, fl, nq, nr);
+                const uint32_t tl = (fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+                W->tag_id[gi] = id;
+                W->tag_flags[gi] = (uint8_t)fl;
+                W->tag_name_off[gi] = W->b_tag + bi + tl;
+                if (tl) L.copy(nq, nr, W->tag_name + bi);
+                gi++;
+                bi += tl;
+            }
+        }
+        c_done += (uint32_t)wave_sum(lc);
+        b_done += (uint32_t)wave_sum(lbytes);
+        if (sb) {
+            cnt = c_done;
+            bytes = b_done;
+            p = (uint32_t)__shfl((int)pend, S, 64);
+            return 0;
+        }
+        if ((w0 + 64) * 64 >= lim) return PJ_BAIL;   // not reached: the last element always stops
+        par = (par ^ (uint32_t)__builtin_popcountll(pb)) & 1;
+    }
 }
 
 // Does the 8-byte prefix at a key start belong to one of the Pet keys as the
@@ -1412,7 +1569,11 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
         flags |= PJ_PET_HAS_TAGS;
         uint32_t g = WRITE ? rel[C_TAGS] : 0, gb = WRITE ? rel[C_TAGB] : 0;
         if (F.at(p) == ']') p++;
-        else {
+        else if constexpr (FL::coop) {
+            if (F.at(p) != '{') return PJ_BAIL;
+            const int e = wave_tags<WRITE>(F, p, n_tags, tag_bytes, W, g, gb);
+            if (e) return e;
+        } else {
             for (;;) {
                 if (F.at(p) != '{') return PJ_BAIL;
                 p++;
@@ -1484,7 +1645,7 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
 // The wave-cooperative reading of one long line, out of line so that its
 // registers do not add to those of the per-thread path.
 template <bool WRITE>
-__device__ __noinline__ int fline_wave(const uint8_t *tile, const uint64_t *spec, uint32_t s0, uint32_t n, LineRec &R,
+__device__ __noinline__ int fline_wave(const PJ_LDS uint8_t *tile, const PJ_LDS uint64_t *spec, uint32_t s0, uint32_t n, LineRec &R,
                                        const BlockCols *W, const uint32_t *rel) {
     const FLineT<true> F{tile + s0, spec, s0, n};
     return fline<WRITE>(F, R, W, rel);
@@ -1826,7 +1987,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 bad = line_bad(badm, nw, s0, n);
                 if (bad) code = PJ_REC_STRING;      // provisional: k_dec_errcode settles it
                 else if (!longl) {
-                    const FLine F{tile + s0, spec, s0, n};
+                    const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
                     code = fline<false>(F, r, nullptr, nullptr);
                     need_gen = code == PJ_BAIL;
                 }
@@ -1836,7 +1997,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 const int k = __builtin_ctzll(m);
                 const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
                 LineRec rr{0, 0, 0, 0, 0, 0, 0, 0};
-                const int cc = fline_wave<false>(tile, spec, ks0, kn, rr, nullptr, nullptr);
+                const int cc = fline_wave<false>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, ks0, kn, rr, nullptr, nullptr);
                 if (lane_id() == k) {
                     r = rr;
                     code = cc;
@@ -1936,14 +2097,14 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
 #pragma unroll
             for (int c = 0; c < PJ_DEC_NCNT; c++) rel[c] = (uint32_t)__shfl((int)(uint32_t)pos[c], k, 64);
             const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
-            fline_wave<true>(tile, spec, ks0, kn, r, &W, rel);
+            fline_wave<true>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, ks0, kn, r, &W, rel);
         }
         if (wmine && !(longl && !general)) {
             if (!general) {
                 uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
-                const FLine F{tile + s0, spec, s0, n};
+                const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
                 fline<true>(F, r, &W, rel);
             } else {
                 uint64_t gp[PJ_DEC_NCNT];

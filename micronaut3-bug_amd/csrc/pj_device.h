@@ -137,7 +137,7 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p 4-byte aligne
 }
 
 // Compile-time packing of up to 8 literal bytes (little endian).
-constexpr uint64_t pack8(const char *s, int k) {
+__host__ __device__ __forceinline__ constexpr uint64_t pack8(const char *s, int k) {
     uint64_t v = 0;
     for (int j = 0; j < k && j < 8; j++) v |= (uint64_t)(uint8_t)s[j] << (8 * j);
     return v;
@@ -192,6 +192,26 @@ __device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
     if (n & 2) { stu16(p, (uint32_t)v); p += 2; v >>= 16; }
     if (n & 1) *p = (uint8_t)v;
 }
+// LDS-qualified pointers: loads through them compile to LDS instructions,
+// which wait only on LDS counters (a generic load must also wait for every
+// outstanding global load and store).  The host pass sees plain pointers.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define PJ_LDS __attribute__((address_space(3)))
+#else
+#define PJ_LDS
+#endif
+__device__ __forceinline__ uint64_t lds_u64(const PJ_LDS uint8_t *p) { return *(const PJ_LDS uint64_t *)p; }
+// n bytes from an LDS buffer (readable up to 8 bytes past the end) to dst
+__device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t *src, uint32_t n) {
+    uint32_t k = 0;
+    for (; k + 16 <= n; k += 16) {
+        const uint64_t a = lds_u64(src + k), b = lds_u64(src + k + 8);
+        stu64(dst + k, a);
+        stu64(dst + k + 8, b);
+    }
+    if (n - k >= 8) { stu64(dst + k, lds_u64(src + k)); k += 8; }
+    if (k < n) st_tail(dst + k, lds_u64(src + k), n - k);
+}
 // n bytes from src (LDS or global, readable up to 8 bytes past the end) to dst
 __device__ __forceinline__ void copy_exact(uint8_t *dst, const uint8_t *src, uint32_t n) {
     uint32_t k = 0;
@@ -214,6 +234,17 @@ struct StoreSink {
         const uint64_t v = (uint64_t)w & ((1ull << (8 * k)) - 1);
         acc |= v << (8 * nacc);
         const uint32_t tot = nacc + (uint32_t)k;
+        if (tot >= 8) {
+            stu64(p, acc);
+            p += 8;
+            acc = nacc ? v >> (8 * (8 - nacc)) : 0;
+            nacc = tot - 8;
+        } else nacc = tot;
+    }
+    __device__ __forceinline__ void put8(uint64_t v, uint32_t k) {  // k (1..8) bytes of v
+        if (k < 8) v &= (1ull << (8 * k)) - 1;
+        acc |= v << (8 * nacc);
+        const uint32_t tot = nacc + k;
         if (tot >= 8) {
             stu64(p, acc);
             p += 8;
