@@ -927,37 +927,18 @@ struct FLineT {
             if (sp < n && s[sp] == '"') return Str{0, sp, sp - q, false};
             return wave_str<false>(q, nullptr);
         }
-        // The current specials word stays in a register while escapes follow
-        // each other inside it, and the 8 bytes read at each special serve
-        // both to tell a quote from a backslash and to decode the escape.
         Str r{0, 0, 0, false};
-        const uint32_t lim = s0 + n;
-        uint32_t a = s0 + q;
-        if (a >= lim) { r.err = PJ_REC_STRING; return r; }
-        uint32_t wi = a >> 6, d = 0;
-        uint64_t m = special[wi] & (~0ull << (a & 63));
+        uint32_t d = 0;
         for (;;) {
-            while (!m) {
-                if ((wi + 1) * 64 >= lim) { r.err = PJ_REC_STRING; return r; }
-                m = special[++wi];
-            }
-            const uint32_t at = wi * 64 + (uint32_t)__builtin_ctzll(m);
-            if (at >= lim) { r.err = PJ_REC_STRING; return r; }
-            const uint32_t sp = at - s0;
-            const uint64_t w = ld8(sp);
+            const uint32_t sp = next_special(q);
+            if (sp >= n) { r.err = PJ_REC_STRING; return r; }
             d += sp - q;
-            if ((w & 0xFF) == '"') { r.end = sp; break; }
-            const Esc e = esc_w(sp, w);
+            if (s[sp] == '"') { r.end = sp; break; }
+            Esc e = esc(sp);
             if (e.err) { r.err = e.err; return r; }
             d += (uint32_t)e.k;
             q = sp + e.adv;
             r.esc = true;
-            a = s0 + q;
-            if (a >= lim) { r.err = PJ_REC_STRING; return r; }
-            if ((a >> 6) != wi) {
-                wi = a >> 6;
-                m = special[wi] & (~0ull << (a & 63));
-            } else m &= ~0ull << (a & 63);
         }
         r.dlen = d;
         return r;
