@@ -118,38 +118,56 @@ __device__ __forceinline__ void emit_long(CountSink &s, int64_t v) {
 }
 
 // ----------------------------------------------------------------- strings
-template <class S> __device__ __forceinline__ void emit_esc_byte(S &s, uint32_t c, uint32_t hexa) {
-    if (c >= 0x20 && c != '"' && c != '\\') { s.put_byte(c); return; }
-    uint32_t e;
-    switch (c) {
-    case '"': e = '"'; break;
-    case '\\': e = '\\'; break;
-    case 8: e = 'b'; break;
-    case 9: e = 't'; break;
-    case 10: e = 'n'; break;
-    case 12: e = 'f'; break;
-    case 13: e = 'r'; break;
-    default: {
-        uint32_t lo = c & 15;
-        uint32_t hc = lo < 10 ? '0' + lo : hexa + lo - 10;
-        s.put8(pack8("\\u00", 4) | ((uint64_t)('0' + (c >> 4)) << 32) | ((uint64_t)hc << 40), 6);
-        return;
-    }
-    }
-    s.put('\\' | (e << 8), 2);
+// Bit 7 of byte k set iff byte k of x needs an output escape (< 0x20, '"'
+// or '\\'); exact per byte, unlike special64's "any" test.
+__device__ __forceinline__ uint64_t special_mask(uint64_t x) {
+    constexpr uint64_t L7 = 0x7F7F7F7F7F7F7F7Full, H = 0x8080808080808080ull;
+    const uint64_t lo = x & L7;
+    const uint64_t lt20 = ~((lo + 0x6060606060606060ull) | x) & H;                 // < 0x20
+    const uint64_t q = (x ^ (0x22 * ONES)) & L7, bsl = (x ^ (0x5C * ONES)) & L7;
+    const uint64_t eq = ~(((q + L7) | (x ^ (0x22 * ONES))) & ((bsl + L7) | (x ^ (0x5C * ONES)))) & H;
+    return lt20 | eq;
 }
-
-__device__ __forceinline__ uint32_t esc_extra(uint32_t c) {  // bytes added by escaping c
-    if (c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13) return 1;
-    return c < 0x20 ? 5 : 0;
+// The escape of byte c (which needs one) as up to 6 bytes, formed without
+// branches: \" \\ \b \t \n \f \r, else \u00XX (hex digits a-f in the case
+// hexa selects).
+__device__ __forceinline__ uint64_t esc_seq(uint32_t c, uint32_t hexa, int *len) {
+    uint32_t e = c;                                   // '"' and '\\' escape as themselves
+    e = c == 8 ? 'b' : e;
+    e = c == 9 ? 't' : e;
+    e = c == 10 ? 'n' : e;
+    e = c == 12 ? 'f' : e;
+    e = c == 13 ? 'r' : e;
+    const bool shrt = c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13;
+    const uint32_t lo = c & 15, hc = lo < 10 ? '0' + lo : hexa + lo - 10;
+    const uint64_t u6 = pack8("\\u00", 4) | ((uint64_t)('0' + (c >> 4)) << 32) | ((uint64_t)hc << 40);
+    *len = shrt ? 2 : 6;
+    return shrt ? (uint64_t)('\\' | (e << 8)) : u6;
 }
-
+// m (1..8) bytes of x, some of which need escapes: the plain runs between
+// them go out whole.
 template <class S> __device__ __forceinline__ void esc_bytes(S &s, uint64_t x, int m, uint32_t hexa) {
-    for (int b = 0; b < m; b++) emit_esc_byte(s, (uint32_t)(x >> (8 * b)) & 0xFF, hexa);
+    uint64_t sp = special_mask(x) & (m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1));
+    int done = 0;
+    while (sp) {
+        const int k = __builtin_ctzll(sp) >> 3;
+        sp &= sp - 1;
+        if (k > done) s.put8(x >> (8 * done), k - done);
+        int len;
+        const uint64_t e = esc_seq((uint32_t)(x >> (8 * k)) & 0xFF, hexa, &len);
+        s.put8(e, len);
+        done = k + 1;
+    }
+    if (m > done) s.put8(x >> (8 * done), m - done);
 }
 __device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint32_t) {
+    uint64_t sp = special_mask(x) & (m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1));
     uint32_t e = 0;
-    for (int b = 0; b < m; b++) e += esc_extra((uint32_t)(x >> (8 * b)) & 0xFF);
+    while (sp) {
+        const uint32_t c = (uint32_t)(x >> (__builtin_ctzll(sp) & ~7)) & 0xFF;
+        sp &= sp - 1;
+        e += (c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13) ? 1 : 5;
+    }
     s.n += (uint64_t)(m + e);
 }
 
