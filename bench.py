@@ -220,8 +220,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="flat", choices=["flat", "nested", "decode"],
-                    help="headline workload; 'decode' runs only the NDJSON decode (for profiling)")
+    ap.add_argument("--workload", default="flat", choices=["flat", "nested", "decode", "skew"],
+                    help="headline workload; 'decode' runs only the NDJSON decode and 'skew' only the "
+                         "configs[4] encode + decode round trip (for profiling)")
     ap.add_argument("--records", type=int, default=10_000_000)
     ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
@@ -247,6 +248,11 @@ def main():
     import torch
     import petjson as pj
     codec = pj.Codec(0)
+    if a.workload == "skew":
+        print(json.dumps({"skew_encode": skew_workload(codec, 2_000_000, a.steps, a.warmup, not a.no_decode)}),
+              flush=True)
+        codec.close()
+        return
     if a.workload == "decode":
         print(json.dumps({"ndjson_decode": decode_workload(codec, a.decode_records, a.steps, a.warmup),
                           "cpu_baseline_decode": cpu_baseline_decode(20_000, a.cpu_budget)}), flush=True)

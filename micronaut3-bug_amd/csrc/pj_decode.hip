@@ -1943,7 +1943,6 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     }
     const bool longl = n > (uint32_t)LONG;
     // ---- pass 0: validate and measure, sub-tile by sub-tile
-    LineInfo L;
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
     bool general = false, bad = false, over = false;
@@ -1992,6 +1991,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         if (need_gen) {
             general = true;
             const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, tb, spec};
+            LineInfo L;
             code = run_line(P, S, over ? gs : s0, n, over, false, L, nullptr);
             if (!code) {
                 r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
@@ -2005,9 +2005,10 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     // ---- scans and look-back
     uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) rec_counts(r, v);
-    uint64_t pos[PJ_DEC_NCNT], agg[PJ_DEC_NCNT];
+    uint32_t pos[PJ_DEC_NCNT];                      // block-relative: a block's columns stay below 2^32 bytes
+    uint64_t agg[PJ_DEC_NCNT];
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
+    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = (uint32_t)block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
     if (t < 64) {
         vlb_publish(P.state_parse, b, agg, (int)t);
         uint64_t excl[PJ_DEC_NCNT];
@@ -2076,15 +2077,16 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
             const int k = __builtin_ctzll(m);
             uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
-            for (int c = 0; c < PJ_DEC_NCNT; c++) rel[c] = (uint32_t)__shfl((int)(uint32_t)pos[c], k, 64);
+            for (int c = 0; c < PJ_DEC_NCNT; c++) rel[c] = (uint32_t)__shfl((int)pos[c], k, 64);
             const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
-            fline_wave<true>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, ks0, kn, r, &W, rel);
+            const BlockCols Wc = W;                 // addressable copy, made only on this path
+            fline_wave<true>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, ks0, kn, r, &Wc, rel);
         }
         if (wmine && !(longl && !general)) {
             if (!general) {
                 uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
-                for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = (uint32_t)pos[k];
+                for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = pos[k];
                 const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
                 fline<true>(F, r, &W, rel);
             } else {
@@ -2092,6 +2094,10 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) gp[k] = pos[k] + base[k];
                 const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, ttb, spec};
+                // the measuring walk again (cheaper than keeping its positions
+                // in registers across the look-back), then the writing walk
+                LineInfo L;
+                run_line(P, S, over ? gs : s0, n, over, false, L, nullptr);
                 run_line(P, S, over ? gs : s0, n, over, true, L, gp);
             }
         }
