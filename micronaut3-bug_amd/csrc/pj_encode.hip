@@ -552,6 +552,65 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 // list, which the whole workgroup measures and writes (slices of the string
 // escaped in parallel and placed by a block scan, items spread over the
 // threads), so one skewed record does not hold its workgroup for long.
+// Copy global bytes [lo, hi) out of an LDS tile whose byte x belongs at
+// global address D + x (all threads of the workgroup).  Global chunk c
+// covers [g0 + 16c, g0 + 16c + 16) with g0 = D - (D & 15), which is tile
+// bytes [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
+// head of word c, joined with one funnel shift.  Whole chunks leave with one
+// aligned 16-byte store; the first and last chunks (shared with neighbouring
+// blocks or segments) with exact 8/4/2/1-byte stores.  The tile must be
+// readable 16 bytes past hi - D.
+template <int BT>
+__device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t s = (uint32_t)(D & 15);
+    const uint64_t g0 = D - s;
+    const uint32_t c_lo = (uint32_t)((lo - g0) >> 4), c_hi = (uint32_t)((hi - g0 + 15) >> 4);
+    const uint4 *W = reinterpret_cast<const uint4 *>(tile);
+    constexpr int U = 4;
+    for (uint32_t c0 = c_lo + t; c0 < c_hi; c0 += U * BT) {
+        unsigned __int128 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t c = c0 + u * BT;
+            v[u] = 0;
+            if (c < c_hi) {
+                const uint4 hi4 = W[c];
+                const unsigned __int128 h = (unsigned __int128)(((uint64_t)hi4.w << 32) | hi4.z) << 64 |
+                                            (((uint64_t)hi4.y << 32) | hi4.x);
+                if (s == 0) v[u] = h;
+                else {
+                    unsigned __int128 l = 0;
+                    if (c > 0) {
+                        const uint4 lo4 = W[c - 1];
+                        l = (unsigned __int128)(((uint64_t)lo4.w << 32) | lo4.z) << 64 |
+                            (((uint64_t)lo4.y << 32) | lo4.x);
+                    }
+                    v[u] = (l >> (8 * (16 - s))) | (h << (8 * s));
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t c = c0 + u * BT;
+            if (c >= c_hi) break;
+            const uint64_t g = g0 + 16ull * c;
+            const uint64_t a = g > lo ? g : lo, e = g + 16 < hi ? g + 16 : hi;
+            const unsigned __int128 x = v[u];
+            if (a == g && e == g + 16) {
+                *reinterpret_cast<uint4 *>(out + g) =
+                    make_uint4((uint32_t)x, (uint32_t)(x >> 32), (uint32_t)(x >> 64), (uint32_t)(x >> 96));
+            } else {
+                unsigned __int128 y = x >> (8 * (uint32_t)(a - g));
+                uint32_t n = (uint32_t)(e - a);
+                uint8_t *q = out + a;
+                if (n & 8) { *reinterpret_cast<uint64_t *>(q) = (uint64_t)y; q += 8; y >>= 64; }
+                st_tail(q, (uint64_t)y, n & 7);
+            }
+        }
+    }
+}
+
 template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP>
 __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
@@ -565,6 +624,10 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4], sh_len;
     __shared__ uint32_t sh_nbig;
+    // hybrid blocks (NESTED): the large records in record order, with their
+    // block offsets, lengths and tile offsets
+    constexpr int RB = NESTED ? R : 1;
+    __shared__ uint32_t sh_big[RB], sh_bpre[RB], sh_blen[RB], sh_bspre[RB];
     static_assert(3 * R * 4 <= TILE, "the fallback path keeps its large-record list in the tile");
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
@@ -617,6 +680,8 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
     uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
     uint64_t len = 0;
+    bool isbig = false;                             // fallback blocks: measured by the whole workgroup
+    uint32_t nbig = 0, bidx = 0;
     if (fast) {
         // ---- phase 0: stage the input slices (4 loads in flight per thread)
         const uint32_t tot = off[4] >> 4;
@@ -675,18 +740,20 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     } else {
         // fallback block: records measured from global memory, one thread
         // each, except large ones, which the whole workgroup measures
-        uint32_t *big = reinterpret_cast<uint32_t *>(tile);     // the tile is unused on this path
-        const bool isbig = live && rec_big<NESTED>(rv);
+        // the large records in record order (the tile holds the list here
+        // for the flat layout, which has no hybrid blocks)
+        uint32_t *big = NESTED ? sh_big : reinterpret_cast<uint32_t *>(tile);
+        isbig = live && rec_big<NESTED>(rv);
         if (live && !isbig) {
             CountSink cs;
             emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
             len = cs.n;
         }
-        if (t == 0) sh_nbig = 0;
+        uint64_t nb64;
+        bidx = (uint32_t)block_excl_scan<BT>(isbig ? 1ull : 0ull, sh_scan, &nb64);
+        nbig = (uint32_t)nb64;
+        if (isbig) big[bidx] = t;
         __syncthreads();
-        if (isbig) big[atomicAdd(&sh_nbig, 1u)] = t;
-        __syncthreads();
-        const uint32_t nbig = sh_nbig;
         for (uint32_t k = 0; k < nbig; k++) {
             const uint32_t r = big[k];
             const RecVals bv = load_rec<NESTED>(P, r0 + r);
@@ -699,6 +766,27 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     const uint64_t pre = block_excl_scan<BT>(len, sh_scan, &agg);
     if (t == 0) lb_publish(P.state, b, agg);
     const bool fits = fast && agg + 16 <= TILE;
+    // Hybrid block (NESTED, fallback measuring): the records other than the
+    // large ones still go through the tile, laid end to end (tile offset
+    // spre), and leave as the segments between the large records, which the
+    // whole workgroup writes straight to global memory.
+    bool hyb = false;
+    uint64_t spre = 0;
+    if (NESTED && !fast) {
+        uint64_t stot;
+        spre = block_excl_scan<BT>(isbig ? 0ull : len, sh_scan, &stot);
+        hyb = stot + 16 <= TILE;
+        if (isbig) {
+            sh_bpre[bidx] = (uint32_t)pre;
+            sh_blen[bidx] = (uint32_t)len;
+            sh_bspre[bidx] = (uint32_t)spre;
+        }
+    }
+    if (hyb && !P.count_only && live && !isbig) {
+        LdsSink ls{tile, (uint32_t)spre};
+        RecItems r2 = ri;
+        emit_rec<NESTED, true>(ls, P, XG, i, rv, r2);
+    }
     EPROF(3);
 
     if (fits && !P.count_only) {
@@ -749,58 +837,22 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     if (P.count_only) return;
     const uint64_t base = sh_base;
     if (fits) {
-        // Global chunk c covers [g0 + 16c, g0 + 16c + 16), which is tile bytes
-        // [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
-        // head of word c, joined with one funnel shift.  Whole chunks leave
-        // with one aligned 16-byte store; the block's first and last chunks
-        // (shared with the neighbouring blocks) with exact 8/4/2/1-byte stores.
         const uint64_t end = min(base + agg, P.cap);
-        if (base >= end) return;
-        const uint32_t s = (uint32_t)(base & 15);
-        const uint64_t g0 = base - s;
-        const uint32_t nc = (uint32_t)((s + (end - base) + 15) >> 4);
-        const uint4 *W = reinterpret_cast<const uint4 *>(tile);
-        constexpr int U = 4;
-        for (uint32_t c0 = t; c0 < nc; c0 += U * BT) {
-            unsigned __int128 v[U];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const uint32_t c = c0 + u * BT;
-                v[u] = 0;
-                if (c < nc) {
-                    const uint4 hi4 = W[c];
-                    const unsigned __int128 hi = (unsigned __int128)(((uint64_t)hi4.w << 32) | hi4.z) << 64 |
-                                                 (((uint64_t)hi4.y << 32) | hi4.x);
-                    if (s == 0) v[u] = hi;
-                    else {
-                        unsigned __int128 lo = 0;
-                        if (c > 0) {
-                            const uint4 lo4 = W[c - 1];
-                            lo = (unsigned __int128)(((uint64_t)lo4.w << 32) | lo4.z) << 64 |
-                                 (((uint64_t)lo4.y << 32) | lo4.x);
-                        }
-                        v[u] = (lo >> (8 * (16 - s))) | (hi << (8 * s));
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const uint32_t c = c0 + u * BT;
-                if (c >= nc) break;
-                const uint64_t g = g0 + 16ull * c;
-                const uint64_t lo = g > base ? g : base, hi = g + 16 < end ? g + 16 : end;
-                const unsigned __int128 x = v[u];
-                if (lo == g && hi == g + 16) {
-                    *reinterpret_cast<uint4 *>(P.out + g) =
-                        make_uint4((uint32_t)x, (uint32_t)(x >> 32), (uint32_t)(x >> 64), (uint32_t)(x >> 96));
-                } else {
-                    unsigned __int128 y = x >> (8 * (uint32_t)(lo - g));
-                    uint32_t n = (uint32_t)(hi - lo);
-                    uint8_t *q = P.out + lo;
-                    if (n & 8) { *reinterpret_cast<uint64_t *>(q) = (uint64_t)y; q += 8; y >>= 64; }
-                    st_tail(q, (uint64_t)y, n & 7);
-                }
-            }
+        if (base < end) tile_copy_out<BT>(tile, P.out, base, base, end);
+        return;
+    }
+    if (hyb) {
+        for (uint32_t k = 0; k <= nbig; k++) {
+            const uint64_t g_lo = k ? (uint64_t)sh_bpre[k - 1] + sh_blen[k - 1] : 0, g_hi = k < nbig ? sh_bpre[k] : agg;
+            const uint64_t t_lo = k ? sh_bspre[k - 1] : 0;
+            const uint64_t lo = base + g_lo, hi = min(base + g_hi, P.cap);
+            if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi);
+        }
+        for (uint32_t k = 0; k < nbig; k++) {
+            const uint64_t p = base + sh_bpre[k];
+            if (p + sh_blen[k] > P.cap) continue;
+            const RecVals bv = load_rec<NESTED>(P, r0 + sh_big[k]);
+            coop_rec<NESTED, BT>(P, P.out + p, r0 + sh_big[k], bv, sh_scan, &sh_len);
         }
         return;
     }
@@ -809,22 +861,22 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     uint32_t *big = reinterpret_cast<uint32_t *>(tile), *bpre = big + R, *blen = bpre + R;
     if (t == 0) sh_nbig = 0;
     __syncthreads();
-    const bool isbig = live && rec_big<NESTED>(rv);
-    if (isbig) {
+    const bool fbig = live && rec_big<NESTED>(rv);
+    if (fbig) {
         const uint32_t k = atomicAdd(&sh_nbig, 1u);
         big[k] = t;
         bpre[k] = (uint32_t)pre;
         blen[k] = (uint32_t)len;
     }
     __syncthreads();
-    if (live && !isbig && base + pre + len <= P.cap) {
+    if (live && !fbig && base + pre + len <= P.cap) {
         WriteSink ws;
         ws.init(P.out, base + pre, P.dummy + t);
         emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
         ws.finish();
     }
-    const uint32_t nbig = sh_nbig;
-    for (uint32_t k = 0; k < nbig; k++) {
+    const uint32_t fnbig = sh_nbig;
+    for (uint32_t k = 0; k < fnbig; k++) {
         const uint64_t p = base + bpre[k];
         if (p + blen[k] > P.cap) continue;
         const RecVals bv = load_rec<NESTED>(P, r0 + big[k]);

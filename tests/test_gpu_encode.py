@@ -156,3 +156,42 @@ def test_encode_item_base_wrap(codec, lists):
         cols = _wrap_case(R, lists)
         for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
             assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt), (R, lists, fmt)
+
+
+def _hybrid_pets():
+    """Nested records where some blocks (96 records each) hold large records
+    (names over 512 bytes, or more than 16 tags) at the block's start, end,
+    side by side and alone, the rest ordinary."""
+    import random
+    from model import Tag, from_columns
+    rnd = random.Random(7)
+    pets = from_columns(pj.generate(3, 96 * 12), as_bytes=True)
+    frag = [b"a", b"\"", b"\\", b"\n", b"\x01", b"\xc3\xa9", b"\xf0\x9f\x98\x80", b"xyz"]
+    big_at = [0, 95, 96, 97, 98, 200, 287, 288, 383, 500, 501, 600, 700, 701, 702, 703, 1100, 1151]
+    for k, i in enumerate(big_at):
+        p = pets[i]
+        if k % 3 != 2:
+            p.name = b"".join(rnd.choice(frag) for _ in range(rnd.randrange(300, 3000)))
+        if k % 3 != 0:
+            p.tags = [Tag(id=rnd.randrange(-10**15, 10**15), name=b"t%d" % j) for j in range(rnd.randrange(17, 220))]
+    return pets
+
+
+def test_encode_hybrid_blocks_match_oracle(codec):
+    """Blocks holding large records keep their other records in the LDS tile
+    and leave as segments between the large ones, which the workgroup writes
+    directly: against the oracle in both framings, and under a capacity cut
+    inside such a block."""
+    cols = to_columns(_hybrid_pets())
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
+    d = cols.to_device()
+    ref = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), np.uint8)
+    for cap in (len(ref) // 3, len(ref) - 5):
+        out = torch.full((len(ref),), 0xEE, dtype=torch.uint8, device="cuda")
+        with pytest.raises(pj.PetJsonError):
+            codec.encode(d, pj.FORMAT_NDJSON, out=out[:cap])
+        host = out.cpu().numpy()
+        assert (host[cap:] == 0xEE).all()
+        written = host[:cap] != 0xEE
+        assert (host[:cap][written] == ref[:cap][written]).all()
