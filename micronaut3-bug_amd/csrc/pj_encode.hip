@@ -517,7 +517,10 @@ __device__ __forceinline__ uint64_t coop_rec(const EncParams &P, uint8_t *out, u
 
 // A record handled cooperatively when its workgroup is on the fallback
 // path: a long name or a long list.
-constexpr uint64_t BIG_STR = 512, BIG_ITEMS = 16;
+#ifndef PJ_ENC_BIG_STR
+#define PJ_ENC_BIG_STR 512
+#endif
+constexpr uint64_t BIG_STR = PJ_ENC_BIG_STR, BIG_ITEMS = 16;
 template <bool NESTED> __device__ __forceinline__ bool rec_big(const RecVals &v) {
     return v.nb - v.na > BIG_STR || (NESTED && (v.u1 - v.u0 > BIG_ITEMS || v.t1 - v.t0 > BIG_ITEMS));
 }
