@@ -84,9 +84,10 @@ __device__ __forceinline__ uint64_t block_excl_scan_idx(uint64_t v, uint64_t *sh
     return idx_combine(before, excl);
 }
 
-// Stage 1, k_dec_lines: each thread owns R consecutive 64-byte words;
-// exact newline masks, block scan + decoupled look-back of newline counts ->
-// line starts.
+// Stage 1, k_dec_lines: each thread owns R 64-byte words of its block's
+// BT * R, one per round (word r * BT + t), so a wave's loads in a round are
+// contiguous; exact newline masks, block scans in word order + decoupled
+// look-back of newline counts -> line starts.
 template <int BT, int R>
 __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
@@ -95,12 +96,14 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     if (t == 0) sh_blk = atomicAdd(&P.tickets[0], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
-    const uint64_t w0 = (b * BT + t) * R;             // first word of this thread
+    // word r * BT + t of the block's BT * R words: in every round the lanes
+    // of a wave read 64 consecutive words
+    const uint64_t wb = b * BT * R;
     uint64_t N[R];
-    uint32_t cnt = 0;
+    uint32_t cnt[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const uint64_t wd = w0 + r, st = wd * 64;
+        const uint64_t wd = wb + (uint64_t)r * BT + t, st = wd * 64;
         uint64_t m = 0;
         if (wd < P.nblk64) {
             if (st + 64 <= P.len) {
@@ -123,25 +126,32 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
             }
         }
         N[r] = m;
-        cnt += (uint32_t)__builtin_popcountll(m);
+        cnt[r] = (uint32_t)__builtin_popcountll(m);
     }
-    uint64_t agg;
-    const uint64_t pre = block_excl_scan<BT>((uint64_t)cnt, sh_scan, &agg);
+    // lines before each word: the rounds in order, threads in order within a round
+    uint64_t pre[R], agg = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        uint64_t tot;
+        pre[r] = agg + block_excl_scan<BT>((uint64_t)cnt[r], sh_scan, &tot);
+        agg += tot;
+    }
     if (t == 0) lb_publish(P.state_idx, b, agg);
     if (t < 64) {
         const uint64_t e = lb_resolve(P.state_idx, b, agg);
         if (t == 0) sh_pre = e;
     }
     __syncthreads();
-    uint64_t li = sh_pre + pre;
+    const uint64_t e0 = sh_pre;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const uint64_t st = (w0 + r) * 64;
+        const uint64_t wd = wb + (uint64_t)r * BT + t, st = wd * 64;
+        uint64_t li = e0 + pre[r];
         for (uint64_t m = N[r]; m; m &= m - 1) {
             li++;
             if (li < P.ls_cap) P.line_start[li] = st + (uint64_t)__builtin_ctzll(m) + 1;
         }
-        if (w0 + r == P.nblk64 - 1) {
+        if (wd == P.nblk64 - 1) {
             const bool open = P.in[P.len - 1] != '\n';  // last line without '\n'
             const uint64_t nl = li + (open ? 1 : 0);
             if (open && nl < P.ls_cap) P.line_start[nl] = P.len + 1;
