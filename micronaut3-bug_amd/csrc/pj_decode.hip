@@ -857,6 +857,120 @@ __device__ __forceinline__ int hex4(uint32_t x) {
     return ok ? (int)cu : -1;
 }
 
+// ---- word-at-a-time string decoding for the lane-parallel walk of long
+// lines.  A 64-byte
+// tile word at ws: xs[] its bytes, ub the mask of its 'u' bytes, nb the byte
+// after it.  Each escape drops its leading bytes and keeps as many bytes as
+// it decodes to (a simple escape drops the backslash and keeps the escaped
+// character; \uXXXX drops 6 - k and keeps k; a surrogate pair drops 8 and
+// keeps 4), so the decoded length of a word is the popcount of its keep
+// mask.
+struct Word {
+    uint64_t xs[8];
+    uint64_t bs, ub;
+    uint32_t nb;
+};
+__device__ __forceinline__ void load_word(const PJ_LDS uint8_t *tile, uint32_t ws, Word &W) {
+    W.bs = 0;
+    W.ub = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        W.xs[j] = lds_u64(tile + ws + 8 * j);
+        W.bs |= (uint64_t)eq_mask8(W.xs[j], '\\') << (8 * j);
+        W.ub |= (uint64_t)eq_mask8(W.xs[j], 'u') << (8 * j);
+    }
+    W.nb = tile[ws + 64];
+}
+// How far the dropped bytes of the last escape among starts (word at ws) reach.
+__device__ __forceinline__ uint32_t last_drop(const PJ_LDS uint8_t *tile, uint32_t ws, uint64_t starts) {
+    if (!starts) return 0;
+    const uint32_t p = ws + 63 - (uint32_t)__builtin_clzll(starts);
+    const uint64_t w = lds_u64(tile + p);
+    const int cu = hex4((uint32_t)(w >> 16));
+    if (((w >> 8) & 0xFF) != 'u') return p + 1;
+    return cu >= 0xD800 && cu <= 0xDBFF ? p + 8                  // pair: 12 bytes, keeps 4
+         : cu >= 0xDC00 && cu <= 0xDFFF ? p + 2                  // low half: the pair began at p - 6
+         : p + 6 - (cu < 0x80 ? 1 : cu < 0x800 ? 2 : 3);
+}
+// The escapes that start in the word (starts, all at or after x, the first
+// byte the word owns): \u escapes decoded for validity and output length
+// (WRITE: their UTF-8 bytes stored in place over their kept bytes), simple
+// escapes checked against "\/bfnrt (WRITE: decoded in place).  Sets err for
+// anything malformed; returns the drop mask.  In-place decoding is only
+// used on a string that has been validated, after which no reader of the
+// line looks at its bytes again.
+template <bool WRITE>
+__device__ __forceinline__ uint64_t word_escapes(const PJ_LDS uint8_t *tile, uint32_t ws, const Word &W, uint64_t starts,
+                                                 uint32_t x, bool &err) {
+    PJ_LDS uint8_t *wt = (PJ_LDS uint8_t *)tile;
+    const uint64_t nu = (W.ub >> 1) | ((uint64_t)(W.nb == 'u') << 63);
+    const uint64_t su = starts & nu, ss = starts & ~nu;
+    uint64_t dropm = ss;                                   // a simple escape drops its backslash
+    uint32_t y = x;
+    for (uint64_t m = su; m; m &= m - 1) {
+        const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
+        if (p < y) continue;                               // the low half of a pair
+        const uint64_t w = lds_u64(tile + p), w2 = lds_u64(tile + p + 6);
+        const int cu = hex4((uint32_t)(w >> 16)), lo = hex4((uint32_t)(w2 >> 16));
+        const bool hs = cu >= 0xD800 && cu <= 0xDBFF, ls = cu >= 0xDC00 && cu <= 0xDFFF;
+        const bool pair = hs && (w2 & 0xFFFF) == ('\\' | ('u' << 8)) && lo >= 0xDC00 && lo <= 0xDFFF;
+        err |= cu < 0 || ls || (hs && !pair);
+        const uint32_t cp = pair ? 0x10000 + (((uint32_t)cu - 0xD800) << 10) + ((uint32_t)lo - 0xDC00) : (uint32_t)cu;
+        const uint32_t k = cp < 0x80 ? 1 : cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+        const uint32_t adv = pair ? 12 : 6, dr = adv - k, b = p - ws;
+        dropm |= (b + dr >= 64 ? ~0ull : ((1ull << (b + dr)) - 1)) & (~0ull << b);
+        if (WRITE) {
+            int kk;
+            const uint32_t u8 = utf8_pack(cp, &kk);
+            for (uint32_t i = 0; i < k; i++) wt[p + dr + i] = (uint8_t)(u8 >> (8 * i));
+        }
+        y = p + adv;
+    }
+    for (uint64_t m = ss; m; m &= m - 1) {
+        const uint32_t i = (uint32_t)__builtin_ctzll(m) + 1;
+        uint64_t qw = W.xs[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) qw = (i >> 3) == (uint32_t)j ? W.xs[j] : qw;
+        const uint32_t c = i == 64 ? W.nb : (uint32_t)(qw >> (8 * (i & 7))) & 0xFF;
+        if (!WRITE) {
+            constexpr uint64_t LO = (1ull << '"') | (1ull << '/');
+            constexpr uint64_t HI = (1ull << ('\\' - 64)) | (1ull << ('b' - 64)) | (1ull << ('f' - 64)) |
+                                    (1ull << ('n' - 64)) | (1ull << ('r' - 64)) | (1ull << ('t' - 64));
+            err |= c >= 128 || !(((c < 64 ? LO : HI) >> (c & 63)) & 1);
+        } else if (c >= 'b') {
+            uint32_t o = 8;                                // 'b'
+            o = c == 'f' ? 12u : o;
+            o = c == 'n' ? 10u : o;
+            o = c == 'r' ? 13u : o;
+            o = c == 't' ? 9u : o;
+            wt[ws + i] = (uint8_t)o;
+        }
+    }
+    return dropm;
+}
+// The bytes of the word at ws kept by km (read after the in-place
+// decoding), compacted, into o.
+__device__ __forceinline__ void word_store(const PJ_LDS uint8_t *tile, uint32_t ws, uint64_t km, StoreSink &o) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t kb = (uint32_t)(km >> (8 * j)) & 0xFF;
+        if (!kb) continue;
+        const uint64_t v = lds_u64(tile + ws + 8 * j);
+        if (kb == 0xFF) {
+            o.put8(v, 8);
+            continue;
+        }
+        uint64_t cv = 0;
+        uint32_t cn = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const bool kp = (kb >> i) & 1;
+            cv |= kp ? ((v >> (8 * i)) & 0xFF) << (8 * cn) : 0ull;
+            cn += kp;
+        }
+        o.put8(cv, cn);
+    }
+}
 // One line of an LDS tile as the fast path reads it.  With COOP false one
 // thread owns the line.  With COOP true the 64 lanes of a wave hold the same
 // line and walk its structure in step (every decision is taken on the same
@@ -1013,7 +1127,6 @@ struct FLineT {
     __device__ __forceinline__ Str wave_str(uint32_t q, uint8_t *dst) const {
         const int l = lane_id();
         const PJ_LDS uint8_t *tile = s - s0;
-        PJ_LDS uint8_t *wt = (PJ_LDS uint8_t *)(s - s0);
         const uint32_t a = s0 + q, lim = s0 + n;
         Str res{0, 0, 0, false};
         uint32_t ecarry = 0;         // the first byte of this step is escaped
@@ -1023,25 +1136,21 @@ struct FLineT {
         for (uint32_t w0 = a >> 6;; w0 += 64) {
             const uint32_t ws = (w0 + (uint32_t)l) * 64;
             const bool act = ws < lim;
-            uint64_t xs[8];
-            uint64_t bs = 0, qt = 0, ub = 0;
-            uint32_t nb = 0;         // the byte after the word
-#pragma unroll
-            for (int j = 0; j < 8; j++) xs[j] = 0;
+            Word Wd;
+            uint64_t bs = 0, qt = 0;
             if (act) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    xs[j] = lds_u64(tile + ws + 8 * j);
-                    bs |= (uint64_t)eq_mask8(xs[j], '\\') << (8 * j);
-                    ub |= (uint64_t)eq_mask8(xs[j], 'u') << (8 * j);
-                }
-                nb = tile[ws + 64];
-                qt = special[ws >> 6] & ~bs;
+                load_word(tile, ws, Wd);
+                qt = special[ws >> 6] & ~Wd.bs;
                 uint64_t m = ~0ull;
                 if (ws < a) m <<= (a - ws);
                 if (lim - ws < 64) m &= (1ull << (lim - ws)) - 1;
-                bs &= m;
+                bs = Wd.bs & m;
                 qt &= m;
+            } else {
+                Wd.bs = Wd.ub = 0;
+                Wd.nb = 0;
+#pragma unroll
+                for (int j = 0; j < 8; j++) Wd.xs[j] = 0;
             }
             // backslash-run carry across the wave: compose c -> cout maps
             uint32_t c0, c1;
@@ -1064,18 +1173,7 @@ struct FLineT {
             if (l == E) starts &= (1ull << (qpos & 63)) - 1;
             const bool mine = l <= E && act;
             // how far the dropped bytes of this word's last escape reach
-            uint32_t drop = 0;
-            if (starts) {
-                const uint32_t p = ws + 63 - (uint32_t)__builtin_clzll(starts);
-                const uint64_t w = lds_u64(tile + p);
-                const int cu = hex4((uint32_t)(w >> 16));
-                drop = p + 1;
-                if (((w >> 8) & 0xFF) == 'u') {
-                    drop = cu >= 0xD800 && cu <= 0xDBFF ? p + 8                 // pair: 12 bytes, keeps 4
-                         : cu >= 0xDC00 && cu <= 0xDFFF ? p + 2                 // low half: pair began at p - 6
-                         : p + 6 - (cu < 0x80 ? 1 : cu < 0x800 ? 2 : 3);
-                }
-            }
+            const uint32_t drop = last_drop(tile, ws, starts);
             const uint32_t dprev = (uint32_t)__shfl_up((int)drop, 1u, 64);
             uint32_t x = ws < a ? a : ws;
             const uint32_t from = l == 0 ? drop_in : dprev;
@@ -1087,56 +1185,8 @@ struct FLineT {
                 if (end - ws < 64) keep &= (1ull << (end - ws)) - 1;
             }
             starts &= keep;
-            const uint64_t nu = (ub >> 1) | ((uint64_t)(nb == 'u') << 63);
-            const uint64_t su = starts & nu, ss = starts & ~nu;
             bool err = false;
-            uint64_t dropm = ss;                        // a simple escape drops its backslash
-            // \u escapes
-            {
-                uint32_t y = x;
-                for (uint64_t m = su; m; m &= m - 1) {
-                    const uint32_t p = ws + (uint32_t)__builtin_ctzll(m);
-                    if (p < y) continue;                    // the low half of a pair
-                    const uint64_t w = lds_u64(tile + p), w2 = lds_u64(tile + p + 6);
-                    const int cu = hex4((uint32_t)(w >> 16)), lo = hex4((uint32_t)(w2 >> 16));
-                    const bool hs = cu >= 0xD800 && cu <= 0xDBFF, ls = cu >= 0xDC00 && cu <= 0xDFFF;
-                    const bool pair = hs && (w2 & 0xFFFF) == ('\\' | ('u' << 8)) && lo >= 0xDC00 && lo <= 0xDFFF;
-                    err |= cu < 0 || ls || (hs && !pair);
-                    const uint32_t cp =
-                        pair ? 0x10000 + (((uint32_t)cu - 0xD800) << 10) + ((uint32_t)lo - 0xDC00) : (uint32_t)cu;
-                    const uint32_t k = cp < 0x80 ? 1 : cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
-                    const uint32_t adv = pair ? 12 : 6, dr = adv - k, b = p - ws;
-                    dropm |= (b + dr >= 64 ? ~0ull : ((1ull << (b + dr)) - 1)) & (~0ull << b);
-                    if (WRITE) {
-                        int kk;
-                        const uint32_t u8 = utf8_pack(cp, &kk);
-                        for (uint32_t i = 0; i < k; i++) wt[p + dr + i] = (uint8_t)(u8 >> (8 * i));
-                    }
-                    y = p + adv;
-                }
-            }
-            // simple escapes: the escaped character must be one of "\/bfnrt
-            // (WRITE: decoded in place)
-            for (uint64_t m = ss; m; m &= m - 1) {
-                const uint32_t i = (uint32_t)__builtin_ctzll(m) + 1;
-                uint64_t qw = xs[0];
-#pragma unroll
-                for (int j = 1; j < 8; j++) qw = (i >> 3) == (uint32_t)j ? xs[j] : qw;
-                const uint32_t c = i == 64 ? nb : (uint32_t)(qw >> (8 * (i & 7))) & 0xFF;
-                if (!WRITE) {
-                    constexpr uint64_t LO = (1ull << '"') | (1ull << '/');
-                    constexpr uint64_t HI = (1ull << ('\\' - 64)) | (1ull << ('b' - 64)) | (1ull << ('f' - 64)) |
-                                            (1ull << ('n' - 64)) | (1ull << ('r' - 64)) | (1ull << ('t' - 64));
-                    err |= c >= 128 || !(((c < 64 ? LO : HI) >> (c & 63)) & 1);
-                } else if (c >= 'b') {
-                    uint32_t o = 8;                         // 'b'
-                    o = c == 'f' ? 12u : o;
-                    o = c == 'n' ? 10u : o;
-                    o = c == 'r' ? 13u : o;
-                    o = c == 't' ? 9u : o;
-                    wt[ws + i] = (uint8_t)o;
-                }
-            }
+            const uint64_t dropm = word_escapes<WRITE>(tile, ws, Wd, starts, x, err);
             const uint64_t km = keep & ~dropm;
             const uint32_t dl = mine ? (uint32_t)__builtin_popcountll(km) : 0u;
             if (!mine) err = false;
@@ -1145,25 +1195,7 @@ struct FLineT {
             if (WRITE && dl) {
                 StoreSink o;
                 o.init(dst + d + off);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const uint32_t kb = (uint32_t)(km >> (8 * j)) & 0xFF;
-                    if (!kb) continue;
-                    const uint64_t v = lds_u64(tile + ws + 8 * j);   // after the in-place decoding
-                    if (kb == 0xFF) {
-                        o.put8(v, 8);
-                        continue;
-                    }
-                    uint64_t cv = 0;
-                    uint32_t cn = 0;
-#pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        const bool kp = (kb >> i) & 1;
-                        cv |= kp ? ((v >> (8 * i)) & 0xFF) << (8 * cn) : 0ull;
-                        cn += kp;
-                    }
-                    o.put8(cv, cn);
-                }
+                word_store(tile, ws, km, o);
                 o.finish();
             }
             any_esc |= __ballot(starts != 0) != 0;
