@@ -290,3 +290,30 @@ def test_decode_long_lines_wave_parallel(codec):
     assert ref[3].n_errors > 40
     for shift in (0, 11):
         assert_same(gpu_decode(codec, data, shift=shift), ref)
+
+
+def test_roundtrip_beyond_4gib(codec):
+    """16M nested records: the NDJSON passes 2^32 bytes, so every 64-bit
+    offset path (line starts, column offsets, look-back sums) is exercised;
+    decode(encode(x)) == x column for column, on the device."""
+    n = 16_000_000
+    cols = pj.generate(3, n)
+    dev = cols.to_device()
+    del cols
+    text = codec.encode(dev, pj.FORMAT_NDJSON)
+    assert text.numel() > 2 ** 32
+    # the array framing of the same records: '[' + the lines joined by ',' + ']'
+    arr = codec.encode(dev, pj.FORMAT_ARRAY)
+    assert arr.numel() == text.numel() + 1
+    assert arr[0].item() == ord("[") and arr[-1].item() == ord("]")
+    body = text[:-1].clone()
+    body[body == ord("\n")] = ord(",")
+    assert torch.equal(arr[1:-1], body)
+    del arr, body
+    dcols, el, ec, res = codec.decode(text)
+    assert res.n_lines == n and res.n_errors == 0 and res.n_pets == n
+    for k in pj.COLS:
+        if dev[k] is not None:
+            assert torch.equal(dev[k].contiguous().view(torch.uint8), dcols[k].contiguous().view(torch.uint8)), k
+    del text, dcols, dev
+    torch.cuda.empty_cache()
