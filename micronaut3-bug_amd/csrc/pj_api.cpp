@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstring>
+#include <cstdlib>
 #include <string>
 
 #include "petjson.h"
@@ -156,15 +157,30 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.total = sc + 1;
     P.dummy = reinterpret_cast<uint32_t *>(sc + 2 + nblk);   // 128 u64 = PJ_BLOCK dwords
     P.state = sc + 2;
-    if ((s = mark(ctx))) return s;
-    PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
-    if ((s = mark(ctx))) return s;
-    PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->stream));
-    if ((s = mark(ctx))) return s;
-    PJ_HIP(hipMemcpyAsync(ctx->pinned, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
-    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    // Blocks take their records in launch order (no ticket atomic on the
+    // critical path).  The look-back waits are bounded: should a block wait
+    // past the bound (a predecessor not yet running), it flags the launch,
+    // which is then redone with ticket-ordered blocks.
+    P.order_by_id = 1;
+    P.spin_limit = 20000000;                                    // 200 ms of the 100 MHz wall clock
+    if (const char *e = std::getenv("PETJSON_SPIN_LIMIT_TICKS")) {  // tests force the redo path with a tiny bound
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v) P.spin_limit = v;
+    }
+    for (int attempt = 0;; attempt++) {
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->stream));
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 2 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if (!P.order_by_id || ctx->pinned[0] == 0 || attempt > 0) break;
+        P.order_by_id = 0;                                      // redo in ticket order
+        ctx->n_ev = 0;
+    }
     if ((s = finish_timing(ctx))) return s;
-    *out_len = ctx->pinned[0];
+    *out_len = ctx->pinned[1];
     if (!count_only && *out_len > cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
     return PJ_OK;
 }

@@ -89,17 +89,22 @@ __device__ __forceinline__ uint64_t lb_load(const uint64_t *p) {
 // Decoupled look-back in two halves.  lb_publish (one lane) announces the
 // block aggregate as early as possible; lb_resolve (one full wave) walks the
 // predecessors 64 at a time, returns the exclusive prefix (same in every
-// lane) and publishes the inclusive prefix.  Predecessors hold smaller
-// tickets, so they are resident and the spin always ends.
+// lane) and publishes the inclusive prefix.  With ticket-ordered blocks the
+// predecessors are resident and the spin always ends.
 __device__ __forceinline__ void lb_publish(uint64_t *state, uint64_t b, uint64_t agg) {
     lb_store(&state[b], (b == 0 ? LB_PRE : LB_AGG) | agg);
 }
 
-__device__ __forceinline__ uint64_t lb_resolve(uint64_t *state, uint64_t b, uint64_t agg) {
+// With a nonzero limit (wall-clock ticks) a wait that outlasts it stores 1 to
+// *gave_up and returns 0: blocks then exit even if a predecessor never runs,
+// and the caller discards the launch's output.
+__device__ __forceinline__ uint64_t lb_resolve(uint64_t *state, uint64_t b, uint64_t agg, uint64_t limit = 0,
+                                               unsigned long long *gave_up = nullptr) {
     const int l = lane_id();
     if (b == 0) return 0;
     uint64_t excl = 0;
     int64_t j = (int64_t)b - 1;
+    const uint64_t t0 = limit ? wall_clock64() : 0;
     for (;;) {
         int64_t idx = j - l;
         uint64_t s = idx >= 0 ? lb_load(&state[idx]) : LB_PRE;
@@ -108,7 +113,14 @@ __device__ __forceinline__ uint64_t lb_resolve(uint64_t *state, uint64_t b, uint
         uint64_t isp = __ballot(fl == 2);
         int fp = isp ? __builtin_ctzll(isp) : 64;
         uint64_t need = fp >= 63 ? ~0ull : ((2ull << fp) - 1);
-        if (notready & need) { __builtin_amdgcn_s_sleep(1); continue; }
+        if (notready & need) {
+            if (limit && wall_clock64() - t0 > limit) {
+                if (l == 0) __hip_atomic_store(gave_up, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return 0;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
         excl += wave_sum(l <= fp ? (s & LB_VAL) : 0);
         if (fp < 64) break;
         j -= 64;

@@ -635,7 +635,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
     if (t == 0) {
-        const uint64_t b = atomicAdd(P.ticket, 1ull);
+        const uint64_t b = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(P.ticket, 1ull);
         sh_blk = b;
         const uint64_t r0 = b * R, r1 = min(r0 + R, P.n);
         const bool pu = NESTED && c.photo_off, pt = NESTED && c.tag_off;
@@ -830,7 +830,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     EPROF(4);
     // ---- phase 4: look-back, then copy out
     if (t < 64) {
-        const uint64_t excl = lb_resolve(P.state, b, agg);
+        const uint64_t excl = lb_resolve(P.state, b, agg, P.order_by_id ? P.spin_limit : 0, P.ticket);
         if (t == 0) {
             sh_base = excl;
             if (b == gridDim.x - 1) *P.total = excl + agg;

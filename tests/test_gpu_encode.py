@@ -195,3 +195,14 @@ def test_encode_hybrid_blocks_match_oracle(codec):
         assert (host[cap:] == 0xEE).all()
         written = host[:cap] != 0xEE
         assert (host[:cap][written] == ref[:cap][written]).all()
+
+
+def test_encode_lookback_redo_in_ticket_order(codec, monkeypatch):
+    """Blocks take their records in launch order and bound their look-back
+    waits; a launch in which some wait ran out is redone with ticket-ordered
+    blocks.  A one-tick bound forces that path: the output is still exact."""
+    monkeypatch.setenv("PETJSON_SPIN_LIMIT_TICKS", "1")
+    for config, n in ((2, 300_000), (3, 100_000), (5, 20_000)):
+        cols = pj.generate(config, n)
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
