@@ -117,6 +117,17 @@ pj_status check_enc_cols(const pj_pet_columns *c) {
     return PJ_OK;
 }
 
+// Look-back wait bound for launch-ordered blocks: 200 ms of the 100 MHz wall
+// clock, or PETJSON_SPIN_LIMIT_TICKS (tests force the redo path with a tiny
+// bound).
+uint64_t spin_limit() {
+    if (const char *e = std::getenv("PETJSON_SPIN_LIMIT_TICKS")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v) return v;
+    }
+    return 20000000;
+}
+
 pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t cap,
                       uint64_t *out_len, bool count_only) {
     pj_status s = bind(ctx);
@@ -162,11 +173,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // past the bound (a predecessor not yet running), it flags the launch,
     // which is then redone with ticket-ordered blocks.
     P.order_by_id = 1;
-    P.spin_limit = 20000000;                                    // 200 ms of the 100 MHz wall clock
-    if (const char *e = std::getenv("PETJSON_SPIN_LIMIT_TICKS")) {  // tests force the redo path with a tiny bound
-        const unsigned long long v = std::strtoull(e, nullptr, 10);
-        if (v) P.spin_limit = v;
-    }
+    P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;
         PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
@@ -425,16 +432,25 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.tickets = reinterpret_cast<unsigned long long *>(X);
         P.dummy = reinterpret_cast<uint32_t *>(X + o_dummy);
         P.gq_count = reinterpret_cast<unsigned long long *>(X + 12);
-        ctx->n_ev = 0;
-        if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(X, 16, 0, ctx->stream));
-        PJ_HIP(pj_launch_fill_u64(X + o_sidx, gidx, 0, ctx->stream));
-        if ((s = mark(ctx))) return s;
-        if (nblk64) PJ_HIP(pj_launch_dec_index(P, ctx->stream));
-        if ((s = mark(ctx))) return s;
-        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 2, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
-        PJ_HIP(hipStreamSynchronize(ctx->stream));
-        const uint64_t lines = ctx->pinned[0];
+        // blocks in launch order with bounded look-back waits; a kernel
+        // whose wait ran out (its ticket word set) is redone in ticket order
+        P.order_by_id = 1;
+        P.spin_limit = spin_limit();
+        for (;;) {
+            ctx->n_ev = 0;
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(pj_launch_fill_u64(X, 16, 0, ctx->stream));
+            PJ_HIP(pj_launch_fill_u64(X + o_sidx, gidx, 0, ctx->stream));
+            if ((s = mark(ctx))) return s;
+            if (nblk64) PJ_HIP(pj_launch_dec_index(P, ctx->stream));
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(hipMemcpyAsync(ctx->pinned, X, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+            PJ_HIP(hipStreamSynchronize(ctx->stream));
+            if (!P.order_by_id || ctx->pinned[0] == 0) break;
+            P.order_by_id = 0;
+        }
+        const int index_order = P.order_by_id;
+        const uint64_t lines = ctx->pinned[2];
         if (lines + 1 > ls_cap) {          // more lines than the first guess: grow and redo
             ls_cap = lines + 2;
             continue;
@@ -446,25 +462,34 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.state_parse = static_cast<uint64_t *>(ctx->scan.p);
         P.dq = P.state_parse + gp * VLB_WORDS;
         P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
-        if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
-        if ((s = mark(ctx))) return s;
-        if (lines) {
-            PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+        P.order_by_id = 1;
+        for (;;) {
             if ((s = mark(ctx))) return s;
-            PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
-        } else {
-            // no lines: the offset arrays still start with 0
-            uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
-                                  out->tag_name_off};
-            for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
+            PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
+            PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
+            PJ_HIP(pj_launch_fill_u64(X + 4, 12, 0, ctx->stream));     // totals and counters
+            if ((s = mark(ctx))) return s;
+            if (lines) {
+                PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+                if ((s = mark(ctx))) return s;
+                PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
+            } else {
+                // no lines: the offset arrays still start with 0
+                uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
+                                      out->tag_name_off};
+                for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
+            }
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(hipMemcpyAsync(ctx->pinned, X, 13 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+            PJ_HIP(hipStreamSynchronize(ctx->stream));
+            if (!P.order_by_id || ctx->pinned[1] == 0) break;
+            P.order_by_id = 0;
+            ctx->n_ev = 0;
         }
-        if ((s = mark(ctx))) return s;
-        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 4, 9 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
-        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        (void)index_order;
         if ((s = finish_timing(ctx))) return s;
-        const uint64_t *T = ctx->pinned;
-        res->n_general = lines ? ctx->pinned[8] : 0;
+        const uint64_t *T = ctx->pinned + 4;
+        res->n_general = lines ? ctx->pinned[12] : 0;
         res->n_lines = lines;
         if (lines) {
             res->n_pets = T[C_PETS];

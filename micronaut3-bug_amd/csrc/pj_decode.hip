@@ -93,7 +93,7 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_blk, sh_pre;
     const uint32_t t = threadIdx.x;
-    if (t == 0) sh_blk = atomicAdd(&P.tickets[0], 1ull);
+    if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[0], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
     // word r * BT + t of the block's BT * R words: in every round the lanes
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     }
     if (t == 0) lb_publish(P.state_idx, b, agg);
     if (t < 64) {
-        const uint64_t e = lb_resolve(P.state_idx, b, agg);
+        const uint64_t e = lb_resolve(P.state_idx, b, agg, P.order_by_id ? P.spin_limit : 0, &P.tickets[0]);
         if (t == 0) sh_pre = e;
     }
     __syncthreads();
@@ -1821,14 +1821,17 @@ __device__ __forceinline__ void vlb_publish(uint64_t *st, uint64_t b, const uint
 }
 
 // one full wave; returns the exclusive prefixes in excl[] (all lanes) and
-// publishes the inclusive ones
-__device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint64_t *agg, uint64_t *excl) {
+// publishes the inclusive ones.  A nonzero limit bounds the wait (wall-clock
+// ticks): past it, 1 goes to *gave_up and the prefixes are left at 0.
+__device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint64_t *agg, uint64_t *excl,
+                                            uint64_t limit = 0, unsigned long long *gave_up = nullptr) {
     const int l = lane_id();
 #pragma unroll
     for (int k = 0; k < PJ_DEC_NCNT; k++) excl[k] = 0;
     if (b == 0) return;
     uint32_t open = (1u << PJ_DEC_NCNT) - 1;            // counters still walking back
     int64_t j = (int64_t)b - 1;
+    const uint64_t t0 = limit ? wall_clock64() : 0;
     while (open) {
         const int64_t idx = j - l;
         uint64_t w[PJ_DEC_NCNT];
@@ -1844,6 +1847,12 @@ __device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint
             wait |= (__ballot((w[k] >> 62) == 0) & need) != 0;
         }
         if (wait) {
+            if (limit && wall_clock64() - t0 > limit) {
+                if (l == 0) __hip_atomic_store(gave_up, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int k = 0; k < PJ_DEC_NCNT; k++) excl[k] = 0;
+                return;
+            }
             __builtin_amdgcn_s_sleep(1);
             continue;
         }
@@ -1950,7 +1959,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     __shared__ uint32_t sh_nsub;
     __shared__ uint64_t sh_blk, sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
-    if (t == 0) sh_blk = atomicAdd(&P.tickets[1], 1ull);
+    if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[1], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
     const uint64_t l0 = b * BT;
@@ -2054,7 +2063,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     if (t < 64) {
         vlb_publish(P.state_parse, b, agg, (int)t);
         uint64_t excl[PJ_DEC_NCNT];
-        vlb_resolve(P.state_parse, b, agg, excl);
+        vlb_resolve(P.state_parse, b, agg, excl, P.order_by_id ? P.spin_limit : 0, &P.tickets[1]);
         if (t < PJ_DEC_NCNT) {
             uint64_t x = 0, y = 0;
 #pragma unroll

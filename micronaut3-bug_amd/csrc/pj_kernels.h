@@ -54,6 +54,12 @@ struct DecParams {
     // invalid from the bitmaps alone)
     uint64_t *dq;
     unsigned long long *dq_count;
+    // 1: block b of each kernel takes its input in launch order (no ticket
+    // atomic) and bounds its look-back wait by spin_limit wall-clock ticks;
+    // a kernel whose wait ran out sets its ticket word to 1 and is redone
+    // in ticket order
+    int order_by_id;
+    uint64_t spin_limit;
 };
 
 // counters carried through the parse-stage scan

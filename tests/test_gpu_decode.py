@@ -317,3 +317,17 @@ def test_roundtrip_beyond_4gib(codec):
             assert torch.equal(dev[k].contiguous().view(torch.uint8), dcols[k].contiguous().view(torch.uint8)), k
     del text, dcols, dev
     torch.cuda.empty_cache()
+
+
+def test_decode_lookback_redo_in_ticket_order(codec, monkeypatch):
+    """The index and parse kernels take blocks in launch order with bounded
+    look-back waits; a kernel whose wait ran out is redone in ticket order.
+    A one-tick bound forces that path: results still equal the oracle's."""
+    monkeypatch.setenv("PETJSON_SPIN_LIMIT_TICKS", "1")
+    cols = pj.generate(3, 60_000, seed=0x5EED0007)
+    buf = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), np.uint8).copy()
+    pj.corrupt_ndjson(buf, 9, 0.01)
+    data = buf.tobytes()
+    assert_same(gpu_decode(codec, data), orc.decode(data))
+    skew = orc.encode(pj.generate(5, 6_000), pj.FORMAT_NDJSON)
+    assert_same(gpu_decode(codec, skew), orc.decode(skew))
