@@ -269,23 +269,45 @@ __device__ __forceinline__ void emit_sub(S &s, const EncParams &P, uint32_t fl, 
     s.put_byte('}');
 }
 
+// One url / tag item's column values, loaded once and kept in registers
+// between the measuring and writing passes.
+struct UrlItem {
+    uint64_t a, b;            // url bytes [a, b)
+};
+struct TagItem {
+    uint64_t a, b;            // name bytes [a, b)
+    int64_t id;
+    uint32_t tf;
+};
+__device__ __forceinline__ UrlItem load_url(const EncParams &P, uint64_t u) {
+    return UrlItem{P.c.url_off[u], P.c.url_off[u + 1]};
+}
+__device__ __forceinline__ TagItem load_tag(const EncParams &P, uint64_t g) {
+    const pj_pet_columns &c = P.c;
+    return TagItem{c.tag_name_off[g], c.tag_name_off[g + 1], c.tag_id[g],
+                   c.tag_flags ? (uint32_t)c.tag_flags[g] : (uint32_t)PJ_SUB_DEFAULT_FLAGS};
+}
+
 // url item: `"url"` + (',' or ']' after the record's last url)
 template <class S>
-__device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, const ColSrc &X, uint64_t u, bool last) {
-    const pj_pet_columns &c = P.c;
-    const uint64_t a = c.url_off[u], b = c.url_off[u + 1];
-    emit_str(s, X.url + (a - X.ub), b - a, P.hexa);
+__device__ __forceinline__ void emit_url_v(S &s, const EncParams &P, const ColSrc &X, const UrlItem &v, bool last) {
+    emit_str(s, X.url + (v.a - X.ub), v.b - v.a, P.hexa);
     s.put_byte(last ? ']' : ',');
+}
+template <class S>
+__device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, const ColSrc &X, uint64_t u, bool last) {
+    emit_url_v(s, P, X, load_url(P, u), last);
 }
 
 // tag item: `{...}` + (',' or ']')
 template <class S>
-__device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, const ColSrc &X, uint64_t g, bool last) {
-    const pj_pet_columns &c = P.c;
-    const uint32_t tf = c.tag_flags ? c.tag_flags[g] : (uint32_t)PJ_SUB_DEFAULT_FLAGS;
-    const uint64_t a = c.tag_name_off[g], b = c.tag_name_off[g + 1];
-    emit_sub(s, P, tf, c.tag_id[g], X.tag + (a - X.tb), b - a);
+__device__ __forceinline__ void emit_tag_v(S &s, const EncParams &P, const ColSrc &X, const TagItem &v, bool last) {
+    emit_sub(s, P, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
     s.put_byte(last ? ']' : ',');
+}
+template <class S>
+__device__ __forceinline__ void emit_tag_item(S &s, const EncParams &P, const ColSrc &X, uint64_t g, bool last) {
+    emit_tag_v(s, P, X, load_tag(P, g), last);
 }
 
 // The pieces of one record, in order: head (separator, '{', id, category,
@@ -682,6 +704,10 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
 
     RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
     uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
+    // this thread's url / tag items (k = t + j BT) on the fast path
+    constexpr int UI = (UCAP + BT - 1) / BT, GI = (GCAP + BT - 1) / BT;
+    UrlItem uv[UI];
+    TagItem gv[GI];
     uint64_t len = 0;
     bool isbig = false;                             // fallback blocks: measured by the whole workgroup
     uint32_t nbig = 0, bidx = 0;
@@ -713,15 +739,25 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
         EPROF(1);
         // ---- phase 1: item lengths and their block scans
         if (NESTED) {
-            for (uint32_t k = t; k < U; k += BT) {
-                CountSink cs;
-                emit_url_item(cs, P, XL, U0 + k, false);
-                su[k] = (uint32_t)cs.n;
+#pragma unroll
+            for (int j = 0; j < UI; j++) {
+                const uint32_t k = t + (uint32_t)j * BT;
+                if (k < U) {
+                    uv[j] = load_url(P, U0 + k);
+                    CountSink cs;
+                    emit_url_v(cs, P, XL, uv[j], false);
+                    su[k] = (uint32_t)cs.n;
+                }
             }
-            for (uint32_t k = t; k < G; k += BT) {
-                CountSink cs;
-                emit_tag_item(cs, P, XL, G0 + k, false);
-                sg[k] = (uint32_t)cs.n;
+#pragma unroll
+            for (int j = 0; j < GI; j++) {
+                const uint32_t k = t + (uint32_t)j * BT;
+                if (k < G) {
+                    gv[j] = load_tag(P, G0 + k);
+                    CountSink cs;
+                    emit_tag_v(cs, P, XL, gv[j], false);
+                    sg[k] = (uint32_t)cs.n;
+                }
             }
             __syncthreads();
             lds_excl_scan<BT>(su, (uint32_t)U, sh_scan);
@@ -813,17 +849,23 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
             emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
         }
         if (NESTED) {
-            for (uint32_t k = t; k < U; k += BT) {
+#pragma unroll
+            for (int j = 0; j < UI; j++) {
+                const uint32_t k = t + (uint32_t)j * BT;
+                if (k >= U) continue;
                 const uint32_t own = uown[k];
                 if (!uon[own]) continue;
                 LdsSink ls{tile, ubase[own] + su[k]};
-                emit_url_item(ls, P, XL, U0 + k, k + 1 == uend[own]);
+                emit_url_v(ls, P, XL, uv[j], k + 1 == uend[own]);
             }
-            for (uint32_t k = t; k < G; k += BT) {
+#pragma unroll
+            for (int j = 0; j < GI; j++) {
+                const uint32_t k = t + (uint32_t)j * BT;
+                if (k >= G) continue;
                 const uint32_t own = gown[k];
                 if (!gon[own]) continue;
                 LdsSink ls{tile, gbase[own] + sg[k]};
-                emit_tag_item(ls, P, XL, G0 + k, k + 1 == gend[own]);
+                emit_tag_v(ls, P, XL, gv[j], k + 1 == gend[own]);
             }
         }
     }
