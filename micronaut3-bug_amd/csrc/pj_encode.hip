@@ -21,6 +21,8 @@
 // Output rules (jackson UTF8JsonGenerator via micronaut-serde, reference
 // build.gradle:104) and property order / inclusion (petstore.json:872-922)
 // are the ones restated by the CPU checker in oracle/pj_oracle.c.
+#include <type_traits>
+
 #include "pj_device.h"
 #include "pj_kernels.h"
 
@@ -39,7 +41,7 @@ struct CountSink {
 };
 
 // Exact unaligned writes into the LDS tile.
-struct LdsSink {
+struct LdsSinkU {
     uint8_t *t;
     uint32_t o;
     __device__ __forceinline__ void put8(uint64_t x, int k) {
@@ -52,7 +54,50 @@ struct LdsSink {
     }
     __device__ __forceinline__ void put(uint32_t w, int k) { put8(w, k); }
     __device__ __forceinline__ void put_byte(uint32_t b) { t[o++] = (uint8_t)b; }
+    __device__ __forceinline__ void finish() {}
     __device__ __forceinline__ void skip(uint32_t k) { o += k; }
+    __device__ __forceinline__ uint32_t pos() const { return o; }
+};
+
+// Writes into the LDS tile with aligned 8-byte stores only (unaligned LDS
+// accesses stall the LDS pipeline): bytes gather in a register that always
+// describes one aligned qword of the tile; a complete qword is stored whole,
+// except that a qword the writer shares with the previous or next writer of
+// the tile (its first and last) is merged with an LDS OR into a tile that
+// was zeroed beforehand, so neighbouring writers need no ordering.  finish()
+// after the last byte; skip(k) leaves k bytes to other writers.
+struct LdsSinkA {
+    uint8_t *t;               // tile base, 8-byte aligned
+    uint32_t o;               // next byte offset
+    uint64_t acc = 0;         // pending bytes of the qword at o & ~7
+    bool head = true;         // the pending qword may hold another writer's bytes
+    __device__ __forceinline__ void flush(bool merge) {
+        uint64_t *q = reinterpret_cast<uint64_t *>(t + (o & ~7u));
+        if (merge) atomicOr(reinterpret_cast<unsigned long long *>(q), (unsigned long long)acc);
+        else *q = acc;
+    }
+    __device__ __forceinline__ void put8(uint64_t x, int k) {   // k (1..8) bytes of x
+        if (k < 8) x &= (1ull << (8 * k)) - 1;
+        const uint32_t n = o & 7;
+        acc |= x << (8 * n);
+        if (n + (uint32_t)k >= 8) {
+            flush(head && n != 0);
+            head = false;
+            acc = n ? x >> (8 * (8 - n)) : 0;
+        }
+        o += (uint32_t)k;
+    }
+    __device__ __forceinline__ void put(uint32_t w, int k) { put8(w, k); }
+    __device__ __forceinline__ void put_byte(uint32_t b) { put8(b & 0xFF, 1); }
+    __device__ __forceinline__ void finish() {
+        if (o & 7) flush(true);
+        acc = 0;
+        head = true;
+    }
+    __device__ __forceinline__ void skip(uint32_t k) {
+        finish();
+        o += k;
+    }
     __device__ __forceinline__ uint32_t pos() const { return o; }
 };
 
@@ -171,10 +216,45 @@ __device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint3
     s.n += (uint64_t)(m + e);
 }
 
+// The string bytes of a staged slice, read as aligned LDS qwords joined by a
+// funnel shift (unaligned LDS reads stall the LDS pipeline).
+template <class S>
+__device__ __forceinline__ void emit_str_lds(S &s, const PJ_LDS uint8_t *p, uint32_t len, uint32_t hexa) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 7;
+    const PJ_LDS uint64_t *q = (const PJ_LDS uint64_t *)(p - sh);
+    uint64_t cur = q[0];
+    uint32_t k = 0, j = 0;
+    for (; k + 8 <= len; k += 8, j++) {
+        const uint64_t nxt = q[j + 1];
+        const uint64_t x = sh ? (cur >> (8 * sh)) | (nxt << (64 - 8 * sh)) : cur;
+        if (!special64(x)) s.put8(x, 8);
+        else esc_bytes(s, x, 8, hexa);
+        cur = nxt;
+    }
+    if (k < len) {
+        const int m = (int)(len - k);
+        uint64_t x = cur >> (8 * sh);
+        if (sh + (uint32_t)m > 8) x |= q[j + 1] << (64 - 8 * sh);
+        const uint64_t mk = (1ull << (8 * m)) - 1;
+        x &= mk;
+        if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
+        else esc_bytes(s, x, m, hexa);
+    }
+}
+
 // A JSON string (quotes included) from raw UTF-8 bytes: 8 bytes per step
-// through the no-escape fast path.
+// through the no-escape fast path.  Strings staged in LDS take the aligned
+// reads of emit_str_lds; global memory takes unaligned 8-byte loads and, for
+// the tail, the aligned reads that never touch another page.
 template <class S> __device__ __forceinline__ void emit_str(S &s, const uint8_t *p, uint64_t len, uint32_t hexa) {
     s.put_byte('"');
+#if defined(__HIP_DEVICE_COMPILE__)
+    if (__builtin_amdgcn_is_shared((const void *)p)) {
+        if (len) emit_str_lds(s, (const PJ_LDS uint8_t *)p, (uint32_t)len, hexa);
+        s.put_byte('"');
+        return;
+    }
+#endif
     uint64_t k = 0;
     for (; k + 8 <= len; k += 8) {
         uint64_t x = ldu64(p + k);
@@ -183,16 +263,7 @@ template <class S> __device__ __forceinline__ void emit_str(S &s, const uint8_t 
     }
     if (k < len) {
         int m = (int)(len - k);
-        // staged slices in LDS are padded to 16-byte chunks (and LDS reads past
-        // the allocation return zeros), so one 8-byte read serves; global
-        // memory takes the aligned reads that never touch another page
-#if defined(__HIP_DEVICE_COMPILE__)
-        uint64_t x = __builtin_amdgcn_is_shared((const void *)(p + k))
-                         ? ldu64(p + k) & ((1ull << (8 * m)) - 1)
-                         : ld_tail(p + k, m);
-#else
-        uint64_t x = ld_tail(p + k, m);               // host pass: never executed
-#endif
+        uint64_t x = ld_tail(p + k, m);
         uint64_t mk = (1ull << (8 * m)) - 1;
         if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
         else esc_bytes(s, x, m, hexa);
@@ -639,6 +710,10 @@ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out,
 template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP>
 __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
+    // flat records write the tile with aligned stores only; nested ones,
+    // whose many short items mostly land in edge qwords shared with a
+    // neighbour, with plain unaligned stores (measured faster there)
+    using LdsSink = typename std::conditional<!NESTED, LdsSinkA, LdsSinkU>::type;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t inb[INCAP];  // staged input slices
     __shared__ uint32_t su[UA + 1], sg[GA + 1];      // item prefix sums (tile-relative)
@@ -656,6 +731,9 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     static_assert(3 * R * 4 <= TILE, "the fallback path keeps its large-record list in the tile");
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
+    // the flat tile starts zeroed: writers merge the qwords they share with an OR
+    if (!NESTED)
+        for (uint32_t k = t; k < (uint32_t)TILE / 16; k += BT) reinterpret_cast<uint4 *>(tile)[k] = make_uint4(0, 0, 0, 0);
     if (t == 0) {
         const uint64_t b = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(P.ticket, 1ull);
         sh_blk = b;
@@ -825,6 +903,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
         LdsSink ls{tile, (uint32_t)spre};
         RecItems r2 = ri;
         emit_rec<NESTED, true>(ls, P, XG, i, rv, r2);
+        ls.finish();
     }
     EPROF(3);
 
@@ -847,6 +926,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
             LdsSink ls{tile, (uint32_t)pre};
             RecItems r2 = ri;
             emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
+            ls.finish();
         }
         if (NESTED) {
 #pragma unroll
@@ -857,6 +937,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
                 if (!uon[own]) continue;
                 LdsSink ls{tile, ubase[own] + su[k]};
                 emit_url_v(ls, P, XL, uv[j], k + 1 == uend[own]);
+                ls.finish();
             }
 #pragma unroll
             for (int j = 0; j < GI; j++) {
@@ -866,6 +947,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
                 if (!gon[own]) continue;
                 LdsSink ls{tile, gbase[own] + sg[k]};
                 emit_tag_v(ls, P, XL, gv[j], k + 1 == gend[own]);
+                ls.finish();
             }
         }
     }
