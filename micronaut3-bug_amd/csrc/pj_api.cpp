@@ -68,6 +68,7 @@ struct pj_ctx {
     DevBuf stage_in;    // host path: input staging
     DevBuf stage_out;   // host path: output staging
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
+    bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
     int n_ev = 0;
     float timings[MAX_EV] = {};
@@ -152,7 +153,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     }
     const uint64_t bt = (uint64_t)pj_encode_block_records(nested_cols(cols));
     const uint64_t nblk = (n + bt - 1) / bt;
-    PJ_HIP(ctx->scan.ensure((nblk + 2 + 128) * sizeof(uint64_t)));
+    PJ_HIP(ctx->scan.ensure((nblk + 3 + 128) * sizeof(uint64_t)));
     uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p);
     EncParams P;
     std::memset(&P, 0, sizeof P);
@@ -164,10 +165,12 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.count_only = count_only ? 1 : 0;
     P.out = out;
     P.cap = count_only ? 0 : cap;
+    // scan buffer: ticket, total, fallback-block count, look-back words, dummy
     P.ticket = reinterpret_cast<unsigned long long *>(sc);
     P.total = sc + 1;
-    P.dummy = reinterpret_cast<uint32_t *>(sc + 2 + nblk);   // 128 u64 = PJ_BLOCK dwords
-    P.state = sc + 2;
+    P.nfall = reinterpret_cast<unsigned long long *>(sc + 2);
+    P.state = sc + 3;
+    P.dummy = reinterpret_cast<uint32_t *>(sc + 3 + nblk);   // 128 u64 = PJ_BLOCK dwords
     // Blocks take their records in launch order (no ticket atomic on the
     // critical path).  The look-back waits are bounded: should a block wait
     // past the bound (a predecessor not yet running), it flags the launch,
@@ -176,16 +179,18 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(sc, nblk + 3, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->stream));
+        PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
         if ((s = mark(ctx))) return s;
-        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 2 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));
         if (!P.order_by_id || ctx->pinned[0] == 0 || attempt > 0) break;
         P.order_by_id = 0;                                      // redo in ticket order
         ctx->n_ev = 0;
     }
+    // flat records too long for the compact tile: later calls use the wide one
+    if (!nested_cols(cols) && !ctx->flat_wide && ctx->pinned[2] * 64 > nblk) ctx->flat_wide = true;
     if ((s = finish_timing(ctx))) return s;
     *out_len = ctx->pinned[1];
     if (!count_only && *out_len > cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");

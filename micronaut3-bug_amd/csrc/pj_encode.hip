@@ -707,8 +707,8 @@ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out,
     }
 }
 
-template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP>
-__global__ __launch_bounds__(BT) void k_encode(EncParams P) {
+template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP, int WPE = 1>
+__global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
     // flat records write the tile with aligned stores only; nested ones,
     // whose many short items mostly land in edge qwords shared with a
@@ -883,6 +883,7 @@ __global__ __launch_bounds__(BT) void k_encode(EncParams P) {
     const uint64_t pre = block_excl_scan<BT>(len, sh_scan, &agg);
     if (t == 0) lb_publish(P.state, b, agg);
     const bool fits = fast && agg + 16 <= TILE;
+    if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
     // Hybrid block (NESTED, fallback measuring): the records other than the
     // large ones still go through the tile, laid end to end (tile offset
     // spre), and leave as the segments between the large records, which the
@@ -1034,13 +1035,19 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 #define PJ_ENC_NEST_R 96
 #endif
 // Workgroup shapes: threads, records, LDS tile bytes, item capacities.
-constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256, ENC_FLAT_TILE = 28 * 1024, ENC_FLAT_IN = 8 * 1024;
+// Flat blocks of 256 records in two shapes: compact (tile 96 B and staged
+// names 24 B per record, 30.6 KB of LDS, five waves per SIMD) for records up
+// to about 90 bytes, wide (112 B / 32 B, four waves per SIMD) once the
+// compact tile has sent more than 1 block in 64 to the fallback path.
+constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256;
+constexpr int ENC_FLAT_TILE = ENC_FLAT_R * 96, ENC_FLAT_IN = ENC_FLAT_R * 24, ENC_FLAT_WPE = 5;
+constexpr int ENC_WIDE_TILE = ENC_FLAT_R * 112, ENC_WIDE_IN = ENC_FLAT_R * 32;
 constexpr int ENC_NEST_BT = 256, ENC_NEST_R = PJ_ENC_NEST_R, ENC_NEST_TILE = 30 * 1024 + 512, ENC_NEST_IN = 14 * 1024,
               ENC_NEST_UCAP = 320, ENC_NEST_GCAP = 256;
 
 int pj_encode_block_records(bool nested) { return nested ? ENC_NEST_R : ENC_FLAT_R; }
 
-hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st) {
+hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st) {
     if (nested) {
         uint64_t g = (P.n + ENC_NEST_R - 1) / ENC_NEST_R;
         hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
@@ -1048,8 +1055,12 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st) {
                            dim3((unsigned)g), dim3(ENC_NEST_BT), 0, st, P);
     } else {
         uint64_t g = (P.n + ENC_FLAT_R - 1) / ENC_FLAT_R;
-        hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1>), dim3((unsigned)g),
-                           dim3(ENC_FLAT_BT), 0, st, P);
+        if (wide)
+            hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_WIDE_TILE, ENC_WIDE_IN, 1, 1>),
+                               dim3((unsigned)g), dim3(ENC_FLAT_BT), 0, st, P);
+        else
+            hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>),
+                               dim3((unsigned)g), dim3(ENC_FLAT_BT), 0, st, P);
     }
     return hipGetLastError();
 }

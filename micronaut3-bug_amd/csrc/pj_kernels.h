@@ -20,6 +20,7 @@ struct EncParams {
     uint64_t spin_limit;       // look-back wait bound (wall-clock ticks) when order_by_id
     uint64_t *total;           // encoded size (written by the last block)
     uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)
+    unsigned long long *nfall; // blocks whose records did not fit the LDS tile (counted)
 };
 
 // What the decode counting kernels learn about each line, read back by the
@@ -66,7 +67,7 @@ struct DecParams {
 enum { C_PETS = 0, C_NAMEB, C_CATB, C_URLS, C_URLB, C_TAGS, C_TAGB, C_ERRS, PJ_DEC_NCNT };
 
 hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);
-hipError_t pj_launch_encode(const EncParams &P, bool nested, hipStream_t st);
+hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 int pj_encode_block_records(bool nested);
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);

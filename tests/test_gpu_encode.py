@@ -206,3 +206,23 @@ def test_encode_lookback_redo_in_ticket_order(codec, monkeypatch):
         cols = pj.generate(config, n)
         for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
             assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
+
+
+def test_encode_flat_long_records_switch_to_wide_tile(codec):
+    """Flat records longer than the compact tile allows: the first call's
+    blocks fall back, and later calls use the wide tile; every call's output
+    equals the oracle's."""
+    rnd = np.random.default_rng(3)
+    base = pj.generate(2, 40_000)
+    n = base.n_pets
+    lens = rnd.integers(40, 120, size=n)
+    off = np.zeros(n + 1, np.uint64)
+    off[1:] = np.cumsum(lens)
+    alnum = np.frombuffer(b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789", np.uint8)
+    nb = alnum[rnd.integers(0, len(alnum), size=int(off[-1]))]
+    cols = pj.Columns(n, dict(base.arrays))
+    cols.arrays["name_off"] = off
+    cols.arrays["name_bytes"] = nb
+    ref = orc.encode(cols, pj.FORMAT_ARRAY)
+    for _ in range(3):
+        assert gpu_encode(codec, cols, pj.FORMAT_ARRAY) == ref
