@@ -404,11 +404,14 @@ __device__ __forceinline__ void rec_head(S &s, const EncParams &P, const ColSrc 
     else lit(s, "\"name\":null");
 }
 
-template <class S> __device__ __forceinline__ void rec_urls_open(S &s, const RecVals &v) {
-    if (v.fl & PJ_PET_HAS_PHOTOURLS) {
+template <class S> __device__ __forceinline__ void rec_urls_open(S &s, uint32_t fl, bool empty) {
+    if (fl & PJ_PET_HAS_PHOTOURLS) {
         lit(s, ",\"photoUrls\":[");
-        if (v.u1 == v.u0) s.put_byte(']');
+        if (empty) s.put_byte(']');
     } else lit(s, ",\"photoUrls\":null");
+}
+template <class S> __device__ __forceinline__ void rec_urls_open(S &s, const RecVals &v) {
+    rec_urls_open(s, v.fl, v.u1 == v.u0);
 }
 
 template <bool NESTED, class S> __device__ __forceinline__ void rec_tags_open(S &s, const EncParams &P, const RecVals &v) {
@@ -434,6 +437,14 @@ template <class S> __device__ __forceinline__ void rec_tail(S &s, const EncParam
 __device__ __forceinline__ bool rec_has_urls(const RecVals &v) { return (v.fl & PJ_PET_HAS_PHOTOURLS) && v.u1 > v.u0; }
 template <bool NESTED> __device__ __forceinline__ bool rec_has_tags(const RecVals &v) {
     return NESTED && (v.fl & PJ_PET_HAS_TAGS) && v.t1 > v.t0;
+}
+
+// The name unit of a record: the name string, then the photoUrls opener.
+// f: the record's HAS_NAME and HAS_PHOTOURLS bits, 0x80 when it has no urls.
+template <class S>
+__device__ __forceinline__ void name_unit(S &s, const EncParams &P, const uint8_t *nm, uint32_t nl, uint32_t f) {
+    if (f & PJ_PET_HAS_NAME) emit_str(s, nm, nl, P.hexa);
+    rec_urls_open(s, f, (f & 0x80u) != 0);
 }
 
 // One record plus its separators: '[' or ',' before (array), '\n' or ']'
@@ -716,8 +727,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     using LdsSink = typename std::conditional<!NESTED, LdsSinkA, LdsSinkU>::type;
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t inb[INCAP];  // staged input slices
-    __shared__ uint32_t su[UA + 1], sg[GA + 1];      // item prefix sums (tile-relative)
-    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: item area base - su[first] (mod 2^32)
+    // NESTED fast blocks: every record is cut into units, laid out in output
+    // order as head, name, url items, tags opener, tag items, tail; a unit's
+    // tile offset is the exclusive scan of the unit lengths (ulen)
+    constexpr int NUC = NESTED ? 4 * R + UCAP + GCAP : 1;
+    __shared__ uint32_t ulen[NUC + 1];
+    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: unit index of its item k is base + k (mod 2^32)
+    __shared__ uint8_t rn_f[RA];                      // per record: flags of its name unit
     __shared__ uint8_t uon[RA], gon[RA];              // per record: its url / tag items are written
     __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
     __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
@@ -782,14 +798,33 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
 
     RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
     uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
-    // this thread's url / tag items (k = t + j BT) on the fast path
-    constexpr int UI = (UCAP + BT - 1) / BT, GI = (GCAP + BT - 1) / BT;
-    UrlItem uv[UI];
-    TagItem gv[GI];
-    uint64_t len = 0;
+    // NESTED fast blocks: thread t holds units t + j BT of the list
+    // [heads (R) | names (R) | url items (U) | tag items (G)]: the record
+    // threads t < R write head, tags opener and tail of record t, threads
+    // R..2R-1 the name and photoUrls opener of record t - R, the rest items
+    static_assert(!NESTED || 2 * R <= BT, "a head and a name unit per record in the first slot");
+    constexpr int NI = NESTED ? (2 * R + UCAP + GCAP + BT - 1) / BT : 1;
+    TagItem iv[NI];                                 // item column values (a url uses a, b)
+    uint32_t hidx = 0;                              // record thread: unit index of its head
+    const uint32_t nrec = (uint32_t)min((uint64_t)R, P.n - r0);
+    uint64_t len = 0, pre = 0, agg = 0;
     bool isbig = false;                             // fallback blocks: measured by the whole workgroup
     uint32_t nbig = 0, bidx = 0;
     if (fast) {
+        if constexpr (NESTED) {
+            // item column values first, so their loads overlap the staging
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const uint32_t q = t + (uint32_t)j * BT;
+                if (q < 2 * R) continue;
+                const uint32_t k = q - 2 * R;
+                if (k < U) {
+                    const UrlItem u = load_url(P, U0 + k);
+                    iv[j].a = u.a;
+                    iv[j].b = u.b;
+                } else if (k < U + G) iv[j] = load_tag(P, G0 + (k - U));
+            }
+        }
         // ---- phase 0: stage the input slices (4 loads in flight per thread)
         const uint32_t tot = off[4] >> 4;
         for (uint32_t j0 = t; j0 < tot; j0 += 4 * BT) {
@@ -813,46 +848,79 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 if (j < tot) reinterpret_cast<uint4 *>(inb)[j] = v[u];
             }
         }
+        if constexpr (NESTED) {
+            // record threads: unit indices, item owners, name unit inputs
+            // (sh_big / sh_bpre / sh_blen serve only hybrid blocks otherwise)
+            if (live) {
+                if (c.photo_off) { ul0 = (uint32_t)(rv.u0 - U0); ul1 = (uint32_t)(rv.u1 - U0); }
+                if (c.tag_off) { gl0 = (uint32_t)(rv.t0 - G0); gl1 = (uint32_t)(rv.t1 - G0); }
+                hidx = 4 * t + ul0 + gl0;
+                sh_big[t] = hidx;
+                sh_bpre[t] = (uint32_t)(rv.na - lo16[0]);
+                sh_blen[t] = (uint32_t)(rv.nb - rv.na);
+                rn_f[t] = (uint8_t)((rv.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (rv.u1 == rv.u0 ? 0x80u : 0u));
+                uon[t] = rec_has_urls(rv);
+                gon[t] = rec_has_tags<NESTED>(rv);
+                ubase[t] = hidx + 2 - ul0;
+                gbase[t] = hidx + 3 + (ul1 - ul0) - gl0;
+                uend[t] = (uint16_t)ul1;
+                gend[t] = (uint16_t)gl1;
+                for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
+                for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
+            }
+        }
         __syncthreads();
         EPROF(1);
-        // ---- phase 1: item lengths and their block scans
-        if (NESTED) {
-#pragma unroll
-            for (int j = 0; j < UI; j++) {
-                const uint32_t k = t + (uint32_t)j * BT;
-                if (k < U) {
-                    uv[j] = load_url(P, U0 + k);
-                    CountSink cs;
-                    emit_url_v(cs, P, XL, uv[j], false);
-                    su[k] = (uint32_t)cs.n;
-                }
+        if constexpr (NESTED) {
+            // ---- phase 1: unit lengths, then their scan
+            if (live) {
+                const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
+                CountSink ch, cm, ct;
+                rec_head<NESTED>(ch, P, XL, i, rv);
+                rec_tags_open<NESTED>(cm, P, rv);
+                rec_tail(ct, P, i, rv);
+                ulen[hidx] = (uint32_t)ch.n;
+                ulen[hidx + 2 + nu] = (uint32_t)cm.n;
+                ulen[hidx + 3 + nu + nt] = (uint32_t)ct.n;
+            }
+            if (t >= (uint32_t)R && t - R < nrec) {
+                const uint32_t r = t - R;
+                CountSink cs;
+                name_unit(cs, P, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                ulen[sh_big[r] + 1] = (uint32_t)cs.n;
             }
 #pragma unroll
-            for (int j = 0; j < GI; j++) {
-                const uint32_t k = t + (uint32_t)j * BT;
-                if (k < G) {
-                    gv[j] = load_tag(P, G0 + k);
-                    CountSink cs;
-                    emit_tag_v(cs, P, XL, gv[j], false);
-                    sg[k] = (uint32_t)cs.n;
+            for (int j = 0; j < NI; j++) {
+                const uint32_t q = t + (uint32_t)j * BT;
+                if (q < 2 * R) continue;
+                const uint32_t k = q - 2 * R;
+                CountSink cs;
+                if (k < U) {
+                    const uint32_t own = uown[k];
+                    if (uon[own]) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
+                    ulen[ubase[own] + k] = (uint32_t)cs.n;
+                } else if (k < U + G) {
+                    const uint32_t kk = k - (uint32_t)U, own = gown[kk];
+                    if (gon[own]) emit_tag_v(cs, P, XL, iv[j], false);
+                    ulen[gbase[own] + kk] = (uint32_t)cs.n;
                 }
             }
             __syncthreads();
-            lds_excl_scan<BT>(su, (uint32_t)U, sh_scan);
-            lds_excl_scan<BT>(sg, (uint32_t)G, sh_scan);
-        }
-        EPROF(2);
-        // ---- phase 2: record lengths
-        if (live) {
-            CountSink cs;
-            if (NESTED) {
-                if (c.photo_off) { ul0 = (uint32_t)(rv.u0 - U0); ul1 = (uint32_t)(rv.u1 - U0); }
-                if (c.tag_off) { gl0 = (uint32_t)(rv.t0 - G0); gl1 = (uint32_t)(rv.t1 - G0); }
-                ri.usz = su[ul1] - su[ul0];
-                ri.tsz = sg[gl1] - sg[gl0];
+            const uint32_t NU = 4 * nrec + (uint32_t)(U + G);
+            lds_excl_scan<BT>(ulen, NU, sh_scan);
+            agg = ulen[NU];
+            if (live) {
+                pre = ulen[hidx];
+                len = ulen[hidx + 4 + (ul1 - ul0) + (gl1 - gl0)] - pre;
             }
-            emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
-            len = cs.n;
+            EPROF(2);
+        } else {
+            // ---- phase 2: record lengths
+            if (live) {
+                CountSink cs;
+                emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
+                len = cs.n;
+            }
         }
     } else {
         // fallback block: records measured from global memory, one thread
@@ -879,8 +947,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         }
     }
     // ---- block scan, publish the aggregate
-    uint64_t agg;
-    const uint64_t pre = block_excl_scan<BT>(len, sh_scan, &agg);
+    if (!(NESTED && fast)) pre = block_excl_scan<BT>(len, sh_scan, &agg);
     if (t == 0) lb_publish(P.state, b, agg);
     const bool fits = fast && agg + 16 <= TILE;
     if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
@@ -910,46 +977,49 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
 
     if (fits && !P.count_only) {
         // ---- phase 3: build the tile
-        if (NESTED && live) {
-            // the bases wrap modulo 2^32 (any value is valid), so whether a
-            // record's items are written is kept apart from them
-            uon[t] = ri.ustart != NO_ITEMS;
-            gon[t] = ri.tstart != NO_ITEMS;
-            ubase[t] = (uint32_t)pre + ri.ustart - su[ul0];
-            gbase[t] = (uint32_t)pre + ri.tstart - sg[gl0];
-            uend[t] = (uint16_t)ul1;
-            gend[t] = (uint16_t)gl1;
-            for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
-            for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
-        }
-        __syncthreads();
-        if (live) {
+        if constexpr (NESTED) {
+            if (live) {
+                const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
+                LdsSink hs{tile, ulen[hidx]};
+                rec_head<NESTED>(hs, P, XL, i, rv);
+                hs.finish();
+                LdsSink ms{tile, ulen[hidx + 2 + nu]};
+                rec_tags_open<NESTED>(ms, P, rv);
+                ms.finish();
+                LdsSink ts{tile, ulen[hidx + 3 + nu + nt]};
+                rec_tail(ts, P, i, rv);
+                ts.finish();
+            }
+            if (t >= (uint32_t)R && t - R < nrec) {
+                const uint32_t r = t - R;
+                LdsSink ns{tile, ulen[sh_big[r] + 1]};
+                name_unit(ns, P, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                ns.finish();
+            }
+#pragma unroll
+            for (int j = 0; j < NI; j++) {
+                const uint32_t q = t + (uint32_t)j * BT;
+                if (q < 2 * R) continue;
+                const uint32_t k = q - 2 * R;
+                if (k < U) {
+                    const uint32_t own = uown[k];
+                    if (!uon[own]) continue;
+                    LdsSink ls{tile, ulen[ubase[own] + k]};
+                    emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, k + 1 == uend[own]);
+                    ls.finish();
+                } else if (k < U + G) {
+                    const uint32_t kk = k - (uint32_t)U, own = gown[kk];
+                    if (!gon[own]) continue;
+                    LdsSink ls{tile, ulen[gbase[own] + kk]};
+                    emit_tag_v(ls, P, XL, iv[j], kk + 1 == gend[own]);
+                    ls.finish();
+                }
+            }
+        } else if (live) {
             LdsSink ls{tile, (uint32_t)pre};
             RecItems r2 = ri;
             emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
             ls.finish();
-        }
-        if (NESTED) {
-#pragma unroll
-            for (int j = 0; j < UI; j++) {
-                const uint32_t k = t + (uint32_t)j * BT;
-                if (k >= U) continue;
-                const uint32_t own = uown[k];
-                if (!uon[own]) continue;
-                LdsSink ls{tile, ubase[own] + su[k]};
-                emit_url_v(ls, P, XL, uv[j], k + 1 == uend[own]);
-                ls.finish();
-            }
-#pragma unroll
-            for (int j = 0; j < GI; j++) {
-                const uint32_t k = t + (uint32_t)j * BT;
-                if (k >= G) continue;
-                const uint32_t own = gown[k];
-                if (!gon[own]) continue;
-                LdsSink ls{tile, gbase[own] + sg[k]};
-                emit_tag_v(ls, P, XL, gv[j], k + 1 == gend[own]);
-                ls.finish();
-            }
         }
     }
     EPROF(4);
@@ -963,6 +1033,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     }
     __syncthreads();
     if (P.count_only) return;
+    EPROF(5);
     const uint64_t base = sh_base;
     if (fits) {
         const uint64_t end = min(base + agg, P.cap);
