@@ -206,14 +206,17 @@ template <class S> __device__ __forceinline__ void esc_bytes(S &s, uint64_t x, i
     if (m > done) s.put8(x >> (8 * done), m - done);
 }
 __device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint32_t) {
-    uint64_t sp = special_mask(x) & (m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1));
-    uint32_t e = 0;
-    while (sp) {
-        const uint32_t c = (uint32_t)(x >> (__builtin_ctzll(sp) & ~7)) & 0xFF;
-        sp &= sp - 1;
-        e += (c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13) ? 1 : 5;
-    }
-    s.n += (uint64_t)(m + e);
+    constexpr uint64_t L7 = 0x7F7F7F7F7F7F7F7Full, H = 0x8080808080808080ull;
+    const uint64_t keep = m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1);
+    const uint64_t sp = special_mask(x) & keep & H;
+    // controls other than \b \t \n \f \r take six bytes, the rest two
+    const uint64_t lo = x & L7;
+    const uint64_t lt20 = ~((lo + 0x6060606060606060ull) | x) & H;
+    const uint64_t ge8 = (lo + 0x7878787878787878ull) & H, lt14 = ~(lo + 0x7272727272727272ull) & H;
+    const uint64_t y = x ^ 0x0B0B0B0B0B0B0B0Bull;
+    const uint64_t eq11 = ~(((y & L7) + L7) | y) & H;
+    const uint64_t lng = lt20 & ~(ge8 & lt14 & ~eq11) & keep;
+    s.n += (uint64_t)(m + __builtin_popcountll(sp) + 4 * __builtin_popcountll(lng));
 }
 
 // The string bytes of a staged slice, read as aligned LDS qwords joined by a
@@ -1105,6 +1108,24 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 #ifndef PJ_ENC_NEST_R
 #define PJ_ENC_NEST_R 96
 #endif
+#ifndef PJ_ENC_NEST_BT
+#define PJ_ENC_NEST_BT 256
+#endif
+#ifndef PJ_ENC_NEST_TILE
+#define PJ_ENC_NEST_TILE (30 * 1024 + 512)
+#endif
+#ifndef PJ_ENC_NEST_IN
+#define PJ_ENC_NEST_IN (14 * 1024)
+#endif
+#ifndef PJ_ENC_NEST_UCAP
+#define PJ_ENC_NEST_UCAP 320
+#endif
+#ifndef PJ_ENC_NEST_GCAP
+#define PJ_ENC_NEST_GCAP 256
+#endif
+#ifndef PJ_ENC_NEST_WPE
+#define PJ_ENC_NEST_WPE 1
+#endif
 // Workgroup shapes: threads, records, LDS tile bytes, item capacities.
 // Flat blocks of 256 records in two shapes: compact (tile 96 B and staged
 // names 24 B per record, 30.6 KB of LDS, five waves per SIMD) for records up
@@ -1113,8 +1134,9 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 constexpr int ENC_FLAT_BT = 256, ENC_FLAT_R = 256;
 constexpr int ENC_FLAT_TILE = ENC_FLAT_R * 96, ENC_FLAT_IN = ENC_FLAT_R * 24, ENC_FLAT_WPE = 5;
 constexpr int ENC_WIDE_TILE = ENC_FLAT_R * 112, ENC_WIDE_IN = ENC_FLAT_R * 32;
-constexpr int ENC_NEST_BT = 256, ENC_NEST_R = PJ_ENC_NEST_R, ENC_NEST_TILE = 30 * 1024 + 512, ENC_NEST_IN = 14 * 1024,
-              ENC_NEST_UCAP = 320, ENC_NEST_GCAP = 256;
+constexpr int ENC_NEST_BT = PJ_ENC_NEST_BT, ENC_NEST_R = PJ_ENC_NEST_R, ENC_NEST_TILE = PJ_ENC_NEST_TILE,
+              ENC_NEST_IN = PJ_ENC_NEST_IN, ENC_NEST_UCAP = PJ_ENC_NEST_UCAP, ENC_NEST_GCAP = PJ_ENC_NEST_GCAP,
+              ENC_NEST_WPE = PJ_ENC_NEST_WPE;
 
 int pj_encode_block_records(bool nested) { return nested ? ENC_NEST_R : ENC_FLAT_R; }
 
@@ -1122,7 +1144,7 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
     if (nested) {
         uint64_t g = (P.n + ENC_NEST_R - 1) / ENC_NEST_R;
         hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
-                                         ENC_NEST_GCAP>),
+                                         ENC_NEST_GCAP, ENC_NEST_WPE>),
                            dim3((unsigned)g), dim3(ENC_NEST_BT), 0, st, P);
     } else {
         uint64_t g = (P.n + ENC_FLAT_R - 1) / ENC_FLAT_R;
