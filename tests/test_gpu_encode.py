@@ -88,6 +88,30 @@ def test_encode_empty_and_single(codec):
     assert gpu_encode(codec, cols, pj.FORMAT_ARRAY) == orc.encode(cols, pj.FORMAT_ARRAY)
 
 
+GROUPS = {"category": ("cat_id", "cat_flags", "cat_name_off", "cat_name_bytes"),
+          "photoUrls": ("photo_off", "url_off", "url_bytes"),
+          "tags": ("tag_off", "tag_id", "tag_flags", "tag_name_off", "tag_name_bytes")}
+
+
+@pytest.mark.parametrize("absent", [("category",), ("photoUrls",), ("tags",), ("photoUrls", "tags"),
+                                    ("category", "tags"), ("category", "photoUrls")])
+@pytest.mark.parametrize("incl", [pj.INCLUDE_NON_EMPTY, pj.INCLUDE_ALWAYS])
+def test_encode_absent_groups_match_oracle(codec, absent, incl):
+    """Nested records with whole column groups absent (NULL pointers): the
+    records still go through the nested kernel, with empty lists or no
+    category for every record."""
+    cols = pj.generate(3, 5_000)
+    for g in absent:
+        for k in GROUPS[g]:
+            cols.arrays[k] = None
+    flags = cols["flags"].copy()
+    if "category" in absent:
+        flags &= ~np.uint8(pj.PET_HAS_CATEGORY)
+    cols.arrays["flags"] = flags
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        assert gpu_encode(codec, cols, fmt, incl) == orc.encode(cols, fmt, incl), (absent, fmt)
+
+
 def test_encode_capacity_guard(codec):
     cols = pj.generate(2, 10_000)
     d = cols.to_device()
