@@ -44,8 +44,12 @@ struct CountSink {
 struct LdsSinkU {
     uint8_t *t;
     uint32_t o;
+    uint32_t e = 0;           // end of this writer's bytes (0: unknown)
     __device__ __forceinline__ void put8(uint64_t x, int k) {
         uint8_t *q = t + o;
+        // with 8 bytes of its own ahead, a writer stores all 8: the bytes
+        // past k are its own and its next puts write them again
+        if (o + 8 <= e) { *reinterpret_cast<uint64_t *>(q) = x; o += (uint32_t)k; return; }
         o += (uint32_t)k;
         if (k & 8) { *reinterpret_cast<uint64_t *>(q) = x; return; }
         if (k & 4) { *reinterpret_cast<uint32_t *>(q) = (uint32_t)x; q += 4; x >>= 32; }
@@ -983,19 +987,19 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         if constexpr (NESTED) {
             if (live) {
                 const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
-                LdsSink hs{tile, ulen[hidx]};
+                LdsSink hs{tile, ulen[hidx], ulen[hidx + 1]};
                 rec_head<NESTED>(hs, P, XL, i, rv);
                 hs.finish();
-                LdsSink ms{tile, ulen[hidx + 2 + nu]};
+                LdsSink ms{tile, ulen[hidx + 2 + nu], ulen[hidx + 3 + nu]};
                 rec_tags_open<NESTED>(ms, P, rv);
                 ms.finish();
-                LdsSink ts{tile, ulen[hidx + 3 + nu + nt]};
+                LdsSink ts{tile, ulen[hidx + 3 + nu + nt], ulen[hidx + 4 + nu + nt]};
                 rec_tail(ts, P, i, rv);
                 ts.finish();
             }
             if (t >= (uint32_t)R && t - R < nrec) {
                 const uint32_t r = t - R;
-                LdsSink ns{tile, ulen[sh_big[r] + 1]};
+                LdsSink ns{tile, ulen[sh_big[r] + 1], ulen[sh_big[r] + 2]};
                 name_unit(ns, P, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
                 ns.finish();
             }
@@ -1007,13 +1011,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 if (k < U) {
                     const uint32_t own = uown[k];
                     if (!uon[own]) continue;
-                    LdsSink ls{tile, ulen[ubase[own] + k]};
+                    LdsSink ls{tile, ulen[ubase[own] + k], ulen[ubase[own] + k + 1]};
                     emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, k + 1 == uend[own]);
                     ls.finish();
                 } else if (k < U + G) {
                     const uint32_t kk = k - (uint32_t)U, own = gown[kk];
                     if (!gon[own]) continue;
-                    LdsSink ls{tile, ulen[gbase[own] + kk]};
+                    LdsSink ls{tile, ulen[gbase[own] + kk], ulen[gbase[own] + kk + 1]};
                     emit_tag_v(ls, P, XL, iv[j], kk + 1 == gend[own]);
                     ls.finish();
                 }
