@@ -2,16 +2,20 @@
 //
 // A workgroup owns R consecutive records, hence a contiguous range of their
 // photoUrls and tags.  Phases (one kernel, one pass over the columns):
-//   1. item lengths: every url / tag item (`"url",` or `{...},`) is measured
-//      item-parallel by all BT threads, and block-scanned into LDS, so the
-//      Poisson-sized lists cost no divergence;
-//   2. record lengths: one thread per record measures its skeleton (integer
-//      digit counts, escape expansion of name / category, list sizes from
-//      the item scans); block scan -> record offsets in the tile; the block
-//      aggregate is published for the decoupled look-back right away;
-//   3. build the block's output tile in LDS: record threads write skeletons,
-//      all threads write the url / tag items, all with exact unaligned
-//      ds_write_b8..b64 (gfx950 runs LDS in unaligned mode);
+//   0. staging: the block's slice of every string column goes into LDS with
+//      16-byte loads; record and item column values go into registers;
+//   1. units (nested): every record is cut into units in output order --
+//      head (separator, id, category, name key), name (+ photoUrls opener),
+//      url items, tags opener, tag items, tail -- held by different threads
+//      (heads on threads 0..R-1, names on R..2R-1, items after), so one
+//      thread no longer writes a whole record and its wave runs one kind;
+//   2. lengths: every unit (flat: every record) is measured by its emitting
+//      code with a counting sink (digit counts, SWAR escape counts); an LDS
+//      scan gives each unit its tile offset; the block aggregate is
+//      published for the decoupled look-back right away;
+//   3. build the block's output tile in LDS (nested: exact unaligned
+//      ds_write_b8..b64, gfx950 runs LDS in unaligned mode; flat: aligned
+//      qwords, shared edges merged with an LDS OR);
 //   4. resolve the look-back (its latency hidden behind phase 3) and copy the
 //      tile to HBM with aligned 16-byte stores, so every cache line leaves
 //      the chip whole.
@@ -748,7 +752,9 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4], sh_len;
     __shared__ uint32_t sh_nbig;
     // hybrid blocks (NESTED): the large records in record order, with their
-    // block offsets, lengths and tile offsets
+    // block offsets, lengths and tile offsets; fast blocks keep each record's
+    // head unit index, name offset in the staged slice and name length in
+    // the first three
     constexpr int RB = NESTED ? R : 1;
     __shared__ uint32_t sh_big[RB], sh_bpre[RB], sh_blen[RB], sh_bspre[RB];
     static_assert(3 * R * 4 <= TILE, "the fallback path keeps its large-record list in the tile");
