@@ -291,7 +291,37 @@ constexpr uint32_t NO_ITEMS = 0xFFFFFFFFu;  // list not written (null / omitted)
 struct ColSrc {
     const uint8_t *name, *cat, *url, *tag;
     uint64_t nb, cb, ub, tb;
+    // staged slices only: bit c of plain[c / 64] is set when 16-byte chunk c
+    // of the staging buffer (from sbase) holds a byte that needs an escape
+    const uint64_t *plain = nullptr;
+    const uint8_t *sbase = nullptr;
 };
+
+// Whether staged bytes [p, p + len) need no escape: every 16-byte chunk they
+// touch is clear in the chunk bitmap (a set chunk may belong to a neighbour).
+__device__ __forceinline__ bool staged_plain(const ColSrc &X, const uint8_t *p, uint64_t len) {
+    if (!X.plain || len == 0) return X.plain != nullptr;
+    const uint32_t a = (uint32_t)(p - X.sbase), c0 = a >> 4, c1 = (a + (uint32_t)len - 1) >> 4;
+    for (uint32_t w = c0 >> 6; w <= (c1 >> 6); w++) {
+        uint64_t m = X.plain[w];
+        if (w == (c0 >> 6)) m &= ~0ull << (c0 & 63);
+        if (w == (c1 >> 6) && (c1 & 63) != 63) m &= (2ull << (c1 & 63)) - 1;
+        if (m) return false;
+    }
+    return true;
+}
+
+// A JSON string from a column source.  Measuring a staged string that
+// needs no escape takes O(1); writing always goes through emit_str (a
+// separate copy path for such strings measured slower there).
+template <class S>
+__device__ __forceinline__ void emit_strx(S &s, const ColSrc &, const uint8_t *p, uint64_t len, uint32_t hexa) {
+    emit_str(s, p, len, hexa);
+}
+__device__ __forceinline__ void emit_strx(CountSink &s, const ColSrc &X, const uint8_t *p, uint64_t len, uint32_t hexa) {
+    if (staged_plain(X, p, len)) s.n += len + 2;
+    else emit_str(s, p, len, hexa);
+}
 
 // One record's scalar fields, loaded once and kept in registers across the
 // measuring and writing passes.
@@ -337,7 +367,7 @@ template <class S> __device__ __forceinline__ void key(S &s, bool &first) {
 }
 
 template <class S>
-__device__ __forceinline__ void emit_sub(S &s, const EncParams &P, uint32_t fl, int64_t id,
+__device__ __forceinline__ void emit_sub(S &s, const EncParams &P, const ColSrc &X, uint32_t fl, int64_t id,
                                          const uint8_t *nm, uint64_t nlen) {
     bool first = true;
     s.put_byte('{');
@@ -345,7 +375,7 @@ __device__ __forceinline__ void emit_sub(S &s, const EncParams &P, uint32_t fl, 
     else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
     if (fl & PJ_SUB_HAS_NAME) {
         if (nlen > 0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
-            key(s, first); lit(s, "\"name\":"); emit_str(s, nm, nlen, P.hexa);
+            key(s, first); lit(s, "\"name\":"); emit_strx(s, X, nm, nlen, P.hexa);
         }
     } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"name\":null"); }
     s.put_byte('}');
@@ -373,7 +403,7 @@ __device__ __forceinline__ TagItem load_tag(const EncParams &P, uint64_t g) {
 // url item: `"url"` + (',' or ']' after the record's last url)
 template <class S>
 __device__ __forceinline__ void emit_url_v(S &s, const EncParams &P, const ColSrc &X, const UrlItem &v, bool last) {
-    emit_str(s, X.url + (v.a - X.ub), v.b - v.a, P.hexa);
+    emit_strx(s, X, X.url + (v.a - X.ub), v.b - v.a, P.hexa);
     s.put_byte(last ? ']' : ',');
 }
 template <class S>
@@ -384,7 +414,7 @@ __device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, const Co
 // tag item: `{...}` + (',' or ']')
 template <class S>
 __device__ __forceinline__ void emit_tag_v(S &s, const EncParams &P, const ColSrc &X, const TagItem &v, bool last) {
-    emit_sub(s, P, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
+    emit_sub(s, P, X, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
     s.put_byte(last ? ']' : ',');
 }
 template <class S>
@@ -408,7 +438,7 @@ __device__ __forceinline__ void rec_head(S &s, const EncParams &P, const ColSrc 
     else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
     if (NESTED && (fl & PJ_PET_HAS_CATEGORY) && c.cat_id) {
         key(s, first); lit(s, "\"category\":");
-        emit_sub(s, P, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
+        emit_sub(s, P, X, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
     } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"category\":null"); }
     key(s, first);
     if (fl & PJ_PET_HAS_NAME) lit(s, "\"name\":");
@@ -453,8 +483,9 @@ template <bool NESTED> __device__ __forceinline__ bool rec_has_tags(const RecVal
 // The name unit of a record: the name string, then the photoUrls opener.
 // f: the record's HAS_NAME and HAS_PHOTOURLS bits, 0x80 when it has no urls.
 template <class S>
-__device__ __forceinline__ void name_unit(S &s, const EncParams &P, const uint8_t *nm, uint32_t nl, uint32_t f) {
-    if (f & PJ_PET_HAS_NAME) emit_str(s, nm, nl, P.hexa);
+__device__ __forceinline__ void name_unit(S &s, const EncParams &P, const ColSrc &X, const uint8_t *nm, uint32_t nl,
+                                          uint32_t f) {
+    if (f & PJ_PET_HAS_NAME) emit_strx(s, X, nm, nl, P.hexa);
     rec_urls_open(s, f, (f & 0x80u) != 0);
 }
 
@@ -465,7 +496,7 @@ template <bool NESTED, bool INLINE, class S>
 __device__ __forceinline__ void emit_rec(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v,
                                          RecItems &ri) {
     rec_head<NESTED>(s, P, X, i, v);
-    if (v.fl & PJ_PET_HAS_NAME) emit_str(s, X.name + (v.na - X.nb), v.nb - v.na, P.hexa);
+    if (v.fl & PJ_PET_HAS_NAME) emit_strx(s, X, X.name + (v.na - X.nb), v.nb - v.na, P.hexa);
     rec_urls_open(s, v);
     if (rec_has_urls(v)) {
         if (INLINE) {
@@ -749,6 +780,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
     __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
     __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint64_t splain[(INCAP / 16 + 63) / 64];  // staged 16-byte chunks that hold a byte to escape
     __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4], sh_len;
     __shared__ uint32_t sh_nbig;
     // hybrid blocks (NESTED): the large records in record order, with their
@@ -806,7 +838,8 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     }
     const bool fast = off[4] <= INCAP && (!NESTED || (U <= UCAP && G <= GCAP));
     const ColSrc XG{c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes, 0, 0, 0, 0};
-    const ColSrc XL{inb + off[0], inb + off[1], inb + off[2], inb + off[3], lo16[0], lo16[1], lo16[2], lo16[3]};
+    const ColSrc XL{inb + off[0], inb + off[1], inb + off[2], inb + off[3], lo16[0], lo16[1], lo16[2], lo16[3],
+                    splain, inb};
     const uint8_t *srcs[4] = {c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes};
 
     RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
@@ -859,6 +892,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             for (int u = 0; u < 4; u++) {
                 const uint32_t j = j0 + u * BT;
                 if (j < tot) reinterpret_cast<uint4 *>(inb)[j] = v[u];
+                // a wave holds 64 consecutive chunks: one ballot per bitmap word
+                const bool esc = j < tot && (special64(((uint64_t)v[u].y << 32) | v[u].x) |
+                                             special64(((uint64_t)v[u].w << 32) | v[u].z)) != 0;
+                const uint64_t m = __ballot(esc);
+                if ((t & 63) == 0 && j < tot) splain[j >> 6] = m;
             }
         }
         if constexpr (NESTED) {
@@ -899,7 +937,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             if (t >= (uint32_t)R && t - R < nrec) {
                 const uint32_t r = t - R;
                 CountSink cs;
-                name_unit(cs, P, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
                 ulen[sh_big[r] + 1] = (uint32_t)cs.n;
             }
 #pragma unroll
@@ -1006,7 +1044,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             if (t >= (uint32_t)R && t - R < nrec) {
                 const uint32_t r = t - R;
                 LdsSink ns{tile, ulen[sh_big[r] + 1], ulen[sh_big[r] + 2]};
-                name_unit(ns, P, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
                 ns.finish();
             }
 #pragma unroll
@@ -1122,7 +1160,7 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 #define PJ_ENC_NEST_BT 256
 #endif
 #ifndef PJ_ENC_NEST_TILE
-#define PJ_ENC_NEST_TILE (30 * 1024 + 512)
+#define PJ_ENC_NEST_TILE (30 * 1024 + 256)
 #endif
 #ifndef PJ_ENC_NEST_IN
 #define PJ_ENC_NEST_IN (14 * 1024)
@@ -1137,6 +1175,9 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 #define PJ_ENC_NEST_WPE 1
 #endif
 // Workgroup shapes: threads, records, LDS tile bytes, item capacities.
+// The nested shape must stay at or below about 53.7 KB of LDS per
+// workgroup (measured: 53,696 bytes still gives three workgroups per CU,
+// 53,808 gives two, which cost 45%).
 // Flat blocks of 256 records in two shapes: compact (tile 96 B and staged
 // names 24 B per record, 30.6 KB of LDS, five waves per SIMD) for records up
 // to about 90 bytes, wide (112 B / 32 B, four waves per SIMD) once the
