@@ -62,6 +62,7 @@ def encode_workload(codec, config, n, steps, warmup):
         "output_bytes": out_bytes, "input_bytes": in_bytes,
         "output_GBps": out_bytes / wall / 1e9, "output_frac_hbm": out_bytes / wall / 1e9 / HBM_PEAK_GBPS,
         "kernel_ms": kms, "kernel_alg_GBps": alg / (kms * 1e-3) / 1e9,
+        "kernel_alg_frac_hbm": alg / (kms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
     }
     return cols, res
 
@@ -111,7 +112,8 @@ def decode_workload(codec, n, steps, warmup):
          "lines_general_parser": int(res.n_general),
          "kernels": {"k_dec_lines_ms": kidx, "k_dec_block_ms": kpar, "k_dec_errcode_ms": kerr,
                      "k_dec_lines_GBps": in_bytes / (kidx * 1e-3) / 1e9,
-                     "k_dec_block_alg_GBps": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9}}
+                     "k_dec_block_alg_GBps": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9,
+                     "k_dec_block_alg_frac_hbm": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9 / HBM_PEAK_GBPS}}
     return r
 
 
@@ -158,7 +160,8 @@ def skew_workload(codec, n, steps, warmup, with_decode):
     out_bytes, wall, kms, out = run_encode(codec, dev, pj.FORMAT_NDJSON, steps, warmup)
     r = {"records": n, "records_per_s": n / wall, "ms_per_step": wall * 1e3, "input_bytes": in_bytes,
          "output_bytes": out_bytes, "kernel_ms": kms,
-         "kernel_alg_GBps": (in_bytes + out_bytes) / (kms * 1e-3) / 1e9}
+         "kernel_alg_GBps": (in_bytes + out_bytes) / (kms * 1e-3) / 1e9,
+         "kernel_alg_frac_hbm": (in_bytes + out_bytes) / (kms * 1e-3) / 1e9 / HBM_PEAK_GBPS}
     if with_decode:
         text = out[:out_bytes]
         res = None
