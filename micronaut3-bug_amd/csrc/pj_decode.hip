@@ -1948,22 +1948,22 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //   * block scans plus a vector look-back over 8 counters give the rows /
 //     byte offsets, and a second walk over the sub-tiles (reloaded only when
 //     there were several) writes the columns.
-template <int BT, int TILE, int LONG>
+template <int BT, int TILE, int LONG, int LPB = BT>
 __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t spec[TILE / 64 + 1];
     __shared__ uint64_t badm[TILE / 64 + 1];
     __shared__ uint64_t sh_scan[BT / 64];
-    __shared__ uint64_t sh_ls[BT + 1];              // the block's line starts, then its end
-    __shared__ uint16_t sh_sub[BT + 1];             // sub-tile boundaries (block-local line indices)
+    __shared__ uint64_t sh_ls[LPB + 1];             // the block's line starts, then its end
+    __shared__ uint16_t sh_sub[LPB + 1];            // sub-tile boundaries (block-local line indices)
     __shared__ uint32_t sh_nsub;
     __shared__ uint64_t sh_blk, sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
     if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[1], 1ull);
     __syncthreads();
     const uint64_t b = sh_blk;
-    const uint64_t l0 = b * BT;
-    const uint32_t cnt = (uint32_t)min((uint64_t)BT, P.lines - l0);
+    const uint64_t l0 = b * LPB;
+    const uint32_t cnt = (uint32_t)min((uint64_t)LPB, P.lines - l0);
     const uint64_t l = l0 + t;
     const bool live = t < cnt;
     if (t < cnt) sh_ls[t] = P.line_start[l0 + t];
@@ -2192,7 +2192,7 @@ __global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
 #define PJ_DEC_LINE_BT 128
 #endif
 #ifndef PJ_DEC_TILE_KB
-#define PJ_DEC_TILE_KB 40
+#define PJ_DEC_TILE_KB 31
 #endif
 #ifndef PJ_DEC_LONG
 #define PJ_DEC_LONG 1024
@@ -2201,7 +2201,11 @@ constexpr int DEC_LONG = PJ_DEC_LONG;
 constexpr int DEC_IDX_BT = 256, DEC_IDX_R = 4, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
 
 int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
-int pj_dec_parse_block() { return DEC_LINE_BT; }
+#ifndef PJ_DEC_LPB
+#define PJ_DEC_LPB 104
+#endif
+constexpr int DEC_LPB = PJ_DEC_LPB;
+int pj_dec_parse_block() { return DEC_LPB; }
 
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.nblk64 + DEC_IDX_BT * DEC_IDX_R - 1) / (DEC_IDX_BT * DEC_IDX_R);
@@ -2215,7 +2219,8 @@ hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
 }
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
-    const uint64_t g = (P.lines + DEC_LINE_BT - 1) / DEC_LINE_BT;
-    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st, P);
+    const uint64_t g = (P.lines + DEC_LPB - 1) / DEC_LPB;
+    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st,
+                       P);
     return hipGetLastError();
 }
