@@ -67,6 +67,7 @@ struct pj_ctx {
     DevBuf index;       // decode: special bitmap, bad flags, line starts
     DevBuf stage_in;    // host path: input staging
     DevBuf stage_out;   // host path: output staging
+    DevBuf tape;        // decode: per-line results of the validating walk
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
@@ -121,6 +122,13 @@ pj_status check_enc_cols(const pj_pet_columns *c) {
 // Look-back wait bound for launch-ordered blocks: 200 ms of the 100 MHz wall
 // clock, or PETJSON_SPIN_LIMIT_TICKS (tests force the redo path with a tiny
 // bound).
+// Whether the decode keeps a line tape (PETJSON_DECODE_TAPE=0 turns it off;
+// tests cover both paths).
+bool decode_tape_enabled() {
+    const char *e = std::getenv("PETJSON_DECODE_TAPE");
+    return !e || std::strtoull(e, nullptr, 10) != 0;
+}
+
 uint64_t spin_limit() {
     if (const char *e = std::getenv("PETJSON_SPIN_LIMIT_TICKS")) {
         const unsigned long long v = std::strtoull(e, nullptr, 10);
@@ -467,6 +475,13 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.state_parse = static_cast<uint64_t *>(ctx->scan.p);
         P.dq = P.state_parse + gp * VLB_WORDS;
         P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
+        // the line tape (192 bytes per line), when it fits a modest bound;
+        // without it the writer walks each line again
+        P.tape = nullptr;
+        if (lines && decode_tape_enabled() && lines * 192 <= (16ull << 30) &&
+            ctx->tape.ensure(lines * 192) == hipSuccess)
+            P.tape = static_cast<uint64_t *>(ctx->tape.p);
+        (void)hipGetLastError();
         P.order_by_id = 1;
         for (;;) {
             if ((s = mark(ctx))) return s;

@@ -825,6 +825,7 @@ __device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
 // missing required property) are the first error of the line, exactly as
 // run_line reports them.
 constexpr int PJ_BAIL = -1;
+constexpr int PJ_TAPE_FULL = -2;  // valid so far, more items than the line tape holds: read by the wave
 
 // bit k set iff byte k of x equals c
 __device__ __forceinline__ uint32_t eq_mask8(uint64_t x, uint32_t c) {
@@ -1510,8 +1511,31 @@ __device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
 // subset of properties their lines hold.
 // Pass 0 (WRITE false) validates and measures into R; pass 1 writes the
 // record at the line's offsets rel[] inside the block's column slices W.
-template <bool WRITE, class FL>
-__device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W, const uint32_t *rel) {
+// ---------------------------------------------------------------- line tape
+// The validating walk of a canonical line records what the writing walk
+// needs, so that the writer stores and copies without parsing again:
+//   word 0 id, word 1 category id,
+//   word 2 flags | status << 8 | category flags << 16 | urls << 24 |
+//          tags << 32, bit 63 set when the record is complete,
+//   word 3 the name string, word 4 the category name string,
+//   words 5.. one word per url, then two per tag (id, name string).
+// A string word holds line-relative start, closing quote and decoded length
+// (16 bits each), bit 48 "has escapes" and, for a tag, its flags in bits
+// 49-50.  A line with more items than the words left (PJ_TAPE_FULL) is read
+// by its wave instead, like a long line.
+#ifndef PJ_TAPE_WORDS
+#define PJ_TAPE_WORDS 24
+#endif
+constexpr int TAPE_WORDS = PJ_TAPE_WORDS;
+constexpr uint64_t TAPE_OK = 1ull << 63;
+__device__ __forceinline__ uint64_t tape_str(uint32_t q, const Str &r) {
+    return (uint64_t)q | ((uint64_t)r.end << 16) | ((uint64_t)r.dlen << 32) | ((uint64_t)r.esc << 48);
+}
+
+template <bool WRITE, class FL, bool TAPE = false>
+__device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W, const uint32_t *rel,
+                                     uint64_t *T = nullptr) {
+    constexpr bool VAL = WRITE || TAPE;             // integer values are needed
     const uint32_t n = F.n;
     if (n == 0) return PJ_REC_EMPTY;
     if (F.at(0) != '{') return PJ_BAIL;
@@ -1526,7 +1550,7 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
     // id
     if (more && (k8 & KP_ID_MASK) == KP_ID) {
         p += 5;
-        const int e = fnum<WRITE>(F, p, id);
+        const int e = fnum<VAL>(F, p, id);
         if (e) return e;
         flags |= PJ_PET_HAS_ID;
         FL_SEP();
@@ -1537,10 +1561,11 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
         p += 12;
         uint32_t nq = 0;
         Str nr{0, 0, 0, false};
-        const int e = fsub<WRITE>(F, p, cat_id, cat_fl, nq, nr);
+        const int e = fsub<VAL>(F, p, cat_id, cat_fl, nq, nr);
         if (e) return e;
         flags |= PJ_PET_HAS_CATEGORY;
         cat_len = (cat_fl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
+        if (TAPE && (cat_fl & PJ_SUB_HAS_NAME)) T[4] = tape_str(nq, nr);
         if (WRITE && cat_len) F.copy(nq, nr, W->cat_name + rel[C_CATB]);
         FL_SEP();
     }
@@ -1553,6 +1578,7 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
         p = r.end + 1;
         flags |= PJ_PET_HAS_NAME;
         name_len = r.dlen;
+        if (TAPE) T[3] = tape_str(q, r);
         if (WRITE && r.dlen) F.copy(q, r, W->name + rel[C_NAMEB]);
         FL_SEP();
     }
@@ -1572,6 +1598,8 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
                 p = r.end + 1;
                 n_urls++;
                 url_bytes += r.dlen;
+                // url k at word 5 + k (n_urls counts it already)
+                if (TAPE && n_urls <= TAPE_WORDS - 5) T[4 + n_urls] = tape_str(q, r);
                 if (WRITE) {
                     if (r.dlen) F.copy(q, r, W->url + ub);
                     ub += r.dlen;
@@ -1603,11 +1631,16 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
                 int64_t tid;
                 uint32_t tfl, nq = 0;
                 Str nr{0, 0, 0, false};
-                const int e = fsub<WRITE>(F, p, tid, tfl, nq, nr);
+                const int e = fsub<VAL>(F, p, tid, tfl, nq, nr);
                 if (e) return e;
                 const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? nr.dlen : 0;
                 n_tags++;
                 tag_bytes += tl;
+                // tag k at words 5 + urls + 2k, + 1 (n_tags counts it already)
+                if (TAPE && n_urls + 2 * n_tags <= TAPE_WORDS - 5) {
+                    T[3 + n_urls + 2 * n_tags] = (uint64_t)tid;
+                    T[4 + n_urls + 2 * n_tags] = (tl ? tape_str(nq, nr) : 0) | ((uint64_t)(tfl & 3) << 49);
+                }
                 if (WRITE) {
                     if (F.lead()) {
                         W->tag_id[g] = tid;
@@ -1648,6 +1681,13 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
     if (!WRITE) {
         R.name_len = name_len; R.cat_len = cat_len; R.n_urls = n_urls; R.url_bytes = url_bytes;
         R.n_tags = n_tags; R.tag_bytes = tag_bytes;
+        if (TAPE) {
+            if (n_urls + 2 * n_tags > TAPE_WORDS - 5) return PJ_TAPE_FULL;
+            T[0] = (uint64_t)id;
+            T[1] = (uint64_t)cat_id;
+            T[2] = (uint64_t)flags | ((uint64_t)status << 8) | ((uint64_t)cat_fl << 16) | ((uint64_t)n_urls << 24) |
+                   ((uint64_t)n_tags << 32) | TAPE_OK;
+        }
     } else if (F.lead()) {
         const uint32_t row = rel[C_PETS];
         W->id[row] = id;
@@ -1664,6 +1704,62 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
 }
 #undef FL_SEP
 #undef FL_UNKNOWN
+
+// Writing a line from its tape: the stores and copies of fline<true>, in the
+// same order, without walking the line again.
+__device__ __forceinline__ void tape_write(const FLine &F, const uint64_t *T, const BlockCols *W, const uint32_t *rel) {
+    const uint64_t M = T[2];
+    const uint32_t flags = (uint32_t)M & 0xFF, status = (uint32_t)(M >> 8) & 0xFF, cat_fl = (uint32_t)(M >> 16) & 0xFF;
+    const uint32_t nu = (uint32_t)(M >> 24) & 0xFF, nt = (uint32_t)(M >> 32) & 0xFF;
+    uint32_t cat_len = 0, name_len = 0;
+    if ((flags & PJ_PET_HAS_CATEGORY) && (cat_fl & PJ_SUB_HAS_NAME)) {
+        const uint64_t w = T[4];
+        cat_len = (uint32_t)(w >> 32) & 0xFFFF;
+        if (cat_len) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, cat_len, ((w >> 48) & 1) != 0},
+                            W->cat_name + rel[C_CATB]);
+    }
+    if (flags & PJ_PET_HAS_NAME) {
+        const uint64_t w = T[3];
+        name_len = (uint32_t)(w >> 32) & 0xFFFF;
+        if (name_len) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, name_len, ((w >> 48) & 1) != 0},
+                             W->name + rel[C_NAMEB]);
+    }
+    uint32_t tw = 5;
+    uint32_t u = rel[C_URLS], ub = rel[C_URLB];
+    for (uint32_t k = 0; k < nu; k++) {
+        const uint64_t w = T[tw++];
+        const uint32_t dl = (uint32_t)(w >> 32) & 0xFFFF;
+        if (dl) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, dl, ((w >> 48) & 1) != 0}, W->url + ub);
+        ub += dl;
+        W->url_off[u] = W->b_url + ub;
+        u++;
+    }
+    uint32_t g = rel[C_TAGS], gb = rel[C_TAGB];
+    for (uint32_t k = 0; k < nt; k++) {
+        const int64_t tid = (int64_t)T[tw];
+        const uint64_t w = T[tw + 1];
+        tw += 2;
+        const uint32_t tfl = (uint32_t)(w >> 49) & 3;
+        const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? (uint32_t)(w >> 32) & 0xFFFF : 0;
+        W->tag_id[g] = tid;
+        W->tag_flags[g] = (uint8_t)tfl;
+        W->tag_name_off[g] = W->b_tag + gb + tl;
+        if (tl) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, tl, ((w >> 48) & 1) != 0},
+                       W->tag_name + gb);
+        gb += tl;
+        g++;
+    }
+    const uint32_t row = rel[C_PETS];
+    W->id[row] = (int64_t)T[0];
+    W->flags[row] = (uint8_t)flags;
+    W->status[row] = (uint8_t)status;
+    W->cat_id[row] = (int64_t)T[1];
+    W->cat_flags[row] = (uint8_t)cat_fl;
+    W->name_off[row] = W->b_name + rel[C_NAMEB] + name_len;
+    W->cat_name_off[row] = W->b_cat + rel[C_CATB] + cat_len;
+    W->photo_off[row] = W->b_urls + rel[C_URLS] + nu;
+    W->tag_off[row] = W->b_tags + rel[C_TAGS] + nt;
+}
 
 // The wave-cooperative reading of one long line, out of line so that its
 // registers do not add to those of the per-thread path.
@@ -1948,7 +2044,7 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //   * block scans plus a vector look-back over 8 counters give the rows /
 //     byte offsets, and a second walk over the sub-tiles (reloaded only when
 //     there were several) writes the columns.
-template <int BT, int TILE, int LONG, int LPB = BT>
+template <int BT, int TILE, int LONG, int LPB = BT, bool TAPE = false>
 __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t spec[TILE / 64 + 1];
@@ -1992,7 +2088,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         gs = sh_ls[t];
         n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
     }
-    const bool longl = n > (uint32_t)LONG;
+    bool longl = n > (uint32_t)LONG;               // read by the owning wave (also: tape full)
     // ---- pass 0: validate and measure, sub-tile by sub-tile
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
@@ -2019,7 +2115,12 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 if (bad) code = PJ_REC_STRING;      // provisional: k_dec_errcode settles it
                 else if (!longl) {
                     const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
-                    code = fline<false>(F, r, nullptr, nullptr);
+                    if constexpr (TAPE) code = fline<false, FLine, true>(F, r, nullptr, nullptr, P.tape + l * TAPE_WORDS);
+                    else code = fline<false>(F, r, nullptr, nullptr);
+                    if (TAPE && code == PJ_TAPE_FULL) {
+                        longl = true;
+                        code = 0;
+                    }
                     need_gen = code == PJ_BAIL;
                 }
             }
@@ -2139,7 +2240,8 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = pos[k];
                 const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
-                fline<true>(F, r, &W, rel);
+                if constexpr (TAPE) tape_write(F, P.tape + l * TAPE_WORDS, &W, rel);
+                else fline<true>(F, r, &W, rel);
             } else {
                 uint64_t gp[PJ_DEC_NCNT];
 #pragma unroll
@@ -2220,7 +2322,11 @@ hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.lines + DEC_LPB - 1) / DEC_LPB;
-    hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB>), dim3((unsigned)g), dim3(DEC_LINE_BT), 0, st,
-                       P);
+    if (P.tape)
+        hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB, true>), dim3((unsigned)g),
+                           dim3(DEC_LINE_BT), 0, st, P);
+    else
+        hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB, false>), dim3((unsigned)g),
+                           dim3(DEC_LINE_BT), 0, st, P);
     return hipGetLastError();
 }

@@ -319,6 +319,20 @@ def test_roundtrip_beyond_4gib(codec):
     torch.cuda.empty_cache()
 
 
+def test_decode_without_line_tape(codec, monkeypatch):
+    """The writing walk reads each line's tape (positions and values recorded
+    by the validating walk); with the tape turned off it parses the line
+    again.  Both give the oracle's columns."""
+    monkeypatch.setenv("PETJSON_DECODE_TAPE", "0")
+    cols = pj.generate(3, 40_000, seed=0x5EED0009)
+    buf = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), np.uint8).copy()
+    pj.corrupt_ndjson(buf, 11, 0.01)
+    data = buf.tobytes()
+    assert_same(gpu_decode(codec, data), orc.decode(data))
+    skew = orc.encode(pj.generate(5, 4_000), pj.FORMAT_NDJSON)
+    assert_same(gpu_decode(codec, skew), orc.decode(skew))
+
+
 def test_decode_lookback_redo_in_ticket_order(codec, monkeypatch):
     """The index and parse kernels take blocks in launch order with bounded
     look-back waits; a kernel whose wait ran out is redone in ticket order.
