@@ -1794,20 +1794,11 @@ __device__ __forceinline__ void tile_bitmaps(const uint8_t *tile, uint32_t nw, u
             x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
         }
         uint64_t Q = 0, B = 0, N = 0;
-        uint32_t anyb = 0, anyn = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             Q |= (uint64_t)zero_bytes4(x[k] ^ 0x22222222u) << (4 * k);
-            anyb |= any_zero(x[k] ^ 0x5C5C5C5Cu);
-            anyn |= any_zero(x[k] ^ 0x0A0A0A0Au);
-        }
-        if (anyb) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) B |= (uint64_t)zero_bytes4(x[k] ^ 0x5C5C5C5Cu) << (4 * k);
-        }
-        if (anyn) {
-#pragma unroll
-            for (int k = 0; k < 16; k++) N |= (uint64_t)zero_bytes4(x[k] ^ 0x0A0A0A0Au) << (4 * k);
+            B |= (uint64_t)zero_bytes4(x[k] ^ 0x5C5C5C5Cu) << (4 * k);
+            N |= (uint64_t)zero_bytes4(x[k] ^ 0x0A0A0A0Au) << (4 * k);
         }
         // backslash run ending just before the word (within the tile)
         uint32_t run = 0;
