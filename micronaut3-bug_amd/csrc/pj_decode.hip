@@ -1506,17 +1506,12 @@ __device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
         FL_SEP();                                                   \
     }
 
-// The properties are tried in schema order, each at most once, as straight
-// code: the lanes of a wave then walk the same instruction stream whatever
-// subset of properties their lines hold.
-// Pass 0 (WRITE false) validates and measures into R; pass 1 writes the
-// record at the line's offsets rel[] inside the block's column slices W.
 // ---------------------------------------------------------------- line tape
 // The validating walk of a canonical line records what the writing walk
 // needs, so that the writer stores and copies without parsing again:
 //   word 0 id, word 1 category id,
 //   word 2 flags | status << 8 | category flags << 16 | urls << 24 |
-//          tags << 32, bit 63 set when the record is complete,
+//          tags << 32,
 //   word 3 the name string, word 4 the category name string,
 //   words 5.. one word per url, then two per tag (id, name string).
 // A string word holds line-relative start, closing quote and decoded length
@@ -1527,11 +1522,16 @@ __device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
 #define PJ_TAPE_WORDS 24
 #endif
 constexpr int TAPE_WORDS = PJ_TAPE_WORDS;
-constexpr uint64_t TAPE_OK = 1ull << 63;
 __device__ __forceinline__ uint64_t tape_str(uint32_t q, const Str &r) {
     return (uint64_t)q | ((uint64_t)r.end << 16) | ((uint64_t)r.dlen << 32) | ((uint64_t)r.esc << 48);
 }
 
+// The properties are tried in schema order, each at most once, as straight
+// code: the lanes of a wave then walk the same instruction stream whatever
+// subset of properties their lines hold.
+// Pass 0 (WRITE false) validates and measures into R; pass 1 writes the
+// record at the line's offsets rel[] inside the block's column slices W.
+// With TAPE, pass 0 also records the line's tape at T.
 template <bool WRITE, class FL, bool TAPE = false>
 __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W, const uint32_t *rel,
                                      uint64_t *T = nullptr) {
@@ -1686,7 +1686,7 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
             T[0] = (uint64_t)id;
             T[1] = (uint64_t)cat_id;
             T[2] = (uint64_t)flags | ((uint64_t)status << 8) | ((uint64_t)cat_fl << 16) | ((uint64_t)n_urls << 24) |
-                   ((uint64_t)n_tags << 32) | TAPE_OK;
+                   ((uint64_t)n_tags << 32);
         }
     } else if (F.lead()) {
         const uint32_t row = rel[C_PETS];
@@ -2037,6 +2037,7 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //     there were several) writes the columns.
 template <int BT, int TILE, int LONG, int LPB = BT, bool TAPE = false>
 __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
+    static_assert(LONG < 65536, "tape positions of per-thread lines are 16-bit");
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t spec[TILE / 64 + 1];
     __shared__ uint64_t badm[TILE / 64 + 1];
