@@ -455,8 +455,10 @@ template <class S> __device__ __forceinline__ void rec_urls_open(S &s, const Rec
     rec_urls_open(s, v.fl, v.u1 == v.u0);
 }
 
+// A record with HAS_TAGS and no tag columns (the flat layout, or tag_off
+// NULL) has an empty list (t0 == t1 == 0).
 template <bool NESTED, class S> __device__ __forceinline__ void rec_tags_open(S &s, const EncParams &P, const RecVals &v) {
-    if (NESTED && (v.fl & PJ_PET_HAS_TAGS)) {
+    if (v.fl & PJ_PET_HAS_TAGS) {
         if (v.t1 > v.t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
             lit(s, ",\"tags\":[");
             if (v.t1 == v.t0) s.put_byte(']');

@@ -96,7 +96,9 @@ def random_columns(rng, n):
 SIZES = [1, 2, 95, 96, 97, 191, 255, 256, 257, 511, 767, 1000, 2049, 3001, 6000, 12000]
 
 
-@pytest.mark.parametrize("seed", range(64))
+# 1074 and 1271: HAS_TAGS set with every nested column group absent (the flat
+# kernel), once written as "tags":null or left out instead of an empty list
+@pytest.mark.parametrize("seed", list(range(64)) + [1074, 1271])
 def test_encode_random_columns_match_oracle(codec, seed):
     rng = np.random.default_rng(0xF022 + seed)
     n = SIZES[seed % len(SIZES)] + int(rng.integers(0, 3))
