@@ -114,13 +114,8 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
                     const uint4 v = q[k];
                     w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
                 }
-                uint32_t any = 0;
 #pragma unroll
-                for (int k = 0; k < 16; k++) any |= any_zero(w[k] ^ 0x0A0A0A0Au);
-                if (any) {
-#pragma unroll
-                    for (int k = 0; k < 16; k++) m |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
-                }
+                for (int k = 0; k < 16; k++) m |= (uint64_t)zero_bytes4(w[k] ^ 0x0A0A0A0Au) << (4 * k);
             } else {
                 for (uint32_t j = 0; st + j < P.len; j++) m |= (uint64_t)(P.in[st + j] == '\n') << j;
             }
