@@ -243,8 +243,10 @@ def test_decode_blocks_over_the_tile(codec):
     assert ref[3].n_errors > 50
     for shift in (0, 3):
         assert_same(gpu_decode(codec, data, shift=shift), ref)
-    # every line as long as possible around the tile size
-    big = [b'{"name":"' + b"x" * k + b'","photoUrls":[]}' for k in (40_900, 40_960, 41_000, 20_000, 39_000)]
+    # every line as long as possible around the tile size (31 KiB; 40 KiB in
+    # an earlier shape)
+    big = [b'{"name":"' + b"x" * k + b'","photoUrls":[]}'
+           for k in (31_680, 31_715, 31_744, 31_800, 40_900, 40_960, 41_000, 20_000, 39_000)]
     data2 = b"\n".join(big * 3) + b"\n"
     assert_same(gpu_decode(codec, data2), orc.decode(data2))
 
