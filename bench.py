@@ -245,8 +245,9 @@ def main():
         print(json.dumps({"calibrate_copy_bytes": a.calibrate_copy}))
         return
     if a.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {a.gpus}); this codec's sharding is described "
-              f"in DESIGN.md and no multi-GPU figure is produced.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {a.gpus}): the codec runs on one GPU's share "
+              f"(records split by row ranges, NDJSON at newlines) and no multi-GPU figure is produced.",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     import petjson as pj
