@@ -253,6 +253,27 @@ __device__ __forceinline__ void emit_str_lds(S &s, const PJ_LDS uint8_t *p, uint
     }
 }
 
+// Staged bytes that need no escape, read as aligned LDS qwords joined by a
+// funnel shift.
+template <class S>
+__device__ __forceinline__ void emit_plain_lds(S &s, const PJ_LDS uint8_t *p, uint32_t len) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 7;
+    const PJ_LDS uint64_t *q = (const PJ_LDS uint64_t *)(p - sh);
+    uint64_t cur = q[0];
+    uint32_t k = 0, j = 0;
+    for (; k + 8 <= len; k += 8, j++) {
+        const uint64_t nxt = q[j + 1];
+        s.put8(sh ? (cur >> (8 * sh)) | (nxt << (64 - 8 * sh)) : cur, 8);
+        cur = nxt;
+    }
+    if (k < len) {
+        const int m = (int)(len - k);
+        uint64_t x = cur >> (8 * sh);
+        if (sh + (uint32_t)m > 8) x |= q[j + 1] << (64 - 8 * sh);
+        s.put8(x, m);
+    }
+}
+
 // A JSON string (quotes included) from raw UTF-8 bytes: 8 bytes per step
 // through the no-escape fast path.  Strings staged in LDS take the aligned
 // reads of emit_str_lds; global memory takes unaligned 8-byte loads and, for
@@ -403,7 +424,17 @@ __device__ __forceinline__ TagItem load_tag(const EncParams &P, uint64_t g) {
 // url item: `"url"` + (',' or ']' after the record's last url)
 template <class S>
 __device__ __forceinline__ void emit_url_v(S &s, const EncParams &P, const ColSrc &X, const UrlItem &v, bool last) {
-    emit_strx(s, X, X.url + (v.a - X.ub), v.b - v.a, P.hexa);
+    const uint8_t *p = X.url + (v.a - X.ub);
+#if defined(__HIP_DEVICE_COMPILE__)
+    // urls are seldom escaped and fill whole waves of items: writing a staged
+    // escape-free url skips the per-qword escape test
+    if (!std::is_same<S, CountSink>::value && staged_plain(X, p, v.b - v.a)) {
+        s.put_byte('"');
+        if (v.b > v.a) emit_plain_lds(s, (const PJ_LDS uint8_t *)p, (uint32_t)(v.b - v.a));
+        s.put_byte('"');
+    } else
+#endif
+        emit_strx(s, X, p, v.b - v.a, P.hexa);
     s.put_byte(last ? ']' : ',');
 }
 template <class S>
