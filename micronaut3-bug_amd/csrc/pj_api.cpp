@@ -475,11 +475,11 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.state_parse = static_cast<uint64_t *>(ctx->scan.p);
         P.dq = P.state_parse + gp * VLB_WORDS;
         P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
-        // the line tape (192 bytes per line), when it fits a modest bound;
+        // the line tape (256 bytes per line), when it fits a modest bound;
         // without it the writer walks each line again
         P.tape = nullptr;
-        if (lines && decode_tape_enabled() && lines * 192 <= (16ull << 30) &&
-            ctx->tape.ensure(lines * 192) == hipSuccess)
+        if (lines && decode_tape_enabled() && lines * 256 <= (16ull << 30) &&
+            ctx->tape.ensure(lines * 256) == hipSuccess)
             P.tape = static_cast<uint64_t *>(ctx->tape.p);
         (void)hipGetLastError();
         P.order_by_id = 1;

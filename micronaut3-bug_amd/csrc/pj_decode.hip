@@ -1514,7 +1514,7 @@ __device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
 // 49-50.  A line with more items than the words left (PJ_TAPE_FULL) is read
 // by its wave instead, like a long line.
 #ifndef PJ_TAPE_WORDS
-#define PJ_TAPE_WORDS 24
+#define PJ_TAPE_WORDS 32
 #endif
 constexpr int TAPE_WORDS = PJ_TAPE_WORDS;
 __device__ __forceinline__ uint64_t tape_str(uint32_t q, const Str &r) {

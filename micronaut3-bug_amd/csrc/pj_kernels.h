@@ -54,7 +54,7 @@ struct DecParams {
     // error slots whose code is settled by k_dec_errcode (lines known to be
     // invalid from the bitmaps alone)
     uint64_t *dq;
-    uint64_t *tape;            // per line: 20 words of the validating walk's results, or null
+    uint64_t *tape;            // per line: 32 words of the validating walk's results, or null
     unsigned long long *dq_count;
     // 1: block b of each kernel takes its input in launch order (no ticket
     // atomic) and bounds its look-back wait by spin_limit wall-clock ticks;
