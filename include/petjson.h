@@ -199,7 +199,11 @@ pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len,
                          pj_pet_columns *out, uint64_t *err_line,
                          uint8_t *err_code, uint64_t err_cap,
                          pj_decode_result *res);
-/* Capacities that always suffice for decoding `len` input bytes. */
+/* Column capacities that always suffice for decoding `len` input bytes.
+ * The error list needs at most one entry per line, and `len` bytes hold at
+ * most `len` lines (blank lines are errors too); a call whose err_cap is too
+ * small returns PJ_ERR_CAPACITY with res->n_errors set, so callers may start
+ * smaller and retry once with that count. */
 void      pj_decode_bounds(uint64_t len, pj_pet_columns *caps_out);
 
 #ifdef __cplusplus

@@ -316,6 +316,7 @@ void pj_destroy(pj_ctx *c) {
     c->index.release();
     c->stage_in.release();
     c->stage_out.release();
+    c->tape.release();
     for (auto &e : c->ev) if (e) (void)hipEventDestroy(e);
     if (c->pinned) (void)hipHostFree(c->pinned);
     if (c->stream) (void)hipStreamDestroy(c->stream);

@@ -46,7 +46,7 @@ struct Rng {  // splitmix64 stream keyed by (seed, record)
     }
     double normal() {  // Box-Muller
         double u1 = unit(), u2 = unit();
-        if (u1 < 1e-300) u1 = 1e-300;
+        if (u1 < 0x1p-53) u1 = 0x1p-53;   // the smallest nonzero draw: |z| < 8.6
         return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
     }
 };
@@ -166,8 +166,10 @@ void gen_record(int cfg, uint64_t seed, uint64_t i, Chunk &c) {
     if (!skew) nlen = r.range(4, 32);
     else if (tail) nlen = r.range(8192, 16384);
     else {
+        // log-normal, median 12, sigma 1.5, uncapped (the normal deviate of
+        // a 53-bit uniform stays below 8.6, so a name stays below 5 MB)
         double v = std::exp(std::log(12.0) + 1.5 * r.normal());
-        nlen = (uint64_t)std::min(4096.0, std::max(1.0, std::floor(v)));
+        nlen = (uint64_t)std::max(1.0, std::floor(v));
     }
     n0 = c.name.size();
     put_name(c.name, r, nlen, skew ? 0.30 : 0.05, skew);

@@ -261,12 +261,21 @@ class PetObjectMapper {
         v.cap_cat_name_bytes = caps.cap_cat_name_bytes; v.cap_urls = caps.cap_urls;
         v.cap_url_bytes = caps.cap_url_bytes; v.cap_tags = caps.cap_tags;
         v.cap_tag_name_bytes = caps.cap_tag_name_bytes;
-        const uint64_t err_cap = len / 2 + 1;
+        // First guess at the error list; every line (blank ones included)
+        // can be an error, so a PJ_ERR_CAPACITY result is retried once with
+        // the count it reports.
+        uint64_t err_cap = len / 16 + 16;
         ReadResult r;
-        r.error_lines.resize(err_cap);
-        r.error_codes.resize(err_cap);
         pj_decode_result res;
-        check(pj_decode_host(ctx_, ndjson, len, &v, r.error_lines.data(), r.error_codes.data(), err_cap, &res));
+        pj_status st;
+        for (int attempt = 0;; attempt++) {
+            r.error_lines.resize(err_cap);
+            r.error_codes.resize(err_cap);
+            st = pj_decode_host(ctx_, ndjson, len, &v, r.error_lines.data(), r.error_codes.data(), err_cap, &res);
+            if (st != PJ_ERR_CAPACITY || attempt > 0 || res.n_errors <= err_cap) break;
+            err_cap = res.n_errors;
+        }
+        check(st);
         r.error_lines.resize(res.n_errors);
         r.error_codes.resize(res.n_errors);
         v.n_pets = res.n_pets;

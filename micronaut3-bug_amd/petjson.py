@@ -286,6 +286,14 @@ def corrupt_ndjson(buf: np.ndarray, seed: int, rate: float):
     return lines[:k].copy(), codes[:k].copy()
 
 
+def default_err_cap(length: int) -> int:
+    """First guess at the error-list capacity for `length` input bytes.  The
+    list can hold at most one entry per line (at most `length` lines), but
+    sizing for that would cost 9 bytes per input byte; the decode calls
+    retry once with the count a PJ_ERR_CAPACITY result reports."""
+    return length // 16 + 16
+
+
 def decode_bounds(length: int) -> Dict[str, int]:
     s = PetColumnsStruct()
     load_lib().pj_decode_bounds(length, C.byref(s))
@@ -391,10 +399,11 @@ class Codec:
         `out` = decode_buffers(...) reuses preallocated outputs."""
         import torch
         n = data.numel()
-        if out is None:
+        own = out is None
+        if own:
             caps = caps or decode_bounds(n)
             if err_cap is None:
-                err_cap = n // 16 + 16
+                err_cap = default_err_cap(n)
             out = self.decode_buffers(caps, err_cap, device)
         cols, el, ec = out
         err_cap = el.numel() if err_cap is None else err_cap
@@ -404,6 +413,16 @@ class Codec:
         ptr = C.c_void_p(data.data_ptr()) if n else C.c_void_p(el.data_ptr())
         rc = self.L.pj_decode_device(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()),
                                      C.c_void_p(ec.data_ptr()), err_cap, C.byref(res))
+        if rc == PJ_ERR_CAPACITY and own and res.n_errors > err_cap:
+            # more invalid lines than the first guess: the call reported how
+            # many there are, so one retry with that capacity suffices
+            err_cap = int(res.n_errors)
+            el = torch.empty(max(1, err_cap), dtype=torch.int64, device=el.device)
+            ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=ec.device)
+            s = cols.struct()
+            res = DecodeResult()
+            rc = self.L.pj_decode_device(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()),
+                                         C.c_void_p(ec.data_ptr()), err_cap, C.byref(res))
         self._check(rc)
         return self._trim(cols, res), el[: res.n_errors], ec[: res.n_errors], res
 
@@ -427,15 +446,21 @@ class Codec:
                  "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
         arrays = {k: np.zeros(max(1, v), dtype=DTYPES[k]) for k, v in sizes.items()}
         cols = Columns(0, arrays, dict(caps))
-        if err_cap is None:
-            err_cap = n // 16 + 16
-        el = np.zeros(max(1, err_cap), np.uint64)
-        ec = np.zeros(max(1, err_cap), np.uint8)
+        guessed = err_cap is None
+        if guessed:
+            err_cap = default_err_cap(n)
         buf = np.frombuffer(data, np.uint8) if n else np.zeros(1, np.uint8)
-        s = cols.struct()
-        res = DecodeResult()
-        self._check(self.L.pj_decode_host(self.ctx, C.c_void_p(buf.ctypes.data), n, C.byref(s),
-                                          C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap,
-                                          C.byref(res)))
+        for _ in range(2):
+            el = np.zeros(max(1, err_cap), np.uint64)
+            ec = np.zeros(max(1, err_cap), np.uint8)
+            s = cols.struct()
+            res = DecodeResult()
+            rc = self.L.pj_decode_host(self.ctx, C.c_void_p(buf.ctypes.data), n, C.byref(s),
+                                       C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap,
+                                       C.byref(res))
+            if not (rc == PJ_ERR_CAPACITY and guessed and res.n_errors > err_cap):
+                break
+            err_cap = int(res.n_errors)     # one retry with the count the call reported
+        self._check(rc)
         t = self._trim(cols, res).to_host()
         return t, el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res

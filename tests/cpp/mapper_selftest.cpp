@@ -113,6 +113,13 @@ int main(int argc, char **argv) {
         CHECK(r.values == normalised(pets));
         CHECK(r.error_lines.size() == 2 && r.error_lines[0] == pets.size() && r.error_lines[1] == pets.size() + 1);
         CHECK(r.error_codes[0] == PJ_REC_MISSING_PHOTOURLS && r.error_codes[1] == PJ_REC_BAD_STATUS);
+        // mostly blank lines: every one is an error, far more than one per
+        // 16 input bytes, so the first error-list guess is too small
+        std::string blank(3000, '\n');
+        blank += "{\"name\":\"z\",\"photoUrls\":[]}\n";
+        ReadResult rb = m.readValue(reinterpret_cast<const uint8_t *>(blank.data()), blank.size());
+        CHECK(rb.values.size() == 1 && rb.error_lines.size() == 3000);
+        CHECK(rb.error_lines[2999] == 2999 && rb.error_codes[0] == PJ_REC_EMPTY);
     }
     std::printf("mapper selftest ok (%s)\n", gpu ? "gpu" : "cpu");
     return 0;

@@ -347,3 +347,80 @@ def test_decode_lookback_redo_in_ticket_order(codec, monkeypatch):
     assert_same(gpu_decode(codec, data), orc.decode(data))
     skew = orc.encode(pj.generate(5, 6_000), pj.FORMAT_NDJSON)
     assert_same(gpu_decode(codec, skew), orc.decode(skew))
+
+
+def test_decode_many_invalid_lines_retry_error_capacity(codec):
+    """More invalid lines than the first error-list guess (one per 16 input
+    bytes): both entry points retry with the count the call reported."""
+    data = b"{}\n" * 1000 + b"\n" * 500 + b'{"name":"a","photoUrls":[]}\n'
+    ref = orc.decode(data)
+    assert ref[3].n_errors == 1500
+    assert_same(gpu_decode(codec, data), ref)
+    assert_same(codec.decode_host(data), ref)
+
+
+def _sentinel_columns(caps, dev="cuda"):
+    """Device columns of exactly the capacities (offset arrays cap + 1) with a
+    64-byte 0xEE tail behind each, to catch stores past a capacity."""
+    cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
+    sizes = {"id": cp, "flags": cp, "status": cp, "name_off": cp + 1, "name_bytes": caps["cap_name_bytes"],
+             "cat_id": cp, "cat_flags": cp, "cat_name_off": cp + 1, "cat_name_bytes": caps["cap_cat_name_bytes"],
+             "photo_off": cp + 1, "url_off": cu + 1, "url_bytes": caps["cap_url_bytes"], "tag_off": cp + 1,
+             "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
+    raw, arrays = {}, {}
+    for k, v in sizes.items():
+        isz = np.dtype(pj.DTYPES[k]).itemsize
+        b = torch.full((v * isz + 64,), 0xEE, dtype=torch.uint8, device=dev)
+        raw[k] = (b, v * isz)
+        arrays[k] = b
+    return pj.Columns(0, arrays, dict(caps)), raw
+
+
+def test_decode_capacity_guard_no_store_past_cap(codec):
+    """Each column capacity cut below what the input needs, in turn: the call
+    reports PJ_ERR_CAPACITY and no byte behind any capacity is written."""
+    cols = pj.generate(3, 3000)
+    text = orc.encode(cols, pj.FORMAT_NDJSON)
+    need = orc.decode(text)[3]
+    full = {"cap_pets": need.n_pets, "cap_name_bytes": need.name_bytes, "cap_cat_name_bytes": need.cat_name_bytes,
+            "cap_urls": need.n_urls, "cap_url_bytes": need.url_bytes, "cap_tags": need.n_tags,
+            "cap_tag_name_bytes": need.tag_name_bytes}
+    data = torch.frombuffer(bytearray(text), dtype=torch.uint8).cuda()
+    for cut in [None] + list(full):
+        for frac in ((0.5, 0.999) if cut else (1.0,)):
+            caps = dict(full)
+            if cut:
+                caps[cut] = int(full[cut] * frac)
+            dc, raw = _sentinel_columns(caps)
+            el = torch.empty(16, dtype=torch.int64, device="cuda")
+            ec = torch.empty(16, dtype=torch.uint8, device="cuda")
+            if cut:
+                with pytest.raises(pj.PetJsonError) as ei:
+                    codec.decode(data, out=(dc, el, ec))
+                assert ei.value.status == pj.PJ_ERR_CAPACITY, (cut, frac)
+            else:
+                codec.decode(data, out=(dc, el, ec))
+            torch.cuda.synchronize()
+            for k, (b, n) in raw.items():
+                tail = b[n:].cpu().numpy()
+                assert (tail == 0xEE).all(), (cut, frac, k)
+
+
+def test_destroy_releases_device_memory():
+    """A context that decoded (line tape, index, staging) gives all of its
+    device memory back when destroyed."""
+    cols = pj.generate(3, 200_000)
+    text = orc.encode(cols, pj.FORMAT_NDJSON)
+    data = torch.frombuffer(bytearray(text), dtype=torch.uint8).cuda()
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        c = pj.Codec(0)
+        c.decode_host(text[: len(text) // 4])
+        out = c.decode(data)
+        del out
+        c.close()
+        torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    free1 = torch.cuda.mem_get_info()[0]
+    assert free1 >= free0 - (64 << 20), (free0, free1)
