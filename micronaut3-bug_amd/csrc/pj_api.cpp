@@ -69,6 +69,7 @@ struct pj_ctx {
     DevBuf stage_out;   // host path: output staging
     DevBuf tape;        // decode: per-line results of the validating walk
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
+    uint64_t *noalloc_scratch = nullptr;  // this device's fixed encode scratch (device address)
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
     int n_ev = 0;
@@ -137,8 +138,11 @@ uint64_t spin_limit() {
     return 20000000;
 }
 
+// fixed_scratch: encode into the device's fixed scratch array instead of
+// the context's growable buffer (pj_encode_device_noalloc); nothing is
+// allocated on that path.
 pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t cap,
-                      uint64_t *out_len, bool count_only) {
+                      uint64_t *out_len, bool count_only, bool fixed_scratch = false) {
     pj_status s = bind(ctx);
     if (s) return s;
     if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
@@ -161,8 +165,17 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     }
     const uint64_t bt = (uint64_t)pj_encode_block_records(nested_cols(cols));
     const uint64_t nblk = (n + bt - 1) / bt;
-    PJ_HIP(ctx->scan.ensure((nblk + 3 + 128) * sizeof(uint64_t)));
-    uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p);
+    uint64_t *sc;
+    if (fixed_scratch) {
+        if (nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
+            return fail(PJ_ERR_INVALID_ARG, "pj_encode_device_noalloc: " + std::to_string(n) +
+                                                " records exceed the fixed scratch (at most " +
+                                                std::to_string(PJ_NOALLOC_MAX_RECORDS(nested_cols(cols))) + ")");
+        sc = ctx->noalloc_scratch;
+    } else {
+        PJ_HIP(ctx->scan.ensure((nblk + 3 + 128) * sizeof(uint64_t)));
+        sc = static_cast<uint64_t *>(ctx->scan.p);
+    }
     EncParams P;
     std::memset(&P, 0, sizeof P);
     P.c = *cols;
@@ -296,7 +309,8 @@ pj_ctx *pj_create(int device, pj_status *status) {
     pj_ctx *c = new pj_ctx();
     c->device = device;
     bool ok = hipSetDevice(device) == hipSuccess && hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) == hipSuccess &&
-              hipHostMalloc((void **)&c->pinned, 64 * sizeof(uint64_t), hipHostMallocDefault) == hipSuccess;
+              hipHostMalloc((void **)&c->pinned, 64 * sizeof(uint64_t), hipHostMallocDefault) == hipSuccess &&
+              pj_noalloc_scratch_init(device, &c->noalloc_scratch) == hipSuccess;
     for (int k = 0; ok && k < MAX_EV; k++) ok = hipEventCreate(&c->ev[k]) == hipSuccess;
     if (!ok) {
         g_err = "context set-up failed";
@@ -342,6 +356,11 @@ int pj_last_timings(const pj_ctx *c, float *ms, int cap) {
 pj_status pj_encode_device(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t out_cap,
                            uint64_t *out_len) {
     return encode_impl(ctx, cols, format, out, out_cap, out_len, false);
+}
+
+pj_status pj_encode_device_noalloc(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out,
+                                   uint64_t out_cap, uint64_t *out_len) {
+    return encode_impl(ctx, cols, format, out, out_cap, out_len, false, true);
 }
 
 pj_status pj_encode_size_device(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint64_t *out_len) {

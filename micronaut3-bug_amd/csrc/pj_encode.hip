@@ -25,6 +25,7 @@
 // Output rules (jackson UTF8JsonGenerator via micronaut-serde, reference
 // build.gradle:104) and property order / inclusion (petstore.json:872-922)
 // are the ones restated by the CPU checker in oracle/pj_oracle.c.
+#include <mutex>
 #include <type_traits>
 
 #include "pj_device.h"
@@ -1245,4 +1246,33 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st) {
     hipLaunchKernelGGL(pj::k_put_bytes, dim3(1), dim3(64), 0, st, out, w, k);
     return hipGetLastError();
+}
+
+// ------------------------------------------------------ no-allocation scratch
+// Encode scratch for pj_encode_device_noalloc: a fixed array every GPU the
+// library runs on holds until the process ends.  In host code `scratch`
+// names a host-side stand-in, not device memory; its device address (one
+// per GPU) is resolved once per device by pj_noalloc_scratch_init, which
+// pj_create calls with the device current, and only that address is ever
+// handed to kernels.  Calls on one GPU share the array, so calls that
+// overlap on one GPU race.
+static __device__ __align__(256) uint64_t scratch[PJ_NOALLOC_SCRATCH_WORDS];
+
+namespace {
+constexpr int PJ_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint64_t *g_scratch_ptr[PJ_MAX_DEVICES] = {};
+}  // namespace
+
+hipError_t pj_noalloc_scratch_init(int device, uint64_t **ptr) {
+    if (device < 0 || device >= PJ_MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = static_cast<uint64_t *>(p);
+    }
+    *ptr = g_scratch_ptr[device];
+    return hipSuccess;
 }

@@ -75,4 +75,7 @@ hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st);
 int pj_dec_index_block();
+// Device address of this GPU's fixed encode scratch (PJ_NOALLOC_SCRATCH_WORDS
+// u64); resolved once per device, with that device current.
+hipError_t pj_noalloc_scratch_init(int device, uint64_t **ptr);
 int pj_dec_parse_block();

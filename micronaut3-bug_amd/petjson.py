@@ -74,7 +74,13 @@ _GEN = None
 
 EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "pj_last_error",
            "pj_last_timings", "pj_encode_device", "pj_encode_size_device", "pj_encode_host",
-           "pj_decode_device", "pj_decode_host", "pj_decode_bounds"]
+           "pj_decode_device", "pj_decode_host", "pj_decode_bounds", "pj_encode_device_noalloc"]
+NOALLOC_SCRATCH_WORDS = 1 << 20
+
+
+def noalloc_max_records(nested: bool) -> int:
+    """Largest n_pets pj_encode_device_noalloc accepts (PJ_NOALLOC_MAX_RECORDS)."""
+    return (NOALLOC_SCRATCH_WORDS - 131) * (96 if nested else 256)
 
 
 def lib_path() -> str:
@@ -107,7 +113,7 @@ def load_lib():
         L.pj_last_error.restype = C.c_char_p
         L.pj_last_timings.argtypes = [vp, C.POINTER(C.c_float), i32]
         L.pj_last_timings.restype = i32
-        for f in ("pj_encode_device", "pj_encode_host"):
+        for f in ("pj_encode_device", "pj_encode_host", "pj_encode_device_noalloc"):
             getattr(L, f).argtypes = [vp, C.POINTER(PetColumnsStruct), i32, vp, u64, C.POINTER(u64)]
             getattr(L, f).restype = i32
         L.pj_encode_size_device.argtypes = [vp, C.POINTER(PetColumnsStruct), i32, C.POINTER(u64)]
@@ -358,6 +364,18 @@ class Codec:
         n = C.c_uint64(0)
         cap = out.numel()
         self._check(self.L.pj_encode_device(self.ctx, C.byref(s), fmt, C.c_void_p(out.data_ptr()), cap, C.byref(n)))
+        return out[: n.value]
+
+    def encode_noalloc(self, cols: Columns, out, fmt: int = FORMAT_ARRAY):
+        """pj_encode_device_noalloc into the caller's device tensor `out`
+        (the call itself allocates nothing); returns the view of `out`
+        holding the JSON bytes."""
+        import torch
+        torch.cuda.synchronize()
+        s = cols.struct()
+        n = C.c_uint64(0)
+        self._check(self.L.pj_encode_device_noalloc(self.ctx, C.byref(s), fmt, C.c_void_p(out.data_ptr()),
+                                                    out.numel(), C.byref(n)))
         return out[: n.value]
 
     def encode_host(self, cols: Columns, fmt: int = FORMAT_ARRAY) -> bytes:
