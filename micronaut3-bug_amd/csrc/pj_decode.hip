@@ -853,6 +853,32 @@ __device__ __forceinline__ int hex4(uint32_t x) {
     return ok ? (int)cu : -1;
 }
 
+// Bit 7 of the first byte of x that is '"', '\\', below 0x20 or above 0x7F
+// (bits above it may be set too: borrows only run upwards from a byte that
+// is flagged itself).
+__device__ __forceinline__ uint64_t str_stop8(uint64_t x) {
+    constexpr uint64_t ONE = 0x0101010101010101ull;
+    const uint64_t q = x ^ (0x22 * ONE), b = x ^ (0x5C * ONE);
+    return (((q - ONE) & ~q) | ((b - ONE) & ~b) | (x - 0x20 * ONE) | x) & (0x80 * ONE);
+}
+// The same for '"' and '\\' only.
+__device__ __forceinline__ uint64_t quote_bs8(uint64_t x) {
+    constexpr uint64_t ONE = 0x0101010101010101ull;
+    const uint64_t q = x ^ (0x22 * ONE), b = x ^ (0x5C * ONE);
+    return (((q - ONE) & ~q) | ((b - ONE) & ~b)) & (0x80 * ONE);
+}
+// Continuation bytes a UTF-8 lead byte c takes under jackson's lead classes
+// (C0-DF one, E0-EF two, F0-F7 three), given x = the 8 bytes from the lead
+// byte on; 0 if c is no lead byte (a control, a stray continuation byte,
+// F8-FF) or a continuation byte is missing.
+__device__ __forceinline__ uint32_t utf8_extra(uint32_t c, uint64_t x) {
+    const uint32_t extra = (uint32_t)(c >= 0xC0) + (uint32_t)(c >= 0xE0) + (uint32_t)(c >= 0xF0);
+    const uint64_t msk = (1ull << (8 * extra)) - 1;
+    const uint64_t cb = (x >> 8) & msk & (0xC0C0C0ull);
+    const bool ok = c >= 0xC0 && c <= 0xF7 && cb == (0x808080ull & msk);
+    return ok ? extra : 0u;
+}
+
 // ---- word-at-a-time string decoding for the lane-parallel walk of long
 // lines.  A 64-byte
 // tile word at ws: xs[] its bytes, ub the mask of its 'u' bytes, nb the byte
@@ -1047,6 +1073,7 @@ struct FLineT {
             if (sp < n && s[sp] == '"') return Str{0, sp, sp - q, false};
             return wave_str<false>(q, nullptr);
         }
+        if (!special) return str_swar(q);
         Str r{0, 0, 0, false};
         uint32_t d = 0;
         for (;;) {
@@ -1063,6 +1090,46 @@ struct FLineT {
         r.dlen = d;
         return r;
     }
+    // String at q read 8 bytes at a time without the bitmaps: the first
+    // byte of each 8 that is a quote, a backslash, a control or non-ASCII
+    // stops the scan (str_stop8), and each kind is settled where it stands:
+    // the closing quote ends the string, an escape is decoded, a UTF-8 lead
+    // byte must carry its continuation bytes (jackson's lead classes), and a
+    // raw control is an error.  The byte after the line is its newline or
+    // the tile's zero padding, a control, so the scan never leaves the line.
+    __device__ __forceinline__ Str str_swar(uint32_t q) const {
+        Str r{0, 0, 0, false};
+        uint32_t d = 0;
+        for (;;) {
+            const uint64_t x = ld8(q);
+            const uint64_t m = str_stop8(x);
+            if (!m) {
+                q += 8;
+                d += 8;
+                continue;
+            }
+            const uint32_t k = (uint32_t)__builtin_ctzll(m) >> 3;
+            q += k;
+            d += k;
+            const uint32_t c = (uint32_t)(x >> (8 * k)) & 0xFF;
+            if (c == '"') break;
+            if (c == '\\') {
+                const Esc e = esc(q);
+                if (e.err) { r.err = e.err; return r; }
+                d += (uint32_t)e.k;
+                q += e.adv;
+                r.esc = true;
+                continue;
+            }
+            const uint32_t extra = utf8_extra(c, ld8(q));
+            if (!extra) { r.err = PJ_REC_STRING; return r; }
+            q += 1 + extra;
+            d += 1 + extra;
+        }
+        r.end = q;
+        r.dlen = d;
+        return r;
+    }
     // copy the decoded string (content from q, described by r) to dst
     __device__ __forceinline__ void copy(uint32_t q, const Str &r, uint8_t *dst) const {
         if (COOP) {
@@ -1074,6 +1141,31 @@ struct FLineT {
         }
         if (!r.esc) {
             copy_from_lds(dst, s + q, r.dlen);
+            return;
+        }
+        if (!special) {
+            // runs between escapes go out whole; the next backslash (or the
+            // closing quote) is found 8 bytes at a time
+            uint8_t *dd = dst;
+            uint32_t x = q;
+            for (;;) {
+                uint32_t stop = x;
+                for (;;) {
+                    const uint64_t m = quote_bs8(ld8(stop));
+                    if (m) { stop += (uint32_t)__builtin_ctzll(m) >> 3; break; }
+                    stop += 8;
+                }
+                stop = min(stop, r.end);
+                if (stop > x) {
+                    copy_from_lds(dd, s + x, stop - x);
+                    dd += stop - x;
+                }
+                if (stop >= r.end) break;
+                const Esc e = esc(stop);
+                st_tail(dd, e.out, (uint32_t)e.k);
+                dd += e.k;
+                x = stop + e.adv;
+            }
             return;
         }
         // runs between escapes go out whole; the specials bitmap finds the
@@ -1957,50 +2049,55 @@ __device__ __forceinline__ void vlb_resolve(uint64_t *st, uint64_t b, const uint
 }
 
 // ---------------------------------------------------------------- stage 2 kernel
-// Tile bytes [a0, a0 + tb) of the input into LDS with 16-byte loads (4 in
-// flight per thread), zero-padded to whole 64-byte words plus 64 bytes; the
-// previous line's bytes in the first chunk (before g0) are cleared: no line
-// reads them, and zeros keep them out of the string state.  All threads.
+// Tile bytes [a0, a0 + tb) of the input into LDS, zero-padded to whole
+// 64-byte words plus 64 bytes; the previous line's bytes in the first chunk
+// (before g0) are cleared: no line reads them, and zeros keep them out of the
+// string state.  16-byte chunks wholly inside the input go from HBM straight
+// into LDS (global_load_lds, 64 chunks per wave instruction, all of a
+// thread's chunks in flight at once) when the input is 16-byte aligned; the
+// chunk holding the input's end and the zero chunks go through registers.
+// All threads; the caller's barrier publishes the tile.
 template <int BT>
 __device__ __forceinline__ void load_tile(const DecParams &P, uint8_t *tile, uint64_t a0, uint64_t g0, uint64_t tb,
                                           uint32_t nw) {
-    const uint32_t t = threadIdx.x;
+    const uint32_t t = threadIdx.x, l = t & 63, w = t >> 6;
     const uint32_t nch = (uint32_t)((tb + 15) >> 4), nall = nw * 4;
-    for (uint32_t c0 = t; c0 < nall; c0 += 4 * BT) {
-        uint4 v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t c = c0 + u * BT;
-            const uint64_t g = a0 + 16ull * c;
-            v[u] = make_uint4(0, 0, 0, 0);
-            if (c < nch) {
-                if (g + 16 <= P.len) v[u] = *reinterpret_cast<const uint4 *>(P.in + g);
-                else {
-                    uint32_t w[4] = {0, 0, 0, 0};
-                    for (uint32_t j = 0; j < 16 && g + j < P.len; j++) w[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
-                    v[u] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t c = c0 + u * BT;
-            if (c >= nall) break;
-            if (c == 0 && a0 < g0) {
-                const uint32_t lead = (uint32_t)(g0 - a0);
-                uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int clr = (int)lead - 4 * k;      // bytes of dword k to clear
-                    if (clr >= 4) w[k] = 0;
-                    else if (clr > 0) w[k] &= ~0u << (8 * clr);
-                }
-                v[u] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-            reinterpret_cast<uint4 *>(tile)[c] = v[u];
-        }
+    const bool aligned = ((uintptr_t)P.in & 15) == 0;
+    const uint64_t whole = P.len > a0 ? (P.len - a0) >> 4 : 0;     // chunks that end inside the input
+    const uint32_t ndma = aligned ? (uint32_t)min((uint64_t)nch, whole) : 0u;
+    for (uint32_t c0 = 64 * w; c0 < ndma; c0 += BT) {
+        if (c0 + l < ndma)
+            __builtin_amdgcn_global_load_lds(P.in + a0 + 16ull * (c0 + l), (PJ_LDS void *)(tile + 16 * c0), 16, 0, 0);
     }
-    if (t < 4) reinterpret_cast<uint4 *>(tile)[nall + t] = make_uint4(0, 0, 0, 0);
+    for (uint32_t c = ndma + t; c < nall + 4; c += BT) {
+        const uint64_t g = a0 + 16ull * c;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (c < nch) {
+            if (g + 16 <= P.len) v = *reinterpret_cast<const uint4 *>(P.in + g);
+            else {
+                uint32_t x[4] = {0, 0, 0, 0};
+                for (uint32_t j = 0; j < 16 && g + j < P.len; j++) x[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
+                v = make_uint4(x[0], x[1], x[2], x[3]);
+            }
+        }
+        reinterpret_cast<uint4 *>(tile)[c] = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0);                  // this wave's chunks are in LDS
+    if (t == 0 && a0 < g0) {                        // chunk 0 came from wave 0, now complete
+        const uint32_t lead = (uint32_t)(g0 - a0);
+        for (uint32_t j = 0; j < lead; j++) tile[j] = 0;
+    }
+}
+
+// Whether any thread of the block holds p (all threads call; one LDS word).
+__device__ __forceinline__ bool block_any(bool p, uint32_t *flag) {
+    if (threadIdx.x == 0) *flag = 0;
+    __syncthreads();
+    if (__ballot(p) && lane_id() == 0) *flag = 1;
+    __syncthreads();
+    const bool r = *flag != 0;
+    __syncthreads();
+    return r;
 }
 
 // A bad byte anywhere in the line at tile offset s0 (its newline included).
@@ -2039,7 +2136,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_ls[LPB + 1];             // the block's line starts, then its end
     __shared__ uint16_t sh_sub[LPB + 1];            // sub-tile boundaries (block-local line indices)
-    __shared__ uint32_t sh_nsub;
+    __shared__ uint32_t sh_nsub, sh_any;
     __shared__ uint64_t sh_blk, sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
     if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[1], 1ull);
@@ -2092,16 +2189,29 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
             const uint32_t nw = (uint32_t)((tb + 63) >> 6);
             load_tile<BT>(P, tile, a0, g0, tb, nw);
             __syncthreads();
-            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
-            __syncthreads();
             if (mine) {
                 s0 = (uint32_t)(gs - a0);
                 ta0 = a0;
                 ttb = tb;
-                bad = line_bad(badm, nw, s0, n);
-                if (bad) code = PJ_REC_STRING;      // provisional: k_dec_errcode settles it
-                else if (!longl) {
+#ifdef PJ_FORCE_BITMAPS
+            }
+            __syncthreads();
+            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+            __syncthreads();
+            if (mine) {
+#endif
+#if PJ_PROBE == 1
+                if (false) {
+#else
+                if (!longl) {
+#endif
+                    // strings are scanned and checked byte class by byte
+                    // class as the walk meets them: no bitmaps needed
+#ifdef PJ_FORCE_BITMAPS
                     const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
+#else
+                    const FLine F{(const PJ_LDS uint8_t *)(tile + s0), nullptr, s0, n};
+#endif
                     if constexpr (TAPE) code = fline<false, FLine, true>(F, r, nullptr, nullptr, P.tape + l * TAPE_WORDS);
                     else code = fline<false>(F, r, nullptr, nullptr);
                     if (TAPE && code == PJ_TAPE_FULL) {
@@ -2111,7 +2221,16 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                     need_gen = code == PJ_BAIL;
                 }
             }
-            // long lines: the wave of the owning thread reads them together
+            // long lines: the wave of the owning thread reads them together,
+            // over the bitmaps, which only sub-tiles holding one build
+            if (block_any(mine && longl, &sh_any)) {
+                tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+                __syncthreads();
+                if (mine && longl) {
+                    bad = line_bad(badm, nw, s0, n);
+                    if (bad) code = PJ_REC_STRING;  // provisional: k_dec_errcode settles it
+                }
+            }
             for (uint64_t m = __ballot(mine && !bad && longl); m; m &= m - 1) {
                 const int k = __builtin_ctzll(m);
                 const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
@@ -2128,10 +2247,11 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
             need_gen = true;
         }
         if (need_gen) {
+            // the general parser checks every string byte itself (slow mode)
             general = true;
-            const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, tb, spec};
+            const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, tb, nullptr};
             LineInfo L;
-            code = run_line(P, S, over ? gs : s0, n, over, false, L, nullptr);
+            code = run_line(P, S, over ? gs : s0, n, true, false, L, nullptr);
             if (!code) {
                 r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
                 r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
@@ -2146,8 +2266,15 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     if (live) rec_counts(r, v);
     uint32_t pos[PJ_DEC_NCNT];                      // block-relative: a block's columns stay below 2^32 bytes
     uint64_t agg[PJ_DEC_NCNT];
+    {
+        uint32_t v32[PJ_DEC_NCNT], a32[PJ_DEC_NCNT];
 #pragma unroll
-    for (int k = 0; k < PJ_DEC_NCNT; k++) pos[k] = (uint32_t)block_excl_scan<BT>(v[k], sh_scan, &agg[k]);
+        for (int k = 0; k < PJ_DEC_NCNT; k++) v32[k] = (uint32_t)v[k];
+        // the bad-byte bitmap is not read after pass 0: its words hold the scan
+        block_excl_scan_n<BT, PJ_DEC_NCNT>(v32, pos, a32, reinterpret_cast<uint32_t *>(badm));
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) agg[k] = a32[k];
+    }
     if (t < 64) {
         vlb_publish(P.state_parse, b, agg, (int)t);
         uint64_t excl[PJ_DEC_NCNT];
@@ -2188,6 +2315,9 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                       base[C_URLB] + agg[C_URLB] <= o.cap_url_bytes && base[C_TAGS] + agg[C_TAGS] <= o.cap_tags &&
                       base[C_TAGB] + agg[C_TAGB] <= o.cap_tag_name_bytes;
     if (!room) return;
+#if PJ_PROBE >= 1
+    return;
+#endif
     BlockCols W;
     W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
     W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
@@ -2204,14 +2334,14 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
         const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
         const bool sub_over = tb > TILE;
-        if (nsub > 1 && !sub_over) {                // a single sub-tile is still in LDS
+        const bool wmine = writer && t >= ka && t < kb;
+        if (nsub > 1 && !sub_over) {                // a single sub-tile is still in LDS (with its bitmaps)
             const uint32_t nw = (uint32_t)((tb + 63) >> 6);
             load_tile<BT>(P, tile, a0, g0, tb, nw);
             __syncthreads();
-            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+            if (block_any(wmine && !general && longl, &sh_any)) tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
             __syncthreads();
         }
-        const bool wmine = writer && t >= ka && t < kb;
         for (uint64_t m = __ballot(wmine && !general && longl); m; m &= m - 1) {
             const int k = __builtin_ctzll(m);
             uint32_t rel[PJ_DEC_NCNT];
@@ -2226,19 +2356,23 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = pos[k];
+#ifdef PJ_FORCE_BITMAPS
                 const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
+#else
+                const FLine F{(const PJ_LDS uint8_t *)(tile + s0), nullptr, s0, n};
+#endif
                 if constexpr (TAPE) tape_write(F, P.tape + l * TAPE_WORDS, &W, rel);
                 else fline<true>(F, r, &W, rel);
             } else {
                 uint64_t gp[PJ_DEC_NCNT];
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) gp[k] = pos[k] + base[k];
-                const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, ttb, spec};
+                const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, ttb, nullptr};
                 // the measuring walk again (cheaper than keeping its positions
                 // in registers across the look-back), then the writing walk
                 LineInfo L;
-                run_line(P, S, over ? gs : s0, n, over, false, L, nullptr);
-                run_line(P, S, over ? gs : s0, n, over, true, L, gp);
+                run_line(P, S, over ? gs : s0, n, true, false, L, nullptr);
+                run_line(P, S, over ? gs : s0, n, true, true, L, gp);
             }
         }
         if (nsub > 1) __syncthreads();

@@ -31,21 +31,45 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return ((uint64_t)hi << 32) | lo;
 }
 
-// Inclusive wave scan (sum) of 64-bit values.
+// Cross-lane moves inside the VALU (DPP): row_shr:n shifts within rows of
+// 16 lanes, row_bcast:15 / row_bcast:31 carry a row's last lane into the
+// next row(s).  Lanes whose source is outside their row, or whose row is
+// masked off, read 0.  All 64 lanes must be active.
+template <int CTRL, int RM>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, 0xf, false);
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    return ((uint64_t)dpp32<CTRL, RM>((uint32_t)(v >> 32)) << 32) | dpp32<CTRL, RM>((uint32_t)v);
+}
+// Inclusive wave scans (sum): Hillis-Steele within rows, then the row
+// totals carried across rows.
+__device__ __forceinline__ uint32_t wave_incl_scan32(uint32_t v) {
+    v += dpp32<0x111, 0xf>(v);
+    v += dpp32<0x112, 0xf>(v);
+    v += dpp32<0x114, 0xf>(v);
+    v += dpp32<0x118, 0xf>(v);
+    v += dpp32<0x142, 0xa>(v);
+    v += dpp32<0x143, 0xc>(v);
+    return v;
+}
 __device__ __forceinline__ uint64_t wave_incl_scan(uint64_t v) {
-    const int l = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        uint64_t t = shfl_up_u64(v, d);
-        if (l >= d) v += t;
-    }
+    v += dpp64<0x111, 0xf>(v);
+    v += dpp64<0x112, 0xf>(v);
+    v += dpp64<0x114, 0xf>(v);
+    v += dpp64<0x118, 0xf>(v);
+    v += dpp64<0x142, 0xa>(v);
+    v += dpp64<0x143, 0xc>(v);
     return v;
 }
-__device__ __forceinline__ uint64_t wave_sum(uint64_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_u64(v, m);
-    return v;
+// lane 63's value, in every lane
+__device__ __forceinline__ uint64_t lane63(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
 }
+__device__ __forceinline__ uint64_t wave_sum(uint64_t v) { return lane63(wave_incl_scan(v)); }
 
 // Block-wide exclusive scan of one 64-bit value per thread (all BT threads
 // must call).  Returns the exclusive prefix; *total gets the block sum.
@@ -56,7 +80,7 @@ __device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t *sh, ui
     const int t = threadIdx.x, w = t >> 6, l = t & 63;
     uint64_t inc = wave_incl_scan(v);
     if (NW == 1) {
-        *total = shfl_u64(inc, 63);
+        *total = lane63(inc);
         return inc - v;
     }
     if (l == 63) sh[w] = inc;
@@ -71,6 +95,36 @@ __device__ __forceinline__ uint64_t block_excl_scan(uint64_t v, uint64_t *sh, ui
     __syncthreads();
     *total = tot;
     return before + inc - v;
+}
+
+// Block-wide exclusive scans of K 32-bit counters per thread at once (all
+// BT threads call): excl[k] gets the prefix, tot[k] the block total.  `sh`
+// needs K * BT / 64 words of LDS; one barrier pair for all K.
+template <int BT, int K>
+__device__ __forceinline__ void block_excl_scan_n(const uint32_t *v, uint32_t *excl, uint32_t *tot, uint32_t *sh) {
+    constexpr int NW = BT / 64;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    uint32_t inc[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) inc[k] = wave_incl_scan32(v[k]);
+    if (l == 63) {
+#pragma unroll
+        for (int k = 0; k < K; k++) sh[w * K + k] = inc[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        uint32_t before = 0, all = 0;
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+            const uint32_t s = sh[j * K + k];
+            before += j < w ? s : 0u;
+            all += s;
+        }
+        excl[k] = before + inc[k] - v[k];
+        tot[k] = all;
+    }
+    __syncthreads();
 }
 
 // ----------------------------------------------------------- look-back
