@@ -91,14 +91,18 @@ def decode_workload(codec, n, steps, warmup):
     for _ in range(warmup):
         codec.decode(data, out=bufs)
     torch.cuda.synchronize()
-    ti, tp, te = [], [], []
+    ti, tp, te, tw = [], [], [], []
     t0 = time.perf_counter()
     for _ in range(steps):
         dcols, el, ec, res = codec.decode(data, out=bufs)
-        tm = codec.timings()            # [total, fill, k_dec_lines, host gap, fill, k_dec_block, k_dec_errcode]
+        # [total, fill, k_dec_lines, host gap, fill, k_dec_block, (k_dec_bscan, k_dec_write, k_dec_long,)
+        #  k_dec_errcode]
+        tm = codec.timings()
         ti.append(tm[2])
         tp.append(tm[5])
-        te.append(tm[6])
+        te.append(tm[-1])
+        if len(tm) >= 10:
+            tw.append(tm[6] + tm[7] + tm[8])
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     ok = (res.n_errors == len(lines) and np.array_equal(el.cpu().numpy().astype(np.uint64), lines)
@@ -113,6 +117,7 @@ def decode_workload(codec, n, steps, warmup):
          "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
          "lines_general_parser": int(res.n_general),
          "kernels": {"k_dec_lines_ms": kidx, "k_dec_block_ms": kpar, "k_dec_errcode_ms": kerr,
+                     "k_dec_scan_write_long_ms": sum(tw) / len(tw) if tw else None,
                      "k_dec_lines_GBps": in_bytes / (kidx * 1e-3) / 1e9,
                      "k_dec_block_alg_GBps": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9,
                      "k_dec_block_alg_frac_hbm": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9 / HBM_PEAK_GBPS}}

@@ -53,7 +53,7 @@ struct DevBuf {
     }
 };
 
-constexpr int MAX_EV = 10;
+constexpr int MAX_EV = 12;
 
 inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
@@ -490,27 +490,54 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         }
         P.lines = lines;
         const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
-        // scan buffer: vector look-back words, then the deferred error-code queue
-        PJ_HIP(ctx->scan.ensure((gp * VLB_WORDS + lines + 8) * 8));
-        P.state_parse = static_cast<uint64_t *>(ctx->scan.p);
-        P.dq = P.state_parse + gp * VLB_WORDS;
-        P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
         // the line tape (256 bytes per line), when it fits a modest bound;
-        // without it the writer walks each line again
+        // with it the decode is split at the scan (the validating kernel
+        // stores per-line offsets, the writers follow a block scan), without
+        // it the single-pass kernel walks each line again to write it
         P.tape = nullptr;
         if (lines && decode_tape_enabled() && lines * 256 <= (16ull << 30) &&
             ctx->tape.ensure(lines * 256) == hipSuccess)
             P.tape = static_cast<uint64_t *>(ctx->tape.p);
         (void)hipGetLastError();
+        const bool split = P.tape != nullptr;
+        // scan buffer: vector look-back words (single pass) or block totals,
+        // bases and scan look-back words (split), then the deferred
+        // error-code queue, then (split) the wave-line list and the per-line
+        // offsets (9 u32 per line)
+        const uint64_t nsb = (gp + pj_dec_bscan_block() - 1) / pj_dec_bscan_block();
+        const uint64_t w_state = split ? 2 * gp * VLB_WORDS + nsb * VLB_WORDS : gp * VLB_WORDS;
+        const uint64_t w_split = split ? lines + (9 * lines + 1) / 2 : 0;
+        PJ_HIP(ctx->scan.ensure((w_state + lines + 8 + w_split) * 8));
+        uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
+        P.state_parse = SB;
+        P.bagg = SB;
+        P.bbase = SB + gp * VLB_WORDS;
+        P.bstate = SB + 2 * gp * VLB_WORDS;
+        P.nblocks = gp;
+        P.dq = SB + w_state;
+        P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
+        P.long_count = reinterpret_cast<unsigned long long *>(X + 14);
+        P.bticket = reinterpret_cast<unsigned long long *>(X + 15);
+        P.long_list = P.dq + lines + 8;
+        P.lpos = reinterpret_cast<uint32_t *>(P.long_list + lines);
         P.order_by_id = 1;
         for (;;) {
             if ((s = mark(ctx))) return s;
-            PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
+            if (split) PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
+            else PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
             PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
             PJ_HIP(pj_launch_fill_u64(X + 4, 12, 0, ctx->stream));     // totals and counters
             if ((s = mark(ctx))) return s;
             if (lines) {
                 PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+                if (split) {
+                    if ((s = mark(ctx))) return s;
+                    PJ_HIP(pj_launch_dec_bscan(P, ctx->stream));
+                    if ((s = mark(ctx))) return s;
+                    PJ_HIP(pj_launch_dec_write(P, ctx->stream));
+                    if ((s = mark(ctx))) return s;
+                    PJ_HIP(pj_launch_dec_long(P, ctx->stream));
+                }
                 if ((s = mark(ctx))) return s;
                 PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
             } else {

@@ -1,22 +1,25 @@
 // pj_decode.hip — NDJSON -> columnar Pet decoder for gfx950.
 //
-// Stage 1, k_dec_index: one thread per 64-byte block of input, simdjson-style:
-//   * exact quote / backslash masks (SWAR byte compares), escaped positions
-//     from odd backslash runs (the run carried in from the previous block is
-//     read back from memory), unescaped-quote mask Qu;
-//   * in-string mask = prefix-XOR of Qu, reset after every newline, with the
-//     carry (quote parity since the last newline) chained across blocks and
-//     workgroups by a block scan + decoupled look-back whose state also
-//     counts newlines;
-//   * outputs: the "specials" bitmap (unescaped quotes | backslashes) that
-//     lets the parser jump over strings, one flag per block for raw control
-//     characters or malformed UTF-8 inside strings, and the line index.
-// Stage 2, k_dec_parse: one thread per line.  A validating pass (string
-// contents skipped through the bitmap; lines touching a flagged block take
-// the byte-by-byte path) yields the record's column sizes; a block scan and
-// a vector look-back over 8 counters give each valid record its row and
-// byte offsets and each invalid one its slot in the error list; a second
-// walk over the same line materialises the columns.
+// k_dec_lines: exact newline masks (SWAR) over 64-byte words, block scans and
+//   a decoupled look-back of newline counts -> every line's start.
+// k_dec_block: one workgroup per LPB lines, one thread per line.  The lines
+//   are tiled into LDS (HBM -> LDS loads); each thread validates and
+//   measures its line with the fast path (properties in schema order as
+//   straight code; strings scanned 16 bytes at a time with every byte class
+//   checked where the walk meets it), recording a tape of what the writer
+//   needs; lines the fast path does not recognise go through the general
+//   pushdown parser; lines over 1 KiB are read by their whole wave over the
+//   tile's quote / backslash bitmaps.  With the tape (the default) the kernel
+//   ends with a block scan of 8 counters: per-line offsets inside the block
+//   and the block totals go to memory, and
+// k_dec_bscan scans the block totals (ticket-ordered workgroups, vector
+//   look-back) into each block's first offsets;
+// k_dec_write tiles each block again and writes its fast-path lines from
+//   their tapes at those offsets, and the error slots;
+// k_dec_long writes the lines of the whole wave and of the general parser;
+// k_dec_errcode settles the code of lines found invalid from the bitmaps.
+// Without the tape, k_dec_block is single-pass: its blocks chain through a
+//   vector look-back and a second walk over each line writes it.
 //
 // The grammar and binding rules (RFC 8259 as enforced by jackson's
 // UTF8StreamJsonParser, comments rejected per reference application.yml:23-28;
@@ -820,6 +823,8 @@ __device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
 // missing required property) are the first error of the line, exactly as
 // run_line reports them.
 constexpr int PJ_BAIL = -1;
+// line kinds of the split decode (above the code in the line's info word)
+constexpr uint32_t LK_GENERAL = 1u << 8, LK_WAVE = 1u << 9, LK_BAD = 1u << 10;
 constexpr int PJ_TAPE_FULL = -2;  // valid so far, more items than the line tape holds: read by the wave
 
 // bit k set iff byte k of x equals c
@@ -877,6 +882,27 @@ __device__ __forceinline__ uint32_t utf8_extra(uint32_t c, uint64_t x) {
     const uint64_t cb = (x >> 8) & msk & (0xC0C0C0ull);
     const bool ok = c >= 0xC0 && c <= 0xF7 && cb == (0x808080ull & msk);
     return ok ? extra : 0u;
+}
+
+// The stop byte c at q of a string (not its closing quote): an escape, a
+// UTF-8 lead byte with its continuation bytes, or an error.  Returns the
+// bytes consumed | the bytes they decode to << 8, or 0 for an error.
+__device__ __noinline__ uint32_t str_step(const PJ_LDS uint8_t *s, uint32_t n, uint32_t q, uint32_t c) {
+    if (c == '\\') {
+        const uint64_t w = lds_u64(s + q);
+        const uint32_t e = (uint32_t)(w >> 8) & 0xFF;
+        if (e == 'u') {
+            const Esc x = escape_at((const uint8_t *)s, n, q);
+            return x.err ? 0u : (x.adv | ((uint32_t)x.k << 8));
+        }
+        constexpr uint64_t LO = (1ull << '"') | (1ull << '/');
+        constexpr uint64_t HI = (1ull << ('\\' - 64)) | (1ull << ('b' - 64)) | (1ull << ('f' - 64)) |
+                                (1ull << ('n' - 64)) | (1ull << ('r' - 64)) | (1ull << ('t' - 64));
+        const bool ok = e < 128 && (((e < 64 ? LO : HI) >> (e & 63)) & 1) && q + 1 < n;
+        return ok ? (2u | (1u << 8)) : 0u;
+    }
+    const uint32_t extra = utf8_extra(c, lds_u64(s + q));
+    return extra ? ((1 + extra) | ((1 + extra) << 8)) : 0u;
 }
 
 // ---- word-at-a-time string decoding for the lane-parallel walk of long
@@ -1099,35 +1125,33 @@ struct FLineT {
     // the tile's zero padding, a control, so the scan never leaves the line.
     __device__ __forceinline__ Str str_swar(uint32_t q) const {
         Str r{0, 0, 0, false};
-        uint32_t d = 0;
+        const uint32_t q0 = q;
+        uint32_t shrink = 0;                       // raw bytes minus decoded bytes of the escapes
         for (;;) {
-            const uint64_t x = ld8(q);
-            const uint64_t m = str_stop8(x);
-            if (!m) {
-                q += 8;
-                d += 8;
+            // 16 bytes per step, both loads in flight together
+            const uint64_t x0 = ld8(q), x1 = ld8(q + 8);
+            const uint64_t m0 = str_stop8(x0), m1 = str_stop8(x1);
+            if (!(m0 | m1)) {
+                q += 16;
                 continue;
             }
-            const uint32_t k = (uint32_t)__builtin_ctzll(m) >> 3;
+            const uint32_t k = m0 ? (uint32_t)__builtin_ctzll(m0) >> 3 : 8 + ((uint32_t)__builtin_ctzll(m1) >> 3);
             q += k;
-            d += k;
-            const uint32_t c = (uint32_t)(x >> (8 * k)) & 0xFF;
+            const uint32_t c = (uint32_t)((m0 ? x0 : x1) >> (8 * (k & 7))) & 0xFF;
             if (c == '"') break;
-            if (c == '\\') {
-                const Esc e = esc(q);
-                if (e.err) { r.err = e.err; return r; }
-                d += (uint32_t)e.k;
-                q += e.adv;
-                r.esc = true;
-                continue;
+            // an escape, a UTF-8 sequence or an error: out of line
+            const uint32_t st = str_step((const PJ_LDS uint8_t *)s, n, q, c);
+            if (!st) {
+                r.err = PJ_REC_STRING;
+                return r;
             }
-            const uint32_t extra = utf8_extra(c, ld8(q));
-            if (!extra) { r.err = PJ_REC_STRING; return r; }
-            q += 1 + extra;
-            d += 1 + extra;
+            const uint32_t adv = st & 0xFF, dk = (st >> 8) & 0xFF;
+            q += adv;
+            shrink += adv - dk;
+            r.esc |= c == '\\';
         }
         r.end = q;
-        r.dlen = d;
+        r.dlen = q - q0 - shrink;
         return r;
     }
     // copy the decoded string (content from q, described by r) to dst
@@ -1609,6 +1633,14 @@ __device__ __noinline__ uint64_t fskip(const FL &F, uint32_t p) {
 #define PJ_TAPE_WORDS 32
 #endif
 constexpr int TAPE_WORDS = PJ_TAPE_WORDS;
+// The tapes are stored word by word across lines (word k of line l at
+// tape[k * lines + l]), so the lanes of a wave reading or writing the same
+// word of their lines touch adjacent addresses.
+struct Tape {
+    uint64_t *p;        // word 0 of the line
+    uint64_t s;         // lines (the stride between words)
+    __device__ __forceinline__ uint64_t &operator[](uint32_t k) const { return p[(uint64_t)k * s]; }
+};
 __device__ __forceinline__ uint64_t tape_str(uint32_t q, const Str &r) {
     return (uint64_t)q | ((uint64_t)r.end << 16) | ((uint64_t)r.dlen << 32) | ((uint64_t)r.esc << 48);
 }
@@ -1621,7 +1653,7 @@ __device__ __forceinline__ uint64_t tape_str(uint32_t q, const Str &r) {
 // With TAPE, pass 0 also records the line's tape at T.
 template <bool WRITE, class FL, bool TAPE = false>
 __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W, const uint32_t *rel,
-                                     uint64_t *T = nullptr) {
+                                     Tape T = Tape{nullptr, 0}) {
     constexpr bool VAL = WRITE || TAPE;             // integer values are needed
     const uint32_t n = F.n;
     if (n == 0) return PJ_REC_EMPTY;
@@ -1793,54 +1825,65 @@ __device__ __forceinline__ int fline(const FL &F, LineRec &R, const BlockCols *W
 #undef FL_UNKNOWN
 
 // Writing a line from its tape: the stores and copies of fline<true>, in the
-// same order, without walking the line again.
-__device__ __forceinline__ void tape_write(const FLine &F, const uint64_t *T, const BlockCols *W, const uint32_t *rel) {
-    const uint64_t M = T[2];
+// same order, without walking the line again.  The first TAPE_PRE words come
+// from registers (loaded together, ahead of the tile, by tape_prefetch); the
+// rest, for lines with many items, from memory.
+constexpr int TAPE_PRE = 12;
+__device__ __forceinline__ void tape_prefetch(const Tape &T, uint64_t *w) {
+#pragma unroll
+    for (int k = 0; k < TAPE_PRE; k++) w[k] = T[k];
+}
+__device__ __forceinline__ uint64_t tape_word(const Tape &T, const uint64_t *w, uint32_t k) {
+    uint64_t v = 0;
+#pragma unroll
+    for (int j = 3; j < TAPE_PRE; j++) v = k == (uint32_t)j ? w[j] : v;
+    return k < (uint32_t)TAPE_PRE ? v : T[k];
+}
+__device__ __forceinline__ void tape_copy(const FLine &F, uint64_t w, uint8_t *dst) {
+    const uint32_t dl = (uint32_t)(w >> 32) & 0xFFFF;
+    if (dl) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, dl, ((w >> 48) & 1) != 0}, dst);
+}
+template <bool COPY = true>
+__device__ __forceinline__ void tape_write(const FLine &F, const Tape &T, const uint64_t *w, const BlockCols *W,
+                                           const uint32_t *rel) {
+    const uint64_t M = w[2];
     const uint32_t flags = (uint32_t)M & 0xFF, status = (uint32_t)(M >> 8) & 0xFF, cat_fl = (uint32_t)(M >> 16) & 0xFF;
     const uint32_t nu = (uint32_t)(M >> 24) & 0xFF, nt = (uint32_t)(M >> 32) & 0xFF;
     uint32_t cat_len = 0, name_len = 0;
     if ((flags & PJ_PET_HAS_CATEGORY) && (cat_fl & PJ_SUB_HAS_NAME)) {
-        const uint64_t w = T[4];
-        cat_len = (uint32_t)(w >> 32) & 0xFFFF;
-        if (cat_len) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, cat_len, ((w >> 48) & 1) != 0},
-                            W->cat_name + rel[C_CATB]);
+        cat_len = (uint32_t)(w[4] >> 32) & 0xFFFF;
+        if (COPY) tape_copy(F, w[4], W->cat_name + rel[C_CATB]);
     }
     if (flags & PJ_PET_HAS_NAME) {
-        const uint64_t w = T[3];
-        name_len = (uint32_t)(w >> 32) & 0xFFFF;
-        if (name_len) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, name_len, ((w >> 48) & 1) != 0},
-                             W->name + rel[C_NAMEB]);
+        name_len = (uint32_t)(w[3] >> 32) & 0xFFFF;
+        if (COPY) tape_copy(F, w[3], W->name + rel[C_NAMEB]);
     }
-    uint32_t tw = 5;
     uint32_t u = rel[C_URLS], ub = rel[C_URLB];
     for (uint32_t k = 0; k < nu; k++) {
-        const uint64_t w = T[tw++];
-        const uint32_t dl = (uint32_t)(w >> 32) & 0xFFFF;
-        if (dl) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, dl, ((w >> 48) & 1) != 0}, W->url + ub);
-        ub += dl;
+        const uint64_t x = tape_word(T, w, 5 + k);
+        if (COPY) tape_copy(F, x, W->url + ub);
+        ub += (uint32_t)(x >> 32) & 0xFFFF;
         W->url_off[u] = W->b_url + ub;
         u++;
     }
     uint32_t g = rel[C_TAGS], gb = rel[C_TAGB];
     for (uint32_t k = 0; k < nt; k++) {
-        const int64_t tid = (int64_t)T[tw];
-        const uint64_t w = T[tw + 1];
-        tw += 2;
-        const uint32_t tfl = (uint32_t)(w >> 49) & 3;
-        const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? (uint32_t)(w >> 32) & 0xFFFF : 0;
+        const int64_t tid = (int64_t)tape_word(T, w, 5 + nu + 2 * k);
+        const uint64_t x = tape_word(T, w, 6 + nu + 2 * k);
+        const uint32_t tfl = (uint32_t)(x >> 49) & 3;
+        const uint32_t tl = (tfl & PJ_SUB_HAS_NAME) ? (uint32_t)(x >> 32) & 0xFFFF : 0;
         W->tag_id[g] = tid;
         W->tag_flags[g] = (uint8_t)tfl;
         W->tag_name_off[g] = W->b_tag + gb + tl;
-        if (tl) F.copy((uint32_t)w & 0xFFFF, Str{0, (uint32_t)(w >> 16) & 0xFFFF, tl, ((w >> 48) & 1) != 0},
-                       W->tag_name + gb);
+        if (COPY && tl) tape_copy(F, x, W->tag_name + gb);
         gb += tl;
         g++;
     }
     const uint32_t row = rel[C_PETS];
-    W->id[row] = (int64_t)T[0];
+    W->id[row] = (int64_t)w[0];
     W->flags[row] = (uint8_t)flags;
     W->status[row] = (uint8_t)status;
-    W->cat_id[row] = (int64_t)T[1];
+    W->cat_id[row] = (int64_t)w[1];
     W->cat_flags[row] = (uint8_t)cat_fl;
     W->name_off[row] = W->b_name + rel[C_NAMEB] + name_len;
     W->cat_name_off[row] = W->b_cat + rel[C_CATB] + cat_len;
@@ -2089,6 +2132,36 @@ __device__ __forceinline__ void load_tile(const DecParams &P, uint8_t *tile, uin
     }
 }
 
+// The line starts of a block's cnt lines from l0 (and the end of the last)
+// into sh_ls, and the block cut into sub-tiles: maximal runs of lines whose
+// bytes fit the LDS tile (normally one), their first lines in sh_sub.
+// Returns the number of sub-tiles.  All threads.
+template <int TILE>
+__device__ __forceinline__ uint32_t block_subtiles(const DecParams &P, uint64_t l0, uint32_t cnt, uint64_t *sh_ls,
+                                                   uint16_t *sh_sub, uint32_t *sh_nsub) {
+    const uint32_t t = threadIdx.x;
+    if (t < cnt) sh_ls[t] = P.line_start[l0 + t];
+    if (t == 0) sh_ls[cnt] = P.line_start[l0 + cnt];  // the end of the last line (cnt may equal BT)
+    __syncthreads();
+    if (t == 0) {
+        uint32_t j = 0;
+        if (min(sh_ls[cnt], P.len) - (sh_ls[0] & ~15ull) <= TILE) sh_sub[j++] = 0;
+        else {
+            for (uint32_t k = 0; k < cnt;) {
+                sh_sub[j++] = (uint16_t)k;
+                const uint64_t a = sh_ls[k] & ~15ull;
+                uint32_t k2 = k + 1;
+                while (k2 < cnt && min(sh_ls[k2 + 1], P.len) - a <= TILE) k2++;
+                k = k2;
+            }
+        }
+        sh_sub[j] = (uint16_t)cnt;
+        *sh_nsub = j;
+    }
+    __syncthreads();
+    return *sh_nsub;
+}
+
 // Whether any thread of the block holds p (all threads call; one LDS word).
 __device__ __forceinline__ bool block_any(bool p, uint32_t *flag) {
     if (threadIdx.x == 0) *flag = 0;
@@ -2131,8 +2204,10 @@ template <int BT, int TILE, int LONG, int LPB = BT, bool TAPE = false>
 __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     static_assert(LONG < 65536, "tape positions of per-thread lines are 16-bit");
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
-    __shared__ uint64_t spec[TILE / 64 + 1];
-    __shared__ uint64_t badm[TILE / 64 + 1];
+    // the specials and bad-byte bitmaps; after pass 0 also the scan's
+    // scratch and the string staging window
+    __shared__ __attribute__((aligned(16))) uint64_t bmaps[2 * (TILE / 64 + 1)];
+    uint64_t *const spec = bmaps, *const badm = bmaps + (TILE / 64 + 1);
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_ls[LPB + 1];             // the block's line starts, then its end
     __shared__ uint16_t sh_sub[LPB + 1];            // sub-tile boundaries (block-local line indices)
@@ -2146,26 +2221,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
     const uint32_t cnt = (uint32_t)min((uint64_t)LPB, P.lines - l0);
     const uint64_t l = l0 + t;
     const bool live = t < cnt;
-    if (t < cnt) sh_ls[t] = P.line_start[l0 + t];
-    if (t == 0) sh_ls[cnt] = P.line_start[l0 + cnt];  // the end of the last line (cnt may equal BT)
-    __syncthreads();
-    if (t == 0) {
-        uint32_t j = 0;
-        if (min(sh_ls[cnt], P.len) - (sh_ls[0] & ~15ull) <= TILE) sh_sub[j++] = 0;
-        else {
-            for (uint32_t k = 0; k < cnt;) {
-                sh_sub[j++] = (uint16_t)k;
-                const uint64_t a = sh_ls[k] & ~15ull;
-                uint32_t k2 = k + 1;
-                while (k2 < cnt && min(sh_ls[k2 + 1], P.len) - a <= TILE) k2++;
-                k = k2;
-            }
-        }
-        sh_sub[j] = (uint16_t)cnt;
-        sh_nsub = j;
-    }
-    __syncthreads();
-    const uint32_t nsub = sh_nsub;
+    const uint32_t nsub = block_subtiles<TILE>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
     uint64_t gs = 0;
     uint32_t n = 0;
     if (live) {
@@ -2193,26 +2249,11 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 s0 = (uint32_t)(gs - a0);
                 ta0 = a0;
                 ttb = tb;
-#ifdef PJ_FORCE_BITMAPS
-            }
-            __syncthreads();
-            tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
-            __syncthreads();
-            if (mine) {
-#endif
-#if PJ_PROBE == 1
-                if (false) {
-#else
                 if (!longl) {
-#endif
                     // strings are scanned and checked byte class by byte
                     // class as the walk meets them: no bitmaps needed
-#ifdef PJ_FORCE_BITMAPS
-                    const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
-#else
                     const FLine F{(const PJ_LDS uint8_t *)(tile + s0), nullptr, s0, n};
-#endif
-                    if constexpr (TAPE) code = fline<false, FLine, true>(F, r, nullptr, nullptr, P.tape + l * TAPE_WORDS);
+                    if constexpr (TAPE) code = fline<false, FLine, true>(F, r, nullptr, nullptr, Tape{P.tape + l, P.lines});
                     else code = fline<false>(F, r, nullptr, nullptr);
                     if (TAPE && code == PJ_TAPE_FULL) {
                         longl = true;
@@ -2275,6 +2316,27 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
 #pragma unroll
         for (int k = 0; k < PJ_DEC_NCNT; k++) agg[k] = a32[k];
     }
+    if constexpr (TAPE) {
+        // split decode: the block's offsets and totals go to memory, and the
+        // scan and the writer kernels take it from there (no waiting here)
+        if (live) {
+            const uint64_t L = P.lines;
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) P.lpos[k * L + l] = pos[k];
+            const bool wave = longl && !general && !bad && code == 0;
+            P.lpos[PJ_DEC_NCNT * L + l] = (uint32_t)code | (general ? LK_GENERAL : 0u) | (wave ? LK_WAVE : 0u) |
+                                          (bad ? LK_BAD : 0u);
+            // lines of the whole wave or the general parser are written by k_dec_long
+            if (code == 0 && (wave || general)) P.long_list[atomicAdd(P.long_count, 1ull)] = l;
+        }
+        if (t < PJ_DEC_NCNT) {
+            uint64_t x = 0;
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) x = k == (int)t ? agg[k] : x;
+            P.bagg[b * PJ_DEC_NCNT + t] = x;
+        }
+        return;
+    }
     if (t < 64) {
         vlb_publish(P.state_parse, b, agg, (int)t);
         uint64_t excl[PJ_DEC_NCNT];
@@ -2315,9 +2377,6 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                       base[C_URLB] + agg[C_URLB] <= o.cap_url_bytes && base[C_TAGS] + agg[C_TAGS] <= o.cap_tags &&
                       base[C_TAGB] + agg[C_TAGB] <= o.cap_tag_name_bytes;
     if (!room) return;
-#if PJ_PROBE >= 1
-    return;
-#endif
     BlockCols W;
     W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
     W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
@@ -2356,12 +2415,12 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 uint32_t rel[PJ_DEC_NCNT];
 #pragma unroll
                 for (int k = 0; k < PJ_DEC_NCNT; k++) rel[k] = pos[k];
-#ifdef PJ_FORCE_BITMAPS
-                const FLine F{(const PJ_LDS uint8_t *)(tile + s0), (const PJ_LDS uint64_t *)spec, s0, n};
-#else
                 const FLine F{(const PJ_LDS uint8_t *)(tile + s0), nullptr, s0, n};
-#endif
-                if constexpr (TAPE) tape_write(F, P.tape + l * TAPE_WORDS, &W, rel);
+                if constexpr (TAPE) {
+                    uint64_t tw[TAPE_PRE];
+                    tape_prefetch(Tape{P.tape + l, P.lines}, tw);
+                    tape_write(F, Tape{P.tape + l, P.lines}, tw, &W, rel);
+                }
                 else fline<true>(F, r, &W, rel);
             } else {
                 uint64_t gp[PJ_DEC_NCNT];
@@ -2378,6 +2437,203 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         if (nsub > 1) __syncthreads();
     }
     (void)ta0;
+}
+
+// ---------------------------------------------------------------- split decode writers
+// A line block's slices of the output columns, from the block's first
+// offsets.
+__device__ __forceinline__ BlockCols block_cols(const pj_pet_columns &o, const uint64_t *base) {
+    BlockCols W;
+    W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
+    W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
+    W.name_off = o.name_off + base[C_PETS] + 1; W.cat_name_off = o.cat_name_off + base[C_PETS] + 1;
+    W.photo_off = o.photo_off + base[C_PETS] + 1; W.tag_off = o.tag_off + base[C_PETS] + 1;
+    W.url_off = o.url_off + base[C_URLS] + 1; W.tag_name_off = o.tag_name_off + base[C_TAGS] + 1;
+    W.tag_id = o.tag_id + base[C_TAGS]; W.tag_flags = o.tag_flags + base[C_TAGS];
+    W.name = o.name_bytes + base[C_NAMEB]; W.cat_name = o.cat_name_bytes + base[C_CATB];
+    W.url = o.url_bytes + base[C_URLB]; W.tag_name = o.tag_name_bytes + base[C_TAGB];
+    W.b_name = base[C_NAMEB]; W.b_cat = base[C_CATB]; W.b_urls = base[C_URLS]; W.b_url = base[C_URLB];
+    W.b_tags = base[C_TAGS]; W.b_tag = base[C_TAGB];
+    return W;
+}
+
+// Do the call's totals fit the output capacities?  (Nothing is written
+// otherwise: the call reports PJ_ERR_CAPACITY with the sizes it needs.)
+__device__ __forceinline__ bool dec_room(const DecParams &P) {
+    const pj_pet_columns &o = P.o;
+    const uint64_t *T = P.totals;
+    return T[C_PETS] <= o.cap_pets && T[C_NAMEB] <= o.cap_name_bytes && T[C_CATB] <= o.cap_cat_name_bytes &&
+           T[C_URLS] <= o.cap_urls && T[C_URLB] <= o.cap_url_bytes && T[C_TAGS] <= o.cap_tags &&
+           T[C_TAGB] <= o.cap_tag_name_bytes;
+}
+
+// Scan of the validating kernel's block totals: BT blocks per workgroup,
+// workgroups in ticket order chained by the vector look-back; bbase gets
+// each line block's first offsets, totals the call's sums.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_dec_bscan(DecParams P) {
+    __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint64_t sh_sb, sh_pre[PJ_DEC_NCNT];
+    const uint32_t t = threadIdx.x;
+    if (t == 0) sh_sb = atomicAdd(P.bticket, 1ull);
+    __syncthreads();
+    const uint64_t sb = sh_sb, i = sb * BT + t;
+    const bool in = i < P.nblocks;
+    uint64_t excl[PJ_DEC_NCNT], agg[PJ_DEC_NCNT];
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++)
+        excl[k] = block_excl_scan<BT>(in ? P.bagg[i * PJ_DEC_NCNT + k] : 0ull, sh_scan, &agg[k]);
+    if (t < 64) {
+        vlb_publish(P.bstate, sb, agg, (int)t);
+        uint64_t pre[PJ_DEC_NCNT];
+        vlb_resolve(P.bstate, sb, agg, pre);
+        if (t < PJ_DEC_NCNT) {
+            uint64_t x = 0;
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) x = k == (int)t ? pre[k] : x;
+            sh_pre[t] = x;
+            if ((sb + 1) * BT >= P.nblocks) {
+                uint64_t y = 0;
+#pragma unroll
+                for (int k = 0; k < PJ_DEC_NCNT; k++) y = k == (int)t ? pre[k] + agg[k] : y;
+                P.totals[t] = y;
+            }
+        }
+    }
+    __syncthreads();
+    if (in) {
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) P.bbase[i * PJ_DEC_NCNT + k] = sh_pre[k] + excl[k];
+    }
+}
+
+// Writer of the split decode, one workgroup per line block of the
+// validating kernel: the block's lines are tiled into LDS again (the same
+// sub-tiles), and each thread writes its fast-path line from its tape at the
+// offsets the scan gave.  Invalid lines get their error slot; lines of the
+// whole wave or the general parser are left to k_dec_long.
+template <int BT, int TILE, int LPB>
+__global__ __launch_bounds__(BT, 2) void k_dec_write(DecParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
+    __shared__ uint64_t sh_ls[LPB + 1];
+    __shared__ uint16_t sh_sub[LPB + 1];
+    __shared__ uint32_t sh_nsub;
+    const uint32_t t = threadIdx.x;
+    const uint64_t L = P.lines, b = blockIdx.x, l0 = b * LPB;
+    const uint32_t cnt = (uint32_t)min((uint64_t)LPB, L - l0);
+    const uint64_t l = l0 + t;
+    const bool live = t < cnt;
+    const pj_pet_columns &o = P.o;
+    const uint32_t nsub = block_subtiles<TILE>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
+    if (b == 0 && t == 0) {
+        o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
+        o.url_off[0] = 0; o.tag_name_off[0] = 0;
+    }
+    uint32_t info = 0, rel[PJ_DEC_NCNT];
+    uint64_t base[PJ_DEC_NCNT];
+#pragma unroll
+    for (int k = 0; k < PJ_DEC_NCNT; k++) {
+        base[k] = P.bbase[b * PJ_DEC_NCNT + k];
+        rel[k] = live ? P.lpos[k * L + l] : 0u;
+    }
+    if (live) info = P.lpos[PJ_DEC_NCNT * L + l];
+    const uint32_t code = info & 0xFF;
+    if (live && code) {
+        const uint64_t e = base[C_ERRS] + rel[C_ERRS];
+        if (e < P.err_cap) {
+            P.err_line[e] = l;
+            P.err_code[e] = (uint8_t)code;
+            if (info & LK_BAD) P.dq[atomicAdd(P.dq_count, 1ull)] = e;
+        }
+    }
+    if (!dec_room(P)) return;
+    const bool fastl = live && code == 0 && !(info & (LK_WAVE | LK_GENERAL));
+    uint64_t gs = 0;
+    uint32_t n = 0;
+    if (live) {
+        gs = sh_ls[t];
+        n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
+    }
+    // the tape's first words, in flight while the tile loads
+    uint64_t tw[TAPE_PRE];
+    if (fastl) tape_prefetch(Tape{P.tape + l, L}, tw);
+    for (uint32_t j = 0; j < nsub; j++) {
+        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
+        const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
+        if (tb <= TILE) {                           // a longer sub-tile is one line of the general parser
+            load_tile<BT>(P, tile, a0, g0, tb, (uint32_t)((tb + 63) >> 6));
+            __syncthreads();
+        }
+        const uint32_t s0 = (uint32_t)(gs - a0);
+        if (fastl && t >= ka && t < kb) {
+            const BlockCols W = block_cols(o, base);
+            const FLine F{(const PJ_LDS uint8_t *)(tile + s0), nullptr, s0, n};
+            tape_write(F, Tape{P.tape + l, L}, tw, &W, rel);
+        }
+        if (nsub > 1) __syncthreads();              // the tile is reused by the next sub-tile
+    }
+}
+
+// Lines read by a whole wave (long lines, and lines with more items than
+// the tape holds), one 64-thread workgroup per line at a time: the line is
+// tiled into LDS with its bitmaps and written by the wave-parallel walk.
+// Lines of the general parser are read again from the input by one thread.
+template <int TILE, int LPB>
+__global__ __launch_bounds__(64) void k_dec_long(DecParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
+    __shared__ uint64_t spec[TILE / 64 + 1];
+    __shared__ uint64_t badm[TILE / 64 + 1];
+    __shared__ uint64_t sh_scan[1];
+    const uint64_t cnt = *P.long_count;
+    if (!dec_room(P)) return;
+    const pj_pet_columns &o = P.o;
+    const uint64_t L = P.lines;
+    for (uint64_t i = blockIdx.x; i < cnt; i += gridDim.x) {
+        const uint64_t l = P.long_list[i];
+        const uint64_t gs = P.line_start[l], ge = P.line_start[l + 1];
+        const uint32_t n = (uint32_t)(ge - 1 - gs);
+        if (P.lpos[PJ_DEC_NCNT * L + l] & LK_GENERAL) {
+            // the general parser, from the input (the measuring walk, then the writing walk)
+            if (threadIdx.x == 0) {
+                uint64_t gp[PJ_DEC_NCNT];
+#pragma unroll
+                for (int k = 0; k < PJ_DEC_NCNT; k++) gp[k] = P.bbase[(l / LPB) * PJ_DEC_NCNT + k] + P.lpos[k * L + l];
+                const Src S{P.in, P.len, nullptr};
+                LineInfo Li;
+                run_line(P, S, gs, n, true, false, Li, nullptr);
+                run_line(P, S, gs, n, true, true, Li, gp);
+            }
+            continue;
+        }
+        const uint64_t a0 = gs & ~15ull, tb = min(ge, P.len) - a0;
+        const uint32_t nw = (uint32_t)((tb + 63) >> 6);
+        load_tile<64>(P, tile, a0, gs, tb, nw);
+        __syncthreads();
+        tile_bitmaps<64>(tile, nw, spec, badm, sh_scan);
+        __syncthreads();
+        const uint64_t pb = l / LPB;
+        uint64_t base[PJ_DEC_NCNT];
+        uint32_t rel[PJ_DEC_NCNT];
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) {
+            base[k] = uniform_u64(P.bbase[pb * PJ_DEC_NCNT + k]);
+            rel[k] = __builtin_amdgcn_readfirstlane(P.lpos[k * L + l]);
+        }
+        BlockCols W;
+        W.id = o.id + base[C_PETS]; W.flags = o.flags + base[C_PETS]; W.status = o.status + base[C_PETS];
+        W.cat_id = o.cat_id + base[C_PETS]; W.cat_flags = o.cat_flags + base[C_PETS];
+        W.name_off = o.name_off + base[C_PETS] + 1; W.cat_name_off = o.cat_name_off + base[C_PETS] + 1;
+        W.photo_off = o.photo_off + base[C_PETS] + 1; W.tag_off = o.tag_off + base[C_PETS] + 1;
+        W.url_off = o.url_off + base[C_URLS] + 1; W.tag_name_off = o.tag_name_off + base[C_TAGS] + 1;
+        W.tag_id = o.tag_id + base[C_TAGS]; W.tag_flags = o.tag_flags + base[C_TAGS];
+        W.name = o.name_bytes + base[C_NAMEB]; W.cat_name = o.cat_name_bytes + base[C_CATB];
+        W.url = o.url_bytes + base[C_URLB]; W.tag_name = o.tag_name_bytes + base[C_TAGB];
+        W.b_name = base[C_NAMEB]; W.b_cat = base[C_CATB]; W.b_urls = base[C_URLS]; W.b_url = base[C_URLB];
+        W.b_tags = base[C_TAGS]; W.b_tag = base[C_TAGB];
+        LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+        fline_wave<true>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, (uint32_t)(gs - a0), n, r, &W, rel);
+        __syncthreads();                            // the tile is reused by the next line
+    }
 }
 
 // ---------------------------------------------------------------- error codes
@@ -2438,6 +2694,26 @@ hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
 
 hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
     hipLaunchKernelGGL((pj::k_dec_errcode<64, 8192>), dim3(8192), dim3(64), 0, st, P);
+    return hipGetLastError();
+}
+
+constexpr int DEC_BSCAN_BT = 256;
+int pj_dec_bscan_block() { return DEC_BSCAN_BT; }
+
+hipError_t pj_launch_dec_bscan(const DecParams &P, hipStream_t st) {
+    const uint64_t g = (P.nblocks + DEC_BSCAN_BT - 1) / DEC_BSCAN_BT;
+    hipLaunchKernelGGL((pj::k_dec_bscan<DEC_BSCAN_BT>), dim3((unsigned)g), dim3(DEC_BSCAN_BT), 0, st, P);
+    return hipGetLastError();
+}
+
+hipError_t pj_launch_dec_write(const DecParams &P, hipStream_t st) {
+    hipLaunchKernelGGL((pj::k_dec_write<DEC_LINE_BT, DEC_TILE, DEC_LPB>), dim3((unsigned)P.nblocks), dim3(DEC_LINE_BT), 0,
+                       st, P);
+    return hipGetLastError();
+}
+
+hipError_t pj_launch_dec_long(const DecParams &P, hipStream_t st) {
+    hipLaunchKernelGGL((pj::k_dec_long<DEC_TILE, DEC_LPB>), dim3(1024), dim3(64), 0, st, P);
     return hipGetLastError();
 }
 

@@ -267,13 +267,15 @@ __device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
 #define PJ_LDS
 #endif
 __device__ __forceinline__ uint64_t lds_u64(const PJ_LDS uint8_t *p) { return *(const PJ_LDS uint64_t *)p; }
-// n bytes from an LDS buffer (readable up to 8 bytes past the end) to dst
+// n bytes from an LDS buffer (readable up to 8 bytes past the end) to dst:
+// 16-byte stores at any address while 16 bytes remain (one store
+// instruction per 16 bytes: scattered per-thread copies are bound by the
+// number of store instructions), then the exact tail.
 __device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t *src, uint32_t n) {
     uint32_t k = 0;
     for (; k + 16 <= n; k += 16) {
         const uint64_t a = lds_u64(src + k), b = lds_u64(src + k + 8);
-        stu64(dst + k, a);
-        stu64(dst + k + 8, b);
+        *reinterpret_cast<uint4 *>(dst + k) = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
     }
     if (n - k >= 8) { stu64(dst + k, lds_u64(src + k)); k += 8; }
     if (k < n) st_tail(dst + k, lds_u64(src + k), n - k);

@@ -56,6 +56,17 @@ struct DecParams {
     uint64_t *dq;
     uint64_t *tape;            // per line: 32 words of the validating walk's results, or null
     unsigned long long *dq_count;
+    // split decode (with the tape): the validating kernel stores per line its
+    // offsets inside its block (lpos, 8 counters column by column, then the
+    // line's code and kind in row 8) and per block the counter totals (bagg);
+    // a scan turns those into each block's first offsets (bbase, with its own
+    // look-back words bstate); the writer kernels then need no waiting
+    uint32_t *lpos;
+    uint64_t *bagg, *bbase, *bstate;
+    uint64_t nblocks;          // line blocks of the validating kernel
+    uint64_t *long_list;       // lines read by a whole wave, written by k_dec_long
+    unsigned long long *long_count;
+    unsigned long long *bticket;  // block ticket of the scan kernel
     // 1: block b of each kernel takes its input in launch order (no ticket
     // atomic) and bounds its look-back wait by spin_limit wall-clock ticks;
     // a kernel whose wait ran out sets its ticket word to 1 and is redone
@@ -74,6 +85,12 @@ hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st);
+// the split decode after the validating kernel: block scan, writers
+hipError_t pj_launch_dec_bscan(const DecParams &P, hipStream_t st);
+hipError_t pj_launch_dec_write(const DecParams &P, hipStream_t st);
+
+hipError_t pj_launch_dec_long(const DecParams &P, hipStream_t st);
+int pj_dec_bscan_block();
 int pj_dec_index_block();
 // Device address of this GPU's fixed encode scratch (PJ_NOALLOC_SCRATCH_WORDS
 // u64); resolved once per device, with that device current.
