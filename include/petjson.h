@@ -36,7 +36,10 @@ typedef enum pj_status {
     PJ_ERR_CAPACITY = 2,      /* an output buffer is too small; sizes reported  */
     PJ_ERR_DEVICE = 3,        /* a HIP call failed (message via pj_last_error)   */
     PJ_ERR_NO_DEVICE = 4,     /* no usable gfx950 device                        */
-    PJ_ERR_OUT_OF_MEMORY = 5
+    PJ_ERR_OUT_OF_MEMORY = 5,
+    PJ_ERR_SYNTAX = 6         /* an array document's frame is malformed ('[',
+                                 the top-level commas, the closing ']'); no
+                                 column is written                           */
 } pj_status;
 
 /* ------------------------------------------------------------ record model */
@@ -217,6 +220,26 @@ pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len,
                          pj_pet_columns *out, uint64_t *err_line,
                          uint8_t *err_code, uint64_t err_cap,
                          pj_decode_result *res);
+/* Parse one JSON array document of Pets into columns
+ * (readValue(bytes, List<Pet>), the reference's bulk shape "array of Pet",
+ * petstore.json:133-140, read as in MyEntityConfig.java:34).  Its frame — '['
+ * after optional whitespace, elements separated by the commas at depth 1
+ * outside strings, the closing ']', then only whitespace — must be intact,
+ * else PJ_ERR_SYNTAX is returned and nothing is written (so are "[,]" and a
+ * trailing comma: an element may not be blank; "[]" and "[ ]" hold none).
+ * Each element is then read exactly as one NDJSON line (whitespace,
+ * newlines included, may surround and separate its tokens) and reported by
+ * its zero-based index like a line: valid ones become rows in order,
+ * invalid ones are listed in err_line / err_code.  Device / host pointers as
+ * pj_decode_device / pj_decode_host. */
+pj_status pj_decode_array_device(pj_ctx *ctx, const uint8_t *in, uint64_t len,
+                                 pj_pet_columns *out, uint64_t *err_line,
+                                 uint8_t *err_code, uint64_t err_cap,
+                                 pj_decode_result *res);
+pj_status pj_decode_array_host(pj_ctx *ctx, const uint8_t *in, uint64_t len,
+                               pj_pet_columns *out, uint64_t *err_line,
+                               uint8_t *err_code, uint64_t err_cap,
+                               pj_decode_result *res);
 /* Column capacities that always suffice for decoding `len` input bytes.
  * The error list needs at most one entry per line, and `len` bytes hold at
  * most `len` lines (blank lines are errors too); a call whose err_cap is too

@@ -428,8 +428,11 @@ bool dec_cols_ok(const pj_pet_columns *o) {
     return true;
 }
 
+// NDJSON (array = false) or one array document (array = true): the line
+// stages are the same, only the index stage differs (newlines, or the
+// array's frame: its elements' starts).
 pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
-                      uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+                      uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array = false) {
     pj_status s = bind(ctx);
     if (s) return s;
     if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
@@ -442,10 +445,15 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
     uint64_t ls_cap = len / 128 + 16;
     for (int attempt = 0; attempt < 2; attempt++) {
         const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
-        // layout (u64 units): header 16 | dummy 32 | state_idx gidx | line_start ls_cap
-        // header: 0-1 tickets, 2 line count, 4-11 totals, 12 lines off the fast path,
-        //         13 deferred error-code queue length
-        const uint64_t o_dummy = 16, o_sidx = 48, o_ls = o_sidx + gidx;
+        // layout (u64 units): header 16 | dummy 32 | array frame scalars 8 |
+        //   state_idx gidx | (arrays: block summaries, entry states) | line_start ls_cap
+        // header: 0-1 tickets, 2 line count, 3 blank lines, 4-11 totals,
+        //         12 lines off the fast path, 13 deferred error-code queue
+        //         length, 14 lines for k_dec_long, 15 scan ticket
+        const uint64_t o_dummy = 16, o_arr = 48, o_sidx = 56;
+        const uint64_t ga = array ? pj_arr_blocks(nblk64) : 0;
+        const uint64_t o_bsum = o_sidx + gidx, o_bpre = o_bsum + (ga * sizeof(FS) + 7) / 8;
+        const uint64_t o_ls = o_bpre + ga;
         PJ_HIP(ctx->index.ensure((o_ls + ls_cap) * 8 + 64));
         uint64_t *X = static_cast<uint64_t *>(ctx->index.p);
         DecParams P;
@@ -465,6 +473,11 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.tickets = reinterpret_cast<unsigned long long *>(X);
         P.dummy = reinterpret_cast<uint32_t *>(X + o_dummy);
         P.gq_count = reinterpret_cast<unsigned long long *>(X + 12);
+        P.empty_count = reinterpret_cast<unsigned long long *>(X + 3);
+        P.array_doc = array ? 1 : 0;
+        P.arr = X + o_arr;
+        P.arr_bsum = reinterpret_cast<FS *>(X + o_bsum);
+        P.arr_bpre = X + o_bpre;
         // blocks in launch order with bounded look-back waits; a kernel
         // whose wait ran out (its ticket word set) is redone in ticket order
         P.order_by_id = 1;
@@ -474,13 +487,25 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             if ((s = mark(ctx))) return s;
             PJ_HIP(pj_launch_fill_u64(X, 16, 0, ctx->stream));
             PJ_HIP(pj_launch_fill_u64(X + o_sidx, gidx, 0, ctx->stream));
+            if (array) {
+                PJ_HIP(pj_launch_fill_u64(X + o_arr, 8, 0, ctx->stream));
+                PJ_HIP(pj_launch_fill_u64(X + o_arr, 1, ~0ull, ctx->stream));      // first non-whitespace
+                PJ_HIP(pj_launch_fill_u64(X + o_arr + 2, 1, ~0ull, ctx->stream));  // the close
+            }
             if ((s = mark(ctx))) return s;
-            if (nblk64) PJ_HIP(pj_launch_dec_index(P, ctx->stream));
+            if (array) PJ_HIP(pj_launch_arr_frame(P, ctx->stream));
+            else if (nblk64) PJ_HIP(pj_launch_dec_index(P, ctx->stream));
             if ((s = mark(ctx))) return s;
             PJ_HIP(hipMemcpyAsync(ctx->pinned, X, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+            if (array) PJ_HIP(hipMemcpyAsync(ctx->pinned + 16, X + o_arr, 8 * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                             ctx->stream));
             PJ_HIP(hipStreamSynchronize(ctx->stream));
-            if (!P.order_by_id || ctx->pinned[0] == 0) break;
+            if (array || !P.order_by_id || ctx->pinned[0] == 0) break;
             P.order_by_id = 0;
+        }
+        if (array && ctx->pinned[16 + 4] == 0) {
+            (void)finish_timing(ctx);
+            return fail(PJ_ERR_SYNTAX, "not a JSON array: '[', the top-level commas or the closing ']' are malformed");
         }
         const int index_order = P.order_by_id;
         const uint64_t lines = ctx->pinned[2];
@@ -526,7 +551,7 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             if (split) PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
             else PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
             PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
-            PJ_HIP(pj_launch_fill_u64(X + 4, 12, 0, ctx->stream));     // totals and counters
+            PJ_HIP(pj_launch_fill_u64(X + 3, 13, 0, ctx->stream));     // totals and counters
             if ((s = mark(ctx))) return s;
             if (lines) {
                 PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
@@ -558,6 +583,13 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         const uint64_t *T = ctx->pinned + 4;
         res->n_general = lines ? ctx->pinned[12] : 0;
         res->n_lines = lines;
+        if (array && lines && ctx->pinned[3]) {
+            // a blank element: "[ ]" holds none, any other is a broken frame
+            if (lines > 1) return fail(PJ_ERR_SYNTAX, "an element of the array is empty");
+            std::memset(res, 0, sizeof *res);
+            out->n_pets = 0;
+            return PJ_OK;
+        }
         if (lines) {
             res->n_pets = T[C_PETS];
             res->name_bytes = T[C_NAMEB];
@@ -588,9 +620,32 @@ extern "C" pj_status pj_decode_device(pj_ctx *ctx, const uint8_t *in, uint64_t l
     return decode_impl(ctx, in, len, out, err_line, err_code, err_cap, res);
 }
 
+extern "C" pj_status pj_decode_array_device(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
+                                            uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
+                                            pj_decode_result *res) {
+    return decode_impl(ctx, in, len, out, err_line, err_code, err_cap, res, true);
+}
+
+namespace {
+pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                           uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array);
+}
+
 extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
                                     uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
                                     pj_decode_result *res) {
+    return decode_host_impl(ctx, in, len, out, err_line, err_code, err_cap, res, false);
+}
+
+extern "C" pj_status pj_decode_array_host(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
+                                          uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
+                                          pj_decode_result *res) {
+    return decode_host_impl(ctx, in, len, out, err_line, err_code, err_cap, res, true);
+}
+
+namespace {
+pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                           uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array) {
     pj_status s = bind(ctx);
     if (s) return s;
     if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
@@ -614,7 +669,7 @@ extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len
     set_col_ptrs(&dc, dp);
     uint64_t *del = reinterpret_cast<uint64_t *>(D + off[17]);
     uint8_t *dec = D + off[18];
-    s = decode_impl(ctx, D, len, &dc, err_cap ? del : nullptr, err_cap ? dec : nullptr, err_cap, res);
+    s = decode_impl(ctx, D, len, &dc, err_cap ? del : nullptr, err_cap ? dec : nullptr, err_cap, res, array);
     if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
     const uint64_t np = std::min(res->n_pets, cp), nu = std::min(res->n_urls, cu), nt = std::min(res->n_tags, ct);
     const uint64_t used[17] = {np * 8, np, np, (np + 1) * 8, std::min(res->name_bytes, out->cap_name_bytes), np * 8,
@@ -635,3 +690,4 @@ extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len
     out->n_pets = np;
     return s;
 }
+}  // namespace

@@ -52,6 +52,18 @@ __device__ __forceinline__ uint64_t prefix_xor(uint64_t x) {
     return x;
 }
 
+// Characters escaped by a backslash in a 64-byte word with backslash mask
+// bs, given whether its first byte is escaped (cin); *cout tells the same of
+// the next word's first byte.  Backslash runs pair up from their start.
+__device__ __forceinline__ uint64_t escaped64(uint64_t bs, uint32_t cin, uint32_t *cout) {
+    constexpr uint64_t EVEN = 0x5555555555555555ull;
+    bs &= ~(uint64_t)cin;
+    const uint64_t follows = (bs << 1) | cin;
+    const uint64_t odd_starts = bs & ~EVEN & ~follows;
+    uint64_t even_seq;
+    *cout = __builtin_add_overflow(odd_starts, bs, &even_seq) ? 1u : 0u;
+    return (EVEN ^ (even_seq << 1)) & follows;
+}
 // Scan state of stage 1: bit 0 quote parity since the last newline, bit 1
 // "a newline was seen", bits 2.. newline count.  a precedes b.
 __device__ __forceinline__ uint64_t idx_combine(uint64_t a, uint64_t b) {
@@ -158,6 +170,278 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
     }
     if (b == 0 && t == 0) P.line_start[0] = 0;
 }
+// =========================================================== array documents
+// The frame of one JSON array document: the top-level commas (depth 1,
+// outside strings) and the closing ']' cut it into elements, which the line
+// stages then read exactly as NDJSON lines.  The rule is the sequential one
+// of the CPU checker: a backslash escapes the next byte (in strings or
+// not), an unescaped quote opens or closes a string, '[' '{' ']' '}' outside
+// strings move the depth.  A 64-byte word is summarised, for each of the
+// four states it may be entered in (inside a string or not, first byte
+// escaped or not), by the state it leaves in, its depth change and the
+// lowest depth reached inside it; summaries compose associatively, so
+// blocks of words are summarised, scanned by one workgroup, and each word
+// then learns the state and depth it is entered with.
+using ::FS;
+__device__ __forceinline__ FS fs_id() {
+    FS f;
+    f.out = 0xE4u;      // s -> s
+#pragma unroll
+    for (int k = 0; k < 4; k++) f.d[k] = f.mn[k] = 0;
+    return f;
+}
+__device__ __forceinline__ int32_t pick4(const int32_t *a, uint32_t k) {
+    return k == 0 ? a[0] : k == 1 ? a[1] : k == 2 ? a[2] : a[3];
+}
+// f, then g
+__device__ __forceinline__ FS fs_cat(const FS &f, const FS &g) {
+    FS r;
+    r.out = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t s1 = (f.out >> (2 * k)) & 3;
+        r.out |= ((g.out >> (2 * s1)) & 3) << (2 * k);
+        r.d[k] = f.d[k] + pick4(g.d, s1);
+        r.mn[k] = min(f.mn[k], f.d[k] + pick4(g.mn, s1));
+    }
+    return r;
+}
+// Byte-class masks of the 64-byte word at g (avail bytes of it are input).
+struct AMasks {
+    uint64_t q, b, o, c, m, nw;     // '"', '\\', '[' '{', ']' '}', ',', not whitespace
+};
+__device__ __forceinline__ AMasks arr_masks(const uint8_t *g, uint64_t avail) {
+    uint32_t w[16];
+    if (avail >= 64) {
+        const uint4 *q4 = reinterpret_cast<const uint4 *>(g);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 v = q4[k];
+            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) w[k] = 0;
+        for (uint32_t j = 0; j < avail; j++) w[j >> 2] |= (uint32_t)g[j] << (8 * (j & 3));
+    }
+    AMasks M{0, 0, 0, 0, 0, 0};
+    uint64_t ws = 0;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const uint32_t x = w[k], lx = x | 0x20202020u;
+        M.q |= (uint64_t)zero_bytes4(x ^ 0x22222222u) << (4 * k);
+        M.b |= (uint64_t)zero_bytes4(x ^ 0x5C5C5C5Cu) << (4 * k);
+        M.o |= (uint64_t)zero_bytes4(lx ^ 0x7B7B7B7Bu) << (4 * k);      // '[' or '{'
+        M.c |= (uint64_t)zero_bytes4(lx ^ 0x7D7D7D7Du) << (4 * k);      // ']' or '}'
+        M.m |= (uint64_t)zero_bytes4(x ^ 0x2C2C2C2Cu) << (4 * k);
+        ws |= (uint64_t)(zero_bytes4(x ^ 0x20202020u) | zero_bytes4(x ^ 0x09090909u) | zero_bytes4(x ^ 0x0D0D0D0Du) |
+                         zero_bytes4(x ^ 0x0A0A0A0Au)) << (4 * k);
+    }
+    M.nw = ~ws & (avail >= 64 ? ~0ull : ((1ull << avail) - 1));
+    return M;
+}
+// The word's structure when entered in state s (bit 0 in a string, bit 1
+// first byte escaped): strings, outside opens / closes / commas, exit state.
+struct AWord {
+    uint64_t od, cd, md;
+    uint32_t out;
+};
+__device__ __forceinline__ AWord arr_word(const AMasks &M, uint32_t s) {
+    uint32_t cout;
+    const uint64_t E = escaped64(M.b, s >> 1, &cout);
+    const uint64_t S = prefix_xor(M.q & ~E) ^ ((s & 1) ? ~0ull : 0ull);
+    AWord a;
+    a.od = M.o & ~S & ~E;
+    a.cd = M.c & ~S & ~E;
+    a.md = M.m & ~S & ~E;
+    a.out = (uint32_t)(S >> 63) | (cout << 1);
+    return a;
+}
+// depth change from the word's start through byte i
+__device__ __forceinline__ int32_t depth_at(const AWord &a, uint32_t i) {
+    const uint64_t le = i == 63 ? ~0ull : ((2ull << i) - 1);
+    return __builtin_popcountll(a.od & le) - __builtin_popcountll(a.cd & le);
+}
+__device__ __forceinline__ FS word_fs(const AMasks &M) {
+    FS f;
+    f.out = 0;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const AWord a = arr_word(M, (uint32_t)s);
+        f.d[s] = __builtin_popcountll(a.od) - __builtin_popcountll(a.cd);
+        int32_t mn = 0;
+        for (uint64_t m = a.cd; m; m &= m - 1) mn = min(mn, depth_at(a, (uint32_t)__builtin_ctzll(m)));
+        f.mn[s] = mn;
+        f.out |= a.out << (2 * s);
+    }
+    return f;
+}
+// Inclusive in-order scan of one FS per thread (all BT threads).
+template <int BT>
+__device__ __forceinline__ FS block_fs_scan(FS v, FS *sh) {
+    const uint32_t t = threadIdx.x;
+    sh[t] = v;
+    __syncthreads();
+#pragma unroll 1
+    for (uint32_t d = 1; d < BT; d <<= 1) {
+        FS o = fs_id();
+        if (t >= d) o = sh[t - d];
+        __syncthreads();
+        if (t >= d) {
+            v = fs_cat(o, v);
+            sh[t] = v;
+        }
+        __syncthreads();
+    }
+    return v;
+}
+// Summary of each block of BT * R words (thread t: words t R .. t R + R - 1).
+template <int BT, int R>
+__global__ __launch_bounds__(BT) void k_arr_sum(DecParams P) {
+    __shared__ FS sh[BT];
+    const uint32_t t = threadIdx.x;
+    const uint64_t b = blockIdx.x, w0 = (b * BT + t) * R;
+    FS acc = fs_id();
+    for (int r = 0; r < R; r++) {
+        const uint64_t w = w0 + r;
+        if (w < P.nblk64) acc = fs_cat(acc, word_fs(arr_masks(P.in + 64 * w, P.len - 64 * w)));
+    }
+    acc = block_fs_scan<BT>(acc, sh);
+    if (t == BT - 1) P.arr_bsum[b] = acc;
+}
+// One workgroup: the state and depth each block is entered with, the
+// document being entered outside strings at depth 0.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_arr_scan(DecParams P, uint64_t nb) {
+    __shared__ FS sh[BT];
+    const uint32_t t = threadIdx.x;
+    const uint64_t per = (nb + BT - 1) / BT, b0 = min(nb, t * per), b1 = min(nb, b0 + per);
+    FS acc = fs_id();
+    for (uint64_t b = b0; b < b1; b++) acc = fs_cat(acc, P.arr_bsum[b]);
+    const FS inc = block_fs_scan<BT>(acc, sh);
+    FS cur = fs_id();
+    if (t) cur = sh[t - 1];
+    (void)inc;
+    for (uint64_t b = b0; b < b1; b++) {
+        P.arr_bpre[b] = (uint64_t)(cur.out & 3) | ((uint64_t)(uint32_t)cur.d[0] << 32);
+        cur = fs_cat(cur, P.arr_bsum[b]);
+    }
+}
+// The frame: per word, entered with its true state and depth, the commas at
+// depth 1 (counted, then written as element starts after a block scan and a
+// look-back of the counts), the first byte whose close brings the depth to
+// 0, and the first and last bytes that are not whitespace (one atomic per
+// block each).
+template <int BT, int R>
+__global__ __launch_bounds__(BT) void k_arr_frame(DecParams P) {
+    __shared__ FS sh[BT];
+    __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint64_t sh_blk, sh_pre, sh_mn[3];
+    const uint32_t t = threadIdx.x;
+    if (t == 0) {
+        sh_blk = atomicAdd((unsigned long long *)&P.arr[5], 1ull);
+        sh_mn[0] = ~0ull; sh_mn[1] = 0; sh_mn[2] = ~0ull;
+    }
+    __syncthreads();
+    const uint64_t b = sh_blk, w0 = (b * BT + t) * R;
+    // the thread's entry state: the block's, then its predecessors' words in the block
+    FS acc = fs_id();
+    for (int r = 0; r < R; r++) {
+        const uint64_t w = w0 + r;
+        if (w < P.nblk64) acc = fs_cat(acc, word_fs(arr_masks(P.in + 64 * w, P.len - 64 * w)));
+    }
+    block_fs_scan<BT>(acc, sh);
+    FS ex = fs_id();
+    if (t) ex = sh[t - 1];
+    const uint64_t bp = P.arr_bpre[b];
+    const uint32_t sb = (uint32_t)bp & 3;
+    uint32_t st0 = (ex.out >> (2 * sb)) & 3;
+    int32_t dep0 = (int32_t)(uint32_t)(bp >> 32) + pick4(ex.d, sb);
+    // pass 1: count the separators; first / last non-whitespace; the close
+    uint64_t cnt = 0, first = ~0ull, lastp1 = 0, close = ~0ull;
+    {
+        uint32_t st = st0;
+        int32_t dep = dep0;
+        for (int r = 0; r < R; r++) {
+            const uint64_t w = w0 + r;
+            if (w >= P.nblk64) break;
+            const AMasks M = arr_masks(P.in + 64 * w, P.len - 64 * w);
+            const AWord a = arr_word(M, st);
+            for (uint64_t m = a.md; m; m &= m - 1) cnt += dep + depth_at(a, (uint32_t)__builtin_ctzll(m)) == 1;
+            if (close == ~0ull)
+                for (uint64_t m = a.cd; m; m &= m - 1) {
+                    const uint32_t i = (uint32_t)__builtin_ctzll(m);
+                    if (dep + depth_at(a, i) == 0) {
+                        close = 64 * w + i;
+                        break;
+                    }
+                }
+            if (M.nw) {
+                if (first == ~0ull) first = 64 * w + (uint64_t)__builtin_ctzll(M.nw);
+                lastp1 = 64 * w + 64 - (uint64_t)__builtin_clzll(M.nw);
+            }
+            dep += __builtin_popcountll(a.od) - __builtin_popcountll(a.cd);
+            st = a.out;
+        }
+    }
+    if (first != ~0ull) atomicMin((unsigned long long *)&sh_mn[0], (unsigned long long)first);
+    if (lastp1) atomicMax((unsigned long long *)&sh_mn[1], (unsigned long long)lastp1);
+    if (close != ~0ull) atomicMin((unsigned long long *)&sh_mn[2], (unsigned long long)close);
+    uint64_t tot;
+    const uint64_t ex_cnt = block_excl_scan<BT>(cnt, sh_scan, &tot);
+    if (t == 0) {
+        lb_publish(P.state_idx, b, tot);
+        if (sh_mn[0] != ~0ull) atomicMin((unsigned long long *)&P.arr[0], (unsigned long long)sh_mn[0]);
+        if (sh_mn[1]) atomicMax((unsigned long long *)&P.arr[1], (unsigned long long)sh_mn[1]);
+        if (sh_mn[2] != ~0ull) atomicMin((unsigned long long *)&P.arr[2], (unsigned long long)sh_mn[2]);
+    }
+    if (t < 64) {
+        const uint64_t e = lb_resolve(P.state_idx, b, tot);
+        if (t == 0) {
+            sh_pre = e;
+            if ((b + 1) * BT * R >= P.nblk64) P.arr[3] = e + tot;
+        }
+    }
+    __syncthreads();
+    // pass 2: element k + 1 starts after the k-th separator
+    uint64_t idx = sh_pre + ex_cnt;
+    uint32_t st = st0;
+    int32_t dep = dep0;
+    for (int r = 0; r < R && cnt; r++) {
+        const uint64_t w = w0 + r;
+        if (w >= P.nblk64) break;
+        const AMasks M = arr_masks(P.in + 64 * w, P.len - 64 * w);
+        const AWord a = arr_word(M, st);
+        for (uint64_t m = a.md; m; m &= m - 1) {
+            const uint32_t i = (uint32_t)__builtin_ctzll(m);
+            if (dep + depth_at(a, i) == 1) {
+                if (1 + idx < P.ls_cap) P.line_start[1 + idx] = 64 * w + i + 1;
+                idx++;
+            }
+        }
+        dep += __builtin_popcountll(a.od) - __builtin_popcountll(a.cd);
+        st = a.out;
+    }
+}
+// The frame's verdict (one thread): the first non-whitespace byte is '[',
+// the close is a ']' after it and nothing but whitespace follows.  Then
+// element 0 starts after the '[' and the last one ends at the ']'.
+__global__ void k_arr_fin(DecParams P) {
+    const uint64_t first = P.arr[0], lastp1 = P.arr[1], close = P.arr[2], nsep = P.arr[3];
+    const bool ok = first != ~0ull && P.in[first] == '[' && close != ~0ull && close > first && P.in[close] == ']' &&
+                    lastp1 == close + 1;
+    P.arr[4] = ok ? 1 : 0;
+    if (!ok) {
+        *P.n_lines = 0;
+        return;
+    }
+    if (nsep + 1 < P.ls_cap) {
+        P.line_start[0] = first + 1;
+        P.line_start[nsep + 1] = close + 1;
+    }
+    *P.n_lines = nsep + 1;
+}
+
 // =========================================================== stage 2
 // Property keys, container contexts and parser states.
 enum { K_UNKNOWN = 0, K_ID, K_CATEGORY, K_NAME, K_PHOTOURLS, K_TAGS, K_STATUS };
@@ -382,7 +666,7 @@ __device__ __forceinline__ int run_line(const DecParams &P, const Src &S, uint64
 #define SKIP_WS()                                                \
     while (p < n) {                                              \
         const int c_ = W.at(p);                                  \
-        if (c_ != ' ' && c_ != '\t' && c_ != '\r') break;        \
+        if (c_ != ' ' && c_ != '\t' && c_ != '\r' && c_ != '\n') break; \
         p++;                                                     \
     }
     if (!write) {
@@ -832,18 +1116,6 @@ __device__ __forceinline__ uint32_t eq_mask8(uint64_t x, uint32_t c) {
     const uint64_t t = x ^ (c * 0x0101010101010101ull), m7 = 0x7F7F7F7F7F7F7F7Full;
     const uint64_t z = ~(((t & m7) + m7) | t) & 0x8080808080808080ull;
     return (uint32_t)(((z >> 7) * 0x0102040810204080ull) >> 56);
-}
-// Characters escaped by a backslash in a 64-byte word with backslash mask
-// bs, given whether its first byte is escaped (cin); *cout tells the same of
-// the next word's first byte.  Backslash runs pair up from their start.
-__device__ __forceinline__ uint64_t escaped64(uint64_t bs, uint32_t cin, uint32_t *cout) {
-    constexpr uint64_t EVEN = 0x5555555555555555ull;
-    bs &= ~(uint64_t)cin;
-    const uint64_t follows = (bs << 1) | cin;
-    const uint64_t odd_starts = bs & ~EVEN & ~follows;
-    uint64_t even_seq;
-    *cout = __builtin_add_overflow(odd_starts, bs, &even_seq) ? 1u : 0u;
-    return (EVEN ^ (even_seq << 1)) & follows;
 }
 // Four hex digits (bytes 0..3 of x) as a code unit, or -1.
 __device__ __forceinline__ int hex4(uint32_t x) {
@@ -2245,6 +2517,11 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
             const uint32_t nw = (uint32_t)((tb + 63) >> 6);
             load_tile<BT>(P, tile, a0, g0, tb, nw);
             __syncthreads();
+            if (P.array_doc) {
+                // an element's separator (',' or the closing ']') reads as its newline
+                if (mine) tile[gs + n - a0] = '\n';
+                __syncthreads();
+            }
             if (mine) {
                 s0 = (uint32_t)(gs - a0);
                 ta0 = a0;
@@ -2302,6 +2579,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         __syncthreads();                            // the tile is reused by the next sub-tile
     }
     r.code = live ? (uint32_t)code : 0;
+    if (live && code == PJ_REC_EMPTY) atomicAdd(P.empty_count, 1ull);
     // ---- scans and look-back
     uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) rec_counts(r, v);
@@ -2609,6 +2887,8 @@ __global__ __launch_bounds__(64) void k_dec_long(DecParams P) {
         const uint32_t nw = (uint32_t)((tb + 63) >> 6);
         load_tile<64>(P, tile, a0, gs, tb, nw);
         __syncthreads();
+        if (P.array_doc && threadIdx.x == 0) tile[gs + n - a0] = '\n';
+        __syncthreads();
         tile_bitmaps<64>(tile, nw, spec, badm, sh_scan);
         __syncthreads();
         const uint64_t pb = l / LPB;
@@ -2689,6 +2969,20 @@ int pj_dec_parse_block() { return DEC_LPB; }
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.nblk64 + DEC_IDX_BT * DEC_IDX_R - 1) / (DEC_IDX_BT * DEC_IDX_R);
     hipLaunchKernelGGL((pj::k_dec_lines<DEC_IDX_BT, DEC_IDX_R>), dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);
+    return hipGetLastError();
+}
+
+constexpr int ARR_BT = 256, ARR_R = 4;
+uint64_t pj_arr_blocks(uint64_t nblk64) { return (nblk64 + ARR_BT * ARR_R - 1) / (ARR_BT * ARR_R); }
+
+hipError_t pj_launch_arr_frame(const DecParams &P, hipStream_t st) {
+    const uint64_t g = pj_arr_blocks(P.nblk64);
+    if (g) {                                        // an empty document has no frame: the verdict says so
+        hipLaunchKernelGGL((pj::k_arr_sum<ARR_BT, ARR_R>), dim3((unsigned)g), dim3(ARR_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_arr_scan<1024>), dim3(1), dim3(1024), 0, st, P, g);
+        hipLaunchKernelGGL((pj::k_arr_frame<ARR_BT, ARR_R>), dim3((unsigned)g), dim3(ARR_BT), 0, st, P);
+    }
+    hipLaunchKernelGGL(pj::k_arr_fin, dim3(1), dim3(1), 0, st, P);
     return hipGetLastError();
 }
 

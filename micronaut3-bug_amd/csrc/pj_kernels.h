@@ -31,6 +31,16 @@ struct LineRec {
     uint32_t general;   // 1: the line is read by the general parser
 };
 
+// Summary of a stretch of an array document, for each of the four states it
+// may be entered in (bit 0 inside a string, bit 1 first byte escaped): the
+// exit state (2 bits each in out), the depth change and the lowest depth
+// reached.  Composed in order by the array frame kernels.
+struct FS {
+    uint32_t out;
+    int32_t d[4];
+    int32_t mn[4];
+};
+
 struct DecParams {
     const uint8_t *in;
     uint64_t len;
@@ -67,6 +77,15 @@ struct DecParams {
     uint64_t *long_list;       // lines read by a whole wave, written by k_dec_long
     unsigned long long *long_count;
     unsigned long long *bticket;  // block ticket of the scan kernel
+    // array documents: the frame's scalars (0 first non-whitespace byte,
+    // 1 last non-whitespace byte + 1, 2 the close, 3 separators, 4 frame
+    // ok, 5 block ticket), per-block summaries and entry states; array_doc
+    // makes the line stages read each element's separator as its newline
+    int array_doc;
+    uint64_t *arr;
+    FS *arr_bsum;
+    uint64_t *arr_bpre;
+    unsigned long long *empty_count;   // lines that are blank (PJ_REC_EMPTY)
     // 1: block b of each kernel takes its input in launch order (no ticket
     // atomic) and bounds its look-back wait by spin_limit wall-clock ticks;
     // a kernel whose wait ran out sets its ticket word to 1 and is redone
@@ -91,6 +110,10 @@ hipError_t pj_launch_dec_write(const DecParams &P, hipStream_t st);
 
 hipError_t pj_launch_dec_long(const DecParams &P, hipStream_t st);
 int pj_dec_bscan_block();
+// array documents: the frame kernels (element starts into line_start, their
+// count into *n_lines, the verdict into arr[4])
+hipError_t pj_launch_arr_frame(const DecParams &P, hipStream_t st);
+uint64_t pj_arr_blocks(uint64_t nblk64);
 int pj_dec_index_block();
 // Device address of this GPU's fixed encode scratch (PJ_NOALLOC_SCRATCH_WORDS
 // u64); resolved once per device, with that device current.

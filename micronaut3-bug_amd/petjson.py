@@ -22,9 +22,10 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT_DIR = os.path.dirname(PKG_DIR)
 
 # ----------------------------------------------------------------- constants
-PJ_OK, PJ_ERR_INVALID_ARG, PJ_ERR_CAPACITY, PJ_ERR_DEVICE, PJ_ERR_NO_DEVICE, PJ_ERR_OUT_OF_MEMORY = range(6)
+PJ_OK, PJ_ERR_INVALID_ARG, PJ_ERR_CAPACITY, PJ_ERR_DEVICE, PJ_ERR_NO_DEVICE, PJ_ERR_OUT_OF_MEMORY, \
+    PJ_ERR_SYNTAX = range(7)
 STATUS_NAMES = {0: "PJ_OK", 1: "PJ_ERR_INVALID_ARG", 2: "PJ_ERR_CAPACITY", 3: "PJ_ERR_DEVICE",
-                4: "PJ_ERR_NO_DEVICE", 5: "PJ_ERR_OUT_OF_MEMORY"}
+                4: "PJ_ERR_NO_DEVICE", 5: "PJ_ERR_OUT_OF_MEMORY", 6: "PJ_ERR_SYNTAX"}
 FORMAT_ARRAY, FORMAT_NDJSON = 0, 1
 INCLUDE_NON_EMPTY, INCLUDE_NON_NULL, INCLUDE_ALWAYS = 0, 1, 2
 STATUS_AVAILABLE, STATUS_PENDING, STATUS_SOLD, STATUS_NULL = 0, 1, 2, 255
@@ -118,7 +119,7 @@ def load_lib():
             getattr(L, f).restype = i32
         L.pj_encode_size_device.argtypes = [vp, C.POINTER(PetColumnsStruct), i32, C.POINTER(u64)]
         L.pj_encode_size_device.restype = i32
-        for f in ("pj_decode_device", "pj_decode_host"):
+        for f in ("pj_decode_device", "pj_decode_host", "pj_decode_array_device", "pj_decode_array_host"):
             getattr(L, f).argtypes = [vp, vp, u64, C.POINTER(PetColumnsStruct), vp, vp, u64,
                                       C.POINTER(DecodeResult)]
             getattr(L, f).restype = i32
@@ -411,11 +412,14 @@ class Codec:
         ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=dev)
         return cols, el, ec
 
-    def decode(self, data, caps=None, err_cap=None, device=None, out=None):
-        """Decode NDJSON held in a uint8 device tensor.  Returns (columns on the
-        device trimmed to size, error line indices, error codes, DecodeResult).
-        `out` = decode_buffers(...) reuses preallocated outputs."""
+    def decode(self, data, caps=None, err_cap=None, device=None, out=None, array=False):
+        """Decode NDJSON (or, with array=True, one JSON array document) held in
+        a uint8 device tensor.  Returns (columns on the device trimmed to
+        size, error line / element indices, error codes, DecodeResult).
+        `out` = decode_buffers(...) reuses preallocated outputs.  A broken
+        array frame raises PetJsonError(PJ_ERR_SYNTAX)."""
         import torch
+        fn = self.L.pj_decode_array_device if array else self.L.pj_decode_device
         n = data.numel()
         own = out is None
         if own:
@@ -429,8 +433,8 @@ class Codec:
         s = cols.struct()
         res = DecodeResult()
         ptr = C.c_void_p(data.data_ptr()) if n else C.c_void_p(el.data_ptr())
-        rc = self.L.pj_decode_device(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()),
-                                     C.c_void_p(ec.data_ptr()), err_cap, C.byref(res))
+        rc = fn(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()), C.c_void_p(ec.data_ptr()), err_cap,
+                C.byref(res))
         if rc == PJ_ERR_CAPACITY and own and res.n_errors > err_cap:
             # more invalid lines than the first guess: the call reported how
             # many there are, so one retry with that capacity suffices
@@ -439,8 +443,8 @@ class Codec:
             ec = torch.empty(max(1, err_cap), dtype=torch.uint8, device=ec.device)
             s = cols.struct()
             res = DecodeResult()
-            rc = self.L.pj_decode_device(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()),
-                                         C.c_void_p(ec.data_ptr()), err_cap, C.byref(res))
+            rc = fn(self.ctx, ptr, n, C.byref(s), C.c_void_p(el.data_ptr()), C.c_void_p(ec.data_ptr()), err_cap,
+                    C.byref(res))
         self._check(rc)
         return self._trim(cols, res), el[: res.n_errors], ec[: res.n_errors], res
 
@@ -453,8 +457,18 @@ class Codec:
                 "tag_id": nt, "tag_flags": nt, "tag_name_off": nt + 1, "tag_name_bytes": res.tag_name_bytes}
         return Columns(np_, cols.arrays, dict(cols.caps), lens)
 
-    def decode_host(self, data: bytes, caps=None, err_cap=None):
-        """Decode NDJSON bytes through the host entry point; numpy results."""
+    def decode_array(self, data, caps=None, err_cap=None, device=None, out=None):
+        """decode(..., array=True): one JSON array document on the device."""
+        return self.decode(data, caps, err_cap, device, out, array=True)
+
+    def decode_array_host(self, data: bytes, caps=None, err_cap=None):
+        """decode_host(..., array=True): one JSON array document from host bytes."""
+        return self.decode_host(data, caps, err_cap, array=True)
+
+    def decode_host(self, data: bytes, caps=None, err_cap=None, array=False):
+        """Decode NDJSON bytes (or one array document) through the host entry
+        point; numpy results."""
+        fn = self.L.pj_decode_array_host if array else self.L.pj_decode_host
         n = len(data)
         caps = caps or decode_bounds(n)
         cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
@@ -473,9 +487,8 @@ class Codec:
             ec = np.zeros(max(1, err_cap), np.uint8)
             s = cols.struct()
             res = DecodeResult()
-            rc = self.L.pj_decode_host(self.ctx, C.c_void_p(buf.ctypes.data), n, C.byref(s),
-                                       C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap,
-                                       C.byref(res))
+            rc = fn(self.ctx, C.c_void_p(buf.ctypes.data), n, C.byref(s), C.c_void_p(el.ctypes.data),
+                    C.c_void_p(ec.ctypes.data), err_cap, C.byref(res))
             if not (rc == PJ_ERR_CAPACITY and guessed and res.n_errors > err_cap):
                 break
             err_cap = int(res.n_errors)     # one retry with the count the call reported

@@ -245,7 +245,10 @@ typedef struct {
     int depth;
 } rd_t;
 
-static int is_ws(uint8_t c) { return c == ' ' || c == '\t' || c == '\r'; }
+/* RFC 8259 whitespace.  An NDJSON line never holds '\n' (lines are cut at
+ * every newline), so '\n' only ever meets this test inside the elements of
+ * an array document. */
+static int is_ws(uint8_t c) { return c == ' ' || c == '\t' || c == '\r' || c == '\n'; }
 static void skip_ws(rd_t *r) { while (r->p < r->n && is_ws(r->s[r->p])) r->p++; }
 static int at_end(const rd_t *r) { return r->p >= r->n; }
 static uint8_t cur(const rd_t *r) { return r->p < r->n ? r->s[r->p] : 0; }
@@ -756,6 +759,97 @@ int or_decode(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *er
         p = e + 1;
     }
     res->n_lines = line;
+    if (out) out->n_pets = res->n_pets < out->cap_pets ? res->n_pets : out->cap_pets;
+    if (res->n_errors > err_cap) return PJ_ERR_CAPACITY;
+    if (out && (res->n_pets > out->cap_pets || res->name_bytes > out->cap_name_bytes ||
+                res->cat_name_bytes > out->cap_cat_name_bytes || res->n_urls > out->cap_urls ||
+                res->url_bytes > out->cap_url_bytes || res->n_tags > out->cap_tags ||
+                res->tag_name_bytes > out->cap_tag_name_bytes))
+        return PJ_ERR_CAPACITY;
+    return PJ_OK;
+}
+
+/* One JSON array of Pets => its elements (readValue(bytes, List<Pet>), the
+ * reference's bulk shape "array of Pet", petstore.json:133-140, read as in
+ * MyEntityConfig.java:34).  The array's frame is read first, sequentially:
+ * whitespace, '[', then the top-level commas, found by counting '[' '{' ']'
+ * '}' outside strings (a quote opens or closes a string unless a backslash
+ * escapes it; a backslash escapes the next byte, in strings or not), up to
+ * the ']' that brings the count back to zero; only whitespace may follow.
+ * A broken frame (no '[', never closed, closed by '}', bytes after it, an
+ * element of whitespace only) fails the whole call with PJ_ERR_SYNTAX, as
+ * jackson's parser throws for it.  Each element is then read exactly as an
+ * NDJSON line (or_decode_line, '\n' being whitespace) and reported under its
+ * index.  "[]" and "[ ]" hold no element. */
+int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                    uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+    if (!res || (len && !in)) return PJ_ERR_INVALID_ARG;
+    memset(res, 0, sizeof *res);
+    if (out && out->cap_pets + 1 > 0) {
+        if (out->name_off) out->name_off[0] = 0;
+        if (out->cat_name_off) out->cat_name_off[0] = 0;
+        if (out->photo_off) out->photo_off[0] = 0;
+        if (out->tag_off) out->tag_off[0] = 0;
+        if (out->url_off) out->url_off[0] = 0;
+        if (out->tag_name_off) out->tag_name_off[0] = 0;
+    }
+    uint64_t p = 0;
+    while (p < len && is_ws(in[p])) p++;
+    if (p >= len || in[p] != '[') return PJ_ERR_SYNTAX;
+    /* the frame: element bounds */
+    uint64_t cap = 16, ne = 0, *start = (uint64_t *)malloc(cap * sizeof *start);
+    if (!start) return PJ_ERR_OUT_OF_MEMORY;
+    start[ne++] = p + 1;
+    int in_str = 0, esc = 0;
+    int64_t depth = 1;
+    uint64_t close = len;
+    for (uint64_t i = p + 1; i < len; i++) {
+        const uint8_t c = in[i];
+        if (esc) { esc = 0; continue; }
+        if (c == '\\') { esc = 1; continue; }
+        if (c == '"') { in_str ^= 1; continue; }
+        if (in_str) continue;
+        if (c == '[' || c == '{') depth++;
+        else if (c == ']' || c == '}') {
+            if (--depth == 0) { close = i; break; }
+        } else if (c == ',' && depth == 1) {
+            if (ne == cap) {
+                uint64_t *t = (uint64_t *)realloc(start, 2 * cap * sizeof *start);
+                if (!t) { free(start); return PJ_ERR_OUT_OF_MEMORY; }
+                start = t;
+                cap *= 2;
+            }
+            start[ne++] = i + 1;
+        }
+    }
+    int bad = close >= len || in[close] != ']';
+    for (uint64_t i = close + 1; !bad && i < len; i++) bad = !is_ws(in[i]);
+    if (bad) { free(start); return PJ_ERR_SYNTAX; }
+    /* elements: [start[k], start[k+1] - 1), the last ending at the ']' */
+    for (uint64_t k = 0; k < ne; k++) {
+        const uint64_t a = start[k], e = k + 1 < ne ? start[k + 1] - 1 : close;
+        uint64_t q = a;
+        while (q < e && is_ws(in[q])) q++;
+        if (q == e) {
+            if (ne == 1) { ne = 0; break; }        /* "[ ]": no element */
+            free(start);
+            memset(res, 0, sizeof *res);
+            return PJ_ERR_SYNTAX;                   /* an empty element */
+        }
+    }
+    for (uint64_t k = 0; k < ne; k++) {
+        const uint64_t a = start[k], e = k + 1 < ne ? start[k + 1] - 1 : close;
+        int code = or_decode_line(in + a, e - a, out, res);
+        if (code) {
+            if (res->n_errors < err_cap) {
+                if (err_line) err_line[res->n_errors] = k;
+                if (err_code) err_code[res->n_errors] = (uint8_t)code;
+            }
+            res->n_errors++;
+        }
+    }
+    free(start);
+    res->n_lines = ne;
     if (out) out->n_pets = res->n_pets < out->cap_pets ? res->n_pets : out->cap_pets;
     if (res->n_errors > err_cap) return PJ_ERR_CAPACITY;
     if (out && (res->n_pets > out->cap_pets || res->name_bytes > out->cap_name_bytes ||

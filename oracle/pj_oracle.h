@@ -31,6 +31,13 @@ int or_decode(const uint8_t *in, uint64_t len, pj_pet_columns *out,
               uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
               pj_decode_result *res);
 
+/* Decode one JSON array document of Pets (host pointers).  Same conventions
+ * as pj_decode_array_host: PJ_ERR_SYNTAX for a broken array frame, element
+ * indices in err_line. */
+int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out,
+                    uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
+                    pj_decode_result *res);
+
 /* Parse one record (line without its '\n').  Returns the PJ_REC_* code; on
  * PJ_REC_OK and when `out` is non-NULL appends the record to `out`, whose
  * n_pets / offset tails give the current fill. Exposed for the tests. */

@@ -27,6 +27,7 @@ def lib():
         L.or_decode.argtypes = [C.c_void_p, C.c_uint64, C.POINTER(pj.PetColumnsStruct), C.c_void_p, C.c_void_p,
                                 C.c_uint64, C.POINTER(pj.DecodeResult)]
         L.or_decode_line.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
+        L.or_decode_array.argtypes = L.or_decode.argtypes
         L.or_format_long.argtypes = [C.c_int64, C.c_char_p]
         _L = L
     return _L
@@ -99,6 +100,32 @@ def decode(data: bytes, caps=None):
                      C.c_void_p(ec.ctypes.data), nl, C.byref(res))
     assert rc == 0, rc
     return trim(cols, res), el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res
+
+
+def decode_array(data: bytes, caps=None):
+    """One array document.  Returns (status, columns trimmed to size, error
+    element indices, error codes, result); status is pj.PJ_OK or
+    pj.PJ_ERR_SYNTAX (a broken frame: columns and lists then empty)."""
+    L = lib()
+    buf = np.frombuffer(data, dtype=np.uint8) if len(data) else np.zeros(1, np.uint8)
+    if caps is None:
+        caps = pj.decode_bounds(len(data)) if pj._LIB is not None or os.path.exists(pj.lib_path()) else None
+    if caps is None:
+        n = len(data)
+        caps = {"cap_pets": n // 27 + 1, "cap_name_bytes": n, "cap_cat_name_bytes": n, "cap_urls": n // 3 + 1,
+                "cap_url_bytes": n, "cap_tags": n // 3 + 1, "cap_tag_name_bytes": n}
+    cols = alloc_decode_columns(caps)
+    s = cols.struct()
+    ne = data.count(b",") + 2
+    el = np.zeros(ne, np.uint64)
+    ec = np.zeros(ne, np.uint8)
+    res = pj.DecodeResult()
+    rc = L.or_decode_array(C.c_void_p(buf.ctypes.data), len(data), C.byref(s), C.c_void_p(el.ctypes.data),
+                           C.c_void_p(ec.ctypes.data), ne, C.byref(res))
+    assert rc in (pj.PJ_OK, pj.PJ_ERR_SYNTAX), rc
+    if rc != pj.PJ_OK:
+        res = pj.DecodeResult()
+    return rc, trim(cols, res), el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res
 
 
 def decode_line_code(line: bytes) -> int:
