@@ -243,7 +243,28 @@ class PetObjectMapper {
     }
 
     // readValue over NDJSON: one Pet per line.
-    ReadResult readValue(const uint8_t *ndjson, uint64_t len) {
+    ReadResult readValue(const uint8_t *ndjson, uint64_t len) { return read(ndjson, len, false); }
+
+    // One JSON array document, element by element: the valid elements in
+    // order plus the index and PJ_REC_* code of each invalid one.  A broken
+    // array frame throws (PJ_ERR_SYNTAX).
+    ReadResult readArray(const uint8_t *json, uint64_t len) { return read(json, len, true); }
+
+    // readValue(bytes, List<Pet>) with jackson's all-or-nothing contract:
+    // any invalid element throws, naming the first one.
+    std::vector<Pet> readValueList(const uint8_t *json, uint64_t len) {
+        ReadResult r = read(json, len, true);
+        if (!r.error_lines.empty())
+            throw SerdeException(PJ_ERR_SYNTAX, "element " + std::to_string(r.error_lines[0]) +
+                                                    " of the array is not a valid Pet (PJ_REC code " +
+                                                    std::to_string((int)r.error_codes[0]) + ")");
+        return std::move(r.values);
+    }
+
+    pj_ctx *context() { return ctx_; }
+
+  private:
+    ReadResult read(const uint8_t *in, uint64_t len, bool array) {
         pj_pet_columns caps;
         std::memset(&caps, 0, sizeof caps);
         pj_decode_bounds(len, &caps);
@@ -271,7 +292,8 @@ class PetObjectMapper {
         for (int attempt = 0;; attempt++) {
             r.error_lines.resize(err_cap);
             r.error_codes.resize(err_cap);
-            st = pj_decode_host(ctx_, ndjson, len, &v, r.error_lines.data(), r.error_codes.data(), err_cap, &res);
+            st = (array ? pj_decode_array_host : pj_decode_host)(ctx_, in, len, &v, r.error_lines.data(),
+                                                                 r.error_codes.data(), err_cap, &res);
             if (st != PJ_ERR_CAPACITY || attempt > 0 || res.n_errors <= err_cap) break;
             err_cap = res.n_errors;
         }
@@ -282,10 +304,6 @@ class PetObjectMapper {
         r.values = from_columns(v);
         return r;
     }
-
-    pj_ctx *context() { return ctx_; }
-
-  private:
     void check(pj_status st) {
         if (st != PJ_OK) throw SerdeException(st, pj_last_error());
     }

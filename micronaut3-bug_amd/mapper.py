@@ -49,5 +49,19 @@ class PetObjectMapper:
         cols, el, ec, res = self.codec.decode_host(ndjson)
         return ReadResult(from_columns(cols, as_bytes=as_bytes), el, ec)
 
+    def read_array(self, data: bytes, as_bytes: bool = False) -> ReadResult:
+        """One JSON array document, element by element (invalid elements are
+        reported by index); a broken array frame raises PJ_ERR_SYNTAX."""
+        cols, el, ec, res = self.codec.decode_array_host(data)
+        return ReadResult(from_columns(cols, as_bytes=as_bytes), el, ec)
+
+    def read_value_list(self, data: bytes, as_bytes: bool = False) -> List[Pet]:
+        """readValue(bytes, List<Pet>): all or nothing, as jackson reads it."""
+        r = self.read_array(data, as_bytes)
+        if len(r.error_lines):
+            raise pj.PetJsonError(pj.PJ_ERR_SYNTAX, f"element {int(r.error_lines[0])} of the array is not a valid "
+                                                    f"Pet (PJ_REC code {int(r.error_codes[0])})")
+        return r.values
+
     def close(self):
         self.codec.close()

@@ -75,7 +75,8 @@ _GEN = None
 
 EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "pj_last_error",
            "pj_last_timings", "pj_encode_device", "pj_encode_size_device", "pj_encode_host",
-           "pj_decode_device", "pj_decode_host", "pj_decode_bounds", "pj_encode_device_noalloc"]
+           "pj_decode_device", "pj_decode_host", "pj_decode_bounds", "pj_encode_device_noalloc",
+           "pj_decode_array_device", "pj_decode_array_host"]
 NOALLOC_SCRATCH_WORDS = 1 << 20
 
 

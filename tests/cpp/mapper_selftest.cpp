@@ -120,6 +120,24 @@ int main(int argc, char **argv) {
         ReadResult rb = m.readValue(reinterpret_cast<const uint8_t *>(blank.data()), blank.size());
         CHECK(rb.values.size() == 1 && rb.error_lines.size() == 3000);
         CHECK(rb.error_lines[2999] == 2999 && rb.error_codes[0] == PJ_REC_EMPTY);
+        // one array document: the writer's own output reads back; an invalid
+        // element is reported by readArray and thrown by readValueList; a
+        // broken frame throws PJ_ERR_SYNTAX
+        std::vector<uint8_t> arr = m.writeValueAsBytes(pets, PJ_FORMAT_ARRAY);
+        CHECK(m.readValueList(arr.data(), arr.size()) == normalised(pets));
+        std::string bad(arr.begin(), arr.end() - 1);
+        bad += ",\n {\"name\":\"y\",\"photoUrls\":[],\"status\":\"lost\"} ]";
+        ReadResult ra = m.readArray(reinterpret_cast<const uint8_t *>(bad.data()), bad.size());
+        CHECK(ra.values == normalised(pets) && ra.error_lines.size() == 1 && ra.error_lines[0] == pets.size() &&
+              ra.error_codes[0] == PJ_REC_BAD_STATUS);
+        int thrown = 0;
+        try { m.readValueList(reinterpret_cast<const uint8_t *>(bad.data()), bad.size()); }
+        catch (const SerdeException &e) { thrown = e.status(); }
+        CHECK(thrown == PJ_ERR_SYNTAX);
+        thrown = 0;
+        try { m.readArray(arr.data(), arr.size() - 1); }
+        catch (const SerdeException &e) { thrown = e.status(); }
+        CHECK(thrown == PJ_ERR_SYNTAX);
     }
     std::printf("mapper selftest ok (%s)\n", gpu ? "gpu" : "cpu");
     return 0;
