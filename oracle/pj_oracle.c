@@ -666,7 +666,7 @@ static void commit(const pet_t *pt, pj_pet_columns *o, pj_decode_result *f) {
         o->cat_flags[i] = pt->has_cat ? pt->cat.flags : 0;
     }
     /* name */
-    if (o && f->name_bytes + pt->name.n <= o->cap_name_bytes)
+    if (o && pt->name.n && f->name_bytes + pt->name.n <= o->cap_name_bytes)
         memcpy(o->name_bytes + f->name_bytes, pt->name.p, pt->name.n);
     f->name_bytes += pt->name.n;
     /* category name */
@@ -678,7 +678,7 @@ static void commit(const pet_t *pt, pj_pet_columns *o, pj_decode_result *f) {
     uint64_t ub = 0;
     for (uint64_t u = 0; u < pt->n_urls; u++) {
         uint64_t L = pt->url_len[u];
-        if (o && f->url_bytes + L <= o->cap_url_bytes)
+        if (o && L && f->url_bytes + L <= o->cap_url_bytes)
             memcpy(o->url_bytes + f->url_bytes, pt->urls.p + ub, L);
         ub += L;
         f->url_bytes += L;

@@ -9,3 +9,21 @@ g++ -O1 -std=c++17 -Wall -I"$ROOT/include" -I"$ROOT/micronaut3-bug_amd/host" -I"
     -Wl,--allow-shlib-undefined \
     -Wl,-rpath,"\$ORIGIN/../../../oracle" -Wl,-rpath,"\$ORIGIN/../../../micronaut3-bug_amd" \
     -o "$HERE/bin/mapper_selftest"
+# The host half of libpetjson under ASan / UBSan (host code only, -fsanitize
+# after -Xarch_host), run by tests/test_sanitizers.py; needs the kernel
+# objects of the in-tree build.
+HIPCC=${HIPCC:-/opt/rocm/bin/hipcc}
+PKG="$ROOT/micronaut3-bug_amd"
+if [ -f "$PKG/_build/pj_encode_hip.o" ] && [ -f "$PKG/_build/pj_decode_hip.o" ]; then
+    SANF="-Xarch_host -fsanitize=address,undefined -Xarch_host -fno-sanitize-recover=all -Xarch_host -fno-omit-frame-pointer"
+    OBJ="$HERE/bin/obj"
+    mkdir -p "$OBJ"
+    for src in "$PKG/csrc/pj_api.cpp" "$PKG/csrc/pj_gen.cpp" "$HERE/api_sanitize.cpp"; do
+        $HIPCC $SANF -g -O1 -std=c++17 --offload-arch=gfx950 -I"$ROOT/include" -I"$PKG/csrc" \
+            -c "$src" -o "$OBJ/$(basename "$src").o" 2>/dev/null
+    done
+    $HIPCC --offload-arch=gfx950 -fsanitize=address,undefined "$OBJ/pj_api.cpp.o" "$OBJ/pj_gen.cpp.o" \
+        "$OBJ/api_sanitize.cpp.o" "$PKG/_build/pj_encode_hip.o" "$PKG/_build/pj_decode_hip.o" -pthread \
+        -o "$HERE/bin/api_sanitize"
+    rm -rf "$OBJ"
+fi
