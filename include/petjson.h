@@ -183,6 +183,13 @@ pj_status pj_encode_device(pj_ctx *ctx, const pj_pet_columns *cols, int format,
 /* Exact encoded size only (length pass). */
 pj_status pj_encode_size_device(pj_ctx *ctx, const pj_pet_columns *cols,
                                 int format, uint64_t *out_len);
+/* An upper bound of the encoded size of n_pets records (host pointers; no
+ * device work): room for every property and its longest value per record,
+ * item, and every string byte written as a six-byte \u00XX escape.  No
+ * counterpart in the reference; callers of pj_encode_host size their buffer
+ * with it and encode in one call instead of asking for the exact size first
+ * (which would copy the columns to the device twice). */
+pj_status pj_encode_bound(const pj_pet_columns *cols, int format, uint64_t *bound);
 /* Same as pj_encode_device with host pointers. */
 pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
                          uint8_t *out, uint64_t out_cap, uint64_t *out_len);

@@ -12,6 +12,8 @@
 #include <cstring>
 #include <cstdlib>
 #include <string>
+#include <thread>
+#include <vector>
 
 #include "petjson.h"
 #include "pj_kernels.h"
@@ -69,6 +71,13 @@ struct pj_ctx {
     DevBuf stage_out;   // host path: output staging
     DevBuf tape;        // decode: per-line results of the validating walk
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
+    // host entry points: a copy stream, two pinned bounce buffers and their
+    // events (made on first use)
+    hipStream_t xs = nullptr;
+    uint8_t *bounce[2] = {nullptr, nullptr};
+    hipEvent_t bev[2] = {nullptr, nullptr};
+    hipEvent_t xev = nullptr;
+    size_t xchunk = 0;
     uint64_t *noalloc_scratch = nullptr;  // this device's fixed encode scratch (device address)
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
@@ -101,6 +110,98 @@ pj_status finish_timing(pj_ctx *c) {
             PJ_HIP(hipEventElapsedTime(&ms, c->ev[k - 1], c->ev[k]));
             c->timings[c->n_timings++] = ms;
         }
+    }
+    return PJ_OK;
+}
+
+// ---------------------------------------------------------------- host copies
+// The host entry points move data between the caller's (pageable) memory and
+// the device through two pinned bounce buffers of 64 MiB on a copy
+// stream: while the DMA engine moves chunk i, host threads copy chunk i + 1
+// into (or chunk i - 1 out of) the other buffer, so PCIe and the host copies
+// overlap instead of the driver's staging path serialising them.
+// (PETJSON_XFER_CHUNK overrides the size when a context first copies; tests
+// use small odd sizes to cross many chunk boundaries.)
+size_t xfer_chunk() {
+    static const size_t v = [] {
+        const char *e = std::getenv("PETJSON_XFER_CHUNK");
+        const size_t x = e ? std::strtoull(e, nullptr, 10) : 0;
+        return x >= 4096 ? x : (size_t)64 << 20;
+    }();
+    return v;
+}
+
+pj_status xfer_init(pj_ctx *c) {
+    if (c->xs) return PJ_OK;
+    c->xchunk = xfer_chunk();
+    PJ_HIP(hipStreamCreateWithFlags(&c->xs, hipStreamNonBlocking));
+    for (int b = 0; b < 2; b++) {
+        PJ_HIP(hipHostMalloc((void **)&c->bounce[b], c->xchunk, hipHostMallocDefault));
+        PJ_HIP(hipEventCreateWithFlags(&c->bev[b], hipEventDisableTiming));
+    }
+    PJ_HIP(hipEventCreateWithFlags(&c->xev, hipEventDisableTiming));
+    return PJ_OK;
+}
+
+// n bytes from s to d on up to 16 host threads (at least 4 MiB each).
+void par_copy(void *d, const void *s, size_t n) {
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t T = std::min<size_t>({(size_t)std::min(hw, 16u), n / (4u << 20) + 1});
+    if (T <= 1) {
+        std::memcpy(d, s, n);
+        return;
+    }
+    const size_t per = ((n + T - 1) / T + 4095) & ~size_t(4095);
+    std::vector<std::thread> th;
+    for (size_t k = 1; k < T && k * per < n; k++)
+        th.emplace_back([=] { std::memcpy(static_cast<uint8_t *>(d) + k * per, static_cast<const uint8_t *>(s) + k * per,
+                                          std::min(per, n - k * per)); });
+    std::memcpy(d, s, std::min(per, n));
+    for (auto &x : th) x.join();
+}
+
+// Host -> device; the context stream waits for the data before its next work.
+pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n) {
+    if (!n) return PJ_OK;
+    pj_status s = xfer_init(c);
+    if (s) return s;
+    for (size_t off = 0, i = 0; off < n; off += c->xchunk, i++) {
+        const size_t k = std::min(c->xchunk, n - off);
+        const int b = (int)(i & 1);
+        if (i >= 2) PJ_HIP(hipEventSynchronize(c->bev[b]));      // the DMA that last read this buffer is done
+        par_copy(c->bounce[b], static_cast<const uint8_t *>(host) + off, k);
+        PJ_HIP(hipMemcpyAsync(static_cast<uint8_t *>(dev) + off, c->bounce[b], k, hipMemcpyHostToDevice, c->xs));
+        PJ_HIP(hipEventRecord(c->bev[b], c->xs));
+    }
+    PJ_HIP(hipEventRecord(c->xev, c->xs));
+    PJ_HIP(hipStreamWaitEvent(c->stream, c->xev, 0));
+    // the bounce buffers are reused by the next copy: wait for the last DMAs
+    PJ_HIP(hipEventSynchronize(c->xev));
+    return PJ_OK;
+}
+
+// Device -> host, after the context stream's work so far; returns when the
+// bytes are in host memory.
+pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n) {
+    if (!n) return PJ_OK;
+    pj_status s = xfer_init(c);
+    if (s) return s;
+    PJ_HIP(hipEventRecord(c->xev, c->stream));
+    PJ_HIP(hipStreamWaitEvent(c->xs, c->xev, 0));
+    const size_t chunks = (n + c->xchunk - 1) / c->xchunk;
+    auto issue = [&](size_t i) -> pj_status {
+        const size_t off = i * c->xchunk, k = std::min(c->xchunk, n - off);
+        PJ_HIP(hipMemcpyAsync(c->bounce[i & 1], static_cast<const uint8_t *>(dev) + off, k, hipMemcpyDeviceToHost, c->xs));
+        PJ_HIP(hipEventRecord(c->bev[i & 1], c->xs));
+        return PJ_OK;
+    };
+    if ((s = issue(0))) return s;
+    for (size_t i = 0; i < chunks; i++) {
+        // the other buffer's host copy (chunk i - 1) is done: start chunk i + 1's DMA into it
+        if (i + 1 < chunks && (s = issue(i + 1))) return s;
+        PJ_HIP(hipEventSynchronize(c->bev[i & 1]));
+        const size_t off = i * c->xchunk;
+        par_copy(static_cast<uint8_t *>(host) + off, c->bounce[i & 1], std::min(c->xchunk, n - off));
     }
     return PJ_OK;
 }
@@ -333,6 +434,13 @@ void pj_destroy(pj_ctx *c) {
     c->tape.release();
     for (auto &e : c->ev) if (e) (void)hipEventDestroy(e);
     if (c->pinned) (void)hipHostFree(c->pinned);
+    if (c->xs) (void)hipStreamSynchronize(c->xs);
+    for (int b = 0; b < 2; b++) {
+        if (c->bounce[b]) (void)hipHostFree(c->bounce[b]);
+        if (c->bev[b]) (void)hipEventDestroy(c->bev[b]);
+    }
+    if (c->xev) (void)hipEventDestroy(c->xev);
+    if (c->xs) (void)hipStreamDestroy(c->xs);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -382,8 +490,7 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, ui
     col_ptrs(&hc, hp);
     for (int k = 0; k < 17; k++) {
         dp[k] = hp[k] ? base + L.off[k] : nullptr;
-        if (hp[k] && L.size[k])
-            PJ_HIP(hipMemcpyAsync(dp[k], hp[k], L.size[k], hipMemcpyHostToDevice, ctx->stream));
+        if (hp[k] && L.size[k] && (s = h2d(ctx, dp[k], hp[k], L.size[k]))) return s;
     }
     set_col_ptrs(&dc, dp);
     uint64_t need = 0;
@@ -395,9 +502,36 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, ui
     PJ_HIP(ctx->stage_out.ensure(need + 4));
     uint64_t got = 0;
     if ((s = pj_encode_device(ctx, &dc, format, static_cast<uint8_t *>(ctx->stage_out.p), need, &got))) return s;
-    PJ_HIP(hipMemcpyAsync(out, ctx->stage_out.p, got, hipMemcpyDeviceToHost, ctx->stream));
-    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if ((s = d2h(ctx, out, ctx->stage_out.p, got))) return s;
     *out_len = got;
+    return PJ_OK;
+}
+
+pj_status pj_encode_bound(const pj_pet_columns *cols, int format, uint64_t *bound) {
+    if (!cols || !bound) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    pj_status s;
+    if ((s = check_enc_cols(cols))) return s;
+    const uint64_t n = cols->n_pets;
+    // per record: every Pet / Category property with a 20-character long,
+    // the longest status and the framing; per url / tag item: its quotes,
+    // separators and (tags) an object with both properties
+    uint64_t b = 2 + n * 256, str = 0;
+    if (n) {
+        str += cols->name_off[n] - cols->name_off[0];
+        if (cols->cat_name_off) str += cols->cat_name_off[n] - cols->cat_name_off[0];
+        if (cols->photo_off) {
+            const uint64_t u0 = cols->photo_off[0], u1 = cols->photo_off[n];
+            b += (u1 - u0) * 4;
+            str += cols->url_off[u1] - cols->url_off[u0];
+        }
+        if (cols->tag_off) {
+            const uint64_t t0 = cols->tag_off[0], t1 = cols->tag_off[n];
+            b += (t1 - t0) * 64;
+            str += cols->tag_name_off[t1] - cols->tag_name_off[t0];
+        }
+    }
+    *bound = b + 6 * str;
     return PJ_OK;
 }
 
@@ -662,7 +796,7 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
     for (int k = 0; k < 19; k++) off[k + 1] = off[k] + align256(sz[k] + 8);
     PJ_HIP(ctx->stage_out.ensure(off[19]));
     uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
-    if (len) PJ_HIP(hipMemcpyAsync(D, in, len, hipMemcpyHostToDevice, ctx->stream));
+    if (len && (s = h2d(ctx, D, in, len))) return s;
     void *dp[17];
     for (int k = 0; k < 17; k++) dp[k] = D + off[k];
     pj_pet_columns dc = *out;
@@ -679,14 +813,11 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
                                std::min(res->tag_name_bytes, out->cap_tag_name_bytes)};
     void *hp[17];
     col_ptrs(out, hp);
+    pj_status t = PJ_OK;
     for (int k = 0; k < 17; k++)
-        if (used[k]) PJ_HIP(hipMemcpyAsync(hp[k], dp[k], used[k], hipMemcpyDeviceToHost, ctx->stream));
+        if (used[k] && (t = d2h(ctx, hp[k], dp[k], used[k]))) return t;
     const uint64_t ne = std::min(res->n_errors, err_cap);
-    if (ne) {
-        PJ_HIP(hipMemcpyAsync(err_line, del, ne * 8, hipMemcpyDeviceToHost, ctx->stream));
-        PJ_HIP(hipMemcpyAsync(err_code, dec, ne, hipMemcpyDeviceToHost, ctx->stream));
-    }
-    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if (ne && ((t = d2h(ctx, err_line, del, ne * 8)) || (t = d2h(ctx, err_code, dec, ne)))) return t;
     out->n_pets = np;
     return s;
 }

@@ -227,11 +227,11 @@ class PetObjectMapper {
     std::vector<uint8_t> writeValueAsBytes(const std::vector<Pet> &pets, pj_format fmt = PJ_FORMAT_ARRAY) {
         ColumnSet cs = to_columns(pets);
         pj_pet_columns v = cs.view();
-        uint64_t need = 0;
-        pj_status st = pj_encode_host(ctx_, &v, fmt, nullptr, 0, &need);
-        if (st != PJ_OK && st != PJ_ERR_CAPACITY) check(st);
-        std::vector<uint8_t> out(need);
-        uint64_t got = 0;
+        // one call into a buffer of the bound's size (the exact size would
+        // need a first call that copies the columns to the device too)
+        uint64_t bound = 0, got = 0;
+        check(pj_encode_bound(&v, fmt, &bound));
+        std::vector<uint8_t> out(bound);
         check(pj_encode_host(ctx_, &v, fmt, out.data(), out.size(), &got));
         out.resize(got);
         return out;

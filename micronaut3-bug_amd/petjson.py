@@ -76,7 +76,7 @@ _GEN = None
 EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "pj_last_error",
            "pj_last_timings", "pj_encode_device", "pj_encode_size_device", "pj_encode_host",
            "pj_decode_device", "pj_decode_host", "pj_decode_bounds", "pj_encode_device_noalloc",
-           "pj_decode_array_device", "pj_decode_array_host"]
+           "pj_decode_array_device", "pj_decode_array_host", "pj_encode_bound"]
 NOALLOC_SCRATCH_WORDS = 1 << 20
 
 
@@ -118,6 +118,8 @@ def load_lib():
         for f in ("pj_encode_device", "pj_encode_host", "pj_encode_device_noalloc"):
             getattr(L, f).argtypes = [vp, C.POINTER(PetColumnsStruct), i32, vp, u64, C.POINTER(u64)]
             getattr(L, f).restype = i32
+        L.pj_encode_bound.argtypes = [C.POINTER(PetColumnsStruct), i32, C.POINTER(u64)]
+        L.pj_encode_bound.restype = i32
         L.pj_encode_size_device.argtypes = [vp, C.POINTER(PetColumnsStruct), i32, C.POINTER(u64)]
         L.pj_encode_size_device.restype = i32
         for f in ("pj_decode_device", "pj_decode_host", "pj_decode_array_device", "pj_decode_array_host"):
@@ -380,16 +382,18 @@ class Codec:
                                                     out.numel(), C.byref(n)))
         return out[: n.value]
 
-    def encode_host(self, cols: Columns, fmt: int = FORMAT_ARRAY) -> bytes:
+    def encode_host(self, cols: Columns, fmt: int = FORMAT_ARRAY, as_array: bool = False):
+        """Encode host columns in one call, into a buffer sized by
+        pj_encode_bound.  Returns bytes (or, with as_array, the numpy uint8
+        view of the buffer, which saves a copy)."""
         s = cols.struct()
+        bound = C.c_uint64(0)
+        self._check(self.L.pj_encode_bound(C.byref(s), fmt, C.byref(bound)))
+        out = np.empty(max(1, bound.value), dtype=np.uint8)
         n = C.c_uint64(0)
-        rc = self.L.pj_encode_host(self.ctx, C.byref(s), fmt, None, 0, C.byref(n))
-        if rc not in (PJ_OK, PJ_ERR_CAPACITY):
-            self._check(rc)
-        out = np.empty(max(1, n.value), dtype=np.uint8)
         self._check(self.L.pj_encode_host(self.ctx, C.byref(s), fmt, C.c_void_p(out.ctypes.data), out.size,
                                           C.byref(n)))
-        return out[: n.value].tobytes()
+        return out[: n.value] if as_array else out[: n.value].tobytes()
 
     # ---- decode
     def _alloc_decode(self, caps, device):

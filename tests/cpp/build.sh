@@ -22,7 +22,7 @@ if [ -f "$PKG/_build/pj_encode_hip.o" ] && [ -f "$PKG/_build/pj_decode_hip.o" ];
         $HIPCC $SANF -g -O1 -std=c++17 --offload-arch=gfx950 -I"$ROOT/include" -I"$PKG/csrc" \
             -c "$src" -o "$OBJ/$(basename "$src").o" 2>/dev/null
     done
-    $HIPCC --offload-arch=gfx950 -fsanitize=address,undefined "$OBJ/pj_api.cpp.o" "$OBJ/pj_gen.cpp.o" \
+    $HIPCC --offload-arch=gfx950 -fsanitize=address,undefined -fno-gpu-sanitize "$OBJ/pj_api.cpp.o" "$OBJ/pj_gen.cpp.o" \
         "$OBJ/api_sanitize.cpp.o" "$PKG/_build/pj_encode_hip.o" "$PKG/_build/pj_decode_hip.o" -pthread \
         -o "$HERE/bin/api_sanitize"
     rm -rf "$OBJ"
