@@ -59,12 +59,18 @@ def encode_workload(codec, config, n, steps, warmup):
     in_bytes = col_bytes(cols)
     out_bytes, wall, kms, _ = run_encode(codec, dev, pj.FORMAT_ARRAY, steps, warmup)
     alg = in_bytes + out_bytes
+    # the host entry point on the same columns (PCIe-inclusive; not the headline)
+    codec.encode_host(cols, pj.FORMAT_ARRAY, as_array=True)
+    th = time.perf_counter()
+    codec.encode_host(cols, pj.FORMAT_ARRAY, as_array=True)
+    th = time.perf_counter() - th
     res = {
         "records": n, "records_per_s": n / wall, "ms_per_step": wall * 1e3,
         "output_bytes": out_bytes, "input_bytes": in_bytes,
         "output_GBps": out_bytes / wall / 1e9, "output_frac_hbm": out_bytes / wall / 1e9 / HBM_PEAK_GBPS,
         "kernel_ms": kms, "kernel_alg_GBps": alg / (kms * 1e-3) / 1e9,
         "kernel_alg_frac_hbm": alg / (kms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "host_entry_point": {"encode_host_ms": th * 1e3, "moved_GBps": alg / th / 1e9},
     }
     return cols, res
 
@@ -83,6 +89,8 @@ def decode_workload(codec, n, steps, warmup):
     torch.cuda.empty_cache()
     lines, codes = pj.corrupt_ndjson(host, 0xBAD, 0.001)
     data = torch.from_numpy(host).cuda()
+    host_text = host.tobytes()
+    del host
     sz = cols.sizes()
     caps = {"cap_pets": n, "cap_name_bytes": sz["name_bytes"], "cap_cat_name_bytes": sz["cat_name_bytes"],
             "cap_urls": sz["n_urls"], "cap_url_bytes": sz["url_bytes"], "cap_tags": sz["n_tags"],
@@ -91,36 +99,40 @@ def decode_workload(codec, n, steps, warmup):
     for _ in range(warmup):
         codec.decode(data, out=bufs)
     torch.cuda.synchronize()
-    ti, tp, te, tw = [], [], [], []
+    names = ["k_dec_lines", "k_dec_block", "k_dec_bscan", "k_dec_write", "k_dec_long", "k_dec_errcode"]
+    per = {k: [] for k in names}
     t0 = time.perf_counter()
     for _ in range(steps):
         dcols, el, ec, res = codec.decode(data, out=bufs)
-        # [total, fill, k_dec_lines, host gap, fill, k_dec_block, (k_dec_bscan, k_dec_write, k_dec_long,)
-        #  k_dec_errcode]
+        # [total, fill, k_dec_lines, host gap, fill, k_dec_block, k_dec_bscan, k_dec_write, k_dec_long,
+        #  k_dec_errcode] (HIP events on the codec stream)
         tm = codec.timings()
-        ti.append(tm[2])
-        tp.append(tm[5])
-        te.append(tm[-1])
-        if len(tm) >= 10:
-            tw.append(tm[6] + tm[7] + tm[8])
+        for k, i in zip(names, (2, 5, 6, 7, 8, 9)):
+            per[k].append(tm[i])
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     ok = (res.n_errors == len(lines) and np.array_equal(el.cpu().numpy().astype(np.uint64), lines)
           and np.array_equal(ec.cpu().numpy(), codes) and res.n_pets == n - len(lines))
     out_bytes = sum(int(dcols[k].numel()) * dcols[k].element_size() for k in pj.COLS)
     in_bytes = int(data.numel())
-    kidx, kpar, kerr = sum(ti) / len(ti), sum(tp) / len(tp), sum(te) / len(te)
+    kern = {k + "_ms": sum(v) / len(v) for k, v in per.items()}
+    ksum = sum(kern.values())
+    kern["kernels_sum_ms"] = ksum
+    kern["k_dec_lines_GBps"] = in_bytes / (kern["k_dec_lines_ms"] * 1e-3) / 1e9
+    kern["alg_frac_hbm_kernels"] = (in_bytes + out_bytes) / (ksum * 1e-3) / 1e9 / HBM_PEAK_GBPS
+    # the host entry point on the same text (PCIe-inclusive; not the headline)
+    host = host_text if host_text is not None else data.cpu().numpy().tobytes()
+    codec.decode_host(host, caps=caps, err_cap=max(16, 2 * len(lines)))
+    th = time.perf_counter()
+    codec.decode_host(host, caps=caps, err_cap=max(16, 2 * len(lines)))
+    th = time.perf_counter() - th
     r = {"records": int(res.n_lines), "records_per_s": res.n_lines / wall, "ms_per_step": wall * 1e3,
          "input_bytes": in_bytes, "output_bytes": out_bytes, "input_GBps": in_bytes / wall / 1e9,
          "alg_GBps": (in_bytes + out_bytes) / wall / 1e9,
          "alg_frac_hbm": (in_bytes + out_bytes) / wall / 1e9 / HBM_PEAK_GBPS,
          "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
-         "lines_general_parser": int(res.n_general),
-         "kernels": {"k_dec_lines_ms": kidx, "k_dec_block_ms": kpar, "k_dec_errcode_ms": kerr,
-                     "k_dec_scan_write_long_ms": sum(tw) / len(tw) if tw else None,
-                     "k_dec_lines_GBps": in_bytes / (kidx * 1e-3) / 1e9,
-                     "k_dec_block_alg_GBps": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9,
-                     "k_dec_block_alg_frac_hbm": (in_bytes + out_bytes) / (kpar * 1e-3) / 1e9 / HBM_PEAK_GBPS}}
+         "lines_general_parser": int(res.n_general), "kernels": kern,
+         "host_entry_point": {"decode_host_ms": th * 1e3, "input_GBps": in_bytes / th / 1e9}}
     return r
 
 
