@@ -21,6 +21,10 @@ HIP_SOURCES = ["pj_api.cpp", "pj_encode.hip", "pj_decode.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function", f"-I{INC}", f"-I{CSRC}"]
+# The encode kernels loop over blocks (persistent workgroups); machine LICM
+# would hoist every literal and SWAR constant of the emitters out of that
+# loop into its own VGPR (about 65 of them, all live for the whole kernel).
+FILE_FLAGS = {"pj_encode.hip": ["-mllvm", "-disable-machine-licm"]}
 
 
 def _run(cmd):
@@ -40,7 +44,7 @@ def build(verbose=False):
     def compile_one(src):
         obj = os.path.join(objdir, src.replace(".", "_") + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        return _run([HIPCC, *HIP_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj]), obj
+        return _run([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(src, []), *lang, "-c", os.path.join(CSRC, src), "-o", obj]), obj
 
     with ThreadPoolExecutor(max_workers=4) as ex:
         fut_gen = ex.submit(_run, ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-pthread",

@@ -293,11 +293,12 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.nfall = reinterpret_cast<unsigned long long *>(sc + 2);
     P.state = sc + 3;
     P.dummy = reinterpret_cast<uint32_t *>(sc + 3 + nblk);   // 128 u64 = PJ_BLOCK dwords
-    // Blocks take their records in launch order (no ticket atomic on the
-    // critical path).  The look-back waits are bounded: should a block wait
-    // past the bound (a predecessor not yet running), it flags the launch,
-    // which is then redone with ticket-ordered blocks.
-    P.order_by_id = 1;
+    // Nested records run on persistent workgroups that claim their blocks by
+    // ticket.  Flat blocks run one per workgroup in launch order (no ticket
+    // atomic on the critical path) with bounded look-back waits: should a
+    // block wait past the bound (a predecessor not yet running), it flags
+    // the launch, which is then redone with ticket-ordered blocks.
+    P.order_by_id = nested_cols(cols) ? 0 : 1;
     P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;

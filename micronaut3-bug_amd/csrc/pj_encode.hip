@@ -726,15 +726,6 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 }
 
 // ------------------------------------------------------------------ kernel
-// Per workgroup: R records.  Fast blocks stage the string bytes of their
-// records (names, category names, urls, tag names: one contiguous slice of
-// each byte column) into LDS with 16-byte loads, measure and build the
-// output tile from there, and copy the tile out with aligned 16-byte stores.
-// Blocks whose slices, lists or output do not fit write each record from one
-// thread, reading global memory, except records with a long name or a long
-// list, which the whole workgroup measures and writes (slices of the string
-// escaped in parallel and placed by a block scan, items spread over the
-// threads), so one skewed record does not hold its workgroup for long.
 // Copy global bytes [lo, hi) out of an LDS tile whose byte x belongs at
 // global address D + x (all threads of the workgroup).  Global chunk c
 // covers [g0 + 16c, g0 + 16c + 16) with g0 = D - (D & 15), which is tile
@@ -744,8 +735,8 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 // blocks or segments) with exact 8/4/2/1-byte stores.  The tile must be
 // readable 16 bytes past hi - D.
 template <int BT>
-__device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi) {
-    const uint32_t t = threadIdx.x;
+__device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi,
+                                              uint32_t t = threadIdx.x) {
     const uint32_t s = (uint32_t)(D & 15);
     const uint64_t g0 = D - s;
     const uint32_t c_lo = (uint32_t)((lo - g0) >> 4), c_hi = (uint32_t)((hi - g0 + 15) >> 4);
@@ -794,6 +785,133 @@ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out,
     }
 }
 
+// Where a block's records, items and string bytes lie: fetched for block nb
+// by the first wave in two dependent rounds.  Lanes 0-7 load the first
+// level (url and tag item ranges, name and category name byte ranges),
+// lanes 0-3 then the url and tag name byte ranges those select.  Laid out
+// as [0] first url item, [1] end, [2] first tag item, [3] end, then
+// (first byte, end) of the name, category name, url and tag name columns.
+constexpr int NX = 12;
+template <bool NESTED, int R>
+__device__ __forceinline__ uint64_t bounds_l1(const EncParams &P, uint64_t nb, uint32_t l) {
+    const pj_pet_columns &c = P.c;
+    if (l >= 8 || nb >= (P.n + R - 1) / R) return 0;
+    const uint64_t r = (l & 1) ? min(nb * R + R, P.n) : nb * R;
+    const uint32_t k = l >> 1;
+    const uint64_t *o = k == 0   ? (NESTED ? c.photo_off : nullptr)
+                        : k == 1 ? (NESTED ? c.tag_off : nullptr)
+                        : k == 2 ? c.name_off
+                                 : (NESTED && c.cat_id ? c.cat_name_off : nullptr);
+    return o ? o[r] : 0;
+}
+template <bool NESTED>
+__device__ __forceinline__ uint64_t bounds_l2(const EncParams &P, uint64_t v1, uint32_t l) {
+    if (!NESTED || l >= 4) return 0;
+    const uint64_t *o = l < 2 ? (P.c.photo_off ? P.c.url_off : nullptr) : (P.c.tag_off ? P.c.tag_name_off : nullptr);
+    return o ? o[v1] : 0;
+}
+__device__ __forceinline__ void bounds_store(uint64_t *nx, uint64_t v1, uint64_t v2, uint32_t l) {
+    if (l < 8) nx[l] = v1;
+    if (l < 4) nx[8 + l] = v2;
+}
+
+// A block's item ranges and staged slices (16-byte aligned chunk ranges of
+// the four string columns, laid end to end in the staging buffer).
+struct Geo {
+    uint64_t r0, U0, G0, U, G;
+    uint64_t lo16[4];
+    uint32_t nch[4], off[5];
+    bool fast;
+};
+template <bool NESTED, int R, int INCAP, int UCAP, int GCAP>
+__device__ __forceinline__ Geo block_geo(const uint64_t *nx, uint64_t b) {
+    Geo g;
+    g.r0 = b * R;
+    g.U0 = nx[0];
+    g.G0 = nx[2];
+    g.U = nx[1] - nx[0];
+    g.G = nx[3] - nx[2];
+    g.off[0] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint64_t lo = nx[4 + 2 * k], hi = nx[5 + 2 * k];
+        g.lo16[k] = lo & ~15ull;
+        const uint64_t hi16 = (hi + 15) & ~15ull;
+        g.nch[k] = hi > lo ? (uint32_t)min((hi16 - g.lo16[k]) >> 4, (uint64_t)INCAP) : 0;
+        g.off[k + 1] = g.off[k] + 16 * g.nch[k];
+    }
+    g.fast = g.off[4] <= INCAP && (!NESTED || (g.U <= UCAP && g.G <= GCAP));
+    return g;
+}
+
+// Unit layout of a nested fast block over its threads' slots (slot j of
+// thread t is list position t + j BT): heads of records 0..R-1 from position
+// 0, names from NAME0, url then tag items from ITEM0, each kind starting on
+// a wave boundary so that no wave runs two kinds of unit in one slot.
+template <int R> constexpr int name0() { return (R + 63) / 64 * 64; }
+template <int R> constexpr int item0() { return (name0<R>() + R + 63) / 64 * 64; }
+
+// Issue the global loads of a block (its record values, the item values of
+// a fast block and the 16-byte chunks of its staged slices, SV per thread)
+// into registers; they are consumed one phase of the previous block later.
+template <bool NESTED, int BT, int R, int NI, int SV>
+__device__ __forceinline__ void enc_prefetch(const EncParams &P, const Geo &g, RecVals &rv, TagItem (&iv)[NI],
+                                             uint4 (&sv)[SV]) {
+    const uint32_t t = threadIdx.x;
+    const uint64_t i = g.r0 + t;
+    rv = RecVals{};
+    if (t < (uint32_t)R && i < P.n) rv = load_rec<NESTED>(P, i);
+    if (!g.fast) return;
+    if constexpr (NESTED) {
+#pragma unroll
+        for (int j = 0; j < NI; j++) {
+            const uint32_t q = t + (uint32_t)j * BT;
+            if (q < (uint32_t)item0<R>()) continue;
+            const uint32_t k = q - item0<R>();
+            if (k < g.U) {
+                const UrlItem u = load_url(P, g.U0 + k);
+                iv[j].a = u.a;
+                iv[j].b = u.b;
+            } else if (k < g.U + g.G) iv[j] = load_tag(P, g.G0 + (k - g.U));
+        }
+    }
+    const pj_pet_columns &c = P.c;
+    const uint8_t *srcs[4] = {c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes};
+    const uint32_t tot = g.off[4] >> 4;
+#pragma unroll
+    for (int u = 0; u < SV; u++) {
+        const uint32_t j = t + u * BT;
+        sv[u] = make_uint4(0, 0, 0, 0);
+        if (j < tot) {
+            const uint32_t byte = 16 * j;
+            const int k = byte >= g.off[1] ? (byte >= g.off[2] ? (byte >= g.off[3] ? 3 : 2) : 1) : 0;
+            const uint8_t *src = (k == 0 ? srcs[0] : k == 1 ? srcs[1] : k == 2 ? srcs[2] : srcs[3]) +
+                                 ((k == 0 ? g.lo16[0] : k == 1 ? g.lo16[1] : k == 2 ? g.lo16[2] : g.lo16[3]) +
+                                  (byte - (k == 0 ? g.off[0] : k == 1 ? g.off[1] : k == 2 ? g.off[2] : g.off[3])));
+            sv[u] = *reinterpret_cast<const uint4 *>(src);
+        }
+    }
+}
+
+// Nested records: persistent workgroups (as many as the device holds), each
+// running blocks of R records until none is left.  Once a block's look-back
+// is resolved, the first wave claims the next block by ticket (so that
+// consecutive tickets start at nearly the same time and a look-back finds
+// its predecessors published; every claimed block belongs to a running
+// workgroup) and fetches its bounds while the other waves copy the tile
+// out; the next block's record, item and staging loads are then in flight
+// across the block boundary.  Flat records: one block per workgroup, in
+// launch order with a bounded look-back wait (or by ticket when the host
+// redoes a launch whose wait ran out).
+// Per block: fast blocks stage the string bytes of their records (names,
+// category names, urls, tag names: one contiguous slice of each byte
+// column) into LDS, measure and build the output tile from there, and copy
+// the tile out with aligned 16-byte stores.  Blocks whose slices, lists or
+// output do not fit write each record from one thread, reading global
+// memory, except records with a long name or a long list, which the whole
+// workgroup measures and writes (slices of the string escaped in parallel
+// and placed by a block scan, items spread over the threads), so one
+// skewed record does not hold its workgroup for long.
 template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP, int WPE = 1>
 __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
@@ -815,7 +933,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t splain[(INCAP / 16 + 63) / 64];  // staged 16-byte chunks that hold a byte to escape
-    __shared__ uint64_t sh_blk, sh_base, sh_rng[4], sh_lo[4], sh_hi[4], sh_len;
+    __shared__ uint64_t sh_nx[NX], sh_nb, sh_base, sh_len;
     __shared__ uint32_t sh_nbig;
     // hybrid blocks (NESTED): the large records in record order, with their
     // block offsets, lengths and tile offsets; fast blocks keep each record's
@@ -824,347 +942,333 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     constexpr int RB = NESTED ? R : 1;
     __shared__ uint32_t sh_big[RB], sh_bpre[RB], sh_blen[RB], sh_bspre[RB];
     static_assert(3 * R * 4 <= TILE, "the fallback path keeps its large-record list in the tile");
+    // NESTED fast blocks: thread t holds units t + j BT of the list
+    // [heads (R) | names (R) | url items (U) | tag items (G)], laid out as
+    // name0 / item0 say: the record threads t < R write head, tags opener
+    // and tail of record t, threads
+    // NAME0..NAME0+R-1 the name and photoUrls opener of record t - NAME0,
+    // the rest items
+    static_assert(!NESTED || item0<R>() <= BT, "a head and a name unit per record in the first slot");
+    // nested workgroups are persistent; flat blocks, with less latency per
+    // block to hide, measured faster one per workgroup
+    constexpr bool PERSIST = NESTED;
+    constexpr int NI = NESTED ? (item0<R>() + UCAP + GCAP + BT - 1) / BT : 1;
+    constexpr int SV = (INCAP / 16 + BT - 1) / BT;   // staged chunks per thread
     const uint32_t t = threadIdx.x;
     const pj_pet_columns &c = P.c;
-    // the flat tile starts zeroed: writers merge the qwords they share with an OR
-    if (!NESTED)
-        for (uint32_t k = t; k < (uint32_t)TILE / 16; k += BT) reinterpret_cast<uint4 *>(tile)[k] = make_uint4(0, 0, 0, 0);
-    if (t == 0) {
-        const uint64_t b = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(P.ticket, 1ull);
-        sh_blk = b;
-        const uint64_t r0 = b * R, r1 = min(r0 + R, P.n);
-        const bool pu = NESTED && c.photo_off, pt = NESTED && c.tag_off;
-        const uint64_t u0 = pu ? c.photo_off[r0] : 0, u1 = pu ? c.photo_off[r1] : 0;
-        const uint64_t g0 = pt ? c.tag_off[r0] : 0, g1 = pt ? c.tag_off[r1] : 0;
-        sh_rng[0] = u0; sh_rng[1] = u1; sh_rng[2] = g0; sh_rng[3] = g1;
-        // byte slices: names, category names, urls, tag names
-        sh_lo[0] = c.name_off[r0]; sh_hi[0] = c.name_off[r1];
-        const bool pc = NESTED && c.cat_id && c.cat_name_off;
-        sh_lo[1] = pc ? c.cat_name_off[r0] : 0; sh_hi[1] = pc ? c.cat_name_off[r1] : 0;
-        sh_lo[2] = u1 > u0 ? c.url_off[u0] : 0; sh_hi[2] = u1 > u0 ? c.url_off[u1] : 0;
-        sh_lo[3] = g1 > g0 ? c.tag_name_off[g0] : 0; sh_hi[3] = g1 > g0 ? c.tag_name_off[g1] : 0;
+    const uint64_t nblk = (P.n + R - 1) / R;
+
+    // ---- the first block: its number and bounds, then its loads
+    if (t < 64) {
+        unsigned long long tk = 0;
+        const bool by_id = !PERSIST && P.order_by_id;
+        if (!by_id && t == 0) tk = atomicAdd(P.ticket, 1ull);
+        const uint64_t b0 = by_id ? (uint64_t)blockIdx.x : (uint64_t)__shfl((long long)tk, 0);
+        const uint64_t v1 = bounds_l1<NESTED, R>(P, b0, t);
+        bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
+        if (t == 0) sh_nb = b0;
     }
     __syncthreads();
-    const uint64_t b = sh_blk;
+    uint64_t b = sh_nb;
+    RecVals rv{};
+    TagItem iv[NI];                                 // item column values (a url uses a, b)
+    uint4 sv[SV];                                   // staged chunks in flight
+    if (b < nblk) enc_prefetch<NESTED, BT, R, NI, SV>(P, block_geo<NESTED, R, INCAP, UCAP, GCAP>(sh_nx, b), rv, iv, sv);
+
+    while (b < nblk) {
 #ifdef PJ_ENC_PROF
 #define EPROF(k) if (t == 0 && !P.count_only && P.out) reinterpret_cast<uint64_t *>(P.out + P.cap)[-1 - (int64_t)(b * 6 + (k))] = wall_clock64();
 #else
 #define EPROF(k)
 #endif
-    EPROF(0);
-    const uint64_t r0 = b * R;
-    const uint64_t U0 = sh_rng[0], G0 = sh_rng[2];
-    const uint64_t U = sh_rng[1] - U0, G = sh_rng[3] - G0;
-    const uint64_t i = r0 + t;
-    const bool live = t < (uint32_t)R && i < P.n;
-    RecVals rv{};
-    if (live) rv = load_rec<NESTED>(P, i);
-    // staged slices: 16-byte aligned chunk ranges, laid end to end in inb
-    uint64_t lo16[4];
-    uint32_t nch[4], off[5];
-    off[0] = 0;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        lo16[k] = sh_lo[k] & ~15ull;
-        const uint64_t hi16 = (sh_hi[k] + 15) & ~15ull;
-        nch[k] = sh_hi[k] > sh_lo[k] ? (uint32_t)min((hi16 - lo16[k]) >> 4, (uint64_t)INCAP) : 0;
-        off[k + 1] = off[k] + 16 * nch[k];
-    }
-    const bool fast = off[4] <= INCAP && (!NESTED || (U <= UCAP && G <= GCAP));
-    const ColSrc XG{c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes, 0, 0, 0, 0};
-    const ColSrc XL{inb + off[0], inb + off[1], inb + off[2], inb + off[3], lo16[0], lo16[1], lo16[2], lo16[3],
-                    splain, inb};
-    const uint8_t *srcs[4] = {c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes};
+        EPROF(0);
+        const Geo g = block_geo<NESTED, R, INCAP, UCAP, GCAP>(sh_nx, b);
+        uint64_t nb = 0;
+        // the flat tile starts zeroed: writers merge the qwords they share with an OR
+        if (!NESTED)
+            for (uint32_t k = t; k < (uint32_t)TILE / 16; k += BT) reinterpret_cast<uint4 *>(tile)[k] = make_uint4(0, 0, 0, 0);
+        const uint64_t r0 = g.r0;
+        const uint64_t U0 = g.U0, G0 = g.G0, U = g.U, G = g.G;
+        const uint64_t i = r0 + t;
+        const bool live = t < (uint32_t)R && i < P.n;
+        const bool fast = g.fast;
+        const ColSrc XG{c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes, 0, 0, 0, 0};
+        const ColSrc XL{inb + g.off[0], inb + g.off[1], inb + g.off[2], inb + g.off[3], g.lo16[0], g.lo16[1], g.lo16[2],
+                        g.lo16[3], splain, inb};
 
-    RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
-    uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
-    // NESTED fast blocks: thread t holds units t + j BT of the list
-    // [heads (R) | names (R) | url items (U) | tag items (G)]: the record
-    // threads t < R write head, tags opener and tail of record t, threads
-    // R..2R-1 the name and photoUrls opener of record t - R, the rest items
-    static_assert(!NESTED || 2 * R <= BT, "a head and a name unit per record in the first slot");
-    constexpr int NI = NESTED ? (2 * R + UCAP + GCAP + BT - 1) / BT : 1;
-    TagItem iv[NI];                                 // item column values (a url uses a, b)
-    uint32_t hidx = 0;                              // record thread: unit index of its head
-    const uint32_t nrec = (uint32_t)min((uint64_t)R, P.n - r0);
-    uint64_t len = 0, pre = 0, agg = 0;
-    bool isbig = false;                             // fallback blocks: measured by the whole workgroup
-    uint32_t nbig = 0, bidx = 0;
-    if (fast) {
-        if constexpr (NESTED) {
-            // item column values first, so their loads overlap the staging
+        RecItems ri{0, 0, NO_ITEMS, NO_ITEMS};
+        uint32_t ul0 = 0, ul1 = 0, gl0 = 0, gl1 = 0;
+        uint32_t hidx = 0;                              // record thread: unit index of its head
+        const uint32_t nrec = (uint32_t)min((uint64_t)R, P.n - r0);
+        uint64_t len = 0, pre = 0, agg = 0;
+        bool isbig = false;                             // fallback blocks: measured by the whole workgroup
+        uint32_t nbig = 0, bidx = 0;
+        if (fast) {
+            // ---- phase 0: the staged chunks go into LDS, with a bitmap of
+            // the chunks that hold a byte to escape
+            const uint32_t tot = g.off[4] >> 4;
 #pragma unroll
-            for (int j = 0; j < NI; j++) {
-                const uint32_t q = t + (uint32_t)j * BT;
-                if (q < 2 * R) continue;
-                const uint32_t k = q - 2 * R;
-                if (k < U) {
-                    const UrlItem u = load_url(P, U0 + k);
-                    iv[j].a = u.a;
-                    iv[j].b = u.b;
-                } else if (k < U + G) iv[j] = load_tag(P, G0 + (k - U));
-            }
-        }
-        // ---- phase 0: stage the input slices (4 loads in flight per thread)
-        const uint32_t tot = off[4] >> 4;
-        for (uint32_t j0 = t; j0 < tot; j0 += 4 * BT) {
-            uint4 v[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t j = j0 + u * BT;
-                v[u] = make_uint4(0, 0, 0, 0);
-                if (j < tot) {
-                    const uint32_t byte = 16 * j;
-                    const int k = byte >= off[1] ? (byte >= off[2] ? (byte >= off[3] ? 3 : 2) : 1) : 0;
-                    const uint8_t *g = (k == 0 ? srcs[0] : k == 1 ? srcs[1] : k == 2 ? srcs[2] : srcs[3]) +
-                                       ((k == 0 ? lo16[0] : k == 1 ? lo16[1] : k == 2 ? lo16[2] : lo16[3]) +
-                                        (byte - (k == 0 ? off[0] : k == 1 ? off[1] : k == 2 ? off[2] : off[3])));
-                    v[u] = *reinterpret_cast<const uint4 *>(g);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const uint32_t j = j0 + u * BT;
-                if (j < tot) reinterpret_cast<uint4 *>(inb)[j] = v[u];
+            for (int u = 0; u < SV; u++) {
+                const uint32_t j = t + u * BT;
+                if (j < tot) reinterpret_cast<uint4 *>(inb)[j] = sv[u];
                 // a wave holds 64 consecutive chunks: one ballot per bitmap word
-                const bool esc = j < tot && (special64(((uint64_t)v[u].y << 32) | v[u].x) |
-                                             special64(((uint64_t)v[u].w << 32) | v[u].z)) != 0;
+                const bool esc = j < tot && (special64(((uint64_t)sv[u].y << 32) | sv[u].x) |
+                                             special64(((uint64_t)sv[u].w << 32) | sv[u].z)) != 0;
                 const uint64_t m = __ballot(esc);
                 if ((t & 63) == 0 && j < tot) splain[j >> 6] = m;
             }
-        }
-        if constexpr (NESTED) {
-            // record threads: unit indices, item owners, name unit inputs
-            // (sh_big / sh_bpre / sh_blen serve only hybrid blocks otherwise)
-            if (live) {
-                if (c.photo_off) { ul0 = (uint32_t)(rv.u0 - U0); ul1 = (uint32_t)(rv.u1 - U0); }
-                if (c.tag_off) { gl0 = (uint32_t)(rv.t0 - G0); gl1 = (uint32_t)(rv.t1 - G0); }
-                hidx = 4 * t + ul0 + gl0;
-                sh_big[t] = hidx;
-                sh_bpre[t] = (uint32_t)(rv.na - lo16[0]);
-                sh_blen[t] = (uint32_t)(rv.nb - rv.na);
-                rn_f[t] = (uint8_t)((rv.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (rv.u1 == rv.u0 ? 0x80u : 0u));
-                uon[t] = rec_has_urls(rv);
-                gon[t] = rec_has_tags<NESTED>(rv);
-                ubase[t] = hidx + 2 - ul0;
-                gbase[t] = hidx + 3 + (ul1 - ul0) - gl0;
-                uend[t] = (uint16_t)ul1;
-                gend[t] = (uint16_t)gl1;
-                for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
-                for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
-            }
-        }
-        __syncthreads();
-        EPROF(1);
-        if constexpr (NESTED) {
-            // ---- phase 1: unit lengths, then their scan
-            if (live) {
-                const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
-                CountSink ch, cm, ct;
-                rec_head<NESTED>(ch, P, XL, i, rv);
-                rec_tags_open<NESTED>(cm, P, rv);
-                rec_tail(ct, P, i, rv);
-                ulen[hidx] = (uint32_t)ch.n;
-                ulen[hidx + 2 + nu] = (uint32_t)cm.n;
-                ulen[hidx + 3 + nu + nt] = (uint32_t)ct.n;
-            }
-            if (t >= (uint32_t)R && t - R < nrec) {
-                const uint32_t r = t - R;
-                CountSink cs;
-                name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
-                ulen[sh_big[r] + 1] = (uint32_t)cs.n;
-            }
-#pragma unroll
-            for (int j = 0; j < NI; j++) {
-                const uint32_t q = t + (uint32_t)j * BT;
-                if (q < 2 * R) continue;
-                const uint32_t k = q - 2 * R;
-                CountSink cs;
-                if (k < U) {
-                    const uint32_t own = uown[k];
-                    if (uon[own]) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
-                    ulen[ubase[own] + k] = (uint32_t)cs.n;
-                } else if (k < U + G) {
-                    const uint32_t kk = k - (uint32_t)U, own = gown[kk];
-                    if (gon[own]) emit_tag_v(cs, P, XL, iv[j], false);
-                    ulen[gbase[own] + kk] = (uint32_t)cs.n;
+            if constexpr (NESTED) {
+                // record threads: unit indices, item owners, name unit inputs
+                // (sh_big / sh_bpre / sh_blen serve only hybrid blocks otherwise)
+                if (live) {
+                    if (c.photo_off) { ul0 = (uint32_t)(rv.u0 - U0); ul1 = (uint32_t)(rv.u1 - U0); }
+                    if (c.tag_off) { gl0 = (uint32_t)(rv.t0 - G0); gl1 = (uint32_t)(rv.t1 - G0); }
+                    hidx = 4 * t + ul0 + gl0;
+                    sh_big[t] = hidx;
+                    sh_bpre[t] = (uint32_t)(rv.na - g.lo16[0]);
+                    sh_blen[t] = (uint32_t)(rv.nb - rv.na);
+                    rn_f[t] = (uint8_t)((rv.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (rv.u1 == rv.u0 ? 0x80u : 0u));
+                    uon[t] = rec_has_urls(rv);
+                    gon[t] = rec_has_tags<NESTED>(rv);
+                    ubase[t] = hidx + 2 - ul0;
+                    gbase[t] = hidx + 3 + (ul1 - ul0) - gl0;
+                    uend[t] = (uint16_t)ul1;
+                    gend[t] = (uint16_t)gl1;
+                    for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
+                    for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
                 }
             }
             __syncthreads();
-            const uint32_t NU = 4 * nrec + (uint32_t)(U + G);
-            lds_excl_scan<BT>(ulen, NU, sh_scan);
-            agg = ulen[NU];
-            if (live) {
-                pre = ulen[hidx];
-                len = ulen[hidx + 4 + (ul1 - ul0) + (gl1 - gl0)] - pre;
-            }
-            EPROF(2);
-        } else {
-            // ---- phase 2: record lengths
-            if (live) {
-                CountSink cs;
-                emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
-                len = cs.n;
-            }
-        }
-    } else {
-        // fallback block: records measured from global memory, one thread
-        // each, except large ones, which the whole workgroup measures
-        // the large records in record order (the tile holds the list here
-        // for the flat layout, which has no hybrid blocks)
-        uint32_t *big = NESTED ? sh_big : reinterpret_cast<uint32_t *>(tile);
-        isbig = live && rec_big<NESTED>(rv);
-        if (live && !isbig) {
-            CountSink cs;
-            emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
-            len = cs.n;
-        }
-        uint64_t nb64;
-        bidx = (uint32_t)block_excl_scan<BT>(isbig ? 1ull : 0ull, sh_scan, &nb64);
-        nbig = (uint32_t)nb64;
-        if (isbig) big[bidx] = t;
-        __syncthreads();
-        for (uint32_t k = 0; k < nbig; k++) {
-            const uint32_t r = big[k];
-            const RecVals bv = load_rec<NESTED>(P, r0 + r);
-            const uint64_t L = coop_rec<NESTED, BT>(P, nullptr, r0 + r, bv, sh_scan, &sh_len);
-            if (t == r) len = L;
-        }
-    }
-    // ---- block scan, publish the aggregate
-    if (!(NESTED && fast)) pre = block_excl_scan<BT>(len, sh_scan, &agg);
-    if (t == 0) lb_publish(P.state, b, agg);
-    const bool fits = fast && agg + 16 <= TILE;
-    if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
-    // Hybrid block (NESTED, fallback measuring): the records other than the
-    // large ones still go through the tile, laid end to end (tile offset
-    // spre), and leave as the segments between the large records, which the
-    // whole workgroup writes straight to global memory.
-    bool hyb = false;
-    uint64_t spre = 0;
-    if (NESTED && !fast) {
-        uint64_t stot;
-        spre = block_excl_scan<BT>(isbig ? 0ull : len, sh_scan, &stot);
-        hyb = stot + 16 <= TILE;
-        if (isbig) {
-            sh_bpre[bidx] = (uint32_t)pre;
-            sh_blen[bidx] = (uint32_t)len;
-            sh_bspre[bidx] = (uint32_t)spre;
-        }
-    }
-    if (hyb && !P.count_only && live && !isbig) {
-        LdsSink ls{tile, (uint32_t)spre};
-        RecItems r2 = ri;
-        emit_rec<NESTED, true>(ls, P, XG, i, rv, r2);
-        ls.finish();
-    }
-    EPROF(3);
-
-    if (fits && !P.count_only) {
-        // ---- phase 3: build the tile
-        if constexpr (NESTED) {
-            if (live) {
-                const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
-                LdsSink hs{tile, ulen[hidx], ulen[hidx + 1]};
-                rec_head<NESTED>(hs, P, XL, i, rv);
-                hs.finish();
-                LdsSink ms{tile, ulen[hidx + 2 + nu], ulen[hidx + 3 + nu]};
-                rec_tags_open<NESTED>(ms, P, rv);
-                ms.finish();
-                LdsSink ts{tile, ulen[hidx + 3 + nu + nt], ulen[hidx + 4 + nu + nt]};
-                rec_tail(ts, P, i, rv);
-                ts.finish();
-            }
-            if (t >= (uint32_t)R && t - R < nrec) {
-                const uint32_t r = t - R;
-                LdsSink ns{tile, ulen[sh_big[r] + 1], ulen[sh_big[r] + 2]};
-                name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
-                ns.finish();
-            }
+            EPROF(1);
+            if constexpr (NESTED) {
+                // ---- phase 1: unit lengths, then their scan
+                if (live) {
+                    const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
+                    CountSink ch, cm, ct;
+                    rec_head<NESTED>(ch, P, XL, i, rv);
+                    rec_tags_open<NESTED>(cm, P, rv);
+                    rec_tail(ct, P, i, rv);
+                    ulen[hidx] = (uint32_t)ch.n;
+                    ulen[hidx + 2 + nu] = (uint32_t)cm.n;
+                    ulen[hidx + 3 + nu + nt] = (uint32_t)ct.n;
+                }
+                if (t >= (uint32_t)name0<R>() && t - name0<R>() < nrec) {
+                    const uint32_t r = t - name0<R>();
+                    CountSink cs;
+                    name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                    ulen[sh_big[r] + 1] = (uint32_t)cs.n;
+                }
 #pragma unroll
-            for (int j = 0; j < NI; j++) {
-                const uint32_t q = t + (uint32_t)j * BT;
-                if (q < 2 * R) continue;
-                const uint32_t k = q - 2 * R;
-                if (k < U) {
-                    const uint32_t own = uown[k];
-                    if (!uon[own]) continue;
-                    LdsSink ls{tile, ulen[ubase[own] + k], ulen[ubase[own] + k + 1]};
-                    emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, k + 1 == uend[own]);
-                    ls.finish();
-                } else if (k < U + G) {
-                    const uint32_t kk = k - (uint32_t)U, own = gown[kk];
-                    if (!gon[own]) continue;
-                    LdsSink ls{tile, ulen[gbase[own] + kk], ulen[gbase[own] + kk + 1]};
-                    emit_tag_v(ls, P, XL, iv[j], kk + 1 == gend[own]);
-                    ls.finish();
+                for (int j = 0; j < NI; j++) {
+                    const uint32_t q = t + (uint32_t)j * BT;
+                    if (q < (uint32_t)item0<R>()) continue;
+                    const uint32_t k = q - item0<R>();
+                    CountSink cs;
+                    if (k < U) {
+                        const uint32_t own = uown[k];
+                        if (uon[own]) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
+                        ulen[ubase[own] + k] = (uint32_t)cs.n;
+                    } else if (k < U + G) {
+                        const uint32_t kk = k - (uint32_t)U, own = gown[kk];
+                        if (gon[own]) emit_tag_v(cs, P, XL, iv[j], false);
+                        ulen[gbase[own] + kk] = (uint32_t)cs.n;
+                    }
+                }
+                __syncthreads();
+                const uint32_t NU = 4 * nrec + (uint32_t)(U + G);
+                lds_excl_scan<BT>(ulen, NU, sh_scan);
+                agg = ulen[NU];
+                if (live) {
+                    pre = ulen[hidx];
+                    len = ulen[hidx + 4 + (ul1 - ul0) + (gl1 - gl0)] - pre;
+                }
+                EPROF(2);
+            } else {
+                // ---- phase 2: record lengths
+                if (live) {
+                    CountSink cs;
+                    emit_rec<NESTED, false>(cs, P, XL, i, rv, ri);
+                    len = cs.n;
                 }
             }
-        } else if (live) {
-            LdsSink ls{tile, (uint32_t)pre};
+        } else {
+            // fallback block: records measured from global memory, one thread
+            // each, except large ones, which the whole workgroup measures
+            // the large records in record order (the tile holds the list here
+            // for the flat layout, which has no hybrid blocks)
+            uint32_t *big = NESTED ? sh_big : reinterpret_cast<uint32_t *>(tile);
+            isbig = live && rec_big<NESTED>(rv);
+            if (live && !isbig) {
+                CountSink cs;
+                emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
+                len = cs.n;
+            }
+            uint64_t nb64;
+            bidx = (uint32_t)block_excl_scan<BT>(isbig ? 1ull : 0ull, sh_scan, &nb64);
+            nbig = (uint32_t)nb64;
+            if (isbig) big[bidx] = t;
+            __syncthreads();
+            for (uint32_t k = 0; k < nbig; k++) {
+                const uint32_t r = big[k];
+                const RecVals bv = load_rec<NESTED>(P, r0 + r);
+                const uint64_t L = coop_rec<NESTED, BT>(P, nullptr, r0 + r, bv, sh_scan, &sh_len);
+                if (t == r) len = L;
+            }
+        }
+        // ---- block scan, publish the aggregate
+        if (!(NESTED && fast)) pre = block_excl_scan<BT>(len, sh_scan, &agg);
+        if (t == 0) lb_publish(P.state, b, agg);
+        const bool fits = fast && agg + 16 <= TILE;
+        if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
+        // Hybrid block (NESTED, fallback measuring): the records other than the
+        // large ones still go through the tile, laid end to end (tile offset
+        // spre), and leave as the segments between the large records, which the
+        // whole workgroup writes straight to global memory.
+        bool hyb = false;
+        uint64_t spre = 0;
+        if (NESTED && !fast) {
+            uint64_t stot;
+            spre = block_excl_scan<BT>(isbig ? 0ull : len, sh_scan, &stot);
+            hyb = stot + 16 <= TILE;
+            if (isbig) {
+                sh_bpre[bidx] = (uint32_t)pre;
+                sh_blen[bidx] = (uint32_t)len;
+                sh_bspre[bidx] = (uint32_t)spre;
+            }
+        }
+        if (hyb && !P.count_only && live && !isbig) {
+            LdsSink ls{tile, (uint32_t)spre};
             RecItems r2 = ri;
-            emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
+            emit_rec<NESTED, true>(ls, P, XG, i, rv, r2);
             ls.finish();
         }
-    }
-    EPROF(4);
-    // ---- phase 4: look-back, then copy out
-    if (t < 64) {
-        const uint64_t excl = lb_resolve(P.state, b, agg, P.order_by_id ? P.spin_limit : 0, P.ticket);
-        if (t == 0) {
-            sh_base = excl;
-            if (b == gridDim.x - 1) *P.total = excl + agg;
+        EPROF(3);
+
+        if (fits && !P.count_only) {
+            // ---- phase 3: build the tile
+            if constexpr (NESTED) {
+                if (live) {
+                    const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
+                    LdsSink hs{tile, ulen[hidx], ulen[hidx + 1]};
+                    rec_head<NESTED>(hs, P, XL, i, rv);
+                    hs.finish();
+                    LdsSink ms{tile, ulen[hidx + 2 + nu], ulen[hidx + 3 + nu]};
+                    rec_tags_open<NESTED>(ms, P, rv);
+                    ms.finish();
+                    LdsSink ts{tile, ulen[hidx + 3 + nu + nt], ulen[hidx + 4 + nu + nt]};
+                    rec_tail(ts, P, i, rv);
+                    ts.finish();
+                }
+                if (t >= (uint32_t)name0<R>() && t - name0<R>() < nrec) {
+                    const uint32_t r = t - name0<R>();
+                    LdsSink ns{tile, ulen[sh_big[r] + 1], ulen[sh_big[r] + 2]};
+                    name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                    ns.finish();
+                }
+#pragma unroll
+                for (int j = 0; j < NI; j++) {
+                    const uint32_t q = t + (uint32_t)j * BT;
+                    if (q < (uint32_t)item0<R>()) continue;
+                    const uint32_t k = q - item0<R>();
+                    if (k < U) {
+                        const uint32_t own = uown[k];
+                        if (!uon[own]) continue;
+                        LdsSink ls{tile, ulen[ubase[own] + k], ulen[ubase[own] + k + 1]};
+                        emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, k + 1 == uend[own]);
+                        ls.finish();
+                    } else if (k < U + G) {
+                        const uint32_t kk = k - (uint32_t)U, own = gown[kk];
+                        if (!gon[own]) continue;
+                        LdsSink ls{tile, ulen[gbase[own] + kk], ulen[gbase[own] + kk + 1]};
+                        emit_tag_v(ls, P, XL, iv[j], kk + 1 == gend[own]);
+                        ls.finish();
+                    }
+                }
+            } else if (live) {
+                LdsSink ls{tile, (uint32_t)pre};
+                RecItems r2 = ri;
+                emit_rec<NESTED, false>(ls, P, XL, i, rv, r2);
+                ls.finish();
+            }
         }
-    }
-    __syncthreads();
-    if (P.count_only) return;
-    EPROF(5);
-    const uint64_t base = sh_base;
-    if (fits) {
-        const uint64_t end = min(base + agg, P.cap);
-        if (base < end) tile_copy_out<BT>(tile, P.out, base, base, end);
-        return;
-    }
-    if (hyb) {
-        for (uint32_t k = 0; k <= nbig; k++) {
-            const uint64_t g_lo = k ? (uint64_t)sh_bpre[k - 1] + sh_blen[k - 1] : 0, g_hi = k < nbig ? sh_bpre[k] : agg;
-            const uint64_t t_lo = k ? sh_bspre[k - 1] : 0;
-            const uint64_t lo = base + g_lo, hi = min(base + g_hi, P.cap);
-            if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi);
+        EPROF(4);
+        // ---- phase 4: look-back; then the next block is claimed (now, so
+        // that consecutive tickets start at nearly the same time and a
+        // look-back finds its predecessors published) and its bounds fetched
+        // by the first wave while the others copy the tile out
+        if (t < 64) {
+            const uint64_t excl = lb_resolve(P.state, b, agg, !PERSIST && P.order_by_id ? P.spin_limit : 0, P.ticket);
+            if (t == 0) {
+                sh_base = excl;
+                if (b == nblk - 1) *P.total = excl + agg;
+            }
         }
-        for (uint32_t k = 0; k < nbig; k++) {
-            const uint64_t p = base + sh_bpre[k];
-            if (p + sh_blen[k] > P.cap) continue;
-            const RecVals bv = load_rec<NESTED>(P, r0 + sh_big[k]);
-            coop_rec<NESTED, BT>(P, P.out + p, r0 + sh_big[k], bv, sh_scan, &sh_len);
+        __syncthreads();
+        EPROF(5);
+        if (PERSIST && t < 64) {
+            unsigned long long tk = 0;
+            if (t == 0) tk = atomicAdd(P.ticket, 1ull);
+            const uint64_t n1 = (uint64_t)__shfl((long long)tk, 0);
+            const uint64_t v1 = bounds_l1<NESTED, R>(P, n1, t);
+            bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
+            if (t == 0) sh_nb = n1;
         }
-        return;
-    }
-    // fallback: one thread per record writes straight to global memory;
-    // large records are written by the whole workgroup
-    uint32_t *big = reinterpret_cast<uint32_t *>(tile), *bpre = big + R, *blen = bpre + R;
-    if (t == 0) sh_nbig = 0;
-    __syncthreads();
-    const bool fbig = live && rec_big<NESTED>(rv);
-    if (fbig) {
-        const uint32_t k = atomicAdd(&sh_nbig, 1u);
-        big[k] = t;
-        bpre[k] = (uint32_t)pre;
-        blen[k] = (uint32_t)len;
-    }
-    __syncthreads();
-    if (live && !fbig && base + pre + len <= P.cap) {
-        WriteSink ws;
-        ws.init(P.out, base + pre, P.dummy + t);
-        emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
-        ws.finish();
-    }
-    const uint32_t fnbig = sh_nbig;
-    for (uint32_t k = 0; k < fnbig; k++) {
-        const uint64_t p = base + bpre[k];
-        if (p + blen[k] > P.cap) continue;
-        const RecVals bv = load_rec<NESTED>(P, r0 + big[k]);
-        coop_rec<NESTED, BT>(P, P.out + p, r0 + big[k], bv, sh_scan, &sh_len);
+        const uint64_t base = sh_base;
+        if (P.count_only) {
+        } else if (fits) {
+            const uint64_t end = min(base + agg, P.cap);
+            if (base < end) {
+                if (!PERSIST) tile_copy_out<BT>(tile, P.out, base, base, end);
+                else if (t >= 64) tile_copy_out<BT - 64>(tile, P.out, base, base, end, t - 64);
+            }
+        } else if (hyb) {
+            for (uint32_t k = 0; k <= nbig; k++) {
+                const uint64_t g_lo = k ? (uint64_t)sh_bpre[k - 1] + sh_blen[k - 1] : 0, g_hi = k < nbig ? sh_bpre[k] : agg;
+                const uint64_t t_lo = k ? sh_bspre[k - 1] : 0;
+                const uint64_t lo = base + g_lo, hi = min(base + g_hi, P.cap);
+                if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi);
+            }
+            for (uint32_t k = 0; k < nbig; k++) {
+                const uint64_t p = base + sh_bpre[k];
+                if (p + sh_blen[k] > P.cap) continue;
+                const RecVals bv = load_rec<NESTED>(P, r0 + sh_big[k]);
+                coop_rec<NESTED, BT>(P, P.out + p, r0 + sh_big[k], bv, sh_scan, &sh_len);
+            }
+        } else {
+            // fallback: one thread per record writes straight to global memory;
+            // large records are written by the whole workgroup
+            uint32_t *big = reinterpret_cast<uint32_t *>(tile), *bpre = big + R, *blen = bpre + R;
+            if (t == 0) sh_nbig = 0;
+            __syncthreads();
+            const bool fbig = live && rec_big<NESTED>(rv);
+            if (fbig) {
+                const uint32_t k = atomicAdd(&sh_nbig, 1u);
+                big[k] = t;
+                bpre[k] = (uint32_t)pre;
+                blen[k] = (uint32_t)len;
+            }
+            __syncthreads();
+            if (live && !fbig && base + pre + len <= P.cap) {
+                WriteSink ws;
+                ws.init(P.out, base + pre, P.dummy + t);
+                emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
+                ws.finish();
+            }
+            const uint32_t fnbig = sh_nbig;
+            for (uint32_t k = 0; k < fnbig; k++) {
+                const uint64_t p = base + bpre[k];
+                if (p + blen[k] > P.cap) continue;
+                const RecVals bv = load_rec<NESTED>(P, r0 + big[k]);
+                coop_rec<NESTED, BT>(P, P.out + p, r0 + big[k], bv, sh_scan, &sh_len);
+            }
+        }
+        if (!PERSIST) break;
+        // the next block's loads (record, item and staging values)
+        __syncthreads();
+        nb = sh_nb;
+        if (nb < nblk)
+            enc_prefetch<NESTED, BT, R, NI, SV>(P, block_geo<NESTED, R, INCAP, UCAP, GCAP>(sh_nx, nb), rv, iv, sv);
+        b = nb;
     }
 }
 
@@ -1206,7 +1310,7 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 #define PJ_ENC_NEST_GCAP 256
 #endif
 #ifndef PJ_ENC_NEST_WPE
-#define PJ_ENC_NEST_WPE 1
+#define PJ_ENC_NEST_WPE 3
 #endif
 // Workgroup shapes: threads, records, LDS tile bytes, item capacities.
 // The nested shape must stay at or below about 53.7 KB of LDS per
@@ -1225,22 +1329,48 @@ constexpr int ENC_NEST_BT = PJ_ENC_NEST_BT, ENC_NEST_R = PJ_ENC_NEST_R, ENC_NEST
 
 int pj_encode_block_records(bool nested) { return nested ? ENC_NEST_R : ENC_FLAT_R; }
 
-hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st) {
-    if (nested) {
-        uint64_t g = (P.n + ENC_NEST_R - 1) / ENC_NEST_R;
-        hipLaunchKernelGGL((pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
-                                         ENC_NEST_GCAP, ENC_NEST_WPE>),
-                           dim3((unsigned)g), dim3(ENC_NEST_BT), 0, st, P);
-    } else {
-        uint64_t g = (P.n + ENC_FLAT_R - 1) / ENC_FLAT_R;
-        if (wide)
-            hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_WIDE_TILE, ENC_WIDE_IN, 1, 1>),
-                               dim3((unsigned)g), dim3(ENC_FLAT_BT), 0, st, P);
-        else
-            hipLaunchKernelGGL((pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>),
-                               dim3((unsigned)g), dim3(ENC_FLAT_BT), 0, st, P);
+namespace {
+// Workgroups of kernel K that the device holds at once (cached per device
+// and kernel): the persistent encode launches no more than that many, so
+// every launched workgroup is resident.
+template <class K> unsigned resident_groups(K kern, int threads) {
+    constexpr int MAXD = 64;
+    static std::mutex mu;
+    static unsigned cache[MAXD] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXD) return 0;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!cache[dev]) {
+        int per_cu = 0, cus = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
+            cus <= 0)
+            return 0;
+        cache[dev] = (unsigned)(per_cu * cus);
     }
+    return cache[dev];
+}
+template <class K>
+hipError_t launch_encode(K kern, int threads, const EncParams &P, uint64_t records, bool persistent, hipStream_t st) {
+    const uint64_t nblk = (P.n + records - 1) / records;
+    const unsigned res = resident_groups(kern, threads);
+    if (!res) return hipErrorInvalidConfiguration;
+    const uint64_t g = nblk < res || !persistent ? nblk : res;
+    hipLaunchKernelGGL(kern, dim3((unsigned)g), dim3(threads), 0, st, P);
     return hipGetLastError();
+}
+}  // namespace
+
+hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st) {
+    if (nested)
+        return launch_encode(pj::k_encode<true, ENC_NEST_BT, ENC_NEST_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
+                                              ENC_NEST_GCAP, ENC_NEST_WPE>,
+                                 ENC_NEST_BT, P, ENC_NEST_R, true, st);
+    if (wide)
+        return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_WIDE_TILE, ENC_WIDE_IN, 1, 1>,
+                                 ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
+    return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>,
+                             ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
 }
 
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st) {

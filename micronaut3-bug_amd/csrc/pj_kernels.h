@@ -14,9 +14,9 @@ struct EncParams {
     uint8_t *out;
     uint64_t cap;
     uint64_t *state;           // look-back words, one per block (zeroed)
-    unsigned long long *ticket;// logical block counter (zeroed); with order_by_id, set to 1 when a
-                               // look-back gave up (the launch is then redone in ticket order)
-    int order_by_id;           // 1: block b handles records [b R, (b+1) R) (no ticket atomic)
+    unsigned long long *ticket;// block tickets (zeroed); with order_by_id, set to 1 when a look-back
+                               // gave up (the launch is then redone in ticket order)
+    int order_by_id;           // one-block workgroups only: block b is workgroup b (no ticket atomic)
     uint64_t spin_limit;       // look-back wait bound (wall-clock ticks) when order_by_id
     uint64_t *total;           // encoded size (written by the last block)
     uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)

@@ -222,14 +222,27 @@ def test_encode_hybrid_blocks_match_oracle(codec):
 
 
 def test_encode_lookback_redo_in_ticket_order(codec, monkeypatch):
-    """Blocks take their records in launch order and bound their look-back
-    waits; a launch in which some wait ran out is redone with ticket-ordered
-    blocks.  A one-tick bound forces that path: the output is still exact."""
+    """Flat blocks take their records in launch order and bound their
+    look-back waits; a launch in which some wait ran out is redone with
+    ticket-ordered blocks.  A one-tick bound forces that path: the output is
+    still exact (nested records, on persistent ticket-ordered workgroups,
+    have no bound and ignore it)."""
     monkeypatch.setenv("PETJSON_SPIN_LIMIT_TICKS", "1")
     for config, n in ((2, 300_000), (3, 100_000), (5, 20_000)):
         cols = pj.generate(config, n)
         for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
             assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
+
+
+def test_encode_persistent_workgroups_many_rounds(codec):
+    """Nested records run on persistent workgroups (as many as the device
+    holds at once: 768 on one MI355X) that claim blocks of 96 records by
+    ticket until none is left; flat records one block of 256 per workgroup.
+    Block counts below, at and far above one round give the oracle's bytes."""
+    for config, n in ((3, 96 * 767 + 5), (3, 96 * 768), (3, 96 * 2305 + 1), (2, 256 * 1280 + 17), (2, 256 * 3900)):
+        cols = pj.generate(config, n)
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt), (config, n, fmt)
 
 
 def test_encode_flat_long_records_switch_to_wide_tile(codec):
