@@ -726,11 +726,28 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 }
 
 // ------------------------------------------------------------------ kernel
+// 16 bytes starting q = 16 - s bytes into L:H (s = 1 .. 15): dword qd = q / 4
+// of the pair, then byte qb = q % 4 of it, joined with v_alignbyte.  qd is
+// the same for every lane (it follows the block's base address), so the
+// branch is uniform.
+__device__ __forceinline__ uint4 funnel16(const uint4 &L, const uint4 &H, uint32_t qd, uint32_t qb) {
+    const uint32_t d0 = L.x, d1 = L.y, d2 = L.z, d3 = L.w, d4 = H.x, d5 = H.y, d6 = H.z, d7 = H.w;
+#define PJ_AB(h, l) __builtin_amdgcn_alignbyte(h, l, qb)
+    switch (qd) {
+    case 0: return make_uint4(PJ_AB(d1, d0), PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3));
+    case 1: return make_uint4(PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3), PJ_AB(d5, d4));
+    case 2: return make_uint4(PJ_AB(d3, d2), PJ_AB(d4, d3), PJ_AB(d5, d4), PJ_AB(d6, d5));
+    default: return make_uint4(PJ_AB(d4, d3), PJ_AB(d5, d4), PJ_AB(d6, d5), PJ_AB(d7, d6));
+    }
+#undef PJ_AB
+}
+
+
 // Copy global bytes [lo, hi) out of an LDS tile whose byte x belongs at
 // global address D + x (all threads of the workgroup).  Global chunk c
 // covers [g0 + 16c, g0 + 16c + 16) with g0 = D - (D & 15), which is tile
 // bytes [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
-// head of word c, joined with one funnel shift.  Whole chunks leave with one
+// head of word c, joined by funnel16.  Whole chunks leave with one
 // aligned 16-byte store; the first and last chunks (shared with neighbouring
 // blocks or segments) with exact 8/4/2/1-byte stores.  The tile must be
 // readable 16 bytes past hi - D.
@@ -738,30 +755,21 @@ template <int BT>
 __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi,
                                               uint32_t t = threadIdx.x) {
     const uint32_t s = (uint32_t)(D & 15);
+    const uint32_t qd = (16 - s) >> 2, qb = (16 - s) & 3;
     const uint64_t g0 = D - s;
     const uint32_t c_lo = (uint32_t)((lo - g0) >> 4), c_hi = (uint32_t)((hi - g0 + 15) >> 4);
     const uint4 *W = reinterpret_cast<const uint4 *>(tile);
     constexpr int U = 4;
     for (uint32_t c0 = c_lo + t; c0 < c_hi; c0 += U * BT) {
-        unsigned __int128 v[U];
+        uint4 v[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const uint32_t c = c0 + u * BT;
-            v[u] = 0;
+            v[u] = make_uint4(0, 0, 0, 0);
             if (c < c_hi) {
-                const uint4 hi4 = W[c];
-                const unsigned __int128 h = (unsigned __int128)(((uint64_t)hi4.w << 32) | hi4.z) << 64 |
-                                            (((uint64_t)hi4.y << 32) | hi4.x);
+                const uint4 h = W[c];
                 if (s == 0) v[u] = h;
-                else {
-                    unsigned __int128 l = 0;
-                    if (c > 0) {
-                        const uint4 lo4 = W[c - 1];
-                        l = (unsigned __int128)(((uint64_t)lo4.w << 32) | lo4.z) << 64 |
-                            (((uint64_t)lo4.y << 32) | lo4.x);
-                    }
-                    v[u] = (l >> (8 * (16 - s))) | (h << (8 * s));
-                }
+                else v[u] = funnel16(c > 0 ? W[c - 1] : make_uint4(0, 0, 0, 0), h, qd, qb);
             }
         }
 #pragma unroll
@@ -770,12 +778,12 @@ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out,
             if (c >= c_hi) break;
             const uint64_t g = g0 + 16ull * c;
             const uint64_t a = g > lo ? g : lo, e = g + 16 < hi ? g + 16 : hi;
-            const unsigned __int128 x = v[u];
             if (a == g && e == g + 16) {
-                *reinterpret_cast<uint4 *>(out + g) =
-                    make_uint4((uint32_t)x, (uint32_t)(x >> 32), (uint32_t)(x >> 64), (uint32_t)(x >> 96));
+                *reinterpret_cast<uint4 *>(out + g) = v[u];
             } else {
-                unsigned __int128 y = x >> (8 * (uint32_t)(a - g));
+                const uint4 x = v[u];
+                unsigned __int128 y = ((unsigned __int128)(((uint64_t)x.w << 32) | x.z) << 64 | (((uint64_t)x.y << 32) | x.x)) >>
+                                      (8 * (uint32_t)(a - g));
                 uint32_t n = (uint32_t)(e - a);
                 uint8_t *q = out + a;
                 if (n & 8) { *reinterpret_cast<uint64_t *>(q) = (uint64_t)y; q += 8; y >>= 64; }
@@ -848,6 +856,7 @@ __device__ __forceinline__ Geo block_geo(const uint64_t *nx, uint64_t b) {
 // thread t is list position t + j BT): heads of records 0..R-1 from position
 // 0, names from NAME0, url then tag items from ITEM0, each kind starting on
 // a wave boundary so that no wave runs two kinds of unit in one slot.
+constexpr uint32_t ITEM_ON = 1u << 31, ITEM_LAST = 1u << 30;
 template <int R> constexpr int name0() { return (R + 63) / 64 * 64; }
 template <int R> constexpr int item0() { return (name0<R>() + R + 63) / 64 * 64; }
 
@@ -926,11 +935,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     // tile offset is the exclusive scan of the unit lengths (ulen)
     constexpr int NUC = NESTED ? 4 * R + UCAP + GCAP : 1;
     __shared__ uint32_t ulen[NUC + 1];
-    __shared__ uint32_t ubase[RA], gbase[RA];         // per record: unit index of its item k is base + k (mod 2^32)
     __shared__ uint8_t rn_f[RA];                      // per record: flags of its name unit
-    __shared__ uint8_t uon[RA], gon[RA];              // per record: its url / tag items are written
-    __shared__ uint16_t uown[UA], gown[GA];           // owner record of each item
-    __shared__ uint16_t uend[RA], gend[RA];           // per record: local end of its items
+    // per url / tag item: its unit index (low 16 bits), ITEM_ON when its
+    // record writes the list, ITEM_LAST for the record's last item
+    __shared__ uint32_t uinfo[UA], ginfo[GA];
+    static_assert(NUC < 65536, "unit indices fit 16 bits");
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t splain[(INCAP / 16 + 63) / 64];  // staged 16-byte chunks that hold a byte to escape
     __shared__ uint64_t sh_nx[NX], sh_nb, sh_base, sh_len;
@@ -1028,14 +1037,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     sh_bpre[t] = (uint32_t)(rv.na - g.lo16[0]);
                     sh_blen[t] = (uint32_t)(rv.nb - rv.na);
                     rn_f[t] = (uint8_t)((rv.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (rv.u1 == rv.u0 ? 0x80u : 0u));
-                    uon[t] = rec_has_urls(rv);
-                    gon[t] = rec_has_tags<NESTED>(rv);
-                    ubase[t] = hidx + 2 - ul0;
-                    gbase[t] = hidx + 3 + (ul1 - ul0) - gl0;
-                    uend[t] = (uint16_t)ul1;
-                    gend[t] = (uint16_t)gl1;
-                    for (uint32_t k = ul0; k < ul1; k++) uown[k] = (uint16_t)t;
-                    for (uint32_t k = gl0; k < gl1; k++) gown[k] = (uint16_t)t;
+                    const uint32_t uf = rec_has_urls(rv) ? ITEM_ON : 0u, gf = rec_has_tags<NESTED>(rv) ? ITEM_ON : 0u;
+                    for (uint32_t k = ul0; k < ul1; k++)
+                        uinfo[k] = (hidx + 2 + k - ul0) | uf | (k + 1 == ul1 ? ITEM_LAST : 0u);
+                    for (uint32_t k = gl0; k < gl1; k++)
+                        ginfo[k] = (hidx + 3 + (ul1 - ul0) + k - gl0) | gf | (k + 1 == gl1 ? ITEM_LAST : 0u);
                 }
             }
             __syncthreads();
@@ -1065,13 +1071,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     const uint32_t k = q - item0<R>();
                     CountSink cs;
                     if (k < U) {
-                        const uint32_t own = uown[k];
-                        if (uon[own]) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
-                        ulen[ubase[own] + k] = (uint32_t)cs.n;
+                        const uint32_t f = uinfo[k];
+                        if (f & ITEM_ON) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
+                        ulen[f & 0xFFFFu] = (uint32_t)cs.n;
                     } else if (k < U + G) {
-                        const uint32_t kk = k - (uint32_t)U, own = gown[kk];
-                        if (gon[own]) emit_tag_v(cs, P, XL, iv[j], false);
-                        ulen[gbase[own] + kk] = (uint32_t)cs.n;
+                        const uint32_t f = ginfo[k - (uint32_t)U];
+                        if (f & ITEM_ON) emit_tag_v(cs, P, XL, iv[j], false);
+                        ulen[f & 0xFFFFu] = (uint32_t)cs.n;
                     }
                 }
                 __syncthreads();
@@ -1171,16 +1177,16 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     if (q < (uint32_t)item0<R>()) continue;
                     const uint32_t k = q - item0<R>();
                     if (k < U) {
-                        const uint32_t own = uown[k];
-                        if (!uon[own]) continue;
-                        LdsSink ls{tile, ulen[ubase[own] + k], ulen[ubase[own] + k + 1]};
-                        emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, k + 1 == uend[own]);
+                        const uint32_t f = uinfo[k], u = f & 0xFFFFu;
+                        if (!(f & ITEM_ON)) continue;
+                        LdsSink ls{tile, ulen[u], ulen[u + 1]};
+                        emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, (f & ITEM_LAST) != 0);
                         ls.finish();
                     } else if (k < U + G) {
-                        const uint32_t kk = k - (uint32_t)U, own = gown[kk];
-                        if (!gon[own]) continue;
-                        LdsSink ls{tile, ulen[gbase[own] + kk], ulen[gbase[own] + kk + 1]};
-                        emit_tag_v(ls, P, XL, iv[j], kk + 1 == gend[own]);
+                        const uint32_t f = ginfo[k - (uint32_t)U], u = f & 0xFFFFu;
+                        if (!(f & ITEM_ON)) continue;
+                        LdsSink ls{tile, ulen[u], ulen[u + 1]};
+                        emit_tag_v(ls, P, XL, iv[j], (f & ITEM_LAST) != 0);
                         ls.finish();
                     }
                 }
