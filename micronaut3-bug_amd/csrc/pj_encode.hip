@@ -986,7 +986,9 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
 
     while (b < nblk) {
 #ifdef PJ_ENC_PROF
-#define EPROF(k) if (t == 0 && !P.count_only && P.out) reinterpret_cast<uint64_t *>(P.out + P.cap)[-1 - (int64_t)(b * 6 + (k))] = wall_clock64();
+// profiling builds: 8 wall-clock stamps per block at the end of the output
+// buffer (slot 7 by the second wave)
+#define EPROF(k) if ((t == 0 || ((k) == 7 && t == 64)) && !P.count_only && P.out) reinterpret_cast<uint64_t *>(P.out + P.cap)[-1 - (int64_t)(b * 8 + (k))] = wall_clock64();
 #else
 #define EPROF(k)
 #endif
@@ -1218,6 +1220,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             const uint64_t v1 = bounds_l1<NESTED, R>(P, n1, t);
             bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
             if (t == 0) sh_nb = n1;
+            EPROF(6);
         }
         const uint64_t base = sh_base;
         if (P.count_only) {
@@ -1225,7 +1228,10 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             const uint64_t end = min(base + agg, P.cap);
             if (base < end) {
                 if (!PERSIST) tile_copy_out<BT>(tile, P.out, base, base, end);
-                else if (t >= 64) tile_copy_out<BT - 64>(tile, P.out, base, base, end, t - 64);
+                else if (t >= 64) {
+                    tile_copy_out<BT - 64>(tile, P.out, base, base, end, t - 64);
+                    EPROF(7);
+                }
             }
         } else if (hyb) {
             for (uint32_t k = 0; k <= nbig; k++) {
