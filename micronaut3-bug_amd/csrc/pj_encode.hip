@@ -234,19 +234,20 @@ template <class S>
 __device__ __forceinline__ void emit_str_lds(S &s, const PJ_LDS uint8_t *p, uint32_t len, uint32_t hexa) {
     const uint32_t sh = (uint32_t)(uintptr_t)p & 7;
     const PJ_LDS uint64_t *q = (const PJ_LDS uint64_t *)(p - sh);
-    uint64_t cur = q[0];
+    uint64_t cur = q[0], nxt = q[1];              // reads run one qword ahead
     uint32_t k = 0, j = 0;
     for (; k + 8 <= len; k += 8, j++) {
-        const uint64_t nxt = q[j + 1];
+        const uint64_t nn = q[j + 2];
         const uint64_t x = sh ? (cur >> (8 * sh)) | (nxt << (64 - 8 * sh)) : cur;
         if (!special64(x)) s.put8(x, 8);
         else esc_bytes(s, x, 8, hexa);
         cur = nxt;
+        nxt = nn;
     }
     if (k < len) {
         const int m = (int)(len - k);
         uint64_t x = cur >> (8 * sh);
-        if (sh + (uint32_t)m > 8) x |= q[j + 1] << (64 - 8 * sh);
+        if (sh + (uint32_t)m > 8) x |= nxt << (64 - 8 * sh);
         const uint64_t mk = (1ull << (8 * m)) - 1;
         x &= mk;
         if (!special64(x | (0x41 * ONES & ~mk))) s.put8(x, m);
@@ -260,17 +261,18 @@ template <class S>
 __device__ __forceinline__ void emit_plain_lds(S &s, const PJ_LDS uint8_t *p, uint32_t len) {
     const uint32_t sh = (uint32_t)(uintptr_t)p & 7;
     const PJ_LDS uint64_t *q = (const PJ_LDS uint64_t *)(p - sh);
-    uint64_t cur = q[0];
+    uint64_t cur = q[0], nxt = q[1];              // reads run one qword ahead
     uint32_t k = 0, j = 0;
     for (; k + 8 <= len; k += 8, j++) {
-        const uint64_t nxt = q[j + 1];
+        const uint64_t nn = q[j + 2];
         s.put8(sh ? (cur >> (8 * sh)) | (nxt << (64 - 8 * sh)) : cur, 8);
         cur = nxt;
+        nxt = nn;
     }
     if (k < len) {
         const int m = (int)(len - k);
         uint64_t x = cur >> (8 * sh);
-        if (sh + (uint32_t)m > 8) x |= q[j + 1] << (64 - 8 * sh);
+        if (sh + (uint32_t)m > 8) x |= nxt << (64 - 8 * sh);
         s.put8(x, m);
     }
 }
