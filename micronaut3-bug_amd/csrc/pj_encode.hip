@@ -824,6 +824,17 @@ __device__ __forceinline__ void bounds_store(uint64_t *nx, uint64_t v1, uint64_t
     if (l < 8) nx[l] = v1;
     if (l < 4) nx[8 + l] = v2;
 }
+// The first wave claims the next block by ticket and stores its number and
+// bounds (lane l of the wave).
+template <bool NESTED, int R>
+__device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uint64_t *nb, uint32_t l) {
+    unsigned long long tk = 0;
+    if (l == 0) tk = atomicAdd(P.ticket, 1ull);
+    const uint64_t n1 = (uint64_t)__shfl((long long)tk, 0);
+    const uint64_t v1 = bounds_l1<NESTED, R>(P, n1, l);
+    bounds_store(nx, v1, bounds_l2<NESTED>(P, v1, l), l);
+    if (l == 0) *nb = n1;
+}
 
 // A block's item ranges and staged slices (16-byte aligned chunk ranges of
 // the four string columns, laid end to end in the staging buffer).
@@ -1215,13 +1226,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         }
         __syncthreads();
         EPROF(5);
-        if (PERSIST && t < 64) {
-            unsigned long long tk = 0;
-            if (t == 0) tk = atomicAdd(P.ticket, 1ull);
-            const uint64_t n1 = (uint64_t)__shfl((long long)tk, 0);
-            const uint64_t v1 = bounds_l1<NESTED, R>(P, n1, t);
-            bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
-            if (t == 0) sh_nb = n1;
+        // a block with nothing left to write but its tile claims now; one
+        // that still writes records after the look-back (fallback or
+        // hybrid), once they are written, so that a claimed block always
+        // starts soon after its ticket
+        const bool early = fits || P.count_only;
+        if (PERSIST && early && t < 64) {
+            claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
             EPROF(6);
         }
         const uint64_t base = sh_base;
@@ -1277,6 +1288,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             }
         }
         if (!PERSIST) break;
+        if (!early && t < 64) claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
         // the next block's loads (record, item and staging values)
         __syncthreads();
         nb = sh_nb;
