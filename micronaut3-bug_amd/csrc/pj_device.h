@@ -280,6 +280,73 @@ __device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t
     if (n - k >= 8) { stu64(dst + k, lds_u64(src + k)); k += 8; }
     if (k < n) st_tail(dst + k, lds_u64(src + k), n - k);
 }
+// 16 bytes starting q = 16 - s bytes into L:H (s = 1 .. 15): dword qd = q / 4
+// of the pair, then byte qb = q % 4 of it, joined with v_alignbyte.  qd is
+// the same for every lane (it follows the block's base address), so the
+// branch is uniform.
+__device__ __forceinline__ uint4 funnel16(const uint4 &L, const uint4 &H, uint32_t qd, uint32_t qb) {
+    const uint32_t d0 = L.x, d1 = L.y, d2 = L.z, d3 = L.w, d4 = H.x, d5 = H.y, d6 = H.z, d7 = H.w;
+#define PJ_AB(h, l) __builtin_amdgcn_alignbyte(h, l, qb)
+    switch (qd) {
+    case 0: return make_uint4(PJ_AB(d1, d0), PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3));
+    case 1: return make_uint4(PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3), PJ_AB(d5, d4));
+    case 2: return make_uint4(PJ_AB(d3, d2), PJ_AB(d4, d3), PJ_AB(d5, d4), PJ_AB(d6, d5));
+    default: return make_uint4(PJ_AB(d4, d3), PJ_AB(d5, d4), PJ_AB(d6, d5), PJ_AB(d7, d6));
+    }
+#undef PJ_AB
+}
+
+
+// Copy global bytes [lo, hi) out of an LDS tile whose byte x belongs at
+// global address D + x (all threads of the workgroup).  Global chunk c
+// covers [g0 + 16c, g0 + 16c + 16) with g0 = D - (D & 15), which is tile
+// bytes [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
+// head of word c, joined by funnel16.  Whole chunks leave with one
+// aligned 16-byte store; the first and last chunks (shared with neighbouring
+// blocks or segments) with exact 8/4/2/1-byte stores.  The tile must be
+// readable 16 bytes past hi - D.
+template <int BT>
+__device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi,
+                                              uint32_t t = threadIdx.x) {
+    const uint32_t s = (uint32_t)(D & 15);
+    const uint32_t qd = (16 - s) >> 2, qb = (16 - s) & 3;
+    const uint64_t g0 = D - s;
+    const uint32_t c_lo = (uint32_t)((lo - g0) >> 4), c_hi = (uint32_t)((hi - g0 + 15) >> 4);
+    const uint4 *W = reinterpret_cast<const uint4 *>(tile);
+    constexpr int U = 4;
+    for (uint32_t c0 = c_lo + t; c0 < c_hi; c0 += U * BT) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t c = c0 + u * BT;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (c < c_hi) {
+                const uint4 h = W[c];
+                if (s == 0) v[u] = h;
+                else v[u] = funnel16(c > 0 ? W[c - 1] : make_uint4(0, 0, 0, 0), h, qd, qb);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t c = c0 + u * BT;
+            if (c >= c_hi) break;
+            const uint64_t g = g0 + 16ull * c;
+            const uint64_t a = g > lo ? g : lo, e = g + 16 < hi ? g + 16 : hi;
+            if (a == g && e == g + 16) {
+                *reinterpret_cast<uint4 *>(out + g) = v[u];
+            } else {
+                const uint4 x = v[u];
+                unsigned __int128 y = ((unsigned __int128)(((uint64_t)x.w << 32) | x.z) << 64 | (((uint64_t)x.y << 32) | x.x)) >>
+                                      (8 * (uint32_t)(a - g));
+                uint32_t n = (uint32_t)(e - a);
+                uint8_t *q = out + a;
+                if (n & 8) { *reinterpret_cast<uint64_t *>(q) = (uint64_t)y; q += 8; y >>= 64; }
+                st_tail(q, (uint64_t)y, n & 7);
+            }
+        }
+    }
+}
+
 // n bytes from src (LDS or global, readable up to 8 bytes past the end) to dst
 __device__ __forceinline__ void copy_exact(uint8_t *dst, const uint8_t *src, uint32_t n) {
     uint32_t k = 0;
