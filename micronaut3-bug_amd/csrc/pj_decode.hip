@@ -105,7 +105,7 @@ __device__ __forceinline__ uint64_t block_excl_scan_idx(uint64_t v, uint64_t *sh
 // look-back of newline counts -> line starts.
 template <int BT, int R>
 __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
-    __shared__ uint64_t sh_scan[BT / 64];
+    __shared__ uint32_t sh_scan[R * BT / 64];
     __shared__ uint64_t sh_blk, sh_pre;
     const uint32_t t = threadIdx.x;
     if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[0], 1ull);
@@ -138,13 +138,15 @@ __global__ __launch_bounds__(BT) void k_dec_lines(DecParams P) {
         N[r] = m;
         cnt[r] = (uint32_t)__builtin_popcountll(m);
     }
-    // lines before each word: the rounds in order, threads in order within a round
+    // lines before each word: the rounds in order, threads in order within a
+    // round (one scan of the R per-round counts)
+    uint32_t ex[R], rt[R];
+    block_excl_scan_n<BT, R>(cnt, ex, rt, sh_scan);
     uint64_t pre[R], agg = 0;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        uint64_t tot;
-        pre[r] = agg + block_excl_scan<BT>((uint64_t)cnt[r], sh_scan, &tot);
-        agg += tot;
+        pre[r] = agg + ex[r];
+        agg += rt[r];
     }
     if (t == 0) lb_publish(P.state_idx, b, agg);
     if (t < 64) {
@@ -2957,7 +2959,10 @@ __global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
 #define PJ_DEC_LONG 1024
 #endif
 constexpr int DEC_LONG = PJ_DEC_LONG;
-constexpr int DEC_IDX_BT = 256, DEC_IDX_R = 4, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
+#ifndef PJ_DEC_IDX_R
+#define PJ_DEC_IDX_R 4
+#endif
+constexpr int DEC_IDX_BT = 256, DEC_IDX_R = PJ_DEC_IDX_R, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
 
 int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
 #ifndef PJ_DEC_LPB
