@@ -662,11 +662,13 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         const bool split = P.tape != nullptr;
         // scan buffer: vector look-back words (single pass) or block totals,
         // bases and scan look-back words (split), then the deferred
-        // error-code queue, then (split) the wave-line list and the per-line
-        // offsets (9 u32 per line)
+        // error-code queue, then (split) the wave-line list, the per-line
+        // offsets (9 u32 per line), the count and list of blocks handed to
+        // the bitmap pass
         const uint64_t nsb = (gp + pj_dec_bscan_block() - 1) / pj_dec_bscan_block();
         const uint64_t w_state = split ? 2 * gp * VLB_WORDS + nsb * VLB_WORDS : gp * VLB_WORDS;
-        const uint64_t w_split = split ? lines + (9 * lines + 1) / 2 : 0;
+        const uint64_t w_lpos = (9 * lines + 1) / 2;
+        const uint64_t w_split = split ? lines + w_lpos + 2 + gp : 0;
         PJ_HIP(ctx->scan.ensure((w_state + lines + 8 + w_split) * 8));
         uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
         P.state_parse = SB;
@@ -680,10 +682,15 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.bticket = reinterpret_cast<unsigned long long *>(X + 15);
         P.long_list = P.dq + lines + 8;
         P.lpos = reinterpret_cast<uint32_t *>(P.long_list + lines);
+        P.bm_count = reinterpret_cast<unsigned long long *>(P.long_list + lines + w_lpos);
+        P.bm_list = P.long_list + lines + w_lpos + 2;
         P.order_by_id = 1;
         for (;;) {
             if ((s = mark(ctx))) return s;
-            if (split) PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
+            if (split) {
+                PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
+                PJ_HIP(pj_launch_fill_u64(reinterpret_cast<uint64_t *>(P.bm_count), 2, 0, ctx->stream));
+            }
             else PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
             PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
             PJ_HIP(pj_launch_fill_u64(X + 3, 13, 0, ctx->stream));     // totals and counters

@@ -2474,23 +2474,26 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //   * block scans plus a vector look-back over 8 counters give the rows /
 //     byte offsets, and a second walk over the sub-tiles (reloaded only when
 //     there were several) writes the columns.
-template <int BT, int TILE, int LONG, int LPB = BT, bool TAPE = false>
-__global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
+// BM false (split decode only): no bitmaps in LDS, so more workgroups share
+// a CU; a block that holds a line for the wave path (long, or too many items
+// for its tape) gives up before it writes anything and joins P.bm_list, whose
+// blocks k_dec_block_bm then reads with the bitmaps.
+template <int BT, int TILE, int LONG, int LPB, bool TAPE, bool BM>
+__device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
     static_assert(LONG < 65536, "tape positions of per-thread lines are 16-bit");
+    static_assert(BM || TAPE, "blocks without bitmaps hand long lines over (split decode)");
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     // the specials and bad-byte bitmaps; after pass 0 also the scan's
-    // scratch and the string staging window
-    __shared__ __attribute__((aligned(16))) uint64_t bmaps[2 * (TILE / 64 + 1)];
-    uint64_t *const spec = bmaps, *const badm = bmaps + (TILE / 64 + 1);
+    // scratch (the only use left without bitmaps)
+    constexpr int BMW = BM ? TILE / 64 + 1 : PJ_DEC_NCNT * BT / 128;
+    __shared__ __attribute__((aligned(16))) uint64_t bmaps[2 * BMW];
+    uint64_t *const spec = bmaps, *const badm = bmaps + BMW;
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_ls[LPB + 1];             // the block's line starts, then its end
     __shared__ uint16_t sh_sub[LPB + 1];            // sub-tile boundaries (block-local line indices)
     __shared__ uint32_t sh_nsub, sh_any;
-    __shared__ uint64_t sh_blk, sh_base[PJ_DEC_NCNT];
+    __shared__ uint64_t sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
-    if (t == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[1], 1ull);
-    __syncthreads();
-    const uint64_t b = sh_blk;
     const uint64_t l0 = b * LPB;
     const uint32_t cnt = (uint32_t)min((uint64_t)LPB, P.lines - l0);
     const uint64_t l = l0 + t;
@@ -2503,6 +2506,13 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
     }
     bool longl = n > (uint32_t)LONG;               // read by the owning wave (also: tape full)
+    if constexpr (!BM) {
+        if (block_any(longl, &sh_any)) {
+            if (t == 0) P.bm_list[atomicAdd(P.bm_count, 1ull)] = b;
+            return;
+        }
+    }
+    bool handover = false;                          // (!BM) a tape filled up: the block is handed over
     // ---- pass 0: validate and measure, sub-tile by sub-tile
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
@@ -2541,9 +2551,15 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                     need_gen = code == PJ_BAIL;
                 }
             }
+            if constexpr (!BM) {
+                if (block_any(mine && longl, &sh_any)) {
+                    handover = true;
+                    break;
+                }
+            }
             // long lines: the wave of the owning thread reads them together,
             // over the bitmaps, which only sub-tiles holding one build
-            if (block_any(mine && longl, &sh_any)) {
+            if (BM && block_any(mine && longl, &sh_any)) {
                 tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
                 __syncthreads();
                 if (mine && longl) {
@@ -2576,10 +2592,16 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
                 r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
                 r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
             }
-            atomicAdd(P.gq_count, 1ull);            // diagnostics: lines off the fast path
         }
         __syncthreads();                            // the tile is reused by the next sub-tile
     }
+    if constexpr (!BM) {
+        if (handover) {
+            if (t == 0) P.bm_list[atomicAdd(P.bm_count, 1ull)] = b;
+            return;
+        }
+    }
+    if (general) atomicAdd(P.gq_count, 1ull);       // diagnostics: lines off the fast path
     r.code = live ? (uint32_t)code : 0;
     if (live && code == PJ_REC_EMPTY) atomicAdd(P.empty_count, 1ull);
     // ---- scans and look-back
@@ -2717,6 +2739,31 @@ __global__ __launch_bounds__(BT, 2) void k_dec_block(DecParams P) {
         if (nsub > 1) __syncthreads();
     }
     (void)ta0;
+}
+
+template <int BT, int TILE, int LONG, int LPB = BT, bool TAPE = false, bool BM = true>
+__global__ __launch_bounds__(BT, BM ? 2 : 3) void k_dec_block(DecParams P) {
+    __shared__ uint64_t sh_blk;
+    if (threadIdx.x == 0) sh_blk = P.order_by_id ? (uint64_t)blockIdx.x : atomicAdd(&P.tickets[1], 1ull);
+    __syncthreads();
+    dec_block<BT, TILE, LONG, LPB, TAPE, BM>(P, sh_blk);
+}
+
+// The blocks the bitmap-free pass handed over, read with the bitmaps: a
+// fixed grid claims them one at a time (their costs differ widely; the list
+// is empty in most calls).
+template <int BT, int TILE, int LONG, int LPB>
+__global__ __launch_bounds__(BT, 2) void k_dec_block_bm(DecParams P) {
+    __shared__ uint64_t sh_i;
+    const uint64_t cnt = *P.bm_count;
+    for (;;) {
+        if (threadIdx.x == 0) sh_i = atomicAdd(P.bm_count + 1, 1ull);
+        __syncthreads();
+        const uint64_t i = sh_i;
+        if (i >= cnt) break;
+        dec_block<BT, TILE, LONG, LPB, true, true>(P, P.bm_list[i]);
+        __syncthreads();                            // LDS is reused by the next block
+    }
 }
 
 // ---------------------------------------------------------------- split decode writers
@@ -2970,6 +3017,8 @@ constexpr int DEC_IDX_BT = 256, DEC_IDX_R = PJ_DEC_IDX_R, DEC_LINE_BT = PJ_DEC_L
 #define PJ_DEC_WTILE_KB 30
 #endif
 constexpr int DEC_WTILE = PJ_DEC_WTILE_KB * 1024;
+// The bitmap-free validating pass: 30 KiB keeps it under 32 KiB of LDS.
+constexpr int DEC_FTILE = PJ_DEC_WTILE_KB * 1024;
 static_assert(DEC_WTILE >= 4 * PJ_DEC_LONG, "fast lines (at most DEC_LONG bytes) fit the writer's tile");
 
 int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
@@ -3026,10 +3075,14 @@ hipError_t pj_launch_dec_long(const DecParams &P, hipStream_t st) {
 
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.lines + DEC_LPB - 1) / DEC_LPB;
-    if (P.tape)
-        hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB, true>), dim3((unsigned)g),
+    if (P.tape) {
+        // every block without bitmaps (five workgroups per CU), then the
+        // blocks it handed over with them
+        hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_FTILE, DEC_LONG, DEC_LPB, true, false>), dim3((unsigned)g),
                            dim3(DEC_LINE_BT), 0, st, P);
-    else
+        hipLaunchKernelGGL((pj::k_dec_block_bm<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB>),
+                           dim3((unsigned)(g < 1024 ? g : 1024)), dim3(DEC_LINE_BT), 0, st, P);
+    } else
         hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB, false>), dim3((unsigned)g),
                            dim3(DEC_LINE_BT), 0, st, P);
     return hipGetLastError();
