@@ -2491,7 +2491,7 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_ls[LPB + 1];             // the block's line starts, then its end
     __shared__ uint16_t sh_sub[LPB + 1];            // sub-tile boundaries (block-local line indices)
-    __shared__ uint32_t sh_nsub, sh_any;
+    __shared__ uint32_t sh_nsub, sh_any, sh_wa, sh_wb;
     __shared__ uint64_t sh_base[PJ_DEC_NCNT];
     const uint32_t t = threadIdx.x;
     const uint64_t l0 = b * LPB;
@@ -2560,7 +2560,21 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
             // long lines: the wave of the owning thread reads them together,
             // over the bitmaps, which only sub-tiles holding one build
             if (BM && block_any(mine && longl, &sh_any)) {
-                tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+                // only the words of the long lines are read: the bitmaps
+                // cover their span (each starts after a newline, where the
+                // string state is known)
+                if (t == 0) {
+                    sh_wa = ~0u;
+                    sh_wb = 0;
+                }
+                __syncthreads();
+                if (mine && longl) {
+                    atomicMin(&sh_wa, s0 >> 6);
+                    atomicMax(&sh_wb, (s0 + n + 64) >> 6);
+                }
+                __syncthreads();
+                const uint32_t wa = sh_wa, wb = min(sh_wb, nw);
+                tile_bitmaps<BT>(tile + 64 * wa, wb - wa, spec + wa, badm + wa, sh_scan);
                 __syncthreads();
                 if (mine && longl) {
                     bad = line_bad(badm, nw, s0, n);
