@@ -267,18 +267,31 @@ __device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
 #define PJ_LDS
 #endif
 __device__ __forceinline__ uint64_t lds_u64(const PJ_LDS uint8_t *p) { return *(const PJ_LDS uint64_t *)p; }
-// n bytes from an LDS buffer (readable up to 8 bytes past the end) to dst:
-// 16-byte stores at any address while 16 bytes remain (one store
-// instruction per 16 bytes: scattered per-thread copies are bound by the
-// number of store instructions), then the exact tail.
+// n bytes from an LDS buffer to dst, exactly (no byte outside [dst, dst+n)
+// is written).  Scattered per-thread copies are bound by the number of store
+// instructions, so: 16-byte stores at any address, the last one ending at
+// the last byte and overlapping its predecessor (the overlapped bytes get
+// the same values again); below 16 bytes two overlapping 8-, 4- or 2-byte
+// stores, or one byte.
+__device__ __forceinline__ void st16(uint8_t *p, const PJ_LDS uint8_t *s) {
+    const uint64_t a = lds_u64(s), b = lds_u64(s + 8);
+    *reinterpret_cast<uint4 *>(p) = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+}
 __device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t *src, uint32_t n) {
-    uint32_t k = 0;
-    for (; k + 16 <= n; k += 16) {
-        const uint64_t a = lds_u64(src + k), b = lds_u64(src + k + 8);
-        *reinterpret_cast<uint4 *>(dst + k) = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
-    }
-    if (n - k >= 8) { stu64(dst + k, lds_u64(src + k)); k += 8; }
-    if (k < n) st_tail(dst + k, lds_u64(src + k), n - k);
+    if (n >= 16) {
+        for (uint32_t k = 0; k + 16 < n; k += 16) st16(dst + k, src + k);
+        st16(dst + n - 16, src + n - 16);
+    } else if (n >= 8) {
+        stu64(dst, lds_u64(src));
+        stu64(dst + n - 8, lds_u64(src + n - 8));
+    } else if (n >= 4) {
+        stu32(dst, (uint32_t)lds_u64(src));
+        stu32(dst + n - 4, (uint32_t)lds_u64(src + n - 4));
+    } else if (n >= 2) {
+        const uint64_t x = lds_u64(src);
+        stu16(dst, (uint32_t)x);
+        stu16(dst + n - 2, (uint32_t)(x >> (8 * (n - 2))));
+    } else if (n) *dst = *src;
 }
 // 16 bytes starting q = 16 - s bytes into L:H (s = 1 .. 15): dword qd = q / 4
 // of the pair, then byte qb = q % 4 of it, joined with v_alignbyte.  qd is
