@@ -2474,6 +2474,12 @@ __device__ __forceinline__ bool line_bad(const uint64_t *badm, uint32_t nw, uint
 //   * block scans plus a vector look-back over 8 counters give the rows /
 //     byte offsets, and a second walk over the sub-tiles (reloaded only when
 //     there were several) writes the columns.
+// The general parser's measuring walk, out of line: few lines take it, and
+// inlined its registers would count against every validating workgroup.
+__device__ __noinline__ int run_line_measure(const DecParams &P, const Src S, uint64_t s0, uint32_t n, LineInfo *L) {
+    return run_line(P, S, s0, n, true, false, *L, nullptr);
+}
+
 // BM false (split decode only): no bitmaps in LDS, so more workgroups share
 // a CU; a block that holds a line for the wave path (long, or too many items
 // for its tape) gives up before it writes anything and joins P.bm_list, whose
@@ -2601,7 +2607,7 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
             general = true;
             const Src S = over ? Src{P.in, P.len, nullptr} : Src{tile, tb, nullptr};
             LineInfo L;
-            code = run_line(P, S, over ? gs : s0, n, true, false, L, nullptr);
+            code = run_line_measure(P, S, over ? gs : s0, n, &L);
             if (!code) {
                 r.name_len = L.name_len; r.cat_len = L.has_cat ? L.cat_len : 0; r.n_urls = L.n_urls;
                 r.url_bytes = L.url_bytes; r.n_tags = L.n_tags; r.tag_bytes = L.tag_bytes;
