@@ -294,6 +294,37 @@ def test_decode_long_lines_wave_parallel(codec):
         assert_same(gpu_decode(codec, data, shift=shift), ref)
 
 
+def test_decode_tape_full_lines_hand_over(codec):
+    """Short lines with more url and tag words than a line's tape holds (27)
+    go to the wave path: the bitmap-free validating pass hands their block to
+    the bitmap pass before writing anything, also when such a line sits in
+    a block's second sub-tile (blocks of 104 lines of about 400 bytes), and
+    next to lines the general parser reads.  Against the oracle."""
+    rnd = random.Random(7)
+
+    def rec(i, nu, nt, pad):
+        urls = ",".join('"u%d"' % k for k in range(nu))
+        tags = ",".join('{"id":%d,"name":"t%d"}' % (k, k) for k in range(nt))
+        return ('{"id":%d,"name":"%s","photoUrls":[%s],"tags":[%s],"status":"available"}'
+                % (i, "n" * pad, urls, tags)).encode()
+
+    lines = []
+    for blk in range(48):
+        full_at = {(blk * 37) % 104, (blk * 61 + 5) % 104} if blk % 3 else set()
+        for j in range(104):
+            if j in full_at:
+                lines.append(rec(len(lines), rnd.choice([14, 20, 27]), rnd.choice([7, 12]), rnd.randrange(0, 40)))
+            else:
+                lines.append(rec(len(lines), rnd.randrange(0, 3), rnd.randrange(0, 3), 330 if blk % 2 else 20))
+        if blk % 5 == 4:
+            lines[-7] = b'{"name":"g", "photoUrls":[], "id":7}'      # the general parser (spaces)
+    mut = [_mutate(rnd, lines[rnd.randrange(len(lines))]) for _ in range(200)]
+    data = b"\n".join(lines + mut) + b"\n"
+    ref = orc.decode(data)
+    for shift in (0, 5):
+        assert_same(gpu_decode(codec, data, shift=shift), ref)
+
+
 def test_roundtrip_beyond_4gib(codec):
     """16M nested records: the NDJSON passes 2^32 bytes, so every 64-bit
     offset path (line starts, column offsets, look-back sums) is exercised;
