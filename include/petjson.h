@@ -123,9 +123,28 @@ typedef enum pj_format {
     PJ_FORMAT_NDJSON = 1       /* rec\nrec\n...                                 */
 } pj_format;
 
+/* The optional properties, for per-property inclusion modes (Jackson's
+ * @JsonInclude on a property overrides the mapper default; petstore.json
+ * Pet :872-922, Category :858-871, Tag :923-936). */
+typedef enum pj_field {
+    PJ_FIELD_PET_ID = 0,
+    PJ_FIELD_PET_CATEGORY,
+    PJ_FIELD_PET_TAGS,
+    PJ_FIELD_PET_STATUS,
+    PJ_FIELD_CATEGORY_ID,
+    PJ_FIELD_CATEGORY_NAME,
+    PJ_FIELD_TAG_ID,
+    PJ_FIELD_TAG_NAME,
+    PJ_FIELD_COUNT
+} pj_field;
+#define PJ_INCLUDE_DEFAULT (-1)  /* field_inclusion entry: use `inclusion` */
+
 typedef struct pj_options {
-    int32_t inclusion;         /* pj_inclusion                                  */
+    int32_t inclusion;         /* pj_inclusion: the mode of every optional
+                                  property without an entry of its own      */
     int32_t hex_upper;         /* 1: \u001F (Jackson >= 2.14 default), 0: \u001f */
+    int32_t field_inclusion[PJ_FIELD_COUNT];  /* pj_inclusion per pj_field, or
+                                  PJ_INCLUDE_DEFAULT (pj_default_options)   */
 } pj_options;
 
 /* --------------------------------------------------------- decode results */

@@ -64,7 +64,8 @@ inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 struct pj_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
-    pj_options opt{PJ_INCLUDE_NON_EMPTY, 1};
+    pj_options opt{PJ_INCLUDE_NON_EMPTY, 1, {PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT,
+                                                 PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT, PJ_INCLUDE_DEFAULT}};
     DevBuf scan;        // tickets, totals, look-back words
     DevBuf index;       // decode: special bitmap, bad flags, line starts
     DevBuf stage_in;    // host path: input staging
@@ -282,7 +283,10 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.c = *cols;
     P.n = n;
     P.format = format;
-    P.incl = ctx->opt.inclusion;
+    for (int k = 0; k < PJ_FIELD_COUNT; k++) {
+        const int32_t m = ctx->opt.field_inclusion[k];
+        P.incl[k] = (uint8_t)(m == PJ_INCLUDE_DEFAULT ? ctx->opt.inclusion : m);
+    }
     P.hexa = ctx->opt.hex_upper ? 'A' : 'a';
     P.count_only = count_only ? 1 : 0;
     P.out = out;
@@ -387,6 +391,7 @@ void pj_default_options(pj_options *o) {
     if (!o) return;
     o->inclusion = PJ_INCLUDE_NON_EMPTY;
     o->hex_upper = 1;
+    for (int k = 0; k < PJ_FIELD_COUNT; k++) o->field_inclusion[k] = PJ_INCLUDE_DEFAULT;
 }
 
 pj_ctx *pj_create(int device, pj_status *status) {
@@ -450,6 +455,10 @@ pj_status pj_set_options(pj_ctx *c, const pj_options *o) {
     if (!c || !o) return fail(PJ_ERR_INVALID_ARG, "null argument");
     if (o->inclusion < PJ_INCLUDE_NON_EMPTY || o->inclusion > PJ_INCLUDE_ALWAYS)
         return fail(PJ_ERR_INVALID_ARG, "bad inclusion mode");
+    for (int k = 0; k < PJ_FIELD_COUNT; k++)
+        if (o->field_inclusion[k] != PJ_INCLUDE_DEFAULT &&
+            (o->field_inclusion[k] < PJ_INCLUDE_NON_EMPTY || o->field_inclusion[k] > PJ_INCLUDE_ALWAYS))
+            return fail(PJ_ERR_INVALID_ARG, "bad inclusion mode for field " + std::to_string(k));
     c->opt = *o;
     c->opt.hex_upper = o->hex_upper ? 1 : 0;
     return PJ_OK;

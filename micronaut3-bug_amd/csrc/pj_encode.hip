@@ -390,18 +390,20 @@ template <class S> __device__ __forceinline__ void key(S &s, bool &first) {
     first = false;
 }
 
-template <class S>
+// A Category or Tag object; F0 is the pj_field of its id (its name follows).
+template <int F0, class S>
 __device__ __forceinline__ void emit_sub(S &s, const EncParams &P, const ColSrc &X, uint32_t fl, int64_t id,
                                          const uint8_t *nm, uint64_t nlen) {
+    const uint32_t ii = P.incl[F0], ni = P.incl[F0 + 1];
     bool first = true;
     s.put_byte('{');
     if (fl & PJ_SUB_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, id); }
-    else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
+    else if (ii == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
     if (fl & PJ_SUB_HAS_NAME) {
-        if (nlen > 0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
+        if (nlen > 0 || ni != PJ_INCLUDE_NON_EMPTY) {
             key(s, first); lit(s, "\"name\":"); emit_strx(s, X, nm, nlen, P.hexa);
         }
-    } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"name\":null"); }
+    } else if (ni == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"name\":null"); }
     s.put_byte('}');
 }
 
@@ -448,7 +450,7 @@ __device__ __forceinline__ void emit_url_item(S &s, const EncParams &P, const Co
 // tag item: `{...}` + (',' or ']')
 template <class S>
 __device__ __forceinline__ void emit_tag_v(S &s, const EncParams &P, const ColSrc &X, const TagItem &v, bool last) {
-    emit_sub(s, P, X, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
+    emit_sub<PJ_FIELD_TAG_ID>(s, P, X, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
     s.put_byte(last ? ']' : ',');
 }
 template <class S>
@@ -469,11 +471,11 @@ __device__ __forceinline__ void rec_head(S &s, const EncParams &P, const ColSrc 
     bool first = true;
     s.put_byte('{');
     if (fl & PJ_PET_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, v.id); }
-    else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
+    else if (P.incl[PJ_FIELD_PET_ID] == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"id\":null"); }
     if (NESTED && (fl & PJ_PET_HAS_CATEGORY) && c.cat_id) {
         key(s, first); lit(s, "\"category\":");
-        emit_sub(s, P, X, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
-    } else if (P.incl == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"category\":null"); }
+        emit_sub<PJ_FIELD_CATEGORY_ID>(s, P, X, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
+    } else if (P.incl[PJ_FIELD_PET_CATEGORY] == PJ_INCLUDE_ALWAYS) { key(s, first); lit(s, "\"category\":null"); }
     key(s, first);
     if (fl & PJ_PET_HAS_NAME) lit(s, "\"name\":");
     else lit(s, "\"name\":null");
@@ -492,12 +494,13 @@ template <class S> __device__ __forceinline__ void rec_urls_open(S &s, const Rec
 // A record with HAS_TAGS and no tag columns (the flat layout, or tag_off
 // NULL) has an empty list (t0 == t1 == 0).
 template <bool NESTED, class S> __device__ __forceinline__ void rec_tags_open(S &s, const EncParams &P, const RecVals &v) {
+    const uint32_t ti = P.incl[PJ_FIELD_PET_TAGS];
     if (v.fl & PJ_PET_HAS_TAGS) {
-        if (v.t1 > v.t0 || P.incl != PJ_INCLUDE_NON_EMPTY) {
+        if (v.t1 > v.t0 || ti != PJ_INCLUDE_NON_EMPTY) {
             lit(s, ",\"tags\":[");
             if (v.t1 == v.t0) s.put_byte(']');
         }
-    } else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"tags\":null");
+    } else if (ti == PJ_INCLUDE_ALWAYS) lit(s, ",\"tags\":null");
 }
 
 template <class S> __device__ __forceinline__ void rec_tail(S &s, const EncParams &P, uint64_t i, const RecVals &v) {
@@ -505,7 +508,7 @@ template <class S> __device__ __forceinline__ void rec_tail(S &s, const EncParam
     if (st == 0) lit(s, ",\"status\":\"available\"}");
     else if (st == 1) lit(s, ",\"status\":\"pending\"}");
     else if (st == 2) lit(s, ",\"status\":\"sold\"}");
-    else if (P.incl == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null}");
+    else if (P.incl[PJ_FIELD_PET_STATUS] == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null}");
     else s.put_byte('}');
     if (P.format == PJ_FORMAT_NDJSON) s.put_byte('\n');
     else if (i == P.n - 1) s.put_byte(']');

@@ -8,7 +8,7 @@ struct EncParams {
     pj_pet_columns c;          // device column pointers
     uint64_t n;                // records
     int format;                // pj_format
-    int incl;                  // pj_inclusion
+    uint8_t incl[PJ_FIELD_COUNT];  // pj_inclusion of each optional property (pj_field)
     uint32_t hexa;             // 'A' or 'a': first letter of hex escapes
     int count_only;            // 1: length pass only
     uint8_t *out;

@@ -18,7 +18,9 @@
 
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 #include <optional>
+#include <utility>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -219,8 +221,15 @@ class PetObjectMapper {
         return m;
     }
 
-    void setOptions(pj_inclusion inclusion, bool hex_upper = true) {
-        pj_options o{inclusion, hex_upper ? 1 : 0};
+    // The mapper-wide inclusion mode and hex case; per-property modes
+    // (pj_field -> pj_inclusion) override the mode for those properties.
+    void setOptions(pj_inclusion inclusion, bool hex_upper = true,
+                    std::initializer_list<std::pair<pj_field, pj_inclusion>> fields = {}) {
+        pj_options o;
+        pj_default_options(&o);
+        o.inclusion = inclusion;
+        o.hex_upper = hex_upper ? 1 : 0;
+        for (const auto &f : fields) o.field_inclusion[f.first] = f.second;
         check(pj_set_options(ctx_, &o));
     }
 

@@ -54,8 +54,22 @@ class PetColumnsStruct(C.Structure):
     _fields_ = [("n_pets", C.c_uint64)] + [(n, C.c_void_p) for n in COLS] + [(n, C.c_uint64) for n in CAPS]
 
 
+# optional properties with an inclusion mode of their own (pj_field)
+FIELDS = ("pet_id", "pet_category", "pet_tags", "pet_status", "category_id", "category_name", "tag_id", "tag_name")
+INCLUDE_DEFAULT = -1
+
+
 class Options(C.Structure):
-    _fields_ = [("inclusion", C.c_int32), ("hex_upper", C.c_int32)]
+    _fields_ = [("inclusion", C.c_int32), ("hex_upper", C.c_int32), ("field_inclusion", C.c_int32 * len(FIELDS))]
+
+
+def make_options(inclusion=0, hex_upper=True, fields=None) -> "Options":
+    """pj_options: the mapper-wide inclusion mode, the hex case, and per-property
+    modes {field name: mode} that override it (the rest follow `inclusion`)."""
+    per = [INCLUDE_DEFAULT] * len(FIELDS)
+    for k, m in (fields or {}).items():
+        per[FIELDS.index(k)] = int(m)
+    return Options(inclusion, 1 if hex_upper else 0, (C.c_int32 * len(FIELDS))(*per))
 
 
 class DecodeResult(C.Structure):
@@ -338,8 +352,8 @@ class Codec:
         if rc != PJ_OK:
             raise PetJsonError(rc, self.L.pj_last_error().decode())
 
-    def set_options(self, inclusion=INCLUDE_NON_EMPTY, hex_upper=True):
-        o = Options(inclusion, 1 if hex_upper else 0)
+    def set_options(self, inclusion=INCLUDE_NON_EMPTY, hex_upper=True, fields=None):
+        o = make_options(inclusion, hex_upper, fields)
         self._check(self.L.pj_set_options(self.ctx, C.byref(o)))
 
     def timings(self):

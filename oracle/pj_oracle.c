@@ -111,39 +111,47 @@ static void w_key(wbuf *w, int *first, const char *key) {
     w_lit(w, "\":");
 }
 
-/* Category / Tag body: {"id":..,"name":".."} with optional-property inclusion. */
-static void w_sub(wbuf *w, int incl, int hex_upper, uint8_t fl, int64_t id,
+/* The inclusion mode of optional property f: its own entry, else the
+ * mapper-wide mode (a property-level @JsonInclude overrides the default). */
+static int incl_of(const pj_options *o, int f) {
+    return o->field_inclusion[f] == PJ_INCLUDE_DEFAULT ? o->inclusion : o->field_inclusion[f];
+}
+
+/* Category / Tag body: {"id":..,"name":".."} with optional-property
+ * inclusion (modes of its id and of its name). */
+static void w_sub(wbuf *w, int id_incl, int name_incl, int hex_upper, uint8_t fl, int64_t id,
                   const uint8_t *name, uint64_t name_len) {
     int first = 1;
     w_char(w, '{');
     if (fl & PJ_SUB_HAS_ID) { w_key(w, &first, "id"); w_long(w, id); }
-    else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
+    else if (id_incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
     if (fl & PJ_SUB_HAS_NAME) {
-        if (name_len > 0 || incl != PJ_INCLUDE_NON_EMPTY) {
+        if (name_len > 0 || name_incl != PJ_INCLUDE_NON_EMPTY) {
             w_key(w, &first, "name");
             w_string(w, name, name_len, hex_upper);
         }
-    } else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "name"); w_lit(w, "null"); }
+    } else if (name_incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "name"); w_lit(w, "null"); }
     w_char(w, '}');
 }
 
 /* One Pet in declaration order (petstore.json:878-917). */
 static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_t i) {
-    const int incl = o->inclusion, hx = o->hex_upper;
+    const int hx = o->hex_upper;
     const uint8_t fl = c->flags ? c->flags[i] : (uint8_t)PJ_PET_DEFAULT_FLAGS;
     int first = 1;
     w_char(w, '{');
     /* id: optional int64 (petstore.json:879-882) */
     if (fl & PJ_PET_HAS_ID) { w_key(w, &first, "id"); w_long(w, c->id[i]); }
-    else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
+    else if (incl_of(o, PJ_FIELD_PET_ID) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
     /* category: optional object (petstore.json:883-885).  A bean is never
      * "empty" for NON_EMPTY, so a present category is always written. */
     if ((fl & PJ_PET_HAS_CATEGORY) && c->cat_id) {
         w_key(w, &first, "category");
         uint8_t cf = c->cat_flags ? c->cat_flags[i] : (uint8_t)PJ_SUB_DEFAULT_FLAGS;
         uint64_t a = c->cat_name_off[i], b = c->cat_name_off[i + 1];
-        w_sub(w, incl, hx, cf, c->cat_id[i], c->cat_name_bytes + a, b - a);
-    } else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "category"); w_lit(w, "null"); }
+        w_sub(w, incl_of(o, PJ_FIELD_CATEGORY_ID), incl_of(o, PJ_FIELD_CATEGORY_NAME), hx, cf, c->cat_id[i],
+              c->cat_name_bytes + a, b - a);
+    } else if (incl_of(o, PJ_FIELD_PET_CATEGORY) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "category"); w_lit(w, "null"); }
     /* name: required => always written (petstore.json:873-876, 886-889) */
     w_key(w, &first, "name");
     if (fl & PJ_PET_HAS_NAME)
@@ -164,18 +172,19 @@ static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_
     /* tags: optional array of Tag (petstore.json:900-908); NON_EMPTY skips [] */
     if (fl & PJ_PET_HAS_TAGS) {
         uint64_t t0 = c->tag_off ? c->tag_off[i] : 0, t1 = c->tag_off ? c->tag_off[i + 1] : 0;
-        if (t1 > t0 || incl != PJ_INCLUDE_NON_EMPTY) {
+        if (t1 > t0 || incl_of(o, PJ_FIELD_PET_TAGS) != PJ_INCLUDE_NON_EMPTY) {
             w_key(w, &first, "tags");
             w_char(w, '[');
             for (uint64_t t = t0; t < t1; t++) {
                 if (t > t0) w_char(w, ',');
                 uint8_t tf = c->tag_flags ? c->tag_flags[t] : (uint8_t)PJ_SUB_DEFAULT_FLAGS;
                 uint64_t a = c->tag_name_off[t], b = c->tag_name_off[t + 1];
-                w_sub(w, incl, hx, tf, c->tag_id[t], c->tag_name_bytes + a, b - a);
+                w_sub(w, incl_of(o, PJ_FIELD_TAG_ID), incl_of(o, PJ_FIELD_TAG_NAME), hx, tf, c->tag_id[t],
+                      c->tag_name_bytes + a, b - a);
             }
             w_char(w, ']');
         }
-    } else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "tags"); w_lit(w, "null"); }
+    } else if (incl_of(o, PJ_FIELD_PET_TAGS) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "tags"); w_lit(w, "null"); }
     /* status: optional enum via @JsonValue (petstore.json:909-917);
      * codes other than 0..2 are null. */
     uint8_t st = c->status ? c->status[i] : (uint8_t)PJ_STATUS_NULL;
@@ -184,13 +193,20 @@ static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_
         w_char(w, '"');
         w_lit(w, STATUS_TXT[st]);
         w_char(w, '"');
-    } else if (incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "status"); w_lit(w, "null"); }
+    } else if (incl_of(o, PJ_FIELD_PET_STATUS) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "status"); w_lit(w, "null"); }
     w_char(w, '}');
+}
+
+void or_default_options(pj_options *o) {
+    o->inclusion = PJ_INCLUDE_NON_EMPTY;
+    o->hex_upper = 1;
+    for (int k = 0; k < PJ_FIELD_COUNT; k++) o->field_inclusion[k] = PJ_INCLUDE_DEFAULT;
 }
 
 int or_encode(const pj_pet_columns *cols, const pj_options *opt, int format,
               uint8_t *out, uint64_t out_cap, uint64_t *out_len) {
-    pj_options def = {PJ_INCLUDE_NON_EMPTY, 1};
+    pj_options def;
+    or_default_options(&def);
     if (!cols || !out_len || (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON))
         return PJ_ERR_INVALID_ARG;
     if (!opt) opt = &def;

@@ -23,6 +23,8 @@ extern "C" {
 
 /* Encode n_pets records (host pointers).  Same column conventions and return
  * codes as pj_encode_host. */
+/* pj_options defaults: NON_EMPTY everywhere, upper-case hex. */
+void or_default_options(pj_options *o);
 int or_encode(const pj_pet_columns *cols, const pj_options *opt, int format,
               uint8_t *out, uint64_t out_cap, uint64_t *out_len);
 

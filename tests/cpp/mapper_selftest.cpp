@@ -55,7 +55,8 @@ static std::vector<Pet> sample_pets(int n, unsigned seed) {
 static std::string oracle_json(std::vector<Pet> &pets, int fmt) {
     ColumnSet cs = to_columns(pets);
     pj_pet_columns v = cs.view();
-    pj_options o{PJ_INCLUDE_NON_EMPTY, 1};
+    pj_options o;
+    pj_default_options(&o);
     uint64_t n = 0;
     or_encode(&v, &o, fmt, nullptr, 0, &n);
     std::string s(n, '\0');

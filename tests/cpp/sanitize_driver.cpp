@@ -53,7 +53,9 @@ struct Cols {
 };
 
 std::vector<uint8_t> encode(const pj_pet_columns &c, int incl, int fmt) {
-    pj_options o{incl, 1};
+    pj_options o;
+    or_default_options(&o);
+    o.inclusion = incl;
     uint64_t n = 0;
     or_encode(&c, &o, fmt, nullptr, 0, &n);
     std::vector<uint8_t> out(n);

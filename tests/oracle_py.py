@@ -33,10 +33,10 @@ def lib():
     return _L
 
 
-def encode(cols: pj.Columns, fmt=pj.FORMAT_ARRAY, inclusion=pj.INCLUDE_NON_EMPTY, hex_upper=True) -> bytes:
+def encode(cols: pj.Columns, fmt=pj.FORMAT_ARRAY, inclusion=pj.INCLUDE_NON_EMPTY, hex_upper=True, fields=None) -> bytes:
     L = lib()
     s = cols.struct()
-    o = pj.Options(inclusion, 1 if hex_upper else 0)
+    o = pj.make_options(inclusion, hex_upper, fields)
     n = C.c_uint64(0)
     L.or_encode(C.byref(s), C.byref(o), fmt, None, 0, C.byref(n))
     out = np.empty(max(1, n.value), dtype=np.uint8)

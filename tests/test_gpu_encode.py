@@ -17,8 +17,8 @@ pytestmark = pytest.mark.gpu
 INCL = {"NON_EMPTY": pj.INCLUDE_NON_EMPTY, "NON_NULL": pj.INCLUDE_NON_NULL, "ALWAYS": pj.INCLUDE_ALWAYS}
 
 
-def gpu_encode(codec, cols, fmt, incl=pj.INCLUDE_NON_EMPTY, hex_upper=True):
-    codec.set_options(incl, hex_upper)
+def gpu_encode(codec, cols, fmt, incl=pj.INCLUDE_NON_EMPTY, hex_upper=True, fields=None):
+    codec.set_options(incl, hex_upper, fields)
     try:
         return codec.encode(cols.to_device(), fmt).cpu().numpy().tobytes()
     finally:
@@ -31,8 +31,9 @@ def test_encode_kat_gpu(codec, case):
     fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
     incl = INCL[case.get("inclusion", "NON_EMPTY")]
     hx = case.get("hex_upper", True)
-    assert gpu_encode(codec, cols, fmt, incl, hx) == case["expected"].encode("utf-8")
-    codec.set_options(incl, hx)
+    fields = {k: INCL[v] for k, v in case.get("fields", {}).items()}
+    assert gpu_encode(codec, cols, fmt, incl, hx, fields) == case["expected"].encode("utf-8")
+    codec.set_options(incl, hx, fields)
     assert codec.encode_host(cols, fmt) == case["expected"].encode("utf-8")
     codec.set_options()
 
@@ -55,6 +56,27 @@ def test_encode_inclusion_options_match_oracle(codec, incl):
     cols.arrays["tag_flags"] = rng.integers(0, 4, cols["tag_flags"].shape[0], dtype=np.uint8)
     assert gpu_encode(codec, cols, pj.FORMAT_ARRAY, incl, False) == \
         orc.encode(cols, pj.FORMAT_ARRAY, incl, False)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_encode_per_field_inclusion_matches_oracle(codec, seed):
+    """Random per-property inclusion modes over records with nulls and
+    empties in every optional property (configs 1, 3 and 5, both framings;
+    the skewed config also goes through the hybrid and whole-workgroup
+    paths)."""
+    rng = np.random.default_rng(seed)
+    modes = [pj.INCLUDE_NON_EMPTY, pj.INCLUDE_NON_NULL, pj.INCLUDE_ALWAYS]
+    for config, n in ((1, 20_000), (3, 30_000), (5, 5_000)):
+        cols = pj.generate(config, n)
+        cols.arrays["flags"] = cols["flags"] & rng.integers(0, 32, cols.n_pets, dtype=np.uint8) | pj.PET_HAS_NAME
+        cols.arrays["status"][rng.random(cols.n_pets) < 0.2] = pj.STATUS_NULL
+        cols.arrays["tag_flags"] = rng.integers(0, 4, cols["tag_flags"].shape[0], dtype=np.uint8)
+        cols.arrays["cat_flags"] = rng.integers(0, 4, cols["cat_flags"].shape[0], dtype=np.uint8)
+        glob = int(rng.choice(modes))
+        fields = {f: int(rng.choice(modes)) for f in pj.FIELDS if rng.random() < 0.6}
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            assert gpu_encode(codec, cols, fmt, glob, True, fields) == orc.encode(cols, fmt, glob, True, fields), \
+                (config, glob, fields, fmt)
 
 
 def test_encode_misaligned_string_columns(codec):

@@ -28,7 +28,8 @@ INCL = {"NON_EMPTY": pj.INCLUDE_NON_EMPTY, "NON_NULL": pj.INCLUDE_NON_NULL, "ALW
 def test_encode_kat(case):
     cols = to_columns([pet_from_dict(p) for p in case["pets"]])
     fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
-    out = orc.encode(cols, fmt, INCL[case.get("inclusion", "NON_EMPTY")], case.get("hex_upper", True))
+    fields = {k: INCL[v] for k, v in case.get("fields", {}).items()}
+    out = orc.encode(cols, fmt, INCL[case.get("inclusion", "NON_EMPTY")], case.get("hex_upper", True), fields)
     assert out == case["expected"].encode("utf-8")
 
 
