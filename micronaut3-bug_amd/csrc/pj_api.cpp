@@ -71,6 +71,7 @@ struct pj_ctx {
     DevBuf stage_in;    // host path: input staging
     DevBuf stage_out;   // host path: output staging
     DevBuf tape;        // decode: per-line results of the validating walk
+    DevBuf seg_in[2];   // streamed host decode: input segments (double buffer)
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
     // host entry points: a copy stream, two pinned bounce buffers and their
     // events (made on first use)
@@ -438,6 +439,8 @@ void pj_destroy(pj_ctx *c) {
     c->stage_in.release();
     c->stage_out.release();
     c->tape.release();
+    c->seg_in[0].release();
+    c->seg_in[1].release();
     for (auto &e : c->ev) if (e) (void)hipEventDestroy(e);
     if (c->pinned) (void)hipHostFree(c->pinned);
     if (c->xs) (void)hipStreamSynchronize(c->xs);
@@ -795,6 +798,159 @@ extern "C" pj_status pj_decode_array_host(pj_ctx *ctx, const uint8_t *in, uint64
 }
 
 namespace {
+// Streamed host decode: an NDJSON input of more than stream_above() bytes
+// is decoded in segments of about segment_bytes(), cut after a newline.
+// Segment k + 1 is copied in (on the copy stream, by a second host thread)
+// while segment k decodes; segment k's columns then go to the caller's
+// arrays at the running offsets, its offset arrays and error line numbers
+// shifted on the device first.  Device memory is bounded by the segment
+// size, not the input's.
+uint64_t segment_bytes() {
+    if (const char *e = std::getenv("PETJSON_DECODE_SEGMENT")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v) return v;
+    }
+    return 1ull << 30;
+}
+uint64_t stream_above() {
+    if (std::getenv("PETJSON_DECODE_SEGMENT")) return segment_bytes();
+    return 16ull << 30;
+}
+
+pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                             uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+    const uint64_t seg = segment_bytes();
+    // segments end after a newline (or at the end); a line longer than a
+    // segment makes its segment longer
+    auto seg_end = [&](uint64_t a) -> uint64_t {
+        if (len - a <= seg) return len;
+        const void *p = memrchr(in + a, '\n', seg);
+        if (p) return (uint64_t)(static_cast<const uint8_t *>(p) - in) + 1;
+        const void *q = std::memchr(in + a + seg, '\n', len - a - seg);
+        return q ? (uint64_t)(static_cast<const uint8_t *>(q) - in) + 1 : len;
+    };
+    std::memset(res, 0, sizeof *res);
+    uint64_t base[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};   // rows, bytes and items written before the segment
+    uint64_t lines = 0;
+    bool over = false;                 // the caller's capacities ran out: only counting from there
+    pj_status s = PJ_OK;
+    uint64_t a = 0, b = seg_end(0);
+    // the first segment in
+    PJ_HIP(ctx->seg_in[0].ensure(b - a + 16));
+    if ((s = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[0].p), in, b - a))) return s;
+    for (int k = 0; a < len; k ^= 1) {
+        const uint64_t n = b - a;
+        const uint64_t a2 = b, b2 = b < len ? seg_end(b) : b;
+        // the next segment in, while this one decodes
+        pj_status s2 = PJ_OK;
+        std::string e2;
+        std::thread copier;
+        if (a2 < len) {
+            if (ctx->seg_in[k ^ 1].ensure(b2 - a2 + 16) != hipSuccess) return fail(PJ_ERR_DEVICE, "segment buffer");
+            copier = std::thread([&, k, a2, b2] {
+                s2 = bind(ctx);                       // (HIP's current device is per thread)
+                if (!s2) s2 = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[k ^ 1].p), in + a2, b2 - a2);
+                if (s2) e2 = pj_last_error();
+            });
+        }
+        // this segment: columns sized for it, on the device
+        pj_pet_columns dc;
+        std::memset(&dc, 0, sizeof dc);
+        pj_decode_bounds(n, &dc);
+        const uint64_t cp = dc.cap_pets, cu = dc.cap_urls, ct = dc.cap_tags;
+        uint64_t ce = n / 16 + 16;           // the error list: a first guess, redone once with the count
+      again:
+        const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, dc.cap_name_bytes, cp * 8, cp, (cp + 1) * 8,
+                                 dc.cap_cat_name_bytes, (cp + 1) * 8, (cu + 1) * 8, dc.cap_url_bytes, (cp + 1) * 8,
+                                 ct * 8, ct, (ct + 1) * 8, dc.cap_tag_name_bytes, ce * 8, ce};
+        uint64_t off[20];
+        off[0] = 0;
+        for (int j = 0; j < 19; j++) off[j + 1] = off[j] + align256(sz[j] + 8);
+        hipError_t he = ctx->stage_out.ensure(off[19]);
+        pj_decode_result r;
+        if (he == hipSuccess) {
+            uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
+            void *dp[17];
+            for (int j = 0; j < 17; j++) dp[j] = D + off[j];
+            set_col_ptrs(&dc, dp);
+            uint64_t *del = reinterpret_cast<uint64_t *>(D + off[17]);
+            uint8_t *dec = D + off[18];
+            s = decode_impl(ctx, static_cast<uint8_t *>(ctx->seg_in[k].p), n, &dc, del, dec, ce, &r);
+            if (s == PJ_ERR_CAPACITY && r.n_errors > ce) {
+                ce = r.n_errors;
+                goto again;
+            }
+            if (s == PJ_OK) {
+                const uint64_t T[PJ_DEC_NCNT] = {r.n_pets, r.name_bytes, r.cat_name_bytes, r.n_urls,
+                                                 r.url_bytes, r.n_tags, r.tag_name_bytes, r.n_errors};
+                over = over || base[C_PETS] + T[C_PETS] > out->cap_pets ||
+                       base[C_NAMEB] + T[C_NAMEB] > out->cap_name_bytes ||
+                       base[C_CATB] + T[C_CATB] > out->cap_cat_name_bytes ||
+                       base[C_URLS] + T[C_URLS] > out->cap_urls || base[C_URLB] + T[C_URLB] > out->cap_url_bytes ||
+                       base[C_TAGS] + T[C_TAGS] > out->cap_tags ||
+                       base[C_TAGB] + T[C_TAGB] > out->cap_tag_name_bytes || base[C_ERRS] + T[C_ERRS] > err_cap;
+                if (!over) {
+                    // offsets and error lines shifted past the earlier segments, then out
+                    const hipError_t h = [&] {
+                        hipError_t x;
+                        const uint64_t np = T[C_PETS];
+                        if ((x = pj_launch_add_u64(dc.name_off, np + 1, base[C_NAMEB], ctx->stream)) ||
+                            (x = pj_launch_add_u64(dc.cat_name_off, np + 1, base[C_CATB], ctx->stream)) ||
+                            (x = pj_launch_add_u64(dc.photo_off, np + 1, base[C_URLS], ctx->stream)) ||
+                            (x = pj_launch_add_u64(dc.tag_off, np + 1, base[C_TAGS], ctx->stream)) ||
+                            (x = pj_launch_add_u64(dc.url_off, T[C_URLS] + 1, base[C_URLB], ctx->stream)) ||
+                            (x = pj_launch_add_u64(dc.tag_name_off, T[C_TAGS] + 1, base[C_TAGB], ctx->stream)) ||
+                            (x = pj_launch_add_u64(del, T[C_ERRS], lines, ctx->stream)))
+                            return x;
+                        return hipStreamSynchronize(ctx->stream);
+                    }();
+                    if (h != hipSuccess) s = fail(PJ_ERR_DEVICE, std::string("segment offsets: ") + hipGetErrorString(h));
+                }
+            }
+        } else s = fail(PJ_ERR_DEVICE, "segment columns: out of device memory");
+        if (copier.joinable()) copier.join();  // the copy stream and bounce buffers are free again
+        if (s) return s;
+        if (s2) return fail(s2, e2);
+        if (!over) {
+            const uint64_t np = r.n_pets, nu = r.n_urls, nt = r.n_tags;
+            // host destination of each column: its element at the running base
+            void *hp[17];
+            col_ptrs(out, hp);
+            const uint64_t bp = base[C_PETS], bu = base[C_URLS], bt = base[C_TAGS];
+            const uint64_t dst_off[17] = {bp * 8, bp, bp, bp * 8, base[C_NAMEB], bp * 8, bp, bp * 8, base[C_CATB],
+                                          bp * 8, bu * 8, base[C_URLB], bp * 8, bt * 8, bt, bt * 8, base[C_TAGB]};
+            const uint64_t used[17] = {np * 8, np, np, (np + 1) * 8, r.name_bytes, np * 8, np, (np + 1) * 8,
+                                       r.cat_name_bytes, (np + 1) * 8, (nu + 1) * 8, r.url_bytes, (np + 1) * 8,
+                                       nt * 8, nt, (nt + 1) * 8, r.tag_name_bytes};
+            void *dp[17];
+            col_ptrs(&dc, dp);
+            for (int j = 0; j < 17; j++)
+                if (used[j] && (s = d2h(ctx, static_cast<uint8_t *>(hp[j]) + dst_off[j], dp[j], used[j]))) return s;
+            uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
+            if (r.n_errors && ((s = d2h(ctx, err_line + base[C_ERRS], D + off[17], r.n_errors * 8)) ||
+                               (s = d2h(ctx, err_code + base[C_ERRS], D + off[18], r.n_errors))))
+                return s;
+        }
+        base[C_PETS] += r.n_pets; base[C_NAMEB] += r.name_bytes; base[C_CATB] += r.cat_name_bytes;
+        base[C_URLS] += r.n_urls; base[C_URLB] += r.url_bytes; base[C_TAGS] += r.n_tags;
+        base[C_TAGB] += r.tag_name_bytes; base[C_ERRS] += r.n_errors;
+        lines += r.n_lines;
+        res->n_general += r.n_general;
+        a = a2;
+        b = b2;
+    }
+    res->n_lines = lines;
+    res->n_pets = base[C_PETS]; res->name_bytes = base[C_NAMEB]; res->cat_name_bytes = base[C_CATB];
+    res->n_urls = base[C_URLS]; res->url_bytes = base[C_URLB]; res->n_tags = base[C_TAGS];
+    res->tag_name_bytes = base[C_TAGB]; res->n_errors = base[C_ERRS];
+    if (over) {
+        out->n_pets = 0;
+        return fail(PJ_ERR_CAPACITY, "capacity too small (sizes needed are in the result)");
+    }
+    out->n_pets = res->n_pets;
+    return PJ_OK;
+}
+
 pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
                            uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array) {
     pj_status s = bind(ctx);
@@ -803,6 +959,7 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
     if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
     if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
     if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    if (!array && len > stream_above()) return decode_host_stream(ctx, in, len, out, err_line, err_code, err_cap, res);
     // device staging: input, then every output column sized by the capacities
     const uint64_t cp = out->cap_pets, cu = out->cap_urls, ct = out->cap_tags;
     const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, out->cap_name_bytes, cp * 8, cp, (cp + 1) * 8,

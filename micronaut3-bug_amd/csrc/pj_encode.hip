@@ -1235,6 +1235,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     }
 }
 
+__global__ void k_add_u64(uint64_t *p, uint64_t n, uint64_t v) {
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] += v;
+}
+
 __global__ void k_fill_u64(uint64_t *p, uint64_t n, uint64_t v) {
     uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -1247,6 +1252,13 @@ __global__ void k_put_bytes(uint8_t *out, uint32_t w, int k) {
 }  // namespace pj
 
 // ------------------------------------------------------------- launchers
+hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st) {
+    if (n == 0 || v == 0) return hipSuccess;
+    uint64_t g = (n + 255) / 256;
+    hipLaunchKernelGGL(pj::k_add_u64, dim3((unsigned)g), dim3(256), 0, st, p, n, v);
+    return hipGetLastError();
+}
+
 hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st) {
     if (n == 0) return hipSuccess;
     uint64_t g = (n + 255) / 256;

@@ -42,3 +42,52 @@ def test_host_entry_points_across_chunks(chunk):
                PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"), os.path.join(ROOT, "tests")]))
     r = subprocess.run([sys.executable, "-c", SCRIPT], capture_output=True, text=True, env=env, timeout=240)
     assert r.returncode == 0 and "host pipeline ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
+
+
+STREAM = r"""
+import numpy as np, torch
+import petjson as pj
+codec = pj.Codec(0)
+parts = []
+for cfg, n in ((3, 40000), (5, 4000)):
+    buf = codec.encode(pj.generate(cfg, n).to_device(), pj.FORMAT_NDJSON).cpu().numpy().copy()
+    pj.corrupt_ndjson(buf, 11 + cfg, 0.01)
+    parts.append(buf.tobytes())
+long_line = b'{"id":1,"name":"' + b"L" * 3_000_000 + b'","photoUrls":["u"],"tags":[]}\n'
+data = parts[0] + b"\n\n" + long_line + parts[1] + b'{"name":"last","photoUrls":[]}'   # no final newline
+d = torch.from_numpy(np.frombuffer(data, np.uint8).copy()).cuda()
+ref, el_r, ec_r, res_r = codec.decode(d)
+ref = ref.to_host()
+el_r, ec_r = el_r.cpu().numpy(), ec_r.cpu().numpy()
+host, el, ec, res = codec.decode_host(data)
+for k in ("n_lines", "n_pets", "n_errors", "name_bytes", "cat_name_bytes", "n_urls", "url_bytes", "n_tags", "tag_name_bytes"):
+    assert getattr(res, k) == getattr(res_r, k), (k, getattr(res, k), getattr(res_r, k))
+for k in pj.COLS:
+    assert np.array_equal(host[k], ref[k]), k
+assert np.array_equal(el, el_r) and np.array_equal(ec, ec_r)
+# capacities one short: PJ_ERR_CAPACITY, with the sizes the whole input needs
+caps = pj.decode_bounds(len(data))
+caps["cap_url_bytes"] = int(res_r.url_bytes) - 1
+try:
+    codec.decode_host(data, caps=caps)
+    raise SystemExit("expected a capacity error")
+except pj.PetJsonError as e:
+    assert e.status == pj.PJ_ERR_CAPACITY, e
+codec.close()
+print("streamed decode ok")
+"""
+
+
+@pytest.mark.parametrize("segment", [1_000_003, 4_194_301])
+def test_host_decode_streamed_in_segments(segment):
+    """Inputs over PETJSON_DECODE_SEGMENT bytes (default: inputs over 16 GiB,
+    in 1 GiB segments) are decoded in segments cut after a newline, the next
+    one copied in while one decodes: columns, error lines and codes, and
+    totals equal the one-shot device decode.  The input holds blank lines,
+    1% corrupted lines, a 3 MB line longer than a segment, skewed records,
+    and a last line without its newline; capacities one short report
+    PJ_ERR_CAPACITY."""
+    env = dict(os.environ, PETJSON_DECODE_SEGMENT=str(segment),
+               PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"), os.path.join(ROOT, "tests")]))
+    r = subprocess.run([sys.executable, "-c", STREAM], capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0 and "streamed decode ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
