@@ -120,7 +120,11 @@ typedef enum pj_inclusion {
 
 typedef enum pj_format {
     PJ_FORMAT_ARRAY  = 0,      /* [rec,rec,...]   (List<Pet> body)             */
-    PJ_FORMAT_NDJSON = 1       /* rec\nrec\n...                                 */
+    PJ_FORMAT_NDJSON = 1,      /* rec\nrec\n...                                 */
+    PJ_FORMAT_PRETTY = 2       /* the List<Pet> body indented as by jackson-core's
+                                  DefaultPrettyPrinter (ObjectMapper with
+                                  pretty printing on): "[ {\n  \"id\" : 1,
+                                  ...\n}, {...} ]"                            */
 } pj_format;
 
 /* The optional properties, for per-property inclusion modes (Jackson's

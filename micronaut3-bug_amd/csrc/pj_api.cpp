@@ -241,6 +241,8 @@ uint64_t spin_limit() {
     return 20000000;
 }
 
+bool format_ok(int f) { return f == PJ_FORMAT_ARRAY || f == PJ_FORMAT_NDJSON || f == PJ_FORMAT_PRETTY; }
+
 // fixed_scratch: encode into the device's fixed scratch array instead of
 // the context's growable buffer (pj_encode_device_noalloc); nothing is
 // allocated on that path.
@@ -249,28 +251,31 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     pj_status s = bind(ctx);
     if (s) return s;
     if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
-    if (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
     if (!count_only && cap > 0 && !out) return fail(PJ_ERR_INVALID_ARG, "null output with capacity");
     if ((s = check_enc_cols(cols))) return s;
     ctx->n_ev = 0;
     const uint64_t n = cols->n_pets;
     if (n == 0) {
-        uint64_t len = format == PJ_FORMAT_ARRAY ? 2 : 0;
+        // "[]", "[ ]" (pretty) or nothing
+        const uint64_t len = format == PJ_FORMAT_ARRAY ? 2 : format == PJ_FORMAT_PRETTY ? 3 : 0;
         *out_len = len;
         if (!count_only && len && len <= cap) {
             if ((s = mark(ctx))) return s;
-            PJ_HIP(pj_launch_put_bytes(out, '[' | (']' << 8), 2, ctx->stream));
+            const uint32_t w = format == PJ_FORMAT_ARRAY ? '[' | (']' << 8) : '[' | (' ' << 8) | (']' << 16);
+            PJ_HIP(pj_launch_put_bytes(out, w, (int)len, ctx->stream));
             if ((s = mark(ctx))) return s;
         }
         PJ_HIP(hipStreamSynchronize(ctx->stream));
         if ((s = finish_timing(ctx))) return s;
         return len > cap && !count_only ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
     }
-    const uint64_t bt = (uint64_t)pj_encode_block_records(nested_cols(cols));
+    const bool pretty = format == PJ_FORMAT_PRETTY;
+    const uint64_t bt = (uint64_t)(pretty ? pj_encode_pretty_records() : pj_encode_block_records(nested_cols(cols)));
     const uint64_t nblk = (n + bt - 1) / bt;
     uint64_t *sc;
     if (fixed_scratch) {
-        if (nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
+        if (n > PJ_NOALLOC_MAX_RECORDS(nested_cols(cols)) || nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
             return fail(PJ_ERR_INVALID_ARG, "pj_encode_device_noalloc: " + std::to_string(n) +
                                                 " records exceed the fixed scratch (at most " +
                                                 std::to_string(PJ_NOALLOC_MAX_RECORDS(nested_cols(cols))) + ")");
@@ -303,13 +308,14 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // atomic on the critical path) with bounded look-back waits: should a
     // block wait past the bound (a predecessor not yet running), it flags
     // the launch, which is then redone with ticket-ordered blocks.
-    P.order_by_id = nested_cols(cols) ? 0 : 1;
+    P.order_by_id = nested_cols(cols) || pretty ? 0 : 1;
     P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;
         PJ_HIP(pj_launch_fill_u64(sc, nblk + 3, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
+        if (pretty) PJ_HIP(pj_launch_encode_pretty(P, ctx->stream));
+        else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
         if ((s = mark(ctx))) return s;
         PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));
@@ -318,7 +324,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
         ctx->n_ev = 0;
     }
     // flat records too long for the compact tile: later calls use the wide one
-    if (!nested_cols(cols) && !ctx->flat_wide && ctx->pinned[2] * 64 > nblk) ctx->flat_wide = true;
+    if (!pretty && !nested_cols(cols) && !ctx->flat_wide && ctx->pinned[2] * 64 > nblk) ctx->flat_wide = true;
     if ((s = finish_timing(ctx))) return s;
     *out_len = ctx->pinned[1];
     if (!count_only && *out_len > cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
@@ -522,25 +528,28 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, ui
 
 pj_status pj_encode_bound(const pj_pet_columns *cols, int format, uint64_t *bound) {
     if (!cols || !bound) return fail(PJ_ERR_INVALID_ARG, "null argument");
-    if (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
     pj_status s;
     if ((s = check_enc_cols(cols))) return s;
     const uint64_t n = cols->n_pets;
     // per record: every Pet / Category property with a 20-character long,
     // the longest status and the framing; per url / tag item: its quotes,
-    // separators and (tags) an object with both properties
-    uint64_t b = 2 + n * 256, str = 0;
+    // separators and (tags) an object with both properties.  Pretty output
+    // adds at most 64 bytes of whitespace per record, 1 per url and 32 per
+    // tag.
+    const bool pretty = format == PJ_FORMAT_PRETTY;
+    uint64_t b = 3 + n * (pretty ? 320 : 256), str = 0;
     if (n) {
         str += cols->name_off[n] - cols->name_off[0];
         if (cols->cat_name_off) str += cols->cat_name_off[n] - cols->cat_name_off[0];
         if (cols->photo_off) {
             const uint64_t u0 = cols->photo_off[0], u1 = cols->photo_off[n];
-            b += (u1 - u0) * 4;
+            b += (u1 - u0) * (pretty ? 5 : 4);
             str += cols->url_off[u1] - cols->url_off[u0];
         }
         if (cols->tag_off) {
             const uint64_t t0 = cols->tag_off[0], t1 = cols->tag_off[n];
-            b += (t1 - t0) * 64;
+            b += (t1 - t0) * (pretty ? 96 : 64);
             str += cols->tag_name_off[t1] - cols->tag_name_off[t0];
         }
     }

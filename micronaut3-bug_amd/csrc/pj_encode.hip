@@ -557,6 +557,106 @@ __device__ __forceinline__ void emit_rec(S &s, const EncParams &P, const ColSrc 
     rec_tail(s, P, i, v);
 }
 
+// ------------------------------------------------ pretty-printed records
+// PJ_FORMAT_PRETTY: the array body as jackson-core's DefaultPrettyPrinter
+// lays it out.  Objects indent their entries on new lines, two spaces per
+// object level ("\n" + 2*level spaces before each entry, ",\n..." between
+// entries, "\n" + 2*(level-1) spaces before '}', "{ }" when empty); arrays
+// stay on one line ("[ a, b ]", "[ ]" when empty) and add no level;
+// property names are followed by " : ".  The schema fixes every object's
+// level: a Pet is at level 1 (the enclosing array adds none), its category
+// and its tags at level 2.
+
+// Separator and indentation before an entry of an object at level ind/2.
+template <class S> __device__ __forceinline__ void pp_entry(S &s, bool &first, int ind) {
+    if (!first) s.put_byte(',');
+    first = false;
+    s.put_byte('\n');
+    s.put8(0x2020202020202020ull, ind);
+}
+// The closing brace of an object at level ind/2 + 1 (ind: its parent's
+// indentation).
+template <class S> __device__ __forceinline__ void pp_close(S &s, bool first, int ind) {
+    if (first) {
+        lit(s, " }");
+        return;
+    }
+    s.put_byte('\n');
+    s.put8(0x2020202020202020ull, ind);
+    s.put_byte('}');
+}
+
+// A Category or Tag object at level 2; F0 is the pj_field of its id.
+template <int F0, class S>
+__device__ __forceinline__ void pp_sub(S &s, const EncParams &P, uint32_t fl, int64_t id, const uint8_t *nm,
+                                       uint64_t nlen) {
+    const uint32_t ii = P.incl[F0], ni = P.incl[F0 + 1];
+    bool first = true;
+    s.put_byte('{');
+    if (fl & PJ_SUB_HAS_ID) { pp_entry(s, first, 4); lit(s, "\"id\" : "); emit_long(s, id); }
+    else if (ii == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 4); lit(s, "\"id\" : null"); }
+    if (fl & PJ_SUB_HAS_NAME) {
+        if (nlen > 0 || ni != PJ_INCLUDE_NON_EMPTY) {
+            pp_entry(s, first, 4); lit(s, "\"name\" : "); emit_str(s, nm, nlen, P.hexa);
+        }
+    } else if (ni == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 4); lit(s, "\"name\" : null"); }
+    pp_close(s, first, 2);
+}
+
+// Record i with its array framing: "[ " or ", " before, " ]" after the last.
+template <class S> __device__ __forceinline__ void pp_rec(S &s, const EncParams &P, uint64_t i, const RecVals &v) {
+    const pj_pet_columns &c = P.c;
+    const uint32_t fl = v.fl;
+    if (i == 0) lit(s, "[ ");
+    else lit(s, ", ");
+    bool first = true;
+    s.put_byte('{');
+    if (fl & PJ_PET_HAS_ID) { pp_entry(s, first, 2); lit(s, "\"id\" : "); emit_long(s, v.id); }
+    else if (P.incl[PJ_FIELD_PET_ID] == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 2); lit(s, "\"id\" : null"); }
+    if ((fl & PJ_PET_HAS_CATEGORY) && c.cat_id) {
+        pp_entry(s, first, 2); lit(s, "\"category\" : ");
+        pp_sub<PJ_FIELD_CATEGORY_ID>(s, P, v.cf, v.cat_id, c.cat_name_bytes + v.ca, v.cb - v.ca);
+    } else if (P.incl[PJ_FIELD_PET_CATEGORY] == PJ_INCLUDE_ALWAYS) {
+        pp_entry(s, first, 2); lit(s, "\"category\" : null");
+    }
+    pp_entry(s, first, 2);
+    if (fl & PJ_PET_HAS_NAME) { lit(s, "\"name\" : "); emit_str(s, c.name_bytes + v.na, v.nb - v.na, P.hexa); }
+    else lit(s, "\"name\" : null");
+    pp_entry(s, first, 2);
+    if (fl & PJ_PET_HAS_PHOTOURLS) {
+        lit(s, "\"photoUrls\" : [");
+        for (uint64_t u = v.u0; u < v.u1; u++) {
+            if (u == v.u0) s.put_byte(' ');
+            else lit(s, ", ");
+            const uint64_t a = c.url_off[u], b = c.url_off[u + 1];
+            emit_str(s, c.url_bytes + a, b - a, P.hexa);
+        }
+        lit(s, " ]");
+    } else lit(s, "\"photoUrls\" : null");
+    const uint32_t ti = P.incl[PJ_FIELD_PET_TAGS];
+    if (fl & PJ_PET_HAS_TAGS) {
+        if (v.t1 > v.t0 || ti != PJ_INCLUDE_NON_EMPTY) {
+            pp_entry(s, first, 2); lit(s, "\"tags\" : [");
+            for (uint64_t g = v.t0; g < v.t1; g++) {
+                if (g == v.t0) s.put_byte(' ');
+                else lit(s, ", ");
+                const TagItem tg = load_tag(P, g);
+                pp_sub<PJ_FIELD_TAG_ID>(s, P, tg.tf, tg.id, c.tag_name_bytes + tg.a, tg.b - tg.a);
+            }
+            lit(s, " ]");
+        }
+    } else if (ti == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 2); lit(s, "\"tags\" : null"); }
+    const uint32_t st = v.st;
+    if (st <= 2) {
+        pp_entry(s, first, 2);
+        if (st == 0) lit(s, "\"status\" : \"available\"");
+        else if (st == 1) lit(s, "\"status\" : \"pending\"");
+        else lit(s, "\"status\" : \"sold\"");
+    } else if (P.incl[PJ_FIELD_PET_STATUS] == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 2); lit(s, "\"status\" : null"); }
+    pp_close(s, first, 0);
+    if (i == P.n - 1) lit(s, " ]");
+}
+
 // ---------------------------------------------------- large records, cooperatively
 // Exact bytes at any global address: 8-byte stores, exact tail.
 struct XSink {
@@ -1235,6 +1335,45 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     }
 }
 
+// PJ_FORMAT_PRETTY: one thread per record, blocks of BT records claimed by
+// ticket.  Each thread measures its record, a block scan places the records,
+// the look-back gives the block's offset, and each thread writes its record
+// straight to global memory.  Records that would end past the capacity are
+// not written; the last block stores the total.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_encode_pretty(EncParams P) {
+    __shared__ uint64_t sh_scan[BT / 64 + 2];
+    __shared__ uint64_t sh_b, sh_base;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) sh_b = atomicAdd(P.ticket, 1ull);
+    __syncthreads();
+    const uint64_t b = sh_b, nblk = (P.n + BT - 1) / BT;
+    const uint64_t i = b * BT + t;
+    const bool live = i < P.n;
+    RecVals v{};
+    CountSink cs;
+    if (live) {
+        v = load_rec<true>(P, i);
+        pp_rec(cs, P, i, v);
+    }
+    uint64_t agg;
+    const uint64_t pre = block_excl_scan<BT>(cs.n, sh_scan, &agg);
+    if (t < 64) {
+        const uint64_t excl = lookback(P.state, b, agg);
+        if (t == 0) {
+            sh_base = excl;
+            if (b == nblk - 1) *P.total = excl + agg;
+        }
+    }
+    __syncthreads();
+    if (P.count_only || !live) return;
+    const uint64_t at = sh_base + pre;
+    if (at + cs.n > P.cap) return;
+    XSink xs{P.out + at, 0, 0};
+    pp_rec(xs, P, i, v);
+    xs.finish();
+}
+
 __global__ void k_add_u64(uint64_t *p, uint64_t n, uint64_t v) {
     uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] += v;
@@ -1346,6 +1485,15 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                                  ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
     return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>,
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
+}
+
+constexpr int ENC_PRETTY_BT = 256;
+int pj_encode_pretty_records() { return ENC_PRETTY_BT; }
+
+hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st) {
+    const uint64_t nblk = (P.n + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
+    hipLaunchKernelGGL(pj::k_encode_pretty<ENC_PRETTY_BT>, dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P);
+    return hipGetLastError();
 }
 
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st) {

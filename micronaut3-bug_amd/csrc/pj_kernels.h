@@ -103,6 +103,8 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);   // p[0, n) += v
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 int pj_encode_block_records(bool nested);
+hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st);
+int pj_encode_pretty_records();
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);
 hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st);

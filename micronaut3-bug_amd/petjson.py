@@ -26,7 +26,7 @@ PJ_OK, PJ_ERR_INVALID_ARG, PJ_ERR_CAPACITY, PJ_ERR_DEVICE, PJ_ERR_NO_DEVICE, PJ_
     PJ_ERR_SYNTAX = range(7)
 STATUS_NAMES = {0: "PJ_OK", 1: "PJ_ERR_INVALID_ARG", 2: "PJ_ERR_CAPACITY", 3: "PJ_ERR_DEVICE",
                 4: "PJ_ERR_NO_DEVICE", 5: "PJ_ERR_OUT_OF_MEMORY", 6: "PJ_ERR_SYNTAX"}
-FORMAT_ARRAY, FORMAT_NDJSON = 0, 1
+FORMAT_ARRAY, FORMAT_NDJSON, FORMAT_PRETTY = 0, 1, 2
 INCLUDE_NON_EMPTY, INCLUDE_NON_NULL, INCLUDE_ALWAYS = 0, 1, 2
 STATUS_AVAILABLE, STATUS_PENDING, STATUS_SOLD, STATUS_NULL = 0, 1, 2, 255
 PET_HAS_ID, PET_HAS_CATEGORY, PET_HAS_NAME, PET_HAS_PHOTOURLS, PET_HAS_TAGS = 1, 2, 4, 8, 16

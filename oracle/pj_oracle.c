@@ -44,7 +44,9 @@
  *                                 ENCODE
  * ====================================================================== */
 
-typedef struct { uint8_t *out; uint64_t cap, len; } wbuf;
+/* pretty: lay the output out as jackson-core's DefaultPrettyPrinter does;
+ * nest: its nesting counter (objects only: its array indenter is inline). */
+typedef struct { uint8_t *out; uint64_t cap, len; int pretty, nest; } wbuf;
 
 static void w_bytes(wbuf *w, const void *p, uint64_t n) {
     if (w->out && w->len < w->cap) {
@@ -102,13 +104,55 @@ static void w_string(wbuf *w, const uint8_t *s, uint64_t n, int hex_upper) {
 
 static const char *const STATUS_TXT[3] = {"available", "pending", "sold"};
 
+/* Structure hooks, after the jackson-core 2.x PrettyPrinter calls the
+ * generator makes (jackson-core is pulled in by micronaut-serde-jackson
+ * 2.15.1, reference build.gradle:14,104; it is not vendored in the
+ * reference).  Compact output writes the punctuation only.  With
+ * DefaultPrettyPrinter:
+ *  - writeStartObject: '{', nesting + 1;
+ *  - beforeObjectEntries / writeObjectEntrySeparator: (',' for the latter)
+ *    then the object indenter: "\n" + two spaces per nesting level;
+ *  - writeObjectFieldValueSeparator: " : ";
+ *  - writeEndObject: nesting - 1, then the indenter if the object had
+ *    entries, else one space; '}';
+ *  - arrays use the inline FixedSpaceIndenter (one space, no nesting
+ *    change): beforeArrayValues ' ', writeArrayValueSeparator ", ",
+ *    writeEndArray ' ' (with or without values) then ']'. */
+static void w_indent(wbuf *w) {
+    w_char(w, '\n');
+    for (int k = 0; k < w->nest; k++) w_lit(w, "  ");
+}
+static void o_start(wbuf *w) {
+    w_char(w, '{');
+    w->nest++;
+}
+static void o_end(wbuf *w, int empty) {
+    w->nest--;
+    if (w->pretty) {
+        if (empty) w_char(w, ' ');
+        else w_indent(w);
+    }
+    w_char(w, '}');
+}
+static void a_start(wbuf *w) { w_char(w, '['); }
+/* Before array value number idx. */
+static void a_value(wbuf *w, uint64_t idx) {
+    if (idx) w_char(w, ',');
+    if (w->pretty) w_char(w, ' ');
+}
+static void a_end(wbuf *w) {
+    if (w->pretty) w_char(w, ' ');
+    w_char(w, ']');
+}
+
 /* "key": with a leading comma when it is not the first property written. */
 static void w_key(wbuf *w, int *first, const char *key) {
     if (!*first) w_char(w, ',');
+    if (w->pretty) w_indent(w);
     *first = 0;
     w_char(w, '"');
     w_lit(w, key);
-    w_lit(w, "\":");
+    w_lit(w, w->pretty ? "\" : " : "\":");
 }
 
 /* The inclusion mode of optional property f: its own entry, else the
@@ -122,7 +166,7 @@ static int incl_of(const pj_options *o, int f) {
 static void w_sub(wbuf *w, int id_incl, int name_incl, int hex_upper, uint8_t fl, int64_t id,
                   const uint8_t *name, uint64_t name_len) {
     int first = 1;
-    w_char(w, '{');
+    o_start(w);
     if (fl & PJ_SUB_HAS_ID) { w_key(w, &first, "id"); w_long(w, id); }
     else if (id_incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
     if (fl & PJ_SUB_HAS_NAME) {
@@ -131,7 +175,7 @@ static void w_sub(wbuf *w, int id_incl, int name_incl, int hex_upper, uint8_t fl
             w_string(w, name, name_len, hex_upper);
         }
     } else if (name_incl == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "name"); w_lit(w, "null"); }
-    w_char(w, '}');
+    o_end(w, first);
 }
 
 /* One Pet in declaration order (petstore.json:878-917). */
@@ -139,7 +183,7 @@ static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_
     const int hx = o->hex_upper;
     const uint8_t fl = c->flags ? c->flags[i] : (uint8_t)PJ_PET_DEFAULT_FLAGS;
     int first = 1;
-    w_char(w, '{');
+    o_start(w);
     /* id: optional int64 (petstore.json:879-882) */
     if (fl & PJ_PET_HAS_ID) { w_key(w, &first, "id"); w_long(w, c->id[i]); }
     else if (incl_of(o, PJ_FIELD_PET_ID) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "id"); w_lit(w, "null"); }
@@ -160,29 +204,29 @@ static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_
     /* photoUrls: required array of string (petstore.json:890-899) */
     w_key(w, &first, "photoUrls");
     if (fl & PJ_PET_HAS_PHOTOURLS) {
-        w_char(w, '[');
+        a_start(w);
         if (c->photo_off) {
             for (uint64_t u = c->photo_off[i]; u < c->photo_off[i + 1]; u++) {
-                if (u > c->photo_off[i]) w_char(w, ',');
+                a_value(w, u - c->photo_off[i]);
                 w_string(w, c->url_bytes + c->url_off[u], c->url_off[u + 1] - c->url_off[u], hx);
             }
         }
-        w_char(w, ']');
+        a_end(w);
     } else w_lit(w, "null");
     /* tags: optional array of Tag (petstore.json:900-908); NON_EMPTY skips [] */
     if (fl & PJ_PET_HAS_TAGS) {
         uint64_t t0 = c->tag_off ? c->tag_off[i] : 0, t1 = c->tag_off ? c->tag_off[i + 1] : 0;
         if (t1 > t0 || incl_of(o, PJ_FIELD_PET_TAGS) != PJ_INCLUDE_NON_EMPTY) {
             w_key(w, &first, "tags");
-            w_char(w, '[');
+            a_start(w);
             for (uint64_t t = t0; t < t1; t++) {
-                if (t > t0) w_char(w, ',');
+                a_value(w, t - t0);
                 uint8_t tf = c->tag_flags ? c->tag_flags[t] : (uint8_t)PJ_SUB_DEFAULT_FLAGS;
                 uint64_t a = c->tag_name_off[t], b = c->tag_name_off[t + 1];
                 w_sub(w, incl_of(o, PJ_FIELD_TAG_ID), incl_of(o, PJ_FIELD_TAG_NAME), hx, tf, c->tag_id[t],
                       c->tag_name_bytes + a, b - a);
             }
-            w_char(w, ']');
+            a_end(w);
         }
     } else if (incl_of(o, PJ_FIELD_PET_TAGS) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "tags"); w_lit(w, "null"); }
     /* status: optional enum via @JsonValue (petstore.json:909-917);
@@ -194,7 +238,7 @@ static void w_pet(wbuf *w, const pj_pet_columns *c, const pj_options *o, uint64_
         w_lit(w, STATUS_TXT[st]);
         w_char(w, '"');
     } else if (incl_of(o, PJ_FIELD_PET_STATUS) == PJ_INCLUDE_ALWAYS) { w_key(w, &first, "status"); w_lit(w, "null"); }
-    w_char(w, '}');
+    o_end(w, first);
 }
 
 void or_default_options(pj_options *o) {
@@ -207,17 +251,19 @@ int or_encode(const pj_pet_columns *cols, const pj_options *opt, int format,
               uint8_t *out, uint64_t out_cap, uint64_t *out_len) {
     pj_options def;
     or_default_options(&def);
-    if (!cols || !out_len || (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON))
+    if (!cols || !out_len ||
+        (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON && format != PJ_FORMAT_PRETTY))
         return PJ_ERR_INVALID_ARG;
     if (!opt) opt = &def;
-    wbuf w = {out, out_cap, 0};
-    if (format == PJ_FORMAT_ARRAY) w_char(&w, '[');
+    wbuf w = {out, out_cap, 0, format == PJ_FORMAT_PRETTY, 0};
+    const int array = format != PJ_FORMAT_NDJSON;
+    if (array) a_start(&w);
     for (uint64_t i = 0; i < cols->n_pets; i++) {
-        if (format == PJ_FORMAT_ARRAY && i) w_char(&w, ',');
+        if (array) a_value(&w, i);
         w_pet(&w, cols, opt, i);
-        if (format == PJ_FORMAT_NDJSON) w_char(&w, '\n');
+        if (!array) w_char(&w, '\n');
     }
-    if (format == PJ_FORMAT_ARRAY) w_char(&w, ']');
+    if (array) a_end(&w);
     *out_len = w.len;
     return w.len > out_cap ? PJ_ERR_CAPACITY : PJ_OK;
 }

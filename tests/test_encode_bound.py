@@ -22,7 +22,7 @@ def bound(cols, fmt):
 @pytest.mark.parametrize("config", [1, 2, 3, 5])
 def test_bound_covers_generated(config):
     cols = pj.generate(config, 2000)
-    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
         for incl in (pj.INCLUDE_NON_EMPTY, pj.INCLUDE_NON_NULL, pj.INCLUDE_ALWAYS):
             assert bound(cols, fmt) >= len(orc.encode(cols, fmt, incl))
 
@@ -31,11 +31,12 @@ def test_bound_covers_random_and_escape_heavy():
     rng = np.random.default_rng(3)
     for _ in range(60):
         cols = random_columns(rng, int(rng.integers(0, 300)))
-        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
             for incl in (pj.INCLUDE_NON_EMPTY, pj.INCLUDE_ALWAYS):
                 assert bound(cols, fmt) >= len(orc.encode(cols, fmt, incl, False))
     # every string byte a control character: each becomes \u00XX
     cols = pj.generate(3, 500)
     for k in ("name_bytes", "cat_name_bytes", "url_bytes", "tag_name_bytes"):
         cols.arrays[k][:] = 1
-    assert bound(cols, pj.FORMAT_ARRAY) >= len(orc.encode(cols, pj.FORMAT_ARRAY, pj.INCLUDE_ALWAYS))
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_PRETTY):
+        assert bound(cols, fmt) >= len(orc.encode(cols, fmt, pj.INCLUDE_ALWAYS))

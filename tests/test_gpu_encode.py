@@ -28,7 +28,7 @@ def gpu_encode(codec, cols, fmt, incl=pj.INCLUDE_NON_EMPTY, hex_upper=True, fiel
 @pytest.mark.parametrize("case", load("encode_kat.json")["cases"], ids=lambda c: c["name"])
 def test_encode_kat_gpu(codec, case):
     cols = to_columns([pet_from_dict(p) for p in case["pets"]])
-    fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
+    fmt = {"ndjson": pj.FORMAT_NDJSON, "pretty": pj.FORMAT_PRETTY}.get(case.get("format"), pj.FORMAT_ARRAY)
     incl = INCL[case.get("inclusion", "NON_EMPTY")]
     hx = case.get("hex_upper", True)
     fields = {k: INCL[v] for k, v in case.get("fields", {}).items()}
@@ -285,3 +285,74 @@ def test_encode_flat_long_records_switch_to_wide_tile(codec):
     ref = orc.encode(cols, pj.FORMAT_ARRAY)
     for _ in range(3):
         assert gpu_encode(codec, cols, pj.FORMAT_ARRAY) == ref
+
+
+# ------------------------------------------------------------ pretty output
+@pytest.mark.parametrize("config,n", [(1, 50_000), (2, 100_000), (3, 60_000), (5, 10_000)])
+def test_encode_pretty_matches_oracle(codec, config, n):
+    print(f"[encode pretty] config={config} n={n}", flush=True)
+    cols = pj.generate(config, n)
+    assert gpu_encode(codec, cols, pj.FORMAT_PRETTY) == orc.encode(cols, pj.FORMAT_PRETTY)
+    assert codec.encode_size(cols.to_device(), pj.FORMAT_PRETTY) == len(orc.encode(cols, pj.FORMAT_PRETTY))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_encode_pretty_inclusion_modes_match_oracle(codec, seed):
+    cols = pj.generate(3, 20_000)
+    rng = np.random.default_rng(seed)
+    cols.arrays["flags"] = cols["flags"] & rng.integers(0, 64, cols.n_pets, dtype=np.uint8)
+    cols.arrays["status"][rng.random(cols.n_pets) < 0.2] = pj.STATUS_NULL
+    cols.arrays["tag_flags"] = rng.integers(0, 4, cols["tag_flags"].shape[0], dtype=np.uint8)
+    cols.arrays["cat_flags"] = rng.integers(0, 4, cols.n_pets, dtype=np.uint8)
+    for incl in (pj.INCLUDE_NON_EMPTY, pj.INCLUDE_NON_NULL, pj.INCLUDE_ALWAYS):
+        fields = {f: int(rng.integers(0, 3)) for f in pj.FIELDS if rng.random() < 0.5}
+        assert gpu_encode(codec, cols, pj.FORMAT_PRETTY, incl, bool(seed), fields) == \
+            orc.encode(cols, pj.FORMAT_PRETTY, incl, bool(seed), fields), (incl, fields)
+
+
+def test_encode_pretty_flat_absent_groups_and_skew(codec):
+    """The flat layout, absent column groups and records with long lists and
+    long names (one thread still writes each record)."""
+    cols = pj.generate(2, 30_000)
+    assert gpu_encode(codec, cols, pj.FORMAT_PRETTY) == orc.encode(cols, pj.FORMAT_PRETTY)
+    cols = pj.generate(3, 5_000)
+    for g in ("photoUrls", "tags"):
+        for k in GROUPS[g]:
+            cols.arrays[k] = None
+    assert gpu_encode(codec, cols, pj.FORMAT_PRETTY, pj.INCLUDE_ALWAYS) == \
+        orc.encode(cols, pj.FORMAT_PRETTY, pj.INCLUDE_ALWAYS)
+    cols = to_columns(_hybrid_pets())
+    assert gpu_encode(codec, cols, pj.FORMAT_PRETTY) == orc.encode(cols, pj.FORMAT_PRETTY)
+
+
+def test_encode_pretty_empty_single_and_capacity(codec):
+    assert gpu_encode(codec, to_columns([]), pj.FORMAT_PRETTY) == b"[ ]"
+    cols = pj.generate(3, 1)
+    assert gpu_encode(codec, cols, pj.FORMAT_PRETTY) == orc.encode(cols, pj.FORMAT_PRETTY)
+    cols = pj.generate(3, 10_000)
+    d = cols.to_device()
+    ref = np.frombuffer(orc.encode(cols, pj.FORMAT_PRETTY), np.uint8)
+    out = torch.full((ref.size,), 0xEE, dtype=torch.uint8, device="cuda")
+    cap = ref.size // 2
+    with pytest.raises(pj.PetJsonError) as ei:
+        codec.encode(d, pj.FORMAT_PRETTY, out=out[:cap])
+    assert ei.value.status == pj.PJ_ERR_CAPACITY
+    host = out.cpu().numpy()
+    assert (host[cap:] == 0xEE).all()
+    written = host[:cap] != 0xEE
+    assert (host[:cap][written] == ref[:cap][written]).all()
+    assert codec.encode_host(cols, pj.FORMAT_PRETTY) == ref.tobytes()
+
+
+def test_encode_pretty_decodes_back_on_gpu(codec):
+    """readValue of what the pretty writer produced: the array decoder gives
+    the records the compact output gives."""
+    cols = pj.generate(3, 40_000)
+    data = torch.from_numpy(np.frombuffer(gpu_encode(codec, cols, pj.FORMAT_PRETTY), np.uint8).copy()).cuda()
+    dec, el, ec, res = codec.decode(data, array=True)
+    assert res.n_errors == 0 and res.n_pets == cols.n_pets
+    dec = dec.to_host()
+    _, ref, _, _, _ = orc.decode_array(orc.encode(cols, pj.FORMAT_ARRAY))
+    for k in pj.COLS:
+        if ref[k] is not None:
+            assert np.array_equal(dec[k], ref[k]), k

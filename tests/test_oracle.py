@@ -27,7 +27,7 @@ INCL = {"NON_EMPTY": pj.INCLUDE_NON_EMPTY, "NON_NULL": pj.INCLUDE_NON_NULL, "ALW
 @pytest.mark.parametrize("case", load("encode_kat.json")["cases"], ids=lambda c: c["name"])
 def test_encode_kat(case):
     cols = to_columns([pet_from_dict(p) for p in case["pets"]])
-    fmt = pj.FORMAT_NDJSON if case.get("format") == "ndjson" else pj.FORMAT_ARRAY
+    fmt = {"ndjson": pj.FORMAT_NDJSON, "pretty": pj.FORMAT_PRETTY}.get(case.get("format"), pj.FORMAT_ARRAY)
     fields = {k: INCL[v] for k, v in case.get("fields", {}).items()}
     out = orc.encode(cols, fmt, INCL[case.get("inclusion", "NON_EMPTY")], case.get("hex_upper", True), fields)
     assert out == case["expected"].encode("utf-8")
@@ -285,3 +285,75 @@ def test_decode_grammar_differential_against_json_loads():
         else:
             assert code != pj.REC_OK, line
     assert compared > 40_000
+
+
+# --------------------------------------------------------- pretty printing
+def _strip_ws_outside_strings(b: bytes) -> bytes:
+    """The bytes of a JSON text with the whitespace between tokens removed."""
+    out, in_str, esc = bytearray(), False, False
+    for c in b:
+        if in_str:
+            out.append(c)
+            if esc:
+                esc = False
+            elif c == 0x5C:
+                esc = True
+            elif c == 0x22:
+                in_str = False
+        elif c in b" \n\r\t":
+            continue
+        else:
+            out.append(c)
+            in_str = c == 0x22
+    return bytes(out)
+
+
+def _pretty_py(v, level=0) -> str:
+    """Jackson DefaultPrettyPrinter layout of a parsed value, as a recursion
+    over the value: an object's entries on new lines at two spaces per object
+    level, arrays inline."""
+    if isinstance(v, list):
+        return "[ " + ", ".join(_pretty_py(x, level) for x in v) + " ]" if v else "[ ]"
+    if isinstance(v, dict):
+        if not v:
+            return "{ }"
+        ind = "\n" + "  " * (level + 1)
+        body = ",".join(ind + json.dumps(k) + " : " + _pretty_py(x, level + 1) for k, x in v.items())
+        return "{" + body + "\n" + "  " * level + "}"
+    return json.dumps(v, ensure_ascii=False)
+
+
+def _knock_out(cols, seed):
+    rng = np.random.default_rng(seed)
+    cols.arrays["flags"] = cols["flags"] & rng.integers(0, 64, cols.n_pets, dtype=np.uint8)
+    cols.arrays["status"][rng.random(cols.n_pets) < 0.2] = pj.STATUS_NULL
+    if cols["tag_flags"] is not None:
+        cols.arrays["tag_flags"] = rng.integers(0, 4, cols["tag_flags"].shape[0], dtype=np.uint8)
+    if cols["cat_flags"] is not None:
+        cols.arrays["cat_flags"] = rng.integers(0, 4, cols.n_pets, dtype=np.uint8)
+    return cols
+
+
+@pytest.mark.parametrize("config", [1, 3, 5])
+@pytest.mark.parametrize("incl", [pj.INCLUDE_NON_EMPTY, pj.INCLUDE_ALWAYS])
+def test_pretty_encode_differs_from_compact_only_in_layout(config, incl):
+    cols = _knock_out(generate_small(config, 2000), config)
+    # lower-case hex escapes, as json.dumps writes them
+    pretty = orc.encode(cols, pj.FORMAT_PRETTY, incl, False)
+    compact = orc.encode(cols, pj.FORMAT_ARRAY, incl, False)
+    # the same tokens, whitespace aside (escapes are written the same way)
+    assert _strip_ws_outside_strings(pretty) == compact
+    # the same value, and the layout a recursion over that value gives
+    val = json.loads(compact)
+    assert json.loads(pretty) == val
+    assert pretty.decode("utf-8") == _pretty_py(val)
+    # it reads back as the same records
+    # (records knocked out of name or photoUrls fail there in both layouts)
+    sa, a, ela, eca, ra = orc.decode_array(pretty)
+    sb, b, elb, ecb, rb = orc.decode_array(compact)
+    assert sa == sb == pj.PJ_OK
+    assert ra.n_lines == rb.n_lines == cols.n_pets and ra.n_pets == rb.n_pets
+    assert np.array_equal(ela, elb) and np.array_equal(eca, ecb)
+    for k in pj.COLS:
+        if b[k] is not None:
+            assert np.array_equal(a[k], b[k]), k

@@ -13,7 +13,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("config,fmt", [(3, pj.FORMAT_ARRAY), (3, pj.FORMAT_NDJSON), (2, pj.FORMAT_ARRAY),
-                                        (5, pj.FORMAT_NDJSON)])
+                                        (5, pj.FORMAT_NDJSON), (3, pj.FORMAT_PRETTY)])
 def test_noalloc_matches_encode_device_twice(config, fmt):
     codec = pj.Codec(0)
     try:
