@@ -277,6 +277,61 @@ pj_status pj_decode_array_host(pj_ctx *ctx, const uint8_t *in, uint64_t len,
  * smaller and retry once with that count. */
 void      pj_decode_bounds(uint64_t len, pj_pet_columns *caps_out);
 
+/* ------------------------------------------------ Order and User models
+ * The petstore's other two schemas (reference petstore.json:824-857 User,
+ * :937-971 Order), through the same ObjectMapper calls as Pet
+ * (writeValueAsBytes(List<Order>), readValue(line, Order.class), ...).
+ * Their properties are all optional and flat, so one column set describes
+ * either model: property k (schema order below) lives in col[k] and, for a
+ * string property, bytes[k].
+ *
+ *   PJ_MODEL_ORDER: 0 id int64, 1 petId int64, 2 quantity int32,
+ *     3 shipDate string (the date-time text as written; not reparsed),
+ *     4 status enum u8 (0 placed, 1 approved, 2 delivered), 5 complete bool.
+ *   PJ_MODEL_USER:  0 id int64, 1 username, 2 firstName, 3 lastName,
+ *     4 email, 5 password, 6 phone (strings), 7 userStatus int32.
+ *
+ * Encoding writes the properties in that order; under pj_options.inclusion
+ * a null property (its `present` bit clear) is skipped unless ALWAYS, and
+ * under NON_EMPTY so is an empty string.  Decoding follows the Pet rules:
+ * keys in any order, the last duplicate wins, unknown keys are validated and
+ * skipped, null means absent, an int property takes an integer token in its
+ * type's range (else PJ_REC_NUMBER), an unknown status is PJ_REC_BAD_STATUS. */
+typedef enum pj_model {
+    PJ_MODEL_ORDER = 1,
+    PJ_MODEL_USER  = 2
+} pj_model;
+#define PJ_MODEL_MAX_PROPS 8
+
+typedef struct pj_model_columns {
+    uint64_t n;                             /* records                      */
+    uint8_t *present;                       /* [n] bit k: property k is non-null;
+                                               NULL on encode: all non-null  */
+    void    *col[PJ_MODEL_MAX_PROPS];       /* int64_t[n] / int32_t[n] /
+                                               uint8_t[n] (enum code, bool 0|1) /
+                                               uint64_t[n+1] string offsets  */
+    uint8_t *bytes[PJ_MODEL_MAX_PROPS];     /* string properties' bytes      */
+    uint64_t cap_n;                         /* decode: records the columns hold */
+    uint64_t cap_bytes[PJ_MODEL_MAX_PROPS]; /* decode: bytes[k] capacity     */
+    uint64_t n_bytes[PJ_MODEL_MAX_PROPS];   /* decode output: bytes of each
+                                               string column written (or needed) */
+} pj_model_columns;
+
+/* writeValueAsBytes(List<Order|User>): format as for Pets (ARRAY, NDJSON or
+ * PRETTY).  Device pointers; capacity rules as pj_encode_device. */
+pj_status pj_encode_model_device(pj_ctx *ctx, int model, const pj_model_columns *cols, int format,
+                                 uint8_t *out, uint64_t out_cap, uint64_t *out_len);
+/* readValue of NDJSON lines (array = 0) or of one JSON array document
+ * (array = 1) of Orders or Users into columns.  Device pointers.  Valid
+ * records go to the columns in input order (out->n, out->n_bytes set); the
+ * invalid ones are listed as in pj_decode_device (res->n_pets counts the
+ * valid records).  Capacities: out->cap_n records, out->cap_bytes[k] bytes;
+ * pj_decode_model_bounds gives ones that always suffice. */
+pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_t *in, uint64_t len, int array,
+                                 pj_model_columns *out, uint64_t *err_line, uint8_t *err_code,
+                                 uint64_t err_cap, pj_decode_result *res);
+void      pj_decode_model_bounds(int model, uint64_t len, pj_model_columns *caps_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 INC = os.path.join(ROOT, "include")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-HIP_SOURCES = ["pj_api.cpp", "pj_encode.hip", "pj_decode.hip"]
+HIP_SOURCES = ["pj_api.cpp", "pj_encode.hip", "pj_decode.hip", "pj_model.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function", f"-I{INC}", f"-I{CSRC}"]

@@ -587,16 +587,13 @@ bool dec_cols_ok(const pj_pet_columns *o) {
 // NDJSON (array = false) or one array document (array = true): the line
 // stages are the same, only the index stage differs (newlines, or the
 // array's frame: its elements' starts).
-pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
-                      uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array = false) {
-    pj_status s = bind(ctx);
-    if (s) return s;
-    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
-    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
-    if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
-    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
-    std::memset(res, 0, sizeof *res);
-    ctx->n_ev = 0;
+// The record index: the start of every NDJSON line, or of every element of
+// one array document, built in ctx->index (X: its header words; 2 holds the
+// record count).  Fills P's index fields (and zeroes the rest of P); the
+// record count goes to *lines.  The array frame's verdict is checked here.
+pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, DecParams &P, uint64_t *&X,
+                      uint64_t *lines_out) {
+    pj_status s;
     const uint64_t nblk64 = (len + 63) / 64;
     uint64_t ls_cap = len / 128 + 16;
     for (int attempt = 0; attempt < 2; attempt++) {
@@ -611,8 +608,7 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         const uint64_t o_bsum = o_sidx + gidx, o_bpre = o_bsum + (ga * sizeof(FS) + 7) / 8;
         const uint64_t o_ls = o_bpre + ga;
         PJ_HIP(ctx->index.ensure((o_ls + ls_cap) * 8 + 64));
-        uint64_t *X = static_cast<uint64_t *>(ctx->index.p);
-        DecParams P;
+        X = static_cast<uint64_t *>(ctx->index.p);
         std::memset(&P, 0, sizeof P);
         P.in = in;
         P.len = len;
@@ -620,10 +616,6 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
         P.line_start = X + o_ls;
         P.ls_cap = ls_cap;
         P.n_lines = X + 2;
-        P.o = *out;
-        P.err_line = err_line;
-        P.err_code = err_code;
-        P.err_cap = err_cap;
         P.totals = X + 4;
         P.state_idx = X + o_sidx;
         P.tickets = reinterpret_cast<unsigned long long *>(X);
@@ -663,116 +655,135 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
             (void)finish_timing(ctx);
             return fail(PJ_ERR_SYNTAX, "not a JSON array: '[', the top-level commas or the closing ']' are malformed");
         }
-        const int index_order = P.order_by_id;
         const uint64_t lines = ctx->pinned[2];
         if (lines + 1 > ls_cap) {          // more lines than the first guess: grow and redo
             ls_cap = lines + 2;
             continue;
         }
-        P.lines = lines;
-        const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
-        // the line tape (256 bytes per line), when it fits a modest bound;
-        // with it the decode is split at the scan (the validating kernel
-        // stores per-line offsets, the writers follow a block scan), without
-        // it the single-pass kernel walks each line again to write it
-        P.tape = nullptr;
-        if (lines && decode_tape_enabled() && lines * 256 <= (16ull << 30) &&
-            ctx->tape.ensure(lines * 256) == hipSuccess)
-            P.tape = static_cast<uint64_t *>(ctx->tape.p);
-        (void)hipGetLastError();
-        const bool split = P.tape != nullptr;
-        // scan buffer: vector look-back words (single pass) or block totals,
-        // bases and scan look-back words (split), then the deferred
-        // error-code queue, then (split) the wave-line list, the per-line
-        // offsets (9 u32 per line), the count and list of blocks handed to
-        // the bitmap pass
-        const uint64_t nsb = (gp + pj_dec_bscan_block() - 1) / pj_dec_bscan_block();
-        const uint64_t w_state = split ? 2 * gp * VLB_WORDS + nsb * VLB_WORDS : gp * VLB_WORDS;
-        const uint64_t w_lpos = (9 * lines + 1) / 2;
-        const uint64_t w_split = split ? lines + w_lpos + 2 + gp : 0;
-        PJ_HIP(ctx->scan.ensure((w_state + lines + 8 + w_split) * 8));
-        uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
-        P.state_parse = SB;
-        P.bagg = SB;
-        P.bbase = SB + gp * VLB_WORDS;
-        P.bstate = SB + 2 * gp * VLB_WORDS;
-        P.nblocks = gp;
-        P.dq = SB + w_state;
-        P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
-        P.long_count = reinterpret_cast<unsigned long long *>(X + 14);
-        P.bticket = reinterpret_cast<unsigned long long *>(X + 15);
-        P.long_list = P.dq + lines + 8;
-        P.lpos = reinterpret_cast<uint32_t *>(P.long_list + lines);
-        P.bm_count = reinterpret_cast<unsigned long long *>(P.long_list + lines + w_lpos);
-        P.bm_list = P.long_list + lines + w_lpos + 2;
-        P.order_by_id = 1;
-        for (;;) {
-            if ((s = mark(ctx))) return s;
-            if (split) {
-                PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
-                PJ_HIP(pj_launch_fill_u64(reinterpret_cast<uint64_t *>(P.bm_count), 2, 0, ctx->stream));
-            }
-            else PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
-            PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
-            PJ_HIP(pj_launch_fill_u64(X + 3, 13, 0, ctx->stream));     // totals and counters
-            if ((s = mark(ctx))) return s;
-            if (lines) {
-                PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
-                if (split) {
-                    if ((s = mark(ctx))) return s;
-                    PJ_HIP(pj_launch_dec_bscan(P, ctx->stream));
-                    if ((s = mark(ctx))) return s;
-                    PJ_HIP(pj_launch_dec_write(P, ctx->stream));
-                    if ((s = mark(ctx))) return s;
-                    PJ_HIP(pj_launch_dec_long(P, ctx->stream));
-                }
-                if ((s = mark(ctx))) return s;
-                PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
-            } else {
-                // no lines: the offset arrays still start with 0
-                uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
-                                      out->tag_name_off};
-                for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
-            }
-            if ((s = mark(ctx))) return s;
-            PJ_HIP(hipMemcpyAsync(ctx->pinned, X, 13 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
-            PJ_HIP(hipStreamSynchronize(ctx->stream));
-            if (!P.order_by_id || ctx->pinned[1] == 0) break;
-            P.order_by_id = 0;
-            ctx->n_ev = 0;
-        }
-        (void)index_order;
-        if ((s = finish_timing(ctx))) return s;
-        const uint64_t *T = ctx->pinned + 4;
-        res->n_general = lines ? ctx->pinned[12] : 0;
-        res->n_lines = lines;
-        if (array && lines && ctx->pinned[3]) {
-            // a blank element: "[ ]" holds none, any other is a broken frame
-            if (lines > 1) return fail(PJ_ERR_SYNTAX, "an element of the array is empty");
-            std::memset(res, 0, sizeof *res);
-            out->n_pets = 0;
-            return PJ_OK;
-        }
-        if (lines) {
-            res->n_pets = T[C_PETS];
-            res->name_bytes = T[C_NAMEB];
-            res->cat_name_bytes = T[C_CATB];
-            res->n_urls = T[C_URLS];
-            res->url_bytes = T[C_URLB];
-            res->n_tags = T[C_TAGS];
-            res->tag_name_bytes = T[C_TAGB];
-            res->n_errors = T[C_ERRS];
-        }
-        out->n_pets = std::min(res->n_pets, out->cap_pets);
-        if (res->n_errors > err_cap) return fail(PJ_ERR_CAPACITY, "error list capacity too small");
-        if (res->n_pets > out->cap_pets || res->name_bytes > out->cap_name_bytes ||
-            res->cat_name_bytes > out->cap_cat_name_bytes || res->n_urls > out->cap_urls ||
-            res->url_bytes > out->cap_url_bytes || res->n_tags > out->cap_tags ||
-            res->tag_name_bytes > out->cap_tag_name_bytes)
-            return fail(PJ_ERR_CAPACITY, "column capacity too small (sizes needed are in the result)");
+        *lines_out = lines;
         return PJ_OK;
     }
     return fail(PJ_ERR_DEVICE, "line index did not converge");
+}
+
+pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                      uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array = false) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
+    if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
+    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    std::memset(res, 0, sizeof *res);
+    ctx->n_ev = 0;
+    DecParams P;
+    uint64_t *X = nullptr, lines = 0;
+    if ((s = index_stage(ctx, in, len, array, P, X, &lines))) return s;
+    P.o = *out;
+    P.err_line = err_line;
+    P.err_code = err_code;
+    P.err_cap = err_cap;
+    P.lines = lines;
+    const uint64_t gp = (lines + pj_dec_parse_block() - 1) / pj_dec_parse_block();
+    // the line tape (256 bytes per line), when it fits a modest bound;
+    // with it the decode is split at the scan (the validating kernel
+    // stores per-line offsets, the writers follow a block scan), without
+    // it the single-pass kernel walks each line again to write it
+    P.tape = nullptr;
+    if (lines && decode_tape_enabled() && lines * 256 <= (16ull << 30) &&
+        ctx->tape.ensure(lines * 256) == hipSuccess)
+        P.tape = static_cast<uint64_t *>(ctx->tape.p);
+    (void)hipGetLastError();
+    const bool split = P.tape != nullptr;
+    // scan buffer: vector look-back words (single pass) or block totals,
+    // bases and scan look-back words (split), then the deferred
+    // error-code queue, then (split) the wave-line list, the per-line
+    // offsets (9 u32 per line), the count and list of blocks handed to
+    // the bitmap pass
+    const uint64_t nsb = (gp + pj_dec_bscan_block() - 1) / pj_dec_bscan_block();
+    const uint64_t w_state = split ? 2 * gp * VLB_WORDS + nsb * VLB_WORDS : gp * VLB_WORDS;
+    const uint64_t w_lpos = (9 * lines + 1) / 2;
+    const uint64_t w_split = split ? lines + w_lpos + 2 + gp : 0;
+    PJ_HIP(ctx->scan.ensure((w_state + lines + 8 + w_split) * 8));
+    uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
+    P.state_parse = SB;
+    P.bagg = SB;
+    P.bbase = SB + gp * VLB_WORDS;
+    P.bstate = SB + 2 * gp * VLB_WORDS;
+    P.nblocks = gp;
+    P.dq = SB + w_state;
+    P.dq_count = reinterpret_cast<unsigned long long *>(X + 13);
+    P.long_count = reinterpret_cast<unsigned long long *>(X + 14);
+    P.bticket = reinterpret_cast<unsigned long long *>(X + 15);
+    P.long_list = P.dq + lines + 8;
+    P.lpos = reinterpret_cast<uint32_t *>(P.long_list + lines);
+    P.bm_count = reinterpret_cast<unsigned long long *>(P.long_list + lines + w_lpos);
+    P.bm_list = P.long_list + lines + w_lpos + 2;
+    P.order_by_id = 1;
+    for (;;) {
+        if ((s = mark(ctx))) return s;
+        if (split) {
+            PJ_HIP(pj_launch_fill_u64(P.bstate, nsb * VLB_WORDS, 0, ctx->stream));
+            PJ_HIP(pj_launch_fill_u64(reinterpret_cast<uint64_t *>(P.bm_count), 2, 0, ctx->stream));
+        }
+        else PJ_HIP(pj_launch_fill_u64(P.state_parse, gp * VLB_WORDS, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(X + 1, 1, 0, ctx->stream));      // the parse ticket / give-up word
+        PJ_HIP(pj_launch_fill_u64(X + 3, 13, 0, ctx->stream));     // totals and counters
+        if ((s = mark(ctx))) return s;
+        if (lines) {
+            PJ_HIP(pj_launch_dec_parse(P, ctx->stream));
+            if (split) {
+                if ((s = mark(ctx))) return s;
+                PJ_HIP(pj_launch_dec_bscan(P, ctx->stream));
+                if ((s = mark(ctx))) return s;
+                PJ_HIP(pj_launch_dec_write(P, ctx->stream));
+                if ((s = mark(ctx))) return s;
+                PJ_HIP(pj_launch_dec_long(P, ctx->stream));
+            }
+            if ((s = mark(ctx))) return s;
+            PJ_HIP(pj_launch_dec_errcode(P, ctx->stream));
+        } else {
+            // no lines: the offset arrays still start with 0
+            uint64_t *heads[6] = {out->name_off, out->cat_name_off, out->photo_off, out->tag_off, out->url_off,
+                                  out->tag_name_off};
+            for (uint64_t *h : heads) PJ_HIP(pj_launch_fill_u64(h, 1, 0, ctx->stream));
+        }
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, X, 13 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if (!P.order_by_id || ctx->pinned[1] == 0) break;
+        P.order_by_id = 0;
+        ctx->n_ev = 0;
+    }
+    if ((s = finish_timing(ctx))) return s;
+    const uint64_t *T = ctx->pinned + 4;
+    res->n_general = lines ? ctx->pinned[12] : 0;
+    res->n_lines = lines;
+    if (array && lines && ctx->pinned[3]) {
+        // a blank element: "[ ]" holds none, any other is a broken frame
+        if (lines > 1) return fail(PJ_ERR_SYNTAX, "an element of the array is empty");
+        std::memset(res, 0, sizeof *res);
+        out->n_pets = 0;
+        return PJ_OK;
+    }
+    if (lines) {
+        res->n_pets = T[C_PETS];
+        res->name_bytes = T[C_NAMEB];
+        res->cat_name_bytes = T[C_CATB];
+        res->n_urls = T[C_URLS];
+        res->url_bytes = T[C_URLB];
+        res->n_tags = T[C_TAGS];
+        res->tag_name_bytes = T[C_TAGB];
+        res->n_errors = T[C_ERRS];
+    }
+    out->n_pets = std::min(res->n_pets, out->cap_pets);
+    if (res->n_errors > err_cap) return fail(PJ_ERR_CAPACITY, "error list capacity too small");
+    if (res->n_pets > out->cap_pets || res->name_bytes > out->cap_name_bytes ||
+        res->cat_name_bytes > out->cap_cat_name_bytes || res->n_urls > out->cap_urls ||
+        res->url_bytes > out->cap_url_bytes || res->n_tags > out->cap_tags ||
+        res->tag_name_bytes > out->cap_tag_name_bytes)
+        return fail(PJ_ERR_CAPACITY, "column capacity too small (sizes needed are in the result)");
+    return PJ_OK;
 }
 
 }  // namespace
@@ -1005,3 +1016,142 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
     return s;
 }
 }  // namespace
+
+// ------------------------------------------------------ Order and User models
+namespace {
+bool model_ok(int m) { return m == PJ_MODEL_ORDER || m == PJ_MODEL_USER; }
+int model_props(int m) { return m == PJ_MODEL_ORDER ? 6 : 8; }
+bool model_str(int m, int k) { return m == PJ_MODEL_ORDER ? k == 3 : (k >= 1 && k <= 6); }
+
+pj_status check_model_cols(int model, const pj_model_columns *c, bool decode) {
+    for (int k = 0; k < model_props(model); k++) {
+        if (!c->col[k]) return fail(PJ_ERR_INVALID_ARG, "model column " + std::to_string(k) + " missing");
+        if (model_str(model, k) && !c->bytes[k])
+            return fail(PJ_ERR_INVALID_ARG, "model string column " + std::to_string(k) + " has no bytes");
+    }
+    if (decode && !c->present) return fail(PJ_ERR_INVALID_ARG, "decode needs the present column");
+    return PJ_OK;
+}
+}  // namespace
+
+extern "C" pj_status pj_encode_model_device(pj_ctx *ctx, int model, const pj_model_columns *cols, int format,
+                                            uint8_t *out, uint64_t out_cap, uint64_t *out_len) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (!model_ok(model)) return fail(PJ_ERR_INVALID_ARG, "unknown model");
+    if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    if (out_cap > 0 && !out) return fail(PJ_ERR_INVALID_ARG, "null output with capacity");
+    const uint64_t n = cols->n;
+    if (n && (s = check_model_cols(model, cols, false))) return s;
+    ctx->n_ev = 0;
+    if (n == 0) {
+        const uint64_t len = format == PJ_FORMAT_ARRAY ? 2 : format == PJ_FORMAT_PRETTY ? 3 : 0;
+        *out_len = len;
+        if (len && len <= out_cap) {
+            const uint32_t w = format == PJ_FORMAT_ARRAY ? '[' | (']' << 8) : '[' | (' ' << 8) | (']' << 16);
+            PJ_HIP(pj_launch_put_bytes(out, w, (int)len, ctx->stream));
+        }
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        return len > out_cap ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
+    }
+    const uint64_t bt = (uint64_t)pj_encode_model_records(), nblk = (n + bt - 1) / bt;
+    PJ_HIP(ctx->scan.ensure((nblk + 2) * sizeof(uint64_t)));
+    uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p);
+    ModelEncParams P;
+    std::memset(&P, 0, sizeof P);
+    P.c = *cols;
+    P.n = n;
+    P.model = model;
+    P.format = format;
+    P.incl = (uint32_t)ctx->opt.inclusion;
+    P.hexa = ctx->opt.hex_upper ? 'A' : 'a';
+    P.out = out;
+    P.cap = out_cap;
+    P.ticket = reinterpret_cast<unsigned long long *>(sc);
+    P.total = sc + 1;
+    P.state = sc + 2;
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_fill_u64(sc, nblk + 2, 0, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_encode_model(P, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(hipMemcpyAsync(ctx->pinned, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if ((s = finish_timing(ctx))) return s;
+    *out_len = ctx->pinned[0];
+    if (*out_len > out_cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    return PJ_OK;
+}
+
+extern "C" pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_t *in, uint64_t len, int array,
+                                            pj_model_columns *out, uint64_t *err_line, uint8_t *err_code,
+                                            uint64_t err_cap, pj_decode_result *res) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (!model_ok(model)) return fail(PJ_ERR_INVALID_ARG, "unknown model");
+    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
+    if ((s = check_model_cols(model, out, true))) return s;
+    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    std::memset(res, 0, sizeof *res);
+    ctx->n_ev = 0;
+    DecParams P;
+    uint64_t *X = nullptr, lines = 0;
+    if ((s = index_stage(ctx, in, len, array != 0, P, X, &lines))) return s;
+    const uint64_t nb = (lines + pj_decode_model_block() - 1) / pj_decode_model_block();
+    PJ_HIP(ctx->scan.ensure((2 * nb * MD_MAXK + MD_MAXK + 1) * sizeof(uint64_t)));
+    uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
+    ModelDecParams M;
+    std::memset(&M, 0, sizeof M);
+    M.in = in;
+    M.line_start = P.line_start;
+    M.lines = lines;
+    M.o = *out;
+    M.err_line = err_line;
+    M.err_code = err_code;
+    M.err_cap = err_cap;
+    M.totals = SB;
+    M.bagg = SB + MD_MAXK + 1;
+    M.bbase = M.bagg + nb * MD_MAXK;
+    M.nblocks = nb;
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_fill_u64(SB, MD_MAXK + 1, 0, ctx->stream));
+    for (int k = 0; k < model_props(model); k++)    // string offsets start at 0
+        if (model_str(model, k)) PJ_HIP(pj_launch_fill_u64(static_cast<uint64_t *>(out->col[k]), 1, 0, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(pj_launch_decode_model(M, model, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(hipMemcpyAsync(ctx->pinned, SB, (MD_MAXK + 1) * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if ((s = finish_timing(ctx))) return s;
+    const uint64_t *T = ctx->pinned;
+    for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) out->n_bytes[k] = 0;
+    if (array && lines && T[MD_MAXK]) {
+        // a blank element: "[ ]" holds none, any other is a broken frame
+        if (lines > 1) return fail(PJ_ERR_SYNTAX, "an element of the array is empty");
+        out->n = 0;
+        return PJ_OK;
+    }
+    res->n_lines = lines;
+    res->n_pets = T[0];
+    res->n_errors = T[1];
+    out->n = std::min(T[0], out->cap_n);
+    bool over = T[0] > out->cap_n;
+    for (int k = 0; k < model_props(model); k++)
+        if (model_str(model, k)) {
+            out->n_bytes[k] = T[2 + k];
+            over = over || T[2 + k] > out->cap_bytes[k];
+        }
+    if (res->n_errors > err_cap) return fail(PJ_ERR_CAPACITY, "error list capacity too small");
+    if (over) return fail(PJ_ERR_CAPACITY, "column capacity too small (sizes needed are in the result)");
+    return PJ_OK;
+}
+
+extern "C" void pj_decode_model_bounds(int model, uint64_t len, pj_model_columns *c) {
+    if (!c) return;
+    // a record needs at least "{}" and a separator
+    c->cap_n = len / 3 + 1;
+    for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++)
+        c->cap_bytes[k] = model_ok(model) && k < model_props(model) && model_str(model, k) ? len : 0;
+}

@@ -1374,6 +1374,151 @@ __global__ __launch_bounds__(BT) void k_encode_pretty(EncParams P) {
     xs.finish();
 }
 
+// ------------------------------------------------- Order and User records
+// Properties in schema order (reference petstore.json:937-971 Order,
+// :824-857 User); a null one is skipped unless ALWAYS, an empty string too
+// under NON_EMPTY.  Compact or pretty (the Pet layout rules at level 1).
+
+// The key of a property, with its separator and indentation.
+template <int N, class S>
+__device__ __forceinline__ void m_key(S &s, bool &first, bool pretty, const char (&name)[N]) {
+    if (!first) s.put_byte(',');
+    first = false;
+    if (pretty) lit(s, "\n  ");
+    s.put_byte('"');
+    lit(s, name);
+    if (pretty) lit(s, "\" : ");
+    else lit(s, "\":");
+}
+
+// Property k of record i: present (bit k of present) or written as null.
+__device__ __forceinline__ bool m_present(const ModelEncParams &P, uint64_t i, int k) {
+    return P.c.present ? ((P.c.present[i] >> k) & 1u) != 0 : true;
+}
+
+template <int N, class S>
+__device__ __forceinline__ void m_null(S &s, const ModelEncParams &P, bool &first, bool pretty, const char (&name)[N]) {
+    if (P.incl != PJ_INCLUDE_ALWAYS) return;
+    m_key(s, first, pretty, name);
+    lit(s, "null");
+}
+
+template <int N, class S>
+__device__ __forceinline__ void m_i64(S &s, const ModelEncParams &P, uint64_t i, int k, bool &first, bool pretty,
+                                      const char (&name)[N]) {
+    if (!m_present(P, i, k)) return m_null(s, P, first, pretty, name);
+    m_key(s, first, pretty, name);
+    emit_long(s, static_cast<const int64_t *>(P.c.col[k])[i]);
+}
+
+template <int N, class S>
+__device__ __forceinline__ void m_i32(S &s, const ModelEncParams &P, uint64_t i, int k, bool &first, bool pretty,
+                                      const char (&name)[N]) {
+    if (!m_present(P, i, k)) return m_null(s, P, first, pretty, name);
+    m_key(s, first, pretty, name);
+    emit_long(s, (int64_t) static_cast<const int32_t *>(P.c.col[k])[i]);
+}
+
+template <int N, class S>
+__device__ __forceinline__ void m_str(S &s, const ModelEncParams &P, uint64_t i, int k, bool &first, bool pretty,
+                                      const char (&name)[N]) {
+    if (!m_present(P, i, k)) return m_null(s, P, first, pretty, name);
+    const uint64_t *off = static_cast<const uint64_t *>(P.c.col[k]);
+    const uint64_t a = off[i], b = off[i + 1];
+    if (a == b && P.incl == PJ_INCLUDE_NON_EMPTY) return;
+    m_key(s, first, pretty, name);
+    emit_str(s, P.c.bytes[k] + a, b - a, P.hexa);
+}
+
+template <int N, class S>
+__device__ __forceinline__ void m_bool(S &s, const ModelEncParams &P, uint64_t i, int k, bool &first, bool pretty,
+                                       const char (&name)[N]) {
+    if (!m_present(P, i, k)) return m_null(s, P, first, pretty, name);
+    m_key(s, first, pretty, name);
+    if (static_cast<const uint8_t *>(P.c.col[k])[i]) lit(s, "true");
+    else lit(s, "false");
+}
+
+// Order.status: codes past the enum are null.
+template <class S>
+__device__ __forceinline__ void m_order_status(S &s, const ModelEncParams &P, uint64_t i, bool &first, bool pretty) {
+    const uint32_t v = static_cast<const uint8_t *>(P.c.col[4])[i];
+    if (!m_present(P, i, 4) || v > 2) return m_null(s, P, first, pretty, "status");
+    m_key(s, first, pretty, "status");
+    if (v == 0) lit(s, "\"placed\"");
+    else if (v == 1) lit(s, "\"approved\"");
+    else lit(s, "\"delivered\"");
+}
+
+template <int MODEL, class S> __device__ __forceinline__ void m_rec(S &s, const ModelEncParams &P, uint64_t i) {
+    const bool pretty = P.format == PJ_FORMAT_PRETTY, array = P.format != PJ_FORMAT_NDJSON;
+    if (array) {
+        s.put_byte(i == 0 ? '[' : ',');
+        if (pretty) s.put_byte(' ');
+    }
+    bool first = true;
+    s.put_byte('{');
+    if (MODEL == PJ_MODEL_ORDER) {
+        m_i64(s, P, i, 0, first, pretty, "id");
+        m_i64(s, P, i, 1, first, pretty, "petId");
+        m_i32(s, P, i, 2, first, pretty, "quantity");
+        m_str(s, P, i, 3, first, pretty, "shipDate");
+        m_order_status(s, P, i, first, pretty);
+        m_bool(s, P, i, 5, first, pretty, "complete");
+    } else {
+        m_i64(s, P, i, 0, first, pretty, "id");
+        m_str(s, P, i, 1, first, pretty, "username");
+        m_str(s, P, i, 2, first, pretty, "firstName");
+        m_str(s, P, i, 3, first, pretty, "lastName");
+        m_str(s, P, i, 4, first, pretty, "email");
+        m_str(s, P, i, 5, first, pretty, "password");
+        m_str(s, P, i, 6, first, pretty, "phone");
+        m_i32(s, P, i, 7, first, pretty, "userStatus");
+    }
+    if (pretty) {
+        if (first) s.put_byte(' ');
+        else s.put_byte('\n');
+    }
+    s.put_byte('}');
+    if (!array) s.put_byte('\n');
+    else if (i == P.n - 1) {
+        if (pretty) s.put_byte(' ');
+        s.put_byte(']');
+    }
+}
+
+// One thread per record in blocks of BT claimed by ticket: measure, block
+// scan, look-back, then each thread writes its record with exact stores.
+template <int MODEL, int BT>
+__global__ __launch_bounds__(BT) void k_encode_model(ModelEncParams P) {
+    __shared__ uint64_t sh_scan[BT / 64 + 2];
+    __shared__ uint64_t sh_b, sh_base;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) sh_b = atomicAdd(P.ticket, 1ull);
+    __syncthreads();
+    const uint64_t b = sh_b, nblk = (P.n + BT - 1) / BT;
+    const uint64_t i = b * BT + t;
+    const bool live = i < P.n;
+    CountSink cs;
+    if (live) m_rec<MODEL>(cs, P, i);
+    uint64_t agg;
+    const uint64_t pre = block_excl_scan<BT>(cs.n, sh_scan, &agg);
+    if (t < 64) {
+        const uint64_t excl = lookback(P.state, b, agg);
+        if (t == 0) {
+            sh_base = excl;
+            if (b == nblk - 1) *P.total = excl + agg;
+        }
+    }
+    __syncthreads();
+    if (P.count_only || !live) return;
+    const uint64_t at = sh_base + pre;
+    if (at + cs.n > P.cap) return;
+    XSink xs{P.out + at, 0, 0};
+    m_rec<MODEL>(xs, P, i);
+    xs.finish();
+}
+
 __global__ void k_add_u64(uint64_t *p, uint64_t n, uint64_t v) {
     uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] += v;
@@ -1493,6 +1638,20 @@ int pj_encode_pretty_records() { return ENC_PRETTY_BT; }
 hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st) {
     const uint64_t nblk = (P.n + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
     hipLaunchKernelGGL(pj::k_encode_pretty<ENC_PRETTY_BT>, dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P);
+    return hipGetLastError();
+}
+
+constexpr int ENC_MODEL_BT = 256;
+int pj_encode_model_records() { return ENC_MODEL_BT; }
+
+hipError_t pj_launch_encode_model(const ModelEncParams &P, hipStream_t st) {
+    const uint64_t nblk = (P.n + ENC_MODEL_BT - 1) / ENC_MODEL_BT;
+    if (P.model == PJ_MODEL_ORDER)
+        hipLaunchKernelGGL((pj::k_encode_model<PJ_MODEL_ORDER, ENC_MODEL_BT>), dim3((unsigned)nblk), dim3(ENC_MODEL_BT),
+                           0, st, P);
+    else
+        hipLaunchKernelGGL((pj::k_encode_model<PJ_MODEL_USER, ENC_MODEL_BT>), dim3((unsigned)nblk), dim3(ENC_MODEL_BT),
+                           0, st, P);
     return hipGetLastError();
 }
 

@@ -23,6 +23,40 @@ struct EncParams {
     unsigned long long *nfall; // blocks whose records did not fit the LDS tile (counted)
 };
 
+// Order / User encode (pj_encode_model_device): one thread per record,
+// blocks claimed by ticket, decoupled look-back.
+struct ModelEncParams {
+    pj_model_columns c;        // device column pointers
+    uint64_t n;                // records
+    int model;                 // pj_model
+    int format;                // pj_format
+    uint32_t incl;             // pj_inclusion (mapper-wide)
+    uint32_t hexa;             // 'A' or 'a'
+    int count_only;
+    uint8_t *out;
+    uint64_t cap;
+    uint64_t *state;           // look-back words, one per block (zeroed)
+    unsigned long long *ticket;// block ticket (zeroed)
+    uint64_t *total;           // encoded size (written by the last block)
+};
+
+// Order / User decode (pj_decode_model_device), after the record index:
+// a counting pass (block totals), a scan of them, a writing pass.
+constexpr int MD_MAXK = 2 + PJ_MODEL_MAX_PROPS;   // valid, errors, one per string property
+struct ModelDecParams {
+    const uint8_t *in;
+    const uint64_t *line_start;// record l spans [line_start[l], line_start[l+1] - 1)
+    uint64_t lines;
+    pj_model_columns o;        // outputs with capacities
+    uint64_t *err_line;
+    uint8_t *err_code;
+    uint64_t err_cap;
+    uint64_t *bagg;            // [nblocks * MD_MAXK] block totals
+    uint64_t *bbase;           // [nblocks * MD_MAXK] block first offsets
+    uint64_t *totals;          // [MD_MAXK + 1] sums (the last: blank records)
+    uint64_t nblocks;
+};
+
 // What the decode counting kernels learn about each line, read back by the
 // writers (32 bytes per line).
 struct LineRec {
@@ -104,6 +138,10 @@ hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 int pj_encode_block_records(bool nested);
 hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st);
+hipError_t pj_launch_encode_model(const ModelEncParams &P, hipStream_t st);
+int pj_encode_model_records();
+hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_t st);
+int pj_decode_model_block();
 int pj_encode_pretty_records();
 hipError_t pj_launch_put_bytes(uint8_t *out, uint32_t w, int k, hipStream_t st);
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st);

@@ -84,6 +84,27 @@ class PetJsonError(RuntimeError):
 
 
 # -------------------------------------------------------------------- loader
+# ------------------------------------------------ Order and User models
+MODEL_ORDER, MODEL_USER = 1, 2
+MODEL_MAX_PROPS = 8
+# property name and kind, in schema order (petstore.json:937-971 Order,
+# :824-857 User)
+MODEL_PROPS = {
+    MODEL_ORDER: (("id", "i64"), ("petId", "i64"), ("quantity", "i32"), ("shipDate", "str"), ("status", "enum"),
+                  ("complete", "bool")),
+    MODEL_USER: (("id", "i64"), ("username", "str"), ("firstName", "str"), ("lastName", "str"), ("email", "str"),
+                 ("password", "str"), ("phone", "str"), ("userStatus", "i32")),
+}
+ORDER_STATUS = ("placed", "approved", "delivered")
+KIND_DTYPE = {"i64": np.int64, "i32": np.int32, "enum": np.uint8, "bool": np.uint8, "str": np.uint64}
+
+
+class ModelColumnsStruct(C.Structure):
+    _fields_ = [("n", C.c_uint64), ("present", C.c_void_p), ("col", C.c_void_p * MODEL_MAX_PROPS),
+                ("bytes", C.c_void_p * MODEL_MAX_PROPS), ("cap_n", C.c_uint64),
+                ("cap_bytes", C.c_uint64 * MODEL_MAX_PROPS), ("n_bytes", C.c_uint64 * MODEL_MAX_PROPS)]
+
+
 _LIB = None
 _GEN = None
 
@@ -141,6 +162,12 @@ def load_lib():
                                       C.POINTER(DecodeResult)]
             getattr(L, f).restype = i32
         L.pj_decode_bounds.argtypes = [u64, C.POINTER(PetColumnsStruct)]
+        L.pj_encode_model_device.argtypes = [vp, i32, C.POINTER(ModelColumnsStruct), i32, vp, u64, C.POINTER(u64)]
+        L.pj_encode_model_device.restype = i32
+        L.pj_decode_model_device.argtypes = [vp, i32, vp, u64, i32, C.POINTER(ModelColumnsStruct), vp, vp, u64,
+                                             C.POINTER(DecodeResult)]
+        L.pj_decode_model_device.restype = i32
+        L.pj_decode_model_bounds.argtypes = [i32, u64, C.POINTER(ModelColumnsStruct)]
         _LIB = L
     return _LIB
 
@@ -514,3 +541,198 @@ class Codec:
         self._check(rc)
         t = self._trim(cols, res).to_host()
         return t, el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res
+
+
+# ------------------------------------------------------ Order / User columns
+@dataclass
+class ModelColumns:
+    """SoA columns of Order or User records (numpy on the host or torch
+    tensors on a GPU): per property k, col[k] holds the values (string
+    properties: n + 1 offsets into bytes[k]); bit k of present[i] marks
+    property k of record i non-null (present None: all non-null)."""
+    model: int
+    n: int
+    present: object = None
+    col: list = field(default_factory=list)
+    bytes: list = field(default_factory=list)
+    cap_n: int = 0
+    cap_bytes: list = field(default_factory=lambda: [0] * MODEL_MAX_PROPS)
+    n_bytes: list = field(default_factory=lambda: [0] * MODEL_MAX_PROPS)
+
+    @property
+    def props(self):
+        return MODEL_PROPS[self.model]
+
+    def struct(self) -> ModelColumnsStruct:
+        s = ModelColumnsStruct()
+        s.n = self.n
+        s.present = _ptr(self.present)
+        for k in range(len(self.props)):
+            s.col[k] = _ptr(self.col[k])
+            s.bytes[k] = _ptr(self.bytes[k]) if k < len(self.bytes) else None
+        s.cap_n = self.cap_n
+        for k in range(MODEL_MAX_PROPS):
+            s.cap_bytes[k] = int(self.cap_bytes[k])
+        return s
+
+    def to_device(self, device="cuda"):
+        import torch
+
+        def up(v):
+            if v is None:
+                return None
+            v = np.ascontiguousarray(v)
+            buf = torch.empty(v.shape[0] + max(1, 8 // v.itemsize), dtype=torch.from_numpy(v[:0]).dtype,
+                              device=device)
+            if v.shape[0]:
+                buf[: v.shape[0]].copy_(torch.from_numpy(v))
+            return buf
+
+        return ModelColumns(self.model, self.n, up(self.present), [up(c) for c in self.col],
+                            [up(b) for b in self.bytes], self.cap_n, list(self.cap_bytes), list(self.n_bytes))
+
+    def to_host(self):
+        """numpy copies trimmed to the record count and string sizes."""
+        def dn(v, count):
+            if v is None:
+                return None
+            v = v if isinstance(v, np.ndarray) else v.cpu().numpy()
+            return v[:count].copy()
+        col, byt = [], []
+        for k, (_, kind) in enumerate(self.props):
+            c = dn(self.col[k], self.n + 1 if kind == "str" else self.n)
+            col.append(c)
+            byt.append(dn(self.bytes[k], int(c[self.n])) if kind == "str" and self.bytes[k] is not None else None)
+        return ModelColumns(self.model, self.n, dn(self.present, self.n), col, byt)
+
+
+def _rand_text(rng, n, lo, hi, fancy):
+    """Offsets and bytes of n strings of lo..hi bytes: ASCII word bytes,
+    and (fancy) one record in 20 with escapes and multi-byte UTF-8."""
+    pool = np.frombuffer(b"abz09-_.@ ", np.uint8)
+    lens = rng.integers(lo, hi + 1, n).astype(np.int64)
+    odd = [b'"', b"\\", b"\n", b"\x01", b"\x1f", b"\xc3\xa9", b"\xe2\x82\xac", b"\xf0\x9f\x98\x80", b"/"]
+    special = {}
+    if fancy:
+        for i in np.nonzero(rng.random(n) < 0.05)[0]:
+            b = bytearray()
+            while len(b) < lens[i]:
+                b += odd[int(rng.integers(len(odd)))] if rng.random() < 0.3 else bytes([pool[int(rng.integers(10))]])
+            special[int(i)] = bytes(b)
+            lens[i] = len(b)
+    off = np.zeros(n + 1, np.uint64)
+    off[1:] = np.cumsum(lens, dtype=np.uint64)
+    data = pool[rng.integers(0, pool.size, int(off[-1]))]
+    for i, b in special.items():
+        data[int(off[i]): int(off[i + 1])] = np.frombuffer(b, np.uint8)
+    return off, data
+
+
+def generate_model(model: int, n: int, seed: int = 0, null_rate: float = 0.1, fancy: bool = True) -> ModelColumns:
+    """Seeded random Order or User records (host columns): extreme and
+    ordinary integers, every enum value, strings with escapes and UTF-8,
+    nulls and empty strings."""
+    rng = np.random.default_rng(seed)
+    props = MODEL_PROPS[model]
+    present = np.zeros(n, np.uint8)
+    col, byt = [], []
+    for k, (name, kind) in enumerate(props):
+        present |= ((rng.random(n) >= null_rate).astype(np.uint8) << k)
+        if kind == "i64":
+            v = rng.integers(-2**63, 2**63 - 1, n, dtype=np.int64, endpoint=True)
+            small = rng.random(n) < 0.5
+            v[small] = rng.integers(-1000, 10**6, int(small.sum()))
+            v[:4] = [0, -1, -2**63, 2**63 - 1][: min(4, n)]
+            col.append(v); byt.append(None)
+        elif kind == "i32":
+            v = rng.integers(-2**31, 2**31 - 1, n, dtype=np.int64, endpoint=True).astype(np.int32)
+            small = rng.random(n) < 0.5
+            v[small] = rng.integers(0, 100, int(small.sum()))
+            v[:3] = [-2**31, 2**31 - 1, 0][: min(3, n)]
+            col.append(v); byt.append(None)
+        elif kind in ("enum", "bool"):
+            col.append(rng.integers(0, 3 if kind == "enum" else 2, n).astype(np.uint8)); byt.append(None)
+        else:
+            if name == "shipDate":
+                y = rng.integers(1970, 2100, n); mo = rng.integers(1, 13, n); d = rng.integers(1, 29, n)
+                hh = rng.integers(0, 24, n); mm = rng.integers(0, 60, n); ms = rng.integers(0, 1000, n)
+                empty = rng.random(n) < 0.05
+                strs = [b"" if empty[i] else
+                        b"%04d-%02d-%02dT%02d:%02d:%02d.%03dZ" % (y[i], mo[i], d[i], hh[i], mm[i], mm[i], ms[i])
+                        for i in range(n)]
+                off = np.zeros(n + 1, np.uint64)
+                off[1:] = np.cumsum([len(x) for x in strs], dtype=np.uint64)
+                data = np.frombuffer(b"".join(strs), np.uint8).copy() if off[-1] else np.zeros(0, np.uint8)
+            else:
+                off, data = _rand_text(rng, n, 0, 24, fancy)
+            col.append(off)
+            byt.append(data)
+    return ModelColumns(model, n, present, col, byt)
+
+
+def decode_model_bounds(model: int, length: int):
+    """(cap_n, cap_bytes) that always suffice for `length` input bytes."""
+    L = load_lib()
+    s = ModelColumnsStruct()
+    L.pj_decode_model_bounds(model, length, C.byref(s))
+    return int(s.cap_n), [int(s.cap_bytes[k]) for k in range(MODEL_MAX_PROPS)]
+
+
+def alloc_model_columns(model: int, cap_n: int, cap_bytes, device=None) -> ModelColumns:
+    """Empty decode outputs (numpy, or torch on `device`)."""
+    def mk(count, dt):
+        if device is None:
+            return np.zeros(count, dt)
+        import torch
+        return torch.zeros(count, dtype=torch.from_numpy(np.zeros(0, dt)).dtype, device=device)
+    col, byt = [], []
+    for k, (_, kind) in enumerate(MODEL_PROPS[model]):
+        col.append(mk(cap_n + 1 if kind == "str" else max(cap_n, 1), KIND_DTYPE[kind]))
+        byt.append(mk(max(int(cap_bytes[k]), 1), np.uint8) if kind == "str" else None)
+    return ModelColumns(model, 0, mk(max(cap_n, 1), np.uint8), col, byt, cap_n, list(cap_bytes))
+
+
+def _model_encode(self, cols: ModelColumns, fmt: int = FORMAT_ARRAY, out=None):
+    """writeValueAsBytes(List<Order|User>) of device columns: a uint8 torch
+    tensor holding exactly the JSON bytes (a view of `out` when given)."""
+    import torch
+    torch.cuda.synchronize()
+    s = cols.struct()
+    n = C.c_uint64(0)
+    if out is None:
+        rc = self.L.pj_encode_model_device(self.ctx, cols.model, C.byref(s), fmt, None, 0, C.byref(n))
+        if rc not in (PJ_OK, PJ_ERR_CAPACITY):
+            self._check(rc)
+        out = torch.empty(n.value + 4, dtype=torch.uint8, device=f"cuda:{self.device}")
+    self._check(self.L.pj_encode_model_device(self.ctx, cols.model, C.byref(s), fmt, C.c_void_p(out.data_ptr()),
+                                              out.numel(), C.byref(n)))
+    return out[: n.value]
+
+
+def _model_decode(self, model: int, data, array: bool = False, caps=None, err_cap=None):
+    """readValue of NDJSON (or one array document) of Orders / Users held in
+    a uint8 device tensor.  Returns (device columns, error indices, error
+    codes, DecodeResult)."""
+    import torch
+    n = data.numel()
+    cap_n, cap_bytes = caps or decode_model_bounds(model, n)
+    dev = f"cuda:{self.device}"
+    cols = alloc_model_columns(model, cap_n, cap_bytes, device=dev)
+    if err_cap is None:
+        err_cap = n + 1
+    el = torch.zeros(max(err_cap, 1), dtype=torch.int64, device=dev)
+    ec = torch.zeros(max(err_cap, 1), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    s = cols.struct()
+    res = DecodeResult()
+    self._check(self.L.pj_decode_model_device(self.ctx, model, C.c_void_p(data.data_ptr()), n, int(array),
+                                              C.byref(s), C.c_void_p(el.data_ptr()), C.c_void_p(ec.data_ptr()),
+                                              err_cap, C.byref(res)))
+    cols.n = int(s.n)
+    cols.n_bytes = [int(s.n_bytes[k]) for k in range(MODEL_MAX_PROPS)]
+    ne = int(res.n_errors)
+    return cols, el[:ne], ec[:ne], res
+
+
+Codec.encode_model = _model_encode
+Codec.decode_model = _model_decode

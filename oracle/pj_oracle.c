@@ -831,30 +831,15 @@ int or_decode(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *er
     return PJ_OK;
 }
 
-/* One JSON array of Pets => its elements (readValue(bytes, List<Pet>), the
- * reference's bulk shape "array of Pet", petstore.json:133-140, read as in
- * MyEntityConfig.java:34).  The array's frame is read first, sequentially:
- * whitespace, '[', then the top-level commas, found by counting '[' '{' ']'
- * '}' outside strings (a quote opens or closes a string unless a backslash
- * escapes it; a backslash escapes the next byte, in strings or not), up to
- * the ']' that brings the count back to zero; only whitespace may follow.
- * A broken frame (no '[', never closed, closed by '}', bytes after it, an
- * element of whitespace only) fails the whole call with PJ_ERR_SYNTAX, as
- * jackson's parser throws for it.  Each element is then read exactly as an
- * NDJSON line (or_decode_line, '\n' being whitespace) and reported under its
- * index.  "[]" and "[ ]" hold no element. */
-int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
-                    uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
-    if (!res || (len && !in)) return PJ_ERR_INVALID_ARG;
-    memset(res, 0, sizeof *res);
-    if (out && out->cap_pets + 1 > 0) {
-        if (out->name_off) out->name_off[0] = 0;
-        if (out->cat_name_off) out->cat_name_off[0] = 0;
-        if (out->photo_off) out->photo_off[0] = 0;
-        if (out->tag_off) out->tag_off[0] = 0;
-        if (out->url_off) out->url_off[0] = 0;
-        if (out->tag_name_off) out->tag_name_off[0] = 0;
-    }
+/* The frame of one array document: whitespace, '[', then the top-level
+ * commas, found by counting '[' '{' ']' '}' outside strings (a quote opens or
+ * closes a string unless a backslash escapes it; a backslash escapes the next
+ * byte, in strings or not), up to the ']' that brings the count back to
+ * zero; only whitespace may follow.  Element k spans [start[k], start[k+1] -
+ * 1), the last one ending at the ']' (*close).  A broken frame or an element
+ * of whitespace only gives PJ_ERR_SYNTAX; "[ ]" has no element.  *start is
+ * malloc'ed (free it). */
+static int array_frame(const uint8_t *in, uint64_t len, uint64_t **start_out, uint64_t *ne_out, uint64_t *close_out) {
     uint64_t p = 0;
     while (p < len && is_ws(in[p])) p++;
     if (p >= len || in[p] != '[') return PJ_ERR_SYNTAX;
@@ -895,10 +880,42 @@ int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64
         if (q == e) {
             if (ne == 1) { ne = 0; break; }        /* "[ ]": no element */
             free(start);
-            memset(res, 0, sizeof *res);
             return PJ_ERR_SYNTAX;                   /* an empty element */
         }
     }
+    *start_out = start;
+    *ne_out = ne;
+    *close_out = close;
+    return PJ_OK;
+}
+
+/* One JSON array of Pets => its elements (readValue(bytes, List<Pet>), the
+ * reference's bulk shape "array of Pet", petstore.json:133-140, read as in
+ * MyEntityConfig.java:34).  The array's frame is read first, sequentially:
+ * whitespace, '[', then the top-level commas, found by counting '[' '{' ']'
+ * '}' outside strings (a quote opens or closes a string unless a backslash
+ * escapes it; a backslash escapes the next byte, in strings or not), up to
+ * the ']' that brings the count back to zero; only whitespace may follow.
+ * A broken frame (no '[', never closed, closed by '}', bytes after it, an
+ * element of whitespace only) fails the whole call with PJ_ERR_SYNTAX, as
+ * jackson's parser throws for it.  Each element is then read exactly as an
+ * NDJSON line (or_decode_line, '\n' being whitespace) and reported under its
+ * index.  "[]" and "[ ]" hold no element. */
+int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
+                    uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+    if (!res || (len && !in)) return PJ_ERR_INVALID_ARG;
+    memset(res, 0, sizeof *res);
+    if (out && out->cap_pets + 1 > 0) {
+        if (out->name_off) out->name_off[0] = 0;
+        if (out->cat_name_off) out->cat_name_off[0] = 0;
+        if (out->photo_off) out->photo_off[0] = 0;
+        if (out->tag_off) out->tag_off[0] = 0;
+        if (out->url_off) out->url_off[0] = 0;
+        if (out->tag_name_off) out->tag_name_off[0] = 0;
+    }
+    uint64_t *start = NULL, ne = 0, close = 0;
+    const int fs = array_frame(in, len, &start, &ne, &close);
+    if (fs) return fs;
     for (uint64_t k = 0; k < ne; k++) {
         const uint64_t a = start[k], e = k + 1 < ne ? start[k + 1] - 1 : close;
         int code = or_decode_line(in + a, e - a, out, res);
@@ -919,5 +936,237 @@ int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64
                 res->url_bytes > out->cap_url_bytes || res->n_tags > out->cap_tags ||
                 res->tag_name_bytes > out->cap_tag_name_bytes))
         return PJ_ERR_CAPACITY;
+    return PJ_OK;
+}
+
+/* ======================================================================
+ *                       ORDER AND USER MODELS
+ * ======================================================================
+ * Schemas: reference petstore.json:824-857 (User: id int64, username,
+ * firstName, lastName, email, password, phone, userStatus int32) and
+ * :937-971 (Order: id int64, petId int64, quantity int32, shipDate
+ * date-time, status enum placed/approved/delivered :955-963, complete
+ * boolean).  No property is required.  Properties are written in schema
+ * order with the same inclusion, escape and number rules as Pet.
+ * Parity unpinned: shipDate is carried as the text written (a generated
+ * class would hold an OffsetDateTime that serde formats itself), booleans
+ * accept only true / false / null (no coercion from numbers or strings). */
+
+enum { MK_I64, MK_I32, MK_STR, MK_ENUM, MK_BOOL };
+typedef struct { const char *name; int kind; } mprop_t;
+typedef struct { int n; const mprop_t *p; const char *const *enum_txt; } mschema_t;
+
+static const mprop_t ORDER_PROPS[6] = {{"id", MK_I64}, {"petId", MK_I64}, {"quantity", MK_I32},
+                                       {"shipDate", MK_STR}, {"status", MK_ENUM}, {"complete", MK_BOOL}};
+static const char *const ORDER_STATUS[3] = {"placed", "approved", "delivered"};
+static const mprop_t USER_PROPS[8] = {{"id", MK_I64}, {"username", MK_STR}, {"firstName", MK_STR},
+                                      {"lastName", MK_STR}, {"email", MK_STR}, {"password", MK_STR},
+                                      {"phone", MK_STR}, {"userStatus", MK_I32}};
+
+static const mschema_t *schema_of(int model) {
+    static const mschema_t ORDER = {6, ORDER_PROPS, ORDER_STATUS}, USER = {8, USER_PROPS, NULL};
+    return model == PJ_MODEL_ORDER ? &ORDER : model == PJ_MODEL_USER ? &USER : NULL;
+}
+
+static void w_model(wbuf *w, const mschema_t *S, const pj_model_columns *c, const pj_options *o, uint64_t i) {
+    int first = 1;
+    o_start(w);
+    for (int k = 0; k < S->n; k++) {
+        const mprop_t *pr = &S->p[k];
+        int present = c->present ? (c->present[i] >> k) & 1 : 1;
+        if (present && pr->kind == MK_ENUM && ((const uint8_t *)c->col[k])[i] > 2) present = 0;
+        if (!present) {
+            if (o->inclusion == PJ_INCLUDE_ALWAYS) { w_key(w, &first, pr->name); w_lit(w, "null"); }
+            continue;
+        }
+        if (pr->kind == MK_STR) {
+            const uint64_t *off = (const uint64_t *)c->col[k];
+            const uint64_t a = off[i], b = off[i + 1];
+            if (b == a && o->inclusion == PJ_INCLUDE_NON_EMPTY) continue;   /* "" is empty */
+            w_key(w, &first, pr->name);
+            w_string(w, c->bytes[k] + a, b - a, o->hex_upper);
+            continue;
+        }
+        w_key(w, &first, pr->name);
+        switch (pr->kind) {
+        case MK_I64: w_long(w, ((const int64_t *)c->col[k])[i]); break;
+        case MK_I32: w_long(w, ((const int32_t *)c->col[k])[i]); break;
+        case MK_ENUM:
+            w_char(w, '"');
+            w_lit(w, S->enum_txt[((const uint8_t *)c->col[k])[i]]);
+            w_char(w, '"');
+            break;
+        default: w_lit(w, ((const uint8_t *)c->col[k])[i] ? "true" : "false"); break;
+        }
+    }
+    o_end(w, first);
+}
+
+int or_encode_model(int model, const pj_model_columns *cols, const pj_options *opt, int format,
+                    uint8_t *out, uint64_t out_cap, uint64_t *out_len) {
+    pj_options def;
+    or_default_options(&def);
+    const mschema_t *S = schema_of(model);
+    if (!S || !cols || !out_len ||
+        (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON && format != PJ_FORMAT_PRETTY))
+        return PJ_ERR_INVALID_ARG;
+    if (!opt) opt = &def;
+    wbuf w = {out, out_cap, 0, format == PJ_FORMAT_PRETTY, 0};
+    const int array = format != PJ_FORMAT_NDJSON;
+    if (array) a_start(&w);
+    for (uint64_t i = 0; i < cols->n; i++) {
+        if (array) a_value(&w, i);
+        w_model(&w, S, cols, opt, i);
+        if (!array) w_char(&w, '\n');
+    }
+    if (array) a_end(&w);
+    *out_len = w.len;
+    return w.len > out_cap ? PJ_ERR_CAPACITY : PJ_OK;
+}
+
+typedef struct {            /* one Order / User while it is being read */
+    const mschema_t *S;
+    uint8_t present;
+    int64_t v[PJ_MODEL_MAX_PROPS];
+    bytes_t str[PJ_MODEL_MAX_PROPS];
+} mrec_t;
+
+static int model_member(rd_t *r, const bytes_t *k, void *ctx) {
+    mrec_t *m = (mrec_t *)ctx;
+    int f = -1;
+    for (int j = 0; j < m->S->n; j++)
+        if (key_is(k, m->S->p[j].name)) f = j;
+    if (f < 0) return rd_skip_value(r);
+    const uint8_t bit = (uint8_t)(1u << f);
+    int pres = 0, e, kind;
+    int64_t v = 0;
+    switch (m->S->p[f].kind) {
+    case MK_I64:
+    case MK_I32:
+        if ((e = rd_long(r, &v, &pres))) return e;
+        if (pres && m->S->p[f].kind == MK_I32 && (v < INT32_MIN || v > INT32_MAX))
+            return PJ_REC_NUMBER;                           /* out of int range */
+        break;
+    case MK_STR:
+        if ((e = rd_str_prop(r, &m->str[f], &pres))) return e;
+        if (!pres) m->str[f].n = 0;
+        break;
+    case MK_ENUM: {
+        bytes_t t = {0, 0, 0};
+        e = rd_str_prop(r, &t, &pres);
+        if (!e && pres) {
+            int hit = -1;
+            for (int s = 0; s < 3; s++) if (key_is(&t, m->S->enum_txt[s])) hit = s;
+            if (hit < 0) e = PJ_REC_BAD_STATUS;             /* @JsonCreator rejects unknown */
+            v = hit;
+        }
+        free(t.p);
+        if (e) return e;
+        break;
+    }
+    default: {                                              /* MK_BOOL */
+        const uint8_t c = cur(r);
+        if (c == '"' || c == '{' || c == '[') return PJ_REC_TYPE;
+        if ((e = rd_scalar(r, &kind))) return e;
+        if (kind == TK_INT || kind == TK_REAL) return PJ_REC_TYPE;
+        pres = kind != TK_NULL;
+        v = kind == TK_TRUE;
+        break;
+    }
+    }
+    if (pres) { m->present |= bit; m->v[f] = v; }
+    else { m->present &= (uint8_t)~bit; m->v[f] = 0; }
+    return PJ_REC_OK;
+}
+
+/* Append a finished record (capacity-checked: only counts past it). */
+static void model_commit(const mrec_t *m, pj_model_columns *o, pj_decode_result *f) {
+    const uint64_t i = f->n_pets;
+    const int row = o && i < o->cap_n;
+    if (row && o->present) o->present[i] = m->present;
+    for (int k = 0; k < m->S->n; k++) {
+        const int kind = m->S->p[k].kind;
+        if (kind == MK_STR) {
+            const uint64_t L = m->str[k].n;
+            if (o && L && o->n_bytes[k] + L <= o->cap_bytes[k]) memcpy(o->bytes[k] + o->n_bytes[k], m->str[k].p, L);
+            if (o) o->n_bytes[k] += L;
+            if (row) ((uint64_t *)o->col[k])[i + 1] = o->n_bytes[k];
+        } else if (row) {
+            if (kind == MK_I64) ((int64_t *)o->col[k])[i] = m->v[k];
+            else if (kind == MK_I32) ((int32_t *)o->col[k])[i] = (int32_t)m->v[k];
+            else ((uint8_t *)o->col[k])[i] = (uint8_t)m->v[k];
+        }
+    }
+    f->n_pets++;
+}
+
+/* One record (an NDJSON line without its '\n', or an array element), read
+ * as or_decode_line reads a Pet. */
+static int model_line(const mschema_t *S, const uint8_t *s, uint64_t n, pj_model_columns *out,
+                      pj_decode_result *fill) {
+    rd_t r = {s, n, 0, 0};
+    skip_ws(&r);
+    if (at_end(&r)) return PJ_REC_EMPTY;
+    if (cur(&r) != '{') return type_mismatch(&r);
+    mrec_t m;
+    memset(&m, 0, sizeof m);
+    m.S = S;
+    int e = rd_object(&r, model_member, &m);
+    if (!e) {
+        skip_ws(&r);
+        if (!at_end(&r)) e = PJ_REC_SYNTAX;
+    }
+    if (!e) model_commit(&m, out, fill);
+    for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) free(m.str[k].p);
+    return e;
+}
+
+int or_decode_model(int model, const uint8_t *in, uint64_t len, int array, pj_model_columns *out,
+                    uint64_t *err_line, uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+    const mschema_t *S = schema_of(model);
+    if (!S || !res || (len && !in)) return PJ_ERR_INVALID_ARG;
+    memset(res, 0, sizeof *res);
+    if (out) {
+        for (int k = 0; k < S->n; k++) {
+            out->n_bytes[k] = 0;
+            if (S->p[k].kind == MK_STR && out->col[k]) ((uint64_t *)out->col[k])[0] = 0;
+        }
+    }
+    uint64_t *start = NULL, ne = 0, close = 0;
+    if (array) {
+        const int fs = array_frame(in, len, &start, &ne, &close);
+        if (fs) return fs;
+    }
+    /* records: the array's elements, or the lines cut at every '\n' */
+    for (uint64_t k = 0, p = 0; array ? k < ne : p < len; k++) {
+        uint64_t a, e;
+        if (array) {
+            a = start[k];
+            e = k + 1 < ne ? start[k + 1] - 1 : close;
+        } else {
+            const uint8_t *nl = (const uint8_t *)memchr(in + p, '\n', len - p);
+            a = p;
+            e = nl ? (uint64_t)(nl - in) : len;
+            p = e + 1;
+            ne = k + 1;
+        }
+        const int code = model_line(S, in + a, e - a, out, res);
+        if (code) {
+            if (res->n_errors < err_cap) {
+                if (err_line) err_line[res->n_errors] = k;
+                if (err_code) err_code[res->n_errors] = (uint8_t)code;
+            }
+            res->n_errors++;
+        }
+    }
+    free(start);
+    res->n_lines = ne;
+    if (out) out->n = res->n_pets < out->cap_n ? res->n_pets : out->cap_n;
+    if (res->n_errors > err_cap) return PJ_ERR_CAPACITY;
+    if (out) {
+        if (res->n_pets > out->cap_n) return PJ_ERR_CAPACITY;
+        for (int k = 0; k < S->n; k++)
+            if (out->n_bytes[k] > out->cap_bytes[k]) return PJ_ERR_CAPACITY;
+    }
     return PJ_OK;
 }

@@ -46,6 +46,13 @@ int or_decode_array(const uint8_t *in, uint64_t len, pj_pet_columns *out,
 int or_decode_line(const uint8_t *s, uint64_t n, pj_pet_columns *out,
                    pj_decode_result *fill);
 
+/* Order / User models (host pointers): same conventions as
+ * pj_encode_model_device / pj_decode_model_device. */
+int or_encode_model(int model, const pj_model_columns *cols, const pj_options *opt, int format,
+                    uint8_t *out, uint64_t out_cap, uint64_t *out_len);
+int or_decode_model(int model, const uint8_t *in, uint64_t len, int array, pj_model_columns *out,
+                    uint64_t *err_line, uint8_t *err_code, uint64_t err_cap, pj_decode_result *res);
+
 /* Long.toString(v) into buf (>= 21 bytes); returns length.  Exposed so the
  * tests can brute-force it against printf. */
 int or_format_long(int64_t v, char *buf);

@@ -14,7 +14,7 @@ g++ -O1 -std=c++17 -Wall -I"$ROOT/include" -I"$ROOT/micronaut3-bug_amd/host" -I"
 # objects of the in-tree build.
 HIPCC=${HIPCC:-/opt/rocm/bin/hipcc}
 PKG="$ROOT/micronaut3-bug_amd"
-if [ -f "$PKG/_build/pj_encode_hip.o" ] && [ -f "$PKG/_build/pj_decode_hip.o" ]; then
+if [ -f "$PKG/_build/pj_encode_hip.o" ] && [ -f "$PKG/_build/pj_decode_hip.o" ] && [ -f "$PKG/_build/pj_model_hip.o" ]; then
     SANF="-Xarch_host -fsanitize=address,undefined -Xarch_host -fno-sanitize-recover=all -Xarch_host -fno-omit-frame-pointer"
     OBJ="$HERE/bin/obj"
     mkdir -p "$OBJ"
@@ -23,7 +23,7 @@ if [ -f "$PKG/_build/pj_encode_hip.o" ] && [ -f "$PKG/_build/pj_decode_hip.o" ];
             -c "$src" -o "$OBJ/$(basename "$src").o" 2>/dev/null
     done
     $HIPCC --offload-arch=gfx950 -fsanitize=address,undefined -fno-gpu-sanitize "$OBJ/pj_api.cpp.o" "$OBJ/pj_gen.cpp.o" \
-        "$OBJ/api_sanitize.cpp.o" "$PKG/_build/pj_encode_hip.o" "$PKG/_build/pj_decode_hip.o" -pthread \
+        "$OBJ/api_sanitize.cpp.o" "$PKG/_build/pj_encode_hip.o" "$PKG/_build/pj_decode_hip.o" "$PKG/_build/pj_model_hip.o" -pthread \
         -o "$HERE/bin/api_sanitize"
     rm -rf "$OBJ"
 fi

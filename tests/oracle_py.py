@@ -29,6 +29,10 @@ def lib():
         L.or_decode_line.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
         L.or_decode_array.argtypes = L.or_decode.argtypes
         L.or_format_long.argtypes = [C.c_int64, C.c_char_p]
+        L.or_encode_model.argtypes = [C.c_int, C.POINTER(pj.ModelColumnsStruct), C.POINTER(pj.Options), C.c_int,
+                                      C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64)]
+        L.or_decode_model.argtypes = [C.c_int, C.c_void_p, C.c_uint64, C.c_int, C.POINTER(pj.ModelColumnsStruct),
+                                      C.c_void_p, C.c_void_p, C.c_uint64, C.POINTER(pj.DecodeResult)]
         _L = L
     return _L
 
@@ -137,3 +141,40 @@ def format_long(v: int) -> str:
     b = C.create_string_buffer(32)
     n = lib().or_format_long(v, b)
     return b.raw[:n].decode()
+
+
+def encode_model(cols: "pj.ModelColumns", fmt=pj.FORMAT_ARRAY, inclusion=pj.INCLUDE_NON_EMPTY, hex_upper=True) -> bytes:
+    """Order / User records (host columns) through the CPU restatement."""
+    L = lib()
+    s = cols.struct()
+    o = pj.make_options(inclusion, hex_upper)
+    n = C.c_uint64(0)
+    L.or_encode_model(cols.model, C.byref(s), C.byref(o), fmt, None, 0, C.byref(n))
+    out = np.empty(max(1, n.value), dtype=np.uint8)
+    rc = L.or_encode_model(cols.model, C.byref(s), C.byref(o), fmt, C.c_void_p(out.ctypes.data), out.size,
+                           C.byref(n))
+    assert rc == 0
+    return out[: n.value].tobytes()
+
+
+def decode_model(model: int, data: bytes, array=False):
+    """Returns (status, host columns trimmed to size, error indices, error
+    codes, result)."""
+    L = lib()
+    n = len(data)
+    buf = np.frombuffer(data, dtype=np.uint8) if n else np.zeros(1, np.uint8)
+    cap_bytes = [n] * pj.MODEL_MAX_PROPS
+    cols = pj.alloc_model_columns(model, n // 3 + 1, cap_bytes)
+    s = cols.struct()
+    ne = n + 1
+    el = np.zeros(ne, np.uint64)
+    ec = np.zeros(ne, np.uint8)
+    res = pj.DecodeResult()
+    rc = L.or_decode_model(model, C.c_void_p(buf.ctypes.data), n, int(array), C.byref(s),
+                           C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), ne, C.byref(res))
+    assert rc in (pj.PJ_OK, pj.PJ_ERR_SYNTAX), rc
+    cols.n = int(s.n) if rc == pj.PJ_OK else 0
+    cols.n_bytes = [int(s.n_bytes[k]) for k in range(pj.MODEL_MAX_PROPS)]
+    if rc != pj.PJ_OK:
+        res = pj.DecodeResult()
+    return rc, cols.to_host(), el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res

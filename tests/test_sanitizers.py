@@ -58,7 +58,7 @@ def build_api_sanitized(out_dir):
         obj = os.path.join(out_dir, os.path.basename(src) + ".o")
         subprocess.run([HIPCC, *hflags, "-c", src, "-o", obj], check=True, capture_output=True)
         objs.append(obj)
-    kern = [os.path.join(PKG, "_build", f) for f in ("pj_encode_hip.o", "pj_decode_hip.o")]
+    kern = [os.path.join(PKG, "_build", f) for f in ("pj_encode_hip.o", "pj_decode_hip.o", "pj_model_hip.o")]
     if not all(os.path.exists(k) for k in kern):
         pytest.skip("kernel objects missing: run __graft_entry__.build() first")
     exe = os.path.join(out_dir, "api_sanitize")
