@@ -213,6 +213,16 @@ pj_status pj_encode_size_device(pj_ctx *ctx, const pj_pet_columns *cols,
  * with it and encode in one call instead of asking for the exact size first
  * (which would copy the columns to the device twice). */
 pj_status pj_encode_bound(const pj_pet_columns *cols, int format, uint64_t *bound);
+/* findPetsByStatus's response body (reference petstore.json:106-140, a
+ * `status` query of several values, default "available"): the records whose
+ * status is in status_mask, in input order, serialised as pj_encode_device
+ * would serialise just those records.  Bit s of status_mask selects status
+ * code s (0 available, 1 pending, 2 sold); bit 3 selects records without a
+ * status.  *n_selected (may be NULL) receives the number of records written.
+ * Device pointers; capacity rules as pj_encode_device. */
+pj_status pj_encode_by_status_device(pj_ctx *ctx, const pj_pet_columns *cols, uint32_t status_mask,
+                                     int format, uint8_t *out, uint64_t out_cap, uint64_t *out_len,
+                                     uint64_t *n_selected);
 /* Same as pj_encode_device with host pointers. */
 pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
                          uint8_t *out, uint64_t out_cap, uint64_t *out_len);

@@ -241,6 +241,15 @@ uint64_t spin_limit() {
     return 20000000;
 }
 
+// The context's options as the encode kernels read them.
+void set_enc_options(const pj_ctx *ctx, EncParams &P) {
+    for (int k = 0; k < PJ_FIELD_COUNT; k++) {
+        const int32_t m = ctx->opt.field_inclusion[k];
+        P.incl[k] = (uint8_t)(m == PJ_INCLUDE_DEFAULT ? ctx->opt.inclusion : m);
+    }
+    P.hexa = ctx->opt.hex_upper ? 'A' : 'a';
+}
+
 bool format_ok(int f) { return f == PJ_FORMAT_ARRAY || f == PJ_FORMAT_NDJSON || f == PJ_FORMAT_PRETTY; }
 
 // fixed_scratch: encode into the device's fixed scratch array instead of
@@ -289,11 +298,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.c = *cols;
     P.n = n;
     P.format = format;
-    for (int k = 0; k < PJ_FIELD_COUNT; k++) {
-        const int32_t m = ctx->opt.field_inclusion[k];
-        P.incl[k] = (uint8_t)(m == PJ_INCLUDE_DEFAULT ? ctx->opt.inclusion : m);
-    }
-    P.hexa = ctx->opt.hex_upper ? 'A' : 'a';
+    set_enc_options(ctx, P);
     P.count_only = count_only ? 1 : 0;
     P.out = out;
     P.cap = count_only ? 0 : cap;
@@ -314,7 +319,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
         if ((s = mark(ctx))) return s;
         PJ_HIP(pj_launch_fill_u64(sc, nblk + 3, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
-        if (pretty) PJ_HIP(pj_launch_encode_pretty(P, ctx->stream));
+        if (pretty) PJ_HIP(pj_launch_encode_rows(P, true, ctx->stream));
         else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
         if ((s = mark(ctx))) return s;
         PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
@@ -478,6 +483,71 @@ int pj_last_timings(const pj_ctx *c, float *ms, int cap) {
     int k = std::min(cap, c->n_timings);
     for (int i = 0; i < k; i++) ms[i] = c->timings[i];
     return k;
+}
+
+pj_status pj_encode_by_status_device(pj_ctx *ctx, const pj_pet_columns *cols, uint32_t status_mask, int format,
+                                     uint8_t *out, uint64_t out_cap, uint64_t *out_len, uint64_t *n_selected) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
+    if (status_mask & ~0xFu) return fail(PJ_ERR_INVALID_ARG, "status mask has bits past 3");
+    if (out_cap > 0 && !out) return fail(PJ_ERR_INVALID_ARG, "null output with capacity");
+    if ((s = check_enc_cols(cols))) return s;
+    ctx->n_ev = 0;
+    const uint64_t n = cols->n_pets, bt = (uint64_t)pj_encode_pretty_records(), nblk = (n + bt - 1) / bt;
+    // scan buffer: selection (ticket, count, look-back words), encode
+    // (ticket, total, look-back words), the selected indices
+    const uint64_t w_sel = 2 + nblk, w_enc = 2 + nblk;
+    PJ_HIP(ctx->scan.ensure((w_sel + w_enc + n + 1) * sizeof(uint64_t)));
+    uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p), *ec = sc + w_sel, *sel = ec + w_enc;
+    EncParams P;
+    std::memset(&P, 0, sizeof P);
+    P.c = *cols;
+    P.format = format;
+    set_enc_options(ctx, P);
+    P.out = out;
+    P.cap = out_cap;
+    uint64_t m = 0;
+    if (n) {
+        P.ticket = reinterpret_cast<unsigned long long *>(sc);
+        P.total = sc + 1;
+        P.state = sc + 2;
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_fill_u64(sc, w_sel + w_enc, 0, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(pj_launch_select_status(P, status_mask, sel, ctx->stream));
+        if ((s = mark(ctx))) return s;
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        m = ctx->pinned[0];
+    }
+    if (n_selected) *n_selected = m;
+    if (m == 0) {
+        // "[]", "[ ]" (pretty) or nothing
+        const uint64_t len = format == PJ_FORMAT_ARRAY ? 2 : format == PJ_FORMAT_PRETTY ? 3 : 0;
+        *out_len = len;
+        if (len && len <= out_cap) {
+            const uint32_t w = format == PJ_FORMAT_ARRAY ? '[' | (']' << 8) : '[' | (' ' << 8) | (']' << 16);
+            PJ_HIP(pj_launch_put_bytes(out, w, (int)len, ctx->stream));
+        }
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if ((s = finish_timing(ctx))) return s;
+        return len > out_cap ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
+    }
+    P.n = m;
+    P.sel = sel;
+    P.ticket = reinterpret_cast<unsigned long long *>(ec);
+    P.total = ec + 1;
+    P.state = ec + 2;
+    PJ_HIP(pj_launch_encode_rows(P, format == PJ_FORMAT_PRETTY, ctx->stream));
+    if ((s = mark(ctx))) return s;
+    PJ_HIP(hipMemcpyAsync(ctx->pinned, ec + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+    PJ_HIP(hipStreamSynchronize(ctx->stream));
+    if ((s = finish_timing(ctx))) return s;
+    *out_len = ctx->pinned[0];
+    if (*out_len > out_cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    return PJ_OK;
 }
 
 pj_status pj_encode_device(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t out_cap,

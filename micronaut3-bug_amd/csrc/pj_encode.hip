@@ -1335,26 +1335,31 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     }
 }
 
-// PJ_FORMAT_PRETTY: one thread per record, blocks of BT records claimed by
-// ticket.  Each thread measures its record, a block scan places the records,
-// the look-back gives the block's offset, and each thread writes its record
-// straight to global memory.  Records that would end past the capacity are
-// not written; the last block stores the total.
-template <int BT>
-__global__ __launch_bounds__(BT) void k_encode_pretty(EncParams P) {
+// One thread per output record, blocks of BT records claimed by ticket:
+// pretty-printed output (PRETTY), and the records a selection names
+// (P.sel: output record j is column record sel[j]; compact or pretty).  Each
+// thread measures its record from global memory, a block scan places the
+// records, the look-back gives the block's offset, and each thread writes
+// its record with exact stores.  Records that would end past the capacity
+// are not written; the last block stores the total.
+template <int BT, bool PRETTY>
+__global__ __launch_bounds__(BT) void k_encode_rows(EncParams P) {
     __shared__ uint64_t sh_scan[BT / 64 + 2];
     __shared__ uint64_t sh_b, sh_base;
+    const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
     const uint32_t t = threadIdx.x;
     if (t == 0) sh_b = atomicAdd(P.ticket, 1ull);
     __syncthreads();
     const uint64_t b = sh_b, nblk = (P.n + BT - 1) / BT;
-    const uint64_t i = b * BT + t;
-    const bool live = i < P.n;
+    const uint64_t j = b * BT + t;
+    const bool live = j < P.n;
     RecVals v{};
+    RecItems ri{};
     CountSink cs;
     if (live) {
-        v = load_rec<true>(P, i);
-        pp_rec(cs, P, i, v);
+        v = load_rec<true>(P, P.sel ? P.sel[j] : j);
+        if (PRETTY) pp_rec(cs, P, j, v);
+        else emit_rec<true, true>(cs, P, XG, j, v, ri);
     }
     uint64_t agg;
     const uint64_t pre = block_excl_scan<BT>(cs.n, sh_scan, &agg);
@@ -1370,8 +1375,39 @@ __global__ __launch_bounds__(BT) void k_encode_pretty(EncParams P) {
     const uint64_t at = sh_base + pre;
     if (at + cs.n > P.cap) return;
     XSink xs{P.out + at, 0, 0};
-    pp_rec(xs, P, i, v);
+    if (PRETTY) pp_rec(xs, P, j, v);
+    else emit_rec<true, true>(xs, P, XG, j, v, ri);
     xs.finish();
+}
+
+// The records whose status code is in the mask (bit s: status s, bit 3: no
+// status), in input order: each block's selected indices placed by a block
+// scan and the look-back.  The last block stores the count.
+template <int BT>
+__global__ __launch_bounds__(BT) void k_select_status(EncParams P, uint32_t mask, uint64_t *sel) {
+    __shared__ uint64_t sh_scan[BT / 64 + 2];
+    __shared__ uint64_t sh_b, sh_base;
+    const uint32_t t = threadIdx.x;
+    if (t == 0) sh_b = atomicAdd(P.ticket, 1ull);
+    __syncthreads();
+    const uint64_t b = sh_b, n = P.c.n_pets, nblk = (n + BT - 1) / BT;
+    const uint64_t i = b * BT + t;
+    uint64_t hit = 0;
+    if (i < n) {
+        const uint32_t st = P.c.status ? P.c.status[i] : (uint32_t)PJ_STATUS_NULL;
+        hit = (mask >> (st <= 2 ? st : 3)) & 1u;
+    }
+    uint64_t agg;
+    const uint64_t pre = block_excl_scan<BT>(hit, sh_scan, &agg);
+    if (t < 64) {
+        const uint64_t excl = lookback(P.state, b, agg);
+        if (t == 0) {
+            sh_base = excl;
+            if (b == nblk - 1) *P.total = excl + agg;
+        }
+    }
+    __syncthreads();
+    if (hit) sel[sh_base + pre] = i;
 }
 
 // ------------------------------------------------- Order and User records
@@ -1635,9 +1671,20 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
 constexpr int ENC_PRETTY_BT = 256;
 int pj_encode_pretty_records() { return ENC_PRETTY_BT; }
 
-hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st) {
+hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st) {
     const uint64_t nblk = (P.n + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
-    hipLaunchKernelGGL(pj::k_encode_pretty<ENC_PRETTY_BT>, dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P);
+    if (pretty)
+        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, true>), dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P);
+    else
+        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, false>), dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st,
+                           P);
+    return hipGetLastError();
+}
+
+hipError_t pj_launch_select_status(const EncParams &P, uint32_t mask, uint64_t *sel, hipStream_t st) {
+    const uint64_t nblk = (P.c.n_pets + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
+    hipLaunchKernelGGL(pj::k_select_status<ENC_PRETTY_BT>, dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P, mask,
+                       sel);
     return hipGetLastError();
 }
 

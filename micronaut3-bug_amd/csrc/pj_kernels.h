@@ -21,6 +21,7 @@ struct EncParams {
     uint64_t *total;           // encoded size (written by the last block)
     uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)
     unsigned long long *nfall; // blocks whose records did not fit the LDS tile (counted)
+    const uint64_t *sel;       // one-thread-per-record kernel: output record j is record sel[j] (or j)
 };
 
 // Order / User encode (pj_encode_model_device): one thread per record,
@@ -137,7 +138,10 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);   // p[0, n) += v
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 int pj_encode_block_records(bool nested);
-hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st);
+// one thread per output record (pretty output, or a selection of records)
+hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);
+// indices of the records whose status is in mask into sel, their count into *P.total
+hipError_t pj_launch_select_status(const EncParams &P, uint32_t mask, uint64_t *sel, hipStream_t st);
 hipError_t pj_launch_encode_model(const ModelEncParams &P, hipStream_t st);
 int pj_encode_model_records();
 hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_t st);

@@ -162,6 +162,9 @@ def load_lib():
                                       C.POINTER(DecodeResult)]
             getattr(L, f).restype = i32
         L.pj_decode_bounds.argtypes = [u64, C.POINTER(PetColumnsStruct)]
+        L.pj_encode_by_status_device.argtypes = [vp, C.POINTER(PetColumnsStruct), C.c_uint32, i32, vp, u64,
+                                                 C.POINTER(u64), C.POINTER(u64)]
+        L.pj_encode_by_status_device.restype = i32
         L.pj_encode_model_device.argtypes = [vp, i32, C.POINTER(ModelColumnsStruct), i32, vp, u64, C.POINTER(u64)]
         L.pj_encode_model_device.restype = i32
         L.pj_decode_model_device.argtypes = [vp, i32, vp, u64, i32, C.POINTER(ModelColumnsStruct), vp, vp, u64,
@@ -734,5 +737,23 @@ def _model_decode(self, model: int, data, array: bool = False, caps=None, err_ca
     return cols, el[:ne], ec[:ne], res
 
 
+def _encode_by_status(self, cols: Columns, mask: int, fmt: int = FORMAT_ARRAY, out=None):
+    """findPetsByStatus body: the records of device columns whose status is in
+    mask (bit s: status s, bit 3: none).  Returns (uint8 tensor, count)."""
+    import torch
+    torch.cuda.synchronize()
+    s = cols.struct()
+    n, m = C.c_uint64(0), C.c_uint64(0)
+    if out is None:
+        rc = self.L.pj_encode_by_status_device(self.ctx, C.byref(s), mask, fmt, None, 0, C.byref(n), C.byref(m))
+        if rc not in (PJ_OK, PJ_ERR_CAPACITY):
+            self._check(rc)
+        out = torch.empty(n.value + 4, dtype=torch.uint8, device=f"cuda:{self.device}")
+    self._check(self.L.pj_encode_by_status_device(self.ctx, C.byref(s), mask, fmt, C.c_void_p(out.data_ptr()),
+                                                  out.numel(), C.byref(n), C.byref(m)))
+    return out[: n.value], m.value
+
+
+Codec.encode_by_status = _encode_by_status
 Codec.encode_model = _model_encode
 Codec.decode_model = _model_decode

@@ -268,6 +268,35 @@ int or_encode(const pj_pet_columns *cols, const pj_options *opt, int format,
     return w.len > out_cap ? PJ_ERR_CAPACITY : PJ_OK;
 }
 
+/* findPetsByStatus (reference petstore.json:106-140): the records whose
+ * status code s (3 for no status) has bit s set in mask, in input order,
+ * written as or_encode writes a column set holding just those records. */
+int or_encode_by_status(const pj_pet_columns *cols, const pj_options *opt, uint32_t mask, int format,
+                        uint8_t *out, uint64_t out_cap, uint64_t *out_len, uint64_t *n_selected) {
+    pj_options def;
+    or_default_options(&def);
+    if (!cols || !out_len || (mask & ~0xFu) ||
+        (format != PJ_FORMAT_ARRAY && format != PJ_FORMAT_NDJSON && format != PJ_FORMAT_PRETTY))
+        return PJ_ERR_INVALID_ARG;
+    if (!opt) opt = &def;
+    wbuf w = {out, out_cap, 0, format == PJ_FORMAT_PRETTY, 0};
+    const int array = format != PJ_FORMAT_NDJSON;
+    uint64_t m = 0;
+    if (array) a_start(&w);
+    for (uint64_t i = 0; i < cols->n_pets; i++) {
+        const uint8_t st = cols->status ? cols->status[i] : (uint8_t)PJ_STATUS_NULL;
+        if (!((mask >> (st <= 2 ? st : 3)) & 1)) continue;
+        if (array) a_value(&w, m);
+        w_pet(&w, cols, opt, i);
+        if (!array) w_char(&w, '\n');
+        m++;
+    }
+    if (array) a_end(&w);
+    *out_len = w.len;
+    if (n_selected) *n_selected = m;
+    return w.len > out_cap ? PJ_ERR_CAPACITY : PJ_OK;
+}
+
 /* ======================================================================
  *                                 DECODE
  * ====================================================================== */

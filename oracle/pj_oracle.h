@@ -28,6 +28,10 @@ void or_default_options(pj_options *o);
 int or_encode(const pj_pet_columns *cols, const pj_options *opt, int format,
               uint8_t *out, uint64_t out_cap, uint64_t *out_len);
 
+/* The records whose status is in mask (pj_encode_by_status_device rules). */
+int or_encode_by_status(const pj_pet_columns *cols, const pj_options *opt, uint32_t mask, int format,
+                        uint8_t *out, uint64_t out_cap, uint64_t *out_len, uint64_t *n_selected);
+
 /* Decode NDJSON (host pointers).  Same conventions as pj_decode_host. */
 int or_decode(const uint8_t *in, uint64_t len, pj_pet_columns *out,
               uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,

@@ -29,6 +29,8 @@ def lib():
         L.or_decode_line.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
         L.or_decode_array.argtypes = L.or_decode.argtypes
         L.or_format_long.argtypes = [C.c_int64, C.c_char_p]
+        L.or_encode_by_status.argtypes = [C.POINTER(pj.PetColumnsStruct), C.POINTER(pj.Options), C.c_uint32, C.c_int,
+                                          C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
         L.or_encode_model.argtypes = [C.c_int, C.POINTER(pj.ModelColumnsStruct), C.POINTER(pj.Options), C.c_int,
                                       C.c_void_p, C.c_uint64, C.POINTER(C.c_uint64)]
         L.or_decode_model.argtypes = [C.c_int, C.c_void_p, C.c_uint64, C.c_int, C.POINTER(pj.ModelColumnsStruct),
@@ -178,3 +180,17 @@ def decode_model(model: int, data: bytes, array=False):
     if rc != pj.PJ_OK:
         res = pj.DecodeResult()
     return rc, cols.to_host(), el[: res.n_errors].copy(), ec[: res.n_errors].copy(), res
+
+
+def encode_by_status(cols: pj.Columns, mask: int, fmt=pj.FORMAT_ARRAY, inclusion=pj.INCLUDE_NON_EMPTY):
+    """(bytes, selected count) of the records whose status is in mask."""
+    L = lib()
+    s = cols.struct()
+    o = pj.make_options(inclusion, True)
+    n, m = C.c_uint64(0), C.c_uint64(0)
+    L.or_encode_by_status(C.byref(s), C.byref(o), mask, fmt, None, 0, C.byref(n), C.byref(m))
+    out = np.empty(max(1, n.value), dtype=np.uint8)
+    rc = L.or_encode_by_status(C.byref(s), C.byref(o), mask, fmt, C.c_void_p(out.ctypes.data), out.size,
+                               C.byref(n), C.byref(m))
+    assert rc == 0
+    return out[: n.value].tobytes(), m.value

@@ -356,3 +356,39 @@ def test_encode_pretty_decodes_back_on_gpu(codec):
     for k in pj.COLS:
         if ref[k] is not None:
             assert np.array_equal(dec[k], ref[k]), k
+
+
+# ----------------------------------------------------- findPetsByStatus body
+@pytest.mark.parametrize("config,n", [(1, 60_000), (2, 100_000), (3, 50_000), (5, 8_000)])
+def test_encode_by_status_matches_oracle(codec, config, n):
+    print(f"[encode by status] config={config} n={n}", flush=True)
+    cols = pj.generate(config, n)
+    cols.arrays["status"][::11] = pj.STATUS_NULL
+    d = cols.to_device()
+    for mask in (1, 0b0101, 0b1000, 0xF, 0):
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
+            got, m = codec.encode_by_status(d, mask, fmt)
+            want, wm = orc.encode_by_status(cols, mask, fmt)
+            assert m == wm and got.cpu().numpy().tobytes() == want, (mask, fmt)
+
+
+def test_encode_by_status_capacity_and_no_status_column(codec):
+    cols = pj.generate(3, 20_000)
+    d = cols.to_device()
+    want, _ = orc.encode_by_status(cols, 0b011, pj.FORMAT_ARRAY)
+    ref = np.frombuffer(want, np.uint8)
+    out = torch.full((ref.size,), 0xEE, dtype=torch.uint8, device="cuda")
+    cap = ref.size // 3
+    with pytest.raises(pj.PetJsonError) as ei:
+        codec.encode_by_status(d, 0b011, pj.FORMAT_ARRAY, out=out[:cap])
+    assert ei.value.status == pj.PJ_ERR_CAPACITY
+    host = out.cpu().numpy()
+    assert (host[cap:] == 0xEE).all()
+    written = host[:cap] != 0xEE
+    assert (host[:cap][written] == ref[:cap][written]).all()
+    cols.arrays["status"] = None                   # no status column: every record has none
+    d = cols.to_device()
+    got, m = codec.encode_by_status(d, 0b1000, pj.FORMAT_ARRAY)
+    assert m == cols.n_pets and got.cpu().numpy().tobytes() == orc.encode(cols, pj.FORMAT_ARRAY)
+    got, m = codec.encode_by_status(d, 0b0111, pj.FORMAT_ARRAY)
+    assert m == 0 and got.cpu().numpy().tobytes() == b"[]"

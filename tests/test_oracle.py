@@ -357,3 +357,23 @@ def test_pretty_encode_differs_from_compact_only_in_layout(config, incl):
     for k in pj.COLS:
         if b[k] is not None:
             assert np.array_equal(a[k], b[k]), k
+
+
+# ----------------------------------------------------- findPetsByStatus body
+def _status_code(p):
+    return 3 if p.status is None else ["available", "pending", "sold"].index(p.status.value)
+
+
+@pytest.mark.parametrize("config", [1, 3, 5])
+def test_encode_by_status_is_encode_of_the_selected_records(config):
+    """The selection restated through the object model: filter the Pet list
+    by status, rebuild columns, encode those."""
+    cols = generate_small(config, 1500)
+    cols.arrays["status"][::7] = pj.STATUS_NULL
+    pets = from_columns(cols, as_bytes=True)
+    for mask in range(16):
+        chosen = [p for p in pets if (mask >> _status_code(p)) & 1]
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
+            got, m = orc.encode_by_status(cols, mask, fmt)
+            assert m == len(chosen)
+            assert got == orc.encode(to_columns(chosen), fmt), (mask, fmt)
