@@ -257,6 +257,82 @@ def cpu_baseline_encode(config, n_sample, budget_s=10.0):
                       f"windows of {budget_s / 10:.1f}s on 1 thread and on {cores} threads"}
 
 
+def _model_bytes(cols):
+    """Bytes of an Order / User column set (host numpy)."""
+    tot = cols.present.nbytes if cols.present is not None else 0
+    for c in cols.col:
+        tot += c.nbytes
+    for b in cols.bytes:
+        tot += b.nbytes if b is not None else 0
+    return tot
+
+
+def _kernel_ms(codec, fn, steps, warmup, idx):
+    """Mean of one HIP-event interval (idx into Codec.timings()) over steps calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ms = []
+    for _ in range(steps):
+        r = fn()
+        ms.append(codec.timings()[idx])
+    return sum(ms) / len(ms), r
+
+
+def option_workloads(codec, steps):
+    """The non-headline paths at a real size, each with its kernel time and
+    algorithmic bytes (columns in + JSON out): pretty printing and the
+    findPetsByStatus body over configs[2] records, and the Order / User
+    models' encode and decode (4M records each, seeded)."""
+    import torch
+    import petjson as pj
+    res = {}
+    cols = pj.generate(3, 10_000_000)
+    dev = cols.to_device()
+    in_bytes = col_bytes(cols)
+    ms, out = _kernel_ms(codec, lambda: codec.encode(dev, pj.FORMAT_PRETTY), steps, 1, -1)
+    alg = in_bytes + out.numel()
+    res["pretty_encode"] = {"records": cols.n_pets, "kernel": "k_encode_rows<PRETTY>", "kernel_ms": ms,
+                            "output_bytes": out.numel(), "alg_frac_hbm": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS}
+    del out
+    ms_sel, (body, m) = _kernel_ms(codec, lambda: codec.encode_by_status(dev, 1, pj.FORMAT_ARRAY), steps, 1, -1)
+    sel_ms = codec.timings()[-2]                   # k_select_status, same call
+    res["by_status_encode"] = {"records": cols.n_pets, "selected": m, "status_mask": 1,
+                               "kernel": "k_select_status + k_encode_rows", "select_ms": sel_ms, "encode_ms": ms_sel,
+                               "output_bytes": body.numel()}
+    del body, dev, cols
+    torch.cuda.empty_cache()
+    # every property present and empty strings kept (ALWAYS), so that the
+    # decoded columns must equal the encoded ones exactly
+    codec.set_options(pj.INCLUDE_ALWAYS)
+    for name, model in (("order", pj.MODEL_ORDER), ("user", pj.MODEL_USER)):
+        mc = pj.generate_model(model, 4_000_000, seed=1, null_rate=0.0, fancy=False)
+        md = mc.to_device()
+        ib = _model_bytes(mc)
+        ems, text = _kernel_ms(codec, lambda: codec.encode_model(md, pj.FORMAT_NDJSON), steps, 1, -1)
+        text = text.clone()
+        dms, (dc, el, ec, r) = _kernel_ms(codec, lambda: codec.decode_model(model, text), steps, 1, -1)
+        n = mc.n
+        same = r.n_pets == n and r.n_errors == 0 and torch.equal(dc.present[:n], md.present[:n])
+        for k, (_, kind) in enumerate(mc.props):
+            cnt = n + 1 if kind == "str" else n
+            same = same and torch.equal(dc.col[k][:cnt], md.col[k][:cnt])
+            if kind == "str":
+                nb = int(mc.col[k][-1])
+                same = same and torch.equal(dc.bytes[k][:nb], md.bytes[k][:nb])
+        res[name + "_encode"] = {"records": mc.n, "kernel": "k_encode_model", "kernel_ms": ems,
+                                 "output_bytes": text.numel(),
+                                 "alg_frac_hbm": (ib + text.numel()) / (ems * 1e-3) / 1e9 / HBM_PEAK_GBPS}
+        res[name + "_decode"] = {"records": mc.n, "kernel": "k_mdec_count + k_mdec_scan + k_mdec_write",
+                                 "kernels_ms": dms, "roundtrip_columns_equal": bool(same),
+                                 "alg_frac_hbm": (ib + text.numel()) / (dms * 1e-3) / 1e9 / HBM_PEAK_GBPS}
+        del md, text, dc
+        torch.cuda.empty_cache()
+    codec.set_options()
+    return res
+
+
 def cpu_baseline_decode(n_sample, budget_s=10.0):
     """Oracle decode of a bounded sample of the decode workload (config 4
     generator, NDJSON, 0.1% corrupted): median of 5 windows on one thread,
@@ -338,6 +414,9 @@ def main():
         torch.cuda.empty_cache()
     if not a.no_extra and not a.no_decode:
         workloads["ndjson_decode"] = decode_workload(codec, a.decode_records, max(3, a.steps // 2), 1)
+        torch.cuda.empty_cache()
+    if not a.no_extra:
+        workloads["options"] = option_workloads(codec, max(3, a.steps // 4))
         torch.cuda.empty_cache()
     cpu = cpu_baseline_encode(cfg, 200_000 if cfg == 2 else 50_000, a.cpu_budget)
     cpu_dec = cpu_baseline_decode(50_000, a.cpu_budget) if not a.no_extra else None

@@ -498,7 +498,7 @@ pj_status pj_encode_by_status_device(pj_ctx *ctx, const pj_pet_columns *cols, ui
     const uint64_t n = cols->n_pets, bt = (uint64_t)pj_encode_pretty_records(), nblk = (n + bt - 1) / bt;
     // scan buffer: selection (ticket, count, look-back words), encode
     // (ticket, total, look-back words), the selected indices
-    const uint64_t w_sel = 2 + nblk, w_enc = 2 + nblk;
+    const uint64_t w_sel = 2 + pj_select_blocks(n), w_enc = 2 + nblk;
     PJ_HIP(ctx->scan.ensure((w_sel + w_enc + n + 1) * sizeof(uint64_t)));
     uint64_t *sc = static_cast<uint64_t *>(ctx->scan.p), *ec = sc + w_sel, *sel = ec + w_enc;
     EncParams P;

@@ -1340,8 +1340,10 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
 // (P.sel: output record j is column record sel[j]; compact or pretty).  Each
 // thread measures its record from global memory, a block scan places the
 // records, the look-back gives the block's offset, and each thread writes
-// its record with exact stores.  Records that would end past the capacity
-// are not written; the last block stores the total.
+// its record with exact stores.  (Staging a block's output in LDS for
+// aligned stores measured slower: these blocks rarely fit a tile that
+// leaves room for other workgroups.)  Records that would end past the
+// capacity are not written; the last block stores the total.
 template <int BT, bool PRETTY>
 __global__ __launch_bounds__(BT) void k_encode_rows(EncParams P) {
     __shared__ uint64_t sh_scan[BT / 64 + 2];
@@ -1381,24 +1383,29 @@ __global__ __launch_bounds__(BT) void k_encode_rows(EncParams P) {
 }
 
 // The records whose status code is in the mask (bit s: status s, bit 3: no
-// status), in input order: each block's selected indices placed by a block
-// scan and the look-back.  The last block stores the count.
-template <int BT>
+// status), in input order: R consecutive records per thread, each block's
+// selected indices placed by a block scan and the look-back.  The last
+// block stores the count.
+template <int BT, int R>
 __global__ __launch_bounds__(BT) void k_select_status(EncParams P, uint32_t mask, uint64_t *sel) {
     __shared__ uint64_t sh_scan[BT / 64 + 2];
     __shared__ uint64_t sh_b, sh_base;
     const uint32_t t = threadIdx.x;
     if (t == 0) sh_b = atomicAdd(P.ticket, 1ull);
     __syncthreads();
-    const uint64_t b = sh_b, n = P.c.n_pets, nblk = (n + BT - 1) / BT;
-    const uint64_t i = b * BT + t;
-    uint64_t hit = 0;
-    if (i < n) {
-        const uint32_t st = P.c.status ? P.c.status[i] : (uint32_t)PJ_STATUS_NULL;
-        hit = (mask >> (st <= 2 ? st : 3)) & 1u;
+    const uint64_t b = sh_b, n = P.c.n_pets, nblk = (n + (uint64_t)BT * R - 1) / ((uint64_t)BT * R);
+    const uint64_t i0 = (b * BT + t) * R;
+    uint32_t hits = 0;                              // bit k: record i0 + k is selected
+#pragma unroll
+    for (int k = 0; k < R; k++) {
+        const uint64_t i = i0 + k;
+        if (i < n) {
+            const uint32_t st = P.c.status ? P.c.status[i] : (uint32_t)PJ_STATUS_NULL;
+            hits |= ((mask >> (st <= 2 ? st : 3)) & 1u) << k;
+        }
     }
     uint64_t agg;
-    const uint64_t pre = block_excl_scan<BT>(hit, sh_scan, &agg);
+    const uint64_t pre = block_excl_scan<BT>((uint64_t)__builtin_popcount(hits), sh_scan, &agg);
     if (t < 64) {
         const uint64_t excl = lookback(P.state, b, agg);
         if (t == 0) {
@@ -1407,7 +1414,8 @@ __global__ __launch_bounds__(BT) void k_select_status(EncParams P, uint32_t mask
         }
     }
     __syncthreads();
-    if (hit) sel[sh_base + pre] = i;
+    uint64_t o = sh_base + pre;
+    for (uint32_t m = hits; m; m &= m - 1) sel[o++] = i0 + __builtin_ctz(m);
 }
 
 // ------------------------------------------------- Order and User records
@@ -1668,27 +1676,36 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
 }
 
-constexpr int ENC_PRETTY_BT = 256;
+// 512-record blocks: measured fastest (256 with three workgroups per CU
+// about the same; 128 and 64 slower, as more blocks chain their look-backs)
+#ifndef PJ_ENC_ROWS_BT
+#define PJ_ENC_ROWS_BT 512
+#endif
+constexpr int ENC_PRETTY_BT = PJ_ENC_ROWS_BT;
 int pj_encode_pretty_records() { return ENC_PRETTY_BT; }
+
+constexpr int ENC_SEL_BT = 256, ENC_SEL_R = 16;
 
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st) {
     const uint64_t nblk = (P.n + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
     if (pretty)
-        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, true>), dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, true>), dim3((unsigned)nblk),
+                           dim3(ENC_PRETTY_BT), 0, st, P);
     else
-        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, false>), dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st,
-                           P);
+        hipLaunchKernelGGL((pj::k_encode_rows<ENC_PRETTY_BT, false>), dim3((unsigned)nblk),
+                           dim3(ENC_PRETTY_BT), 0, st, P);
     return hipGetLastError();
 }
+
+uint64_t pj_select_blocks(uint64_t n) { return (n + ENC_SEL_BT * ENC_SEL_R - 1) / (ENC_SEL_BT * ENC_SEL_R); }
 
 hipError_t pj_launch_select_status(const EncParams &P, uint32_t mask, uint64_t *sel, hipStream_t st) {
-    const uint64_t nblk = (P.c.n_pets + ENC_PRETTY_BT - 1) / ENC_PRETTY_BT;
-    hipLaunchKernelGGL(pj::k_select_status<ENC_PRETTY_BT>, dim3((unsigned)nblk), dim3(ENC_PRETTY_BT), 0, st, P, mask,
-                       sel);
+    hipLaunchKernelGGL((pj::k_select_status<ENC_SEL_BT, ENC_SEL_R>), dim3((unsigned)pj_select_blocks(P.c.n_pets)),
+                       dim3(ENC_SEL_BT), 0, st, P, mask, sel);
     return hipGetLastError();
 }
 
-constexpr int ENC_MODEL_BT = 256;
+constexpr int ENC_MODEL_BT = 512;   // as for k_encode_rows: larger blocks, fewer chained look-backs
 int pj_encode_model_records() { return ENC_MODEL_BT; }
 
 hipError_t pj_launch_encode_model(const ModelEncParams &P, hipStream_t st) {

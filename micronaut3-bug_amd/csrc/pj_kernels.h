@@ -142,6 +142,7 @@ int pj_encode_block_records(bool nested);
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);
 // indices of the records whose status is in mask into sel, their count into *P.total
 hipError_t pj_launch_select_status(const EncParams &P, uint32_t mask, uint64_t *sel, hipStream_t st);
+uint64_t pj_select_blocks(uint64_t n);   // workgroups (look-back words) of the selection kernel
 hipError_t pj_launch_encode_model(const ModelEncParams &P, hipStream_t st);
 int pj_encode_model_records();
 hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_t st);
