@@ -217,11 +217,11 @@ constexpr uint32_t pack4(const char *s, int k) {
 
 // ------------------------------------------------------- memory helpers
 // Unaligned 8-byte global load (gfx950 global memory is in unaligned mode).
-__device__ __forceinline__ uint64_t ldu64(const uint8_t *p) { return *reinterpret_cast<const uint64_t *>(p); }
+__host__ __device__ __forceinline__ uint64_t ldu64(const uint8_t *p) { return *reinterpret_cast<const uint64_t *>(p); }
 
 // The n (1..7) bytes at p, touching only aligned qwords that hold some of
 // them (so never a page past the end of the buffer).
-__device__ __forceinline__ uint64_t ld_tail(const uint8_t *p, int n) {
+__host__ __device__ __forceinline__ uint64_t ld_tail(const uint8_t *p, int n) {
     // The aligned address is formed as an integer on purpose: written as
     // pointer arithmetic (p - (p & 7)) on a generic pointer, the compiler may
     // fold a constant into the flat load's immediate offset and leave a base
@@ -249,11 +249,11 @@ __device__ __forceinline__ uint64_t special64(uint64_t x) {
 // Exact-size stores at any byte address (gfx950 runs global memory in
 // unaligned mode; bytes outside [p, p+n) are never written, so neighbouring
 // writers need no coordination).
-__device__ __forceinline__ void stu64(uint8_t *p, uint64_t v) { *reinterpret_cast<uint64_t *>(p) = v; }
-__device__ __forceinline__ void stu32(uint8_t *p, uint32_t v) { *reinterpret_cast<uint32_t *>(p) = v; }
-__device__ __forceinline__ void stu16(uint8_t *p, uint32_t v) { *reinterpret_cast<uint16_t *>(p) = (uint16_t)v; }
+__host__ __device__ __forceinline__ void stu64(uint8_t *p, uint64_t v) { *reinterpret_cast<uint64_t *>(p) = v; }
+__host__ __device__ __forceinline__ void stu32(uint8_t *p, uint32_t v) { *reinterpret_cast<uint32_t *>(p) = v; }
+__host__ __device__ __forceinline__ void stu16(uint8_t *p, uint32_t v) { *reinterpret_cast<uint16_t *>(p) = (uint16_t)v; }
 // the low n (0..7) bytes of v
-__device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
+__host__ __device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
     if (n & 4) { stu32(p, (uint32_t)v); p += 4; v >>= 32; }
     if (n & 2) { stu16(p, (uint32_t)v); p += 2; v >>= 16; }
     if (n & 1) *p = (uint8_t)v;
@@ -266,18 +266,18 @@ __device__ __forceinline__ void st_tail(uint8_t *p, uint64_t v, uint32_t n) {
 #else
 #define PJ_LDS
 #endif
-__device__ __forceinline__ uint64_t lds_u64(const PJ_LDS uint8_t *p) { return *(const PJ_LDS uint64_t *)p; }
+__host__ __device__ __forceinline__ uint64_t lds_u64(const PJ_LDS uint8_t *p) { return *(const PJ_LDS uint64_t *)p; }
 // n bytes from an LDS buffer to dst, exactly (no byte outside [dst, dst+n)
 // is written).  Scattered per-thread copies are bound by the number of store
 // instructions, so: 16-byte stores at any address, the last one ending at
 // the last byte and overlapping its predecessor (the overlapped bytes get
 // the same values again); below 16 bytes two overlapping 8-, 4- or 2-byte
 // stores, or one byte.
-__device__ __forceinline__ void st16(uint8_t *p, const PJ_LDS uint8_t *s) {
+__host__ __device__ __forceinline__ void st16(uint8_t *p, const PJ_LDS uint8_t *s) {
     const uint64_t a = lds_u64(s), b = lds_u64(s + 8);
     *reinterpret_cast<uint4 *>(p) = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
 }
-__device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t *src, uint32_t n) {
+__host__ __device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t *src, uint32_t n) {
     if (n >= 16) {
         for (uint32_t k = 0; k + 16 < n; k += 16) st16(dst + k, src + k);
         st16(dst + n - 16, src + n - 16);
@@ -297,9 +297,13 @@ __device__ __forceinline__ void copy_from_lds(uint8_t *dst, const PJ_LDS uint8_t
 // of the pair, then byte qb = q % 4 of it, joined with v_alignbyte.  qd is
 // the same for every lane (it follows the block's base address), so the
 // branch is uniform.
-__device__ __forceinline__ uint4 funnel16(const uint4 &L, const uint4 &H, uint32_t qd, uint32_t qb) {
+__host__ __device__ __forceinline__ uint4 funnel16(const uint4 &L, const uint4 &H, uint32_t qd, uint32_t qb) {
     const uint32_t d0 = L.x, d1 = L.y, d2 = L.z, d3 = L.w, d4 = H.x, d5 = H.y, d6 = H.z, d7 = H.w;
+#if defined(__HIP_DEVICE_COMPILE__)
 #define PJ_AB(h, l) __builtin_amdgcn_alignbyte(h, l, qb)
+#else   // host build of the helpers (index checks): the same byte funnel
+#define PJ_AB(h, l) (uint32_t)((((uint64_t)(h) << 32) | (l)) >> (8 * (qb & 3)))
+#endif
     switch (qd) {
     case 0: return make_uint4(PJ_AB(d1, d0), PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3));
     case 1: return make_uint4(PJ_AB(d2, d1), PJ_AB(d3, d2), PJ_AB(d4, d3), PJ_AB(d5, d4));
@@ -316,11 +320,12 @@ __device__ __forceinline__ uint4 funnel16(const uint4 &L, const uint4 &H, uint32
 // bytes [16c - s, 16c - s + 16): the tail of aligned tile word c-1 and the
 // head of word c, joined by funnel16.  Whole chunks leave with one
 // aligned 16-byte store; the first and last chunks (shared with neighbouring
-// blocks or segments) with exact 8/4/2/1-byte stores.  The tile must be
-// readable 16 bytes past hi - D.
+// blocks or segments) with exact 8/4/2/1-byte stores.  Whole aligned tile
+// words are read, the last one holding global byte g0 + 16 c_hi - 1: up to
+// 29 bytes past hi - D, so the tile must be readable 32 bytes past hi - D.
 template <int BT>
-__device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo, uint64_t hi,
-                                              uint32_t t = threadIdx.x) {
+__host__ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out, uint64_t D, uint64_t lo,
+                                                       uint64_t hi, uint32_t t) {
     const uint32_t s = (uint32_t)(D & 15);
     const uint32_t qd = (16 - s) >> 2, qb = (16 - s) & 3;
     const uint64_t g0 = D - s;
@@ -361,7 +366,7 @@ __device__ __forceinline__ void tile_copy_out(const uint8_t *tile, uint8_t *out,
 }
 
 // n bytes from src (LDS or global, readable up to 8 bytes past the end) to dst
-__device__ __forceinline__ void copy_exact(uint8_t *dst, const uint8_t *src, uint32_t n) {
+__host__ __device__ __forceinline__ void copy_exact(uint8_t *dst, const uint8_t *src, uint32_t n) {
     uint32_t k = 0;
     for (; k + 16 <= n; k += 16) {
         const uint64_t a = ldu64(src + k), b = ldu64(src + k + 8);
@@ -377,8 +382,8 @@ struct StoreSink {
     uint8_t *p;
     uint64_t acc;
     uint32_t nacc;
-    __device__ __forceinline__ void init(uint8_t *dst) { p = dst; acc = 0; nacc = 0; }
-    __device__ __forceinline__ void put(uint32_t w, int k) {     // k (1..4) bytes of w
+    __host__ __device__ __forceinline__ void init(uint8_t *dst) { p = dst; acc = 0; nacc = 0; }
+    __host__ __device__ __forceinline__ void put(uint32_t w, int k) {     // k (1..4) bytes of w
         const uint64_t v = (uint64_t)w & ((1ull << (8 * k)) - 1);
         acc |= v << (8 * nacc);
         const uint32_t tot = nacc + (uint32_t)k;
@@ -389,7 +394,7 @@ struct StoreSink {
             nacc = tot - 8;
         } else nacc = tot;
     }
-    __device__ __forceinline__ void put8(uint64_t v, uint32_t k) {  // k (1..8) bytes of v
+    __host__ __device__ __forceinline__ void put8(uint64_t v, uint32_t k) {  // k (1..8) bytes of v
         if (k < 8) v &= (1ull << (8 * k)) - 1;
         acc |= v << (8 * nacc);
         const uint32_t tot = nacc + k;
@@ -400,7 +405,7 @@ struct StoreSink {
             nacc = tot - 8;
         } else nacc = tot;
     }
-    __device__ __forceinline__ void finish() { st_tail(p, acc, nacc); }
+    __host__ __device__ __forceinline__ void finish() { st_tail(p, acc, nacc); }
 };
 
 struct WriteSink {
@@ -410,7 +415,7 @@ struct WriteSink {
     uint32_t head;
     int nacc, lead;
 
-    __device__ __forceinline__ void init(uint8_t *o, uint64_t p, uint32_t *dummy) {
+    __host__ __device__ __forceinline__ void init(uint8_t *o, uint64_t p, uint32_t *dummy) {
         out = o;
         ps = ps0 = p & ~3ull;
         lead = nacc = (int)(p & 3);
@@ -418,7 +423,7 @@ struct WriteSink {
         head = 0;
         dst = lead ? dummy : reinterpret_cast<uint32_t *>(out + ps);
     }
-    __device__ __forceinline__ void put(uint32_t w, int k) {
+    __host__ __device__ __forceinline__ void put(uint32_t w, int k) {
         uint64_t m = (1ull << (8 * k)) - 1;
         acc |= ((uint64_t)w & m) << (8 * nacc);
         nacc += k;
@@ -431,14 +436,14 @@ struct WriteSink {
             nacc -= 4;
         }
     }
-    __device__ __forceinline__ void put8(uint64_t x, int k) {
+    __host__ __device__ __forceinline__ void put8(uint64_t x, int k) {
         if (k > 4) { put((uint32_t)x, 4); put((uint32_t)(x >> 32), k - 4); }
         else if (k > 0) put((uint32_t)x, k);
     }
-    __device__ __forceinline__ void put_byte(uint32_t b) { put(b & 0xFF, 1); }
-    __device__ __forceinline__ void skip(uint32_t) {}
-    __device__ __forceinline__ uint32_t pos() const { return 0; }
-    __device__ __forceinline__ void finish() {
+    __host__ __device__ __forceinline__ void put_byte(uint32_t b) { put(b & 0xFF, 1); }
+    __host__ __device__ __forceinline__ void skip(uint32_t) {}
+    __host__ __device__ __forceinline__ uint32_t pos() const { return 0; }
+    __host__ __device__ __forceinline__ void finish() {
         if (ps == ps0) {
             for (int b = lead; b < nacc; b++) out[ps + b] = (uint8_t)(acc >> (8 * b));
             return;

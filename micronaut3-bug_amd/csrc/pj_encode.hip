@@ -1176,7 +1176,8 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         // ---- block scan, publish the aggregate
         if (!(NESTED && fast)) pre = block_excl_scan<BT>(len, sh_scan, &agg);
         if (t == 0) lb_publish(P.state, b, agg);
-        const bool fits = fast && agg + 16 <= TILE;
+        // (the copy-out reads up to 32 bytes past the block's bytes)
+        const bool fits = fast && agg + 32 <= TILE;
         if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
         // Hybrid block (NESTED, fallback measuring): the records other than the
         // large ones still go through the tile, laid end to end (tile offset
@@ -1187,7 +1188,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         if (NESTED && !fast) {
             uint64_t stot;
             spre = block_excl_scan<BT>(isbig ? 0ull : len, sh_scan, &stot);
-            hyb = stot + 16 <= TILE;
+            hyb = stot + 32 <= TILE;
             if (isbig) {
                 sh_bpre[bidx] = (uint32_t)pre;
                 sh_blen[bidx] = (uint32_t)len;
@@ -1277,7 +1278,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         } else if (fits) {
             const uint64_t end = min(base + agg, P.cap);
             if (base < end) {
-                if (!PERSIST) tile_copy_out<BT>(tile, P.out, base, base, end);
+                if (!PERSIST) tile_copy_out<BT>(tile, P.out, base, base, end, t);
                 else if (t >= 64) {
                     tile_copy_out<BT - 64>(tile, P.out, base, base, end, t - 64);
                     EPROF(7);
@@ -1288,7 +1289,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 const uint64_t g_lo = k ? (uint64_t)sh_bpre[k - 1] + sh_blen[k - 1] : 0, g_hi = k < nbig ? sh_bpre[k] : agg;
                 const uint64_t t_lo = k ? sh_bspre[k - 1] : 0;
                 const uint64_t lo = base + g_lo, hi = min(base + g_hi, P.cap);
-                if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi);
+                if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi, t);
             }
             for (uint32_t k = 0; k < nbig; k++) {
                 const uint64_t p = base + sh_bpre[k];
