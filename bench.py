@@ -10,7 +10,7 @@ figures under "workloads", each with its own fraction of the HBM roofline,
 the roofline of the headline kernel measured with HIP events on the codec's
 stream, and the CPU restatement timed on this host's cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload nested|flat|decode|skew]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload nested|flat|decode|skew|options]
 """
 import argparse
 import json
@@ -361,9 +361,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="nested", choices=["flat", "nested", "decode", "skew"],
+    ap.add_argument("--workload", default="nested", choices=["flat", "nested", "decode", "skew", "options"],
                     help="headline workload; 'decode' runs only the NDJSON decode and 'skew' only the "
-                         "configs[4] encode + decode round trip (for profiling)")
+                         "configs[4] encode + decode round trip, 'options' only the pretty, findPetsByStatus and "
+                         "Order / User paths (for profiling)")
     ap.add_argument("--records", type=int, default=10_000_000)
     ap.add_argument("--decode-records", type=int, default=14_600_000)
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
@@ -393,6 +394,10 @@ def main():
     if a.workload == "skew":
         print(json.dumps({"skew_encode": skew_workload(codec, 2_000_000, a.steps, a.warmup, not a.no_decode)}),
               flush=True)
+        codec.close()
+        return
+    if a.workload == "options":
+        print(json.dumps({"options": option_workloads(codec, a.steps)}), flush=True)
         codec.close()
         return
     if a.workload == "decode":

@@ -1175,6 +1175,7 @@ extern "C" pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_
     ModelDecParams M;
     std::memset(&M, 0, sizeof M);
     M.in = in;
+    M.len = len;
     M.line_start = P.line_start;
     M.lines = lines;
     M.o = *out;

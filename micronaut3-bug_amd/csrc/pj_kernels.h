@@ -46,6 +46,7 @@ struct ModelEncParams {
 constexpr int MD_MAXK = 2 + PJ_MODEL_MAX_PROPS;   // valid, errors, one per string property
 struct ModelDecParams {
     const uint8_t *in;
+    uint64_t len;              // input bytes
     const uint64_t *line_start;// record l spans [line_start[l], line_start[l+1] - 1)
     uint64_t lines;
     pj_model_columns o;        // outputs with capacities

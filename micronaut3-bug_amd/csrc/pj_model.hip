@@ -56,6 +56,14 @@ struct MOut {
         else if (k < 16) w1 |= (uint64_t)(b & 0xFF) << (8 * (k - 8));
         k++;
     }
+    __device__ __forceinline__ void put8(uint64_t x) {   // 8 bytes at once
+        if (k < 16) {
+            for (int j = 0; j < 8; j++) put((uint32_t)(x >> (8 * j)));
+            return;
+        }
+        if (dst) stu64(dst + k, x);
+        k += 8;
+    }
 };
 
 __device__ __forceinline__ bool m_u4(MLine &L, uint32_t *cu) {
@@ -74,9 +82,17 @@ __device__ __forceinline__ bool m_u4(MLine &L, uint32_t *cu) {
 // A string starting at its opening quote: escapes (\uXXXX pairs joined,
 // lone surrogates rejected), no raw controls, UTF-8 lead bytes C0-DF /
 // E0-EF / F0-F7 each with its 10xxxxxx continuations.
-__device__ int m_string(MLine &L, MOut &o) {
+__device__ __forceinline__ int m_string(MLine &L, MOut &o) {
     L.p++;
     for (;;) {
+        // 8 bytes at a time while none is a quote, a backslash, a control
+        // byte or a UTF-8 byte
+        while (L.p + 8 <= L.n) {
+            const uint64_t x = ldu64(L.s + L.p);
+            if (special64(x) | (x & (0x80 * ONES))) break;
+            o.put8(x);
+            L.p += 8;
+        }
         if (m_end(L)) return PJ_REC_STRING;
         const uint32_t c = L.s[L.p];
         if (c == '"') {
@@ -145,7 +161,7 @@ __device__ int m_string(MLine &L, MOut &o) {
 
 // A number token (RFC 8259 grammar): T_INT without fraction or exponent,
 // with its value in *v and *big set when it is outside the int64 range.
-__device__ int m_number(MLine &L, int *kind, int64_t *v, bool *big) {
+__device__ __forceinline__ int m_number(MLine &L, int *kind, int64_t *v, bool *big) {
     const uint8_t *s = L.s;
     uint64_t p = L.p;
     const bool neg = p < L.n && s[p] == '-';
@@ -187,7 +203,7 @@ __device__ int m_number(MLine &L, int *kind, int64_t *v, bool *big) {
 }
 
 // A literal (null, true, false) or a number.
-__device__ int m_scalar(MLine &L, int *kind, int64_t *v, bool *big) {
+__device__ __forceinline__ int m_scalar(MLine &L, int *kind, int64_t *v, bool *big) {
     const uint32_t c = m_cur(L);
     if (c == '-' || (c >= '0' && c <= '9')) return m_number(L, kind, v, big);
     uint32_t lit, len;
@@ -206,7 +222,7 @@ __device__ int m_scalar(MLine &L, int *kind, int64_t *v, bool *big) {
 
 // A known property holding a value of the wrong JSON type: literals and
 // numbers are still tokenised first (a malformed one is a syntax error).
-__device__ int m_type_mismatch(MLine &L) {
+__device__ __forceinline__ int m_type_mismatch(MLine &L) {
     const uint32_t c = m_cur(L);
     if (c == '"' || c == '{' || c == '[') return PJ_REC_TYPE;
     int kind;
@@ -216,9 +232,12 @@ __device__ int m_type_mismatch(MLine &L) {
     return e ? e : PJ_REC_TYPE;
 }
 
-// Any value, validated and skipped; depth0 containers are open around it.
-// Containers opened here are kept on a bit stack (1 = object).
-__device__ __noinline__ int m_skip(MLine &L, int depth0) {
+// Any value at p, validated and skipped; depth0 containers are open around
+// it.  Containers opened here are kept on a bit stack (1 = object).  Out of
+// line (unknown properties are rare), with the line passed by value so the
+// callers' cursor stays in registers; *p_out receives the position after
+// the value.
+__device__ __forceinline__ int m_skip_body(MLine &L, int depth0) {
     uint64_t stk[(PJ_MAX_DEPTH + 63) / 64];
     int d = 0;
     int kind, e;
@@ -288,6 +307,13 @@ __device__ __noinline__ int m_skip(MLine &L, int depth0) {
     }
 }
 
+__device__ __noinline__ int m_skip(const uint8_t *s, uint64_t n, uint64_t p, int depth0, uint64_t *p_out) {
+    MLine L{s, n, p};
+    const int r = m_skip_body(L, depth0);
+    *p_out = L.p;
+    return r;
+}
+
 // ------------------------------------------------------------- schemas
 constexpr uint64_t pk8(const char *s, int n, int w) {
     uint64_t r = 0;
@@ -305,6 +331,9 @@ struct MProp {
 template <int MODEL> struct MSchema;
 template <> struct MSchema<PJ_MODEL_ORDER> {
     static constexpr int N = 6;
+    static constexpr int kind(int k) {
+        return k < 2 ? K_I64 : k == 2 ? K_I32 : k == 3 ? K_STR : k == 4 ? K_ENUM : K_BOOL;
+    }
     __device__ static MProp prop(int k) {
         constexpr MProp P[6] = {MPROP("id", K_I64),       MPROP("petId", K_I64),  MPROP("quantity", K_I32),
                                 MPROP("shipDate", K_STR), MPROP("status", K_ENUM), MPROP("complete", K_BOOL)};
@@ -313,6 +342,7 @@ template <> struct MSchema<PJ_MODEL_ORDER> {
 };
 template <> struct MSchema<PJ_MODEL_USER> {
     static constexpr int N = 8;
+    static constexpr int kind(int k) { return k == 0 ? K_I64 : k == 7 ? K_I32 : K_STR; }
     __device__ static MProp prop(int k) {
         constexpr MProp P[8] = {MPROP("id", K_I64),        MPROP("username", K_STR), MPROP("firstName", K_STR),
                                 MPROP("lastName", K_STR),  MPROP("email", K_STR),    MPROP("password", K_STR),
@@ -345,13 +375,15 @@ struct MRec {
     uint64_t slen[PJ_MODEL_MAX_PROPS];   // decoded bytes
 };
 
-template <int MODEL> __device__ int m_value(MLine &L, int f, MRec &R) {
-    const MProp pr = MSchema<MODEL>::prop(f);
+// Property F's value at L.p (every index static, so R stays in registers).
+template <int MODEL, int F> __device__ __forceinline__ int m_value(MLine &L, MRec &R) {
+    constexpr int KIND = MSchema<MODEL>::kind(F);
+    constexpr int f = F;
     const uint32_t c = m_cur(L);
     int kind, e;
     int64_t v = 0;
     bool big = false, pres = false;
-    if (pr.kind == K_I64 || pr.kind == K_I32) {
+    if (KIND == K_I64 || KIND == K_I32) {
         if (c == 'n') {
             if ((e = m_scalar(L, &kind, &v, &big))) return e;
             if (kind != T_NULL) return PJ_REC_TYPE;
@@ -359,16 +391,16 @@ template <int MODEL> __device__ int m_value(MLine &L, int f, MRec &R) {
         } else if (c == '-' || (c >= '0' && c <= '9')) {
             if ((e = m_number(L, &kind, &v, &big))) return e;
             if (kind != T_INT || big) return PJ_REC_NUMBER;
-            if (pr.kind == K_I32 && (v < -2147483648ll || v > 2147483647ll)) return PJ_REC_NUMBER;
+            if (KIND == K_I32 && (v < -2147483648ll || v > 2147483647ll)) return PJ_REC_NUMBER;
             pres = true;
         } else return m_type_mismatch(L);
-    } else if (pr.kind == K_STR || pr.kind == K_ENUM) {
+    } else if (KIND == K_STR || KIND == K_ENUM) {
         if (c == '"') {
             const uint64_t q = L.p;
             MOut o{nullptr};
             if ((e = m_string(L, o))) return e;
             pres = true;
-            if (pr.kind == K_STR) {
+            if (KIND == K_STR) {
                 R.spos[f] = q;
                 R.slen[f] = o.k;
             } else {
@@ -401,7 +433,7 @@ template <int MODEL> __device__ int m_value(MLine &L, int f, MRec &R) {
 }
 
 // One record [s, s + n): its PJ_REC_* code, and its values in R.
-template <int MODEL> __device__ int m_line(const uint8_t *s, uint64_t n, MRec &R) {
+template <int MODEL> __device__ __forceinline__ int m_line(const uint8_t *s, uint64_t n, MRec &R) {
     MLine L{s, n, 0};
     R.present = 0;
 #pragma unroll
@@ -430,8 +462,22 @@ template <int MODEL> __device__ int m_line(const uint8_t *s, uint64_t n, MRec &R
             m_skip_ws(L);
             if (m_end(L)) return PJ_REC_SYNTAX;
             const int f = key.k <= 16 ? m_prop_of<MODEL>(key) : -1;
-            if (f < 0) e = m_skip(L, 1);
-            else e = m_value<MODEL>(L, f, R);
+            switch (f) {
+            case 0: e = m_value<MODEL, 0>(L, R); break;
+            case 1: e = m_value<MODEL, 1>(L, R); break;
+            case 2: e = m_value<MODEL, 2>(L, R); break;
+            case 3: e = m_value<MODEL, 3>(L, R); break;
+            case 4: e = m_value<MODEL, 4>(L, R); break;
+            case 5: e = m_value<MODEL, 5>(L, R); break;
+            case 6: e = MSchema<MODEL>::N > 6 ? m_value<MODEL, 6 % MSchema<MODEL>::N>(L, R) : PJ_REC_OK; break;
+            case 7: e = MSchema<MODEL>::N > 7 ? m_value<MODEL, 7 % MSchema<MODEL>::N>(L, R) : PJ_REC_OK; break;
+            default: {
+                uint64_t np;
+                e = m_skip(L.s, L.n, L.p, 1, &np);
+                L.p = np;
+                break;
+            }
+            }
             if (e) return e;
             m_skip_ws(L);
             if (m_end(L)) return PJ_REC_SYNTAX;
@@ -450,31 +496,71 @@ template <int MODEL> __device__ int m_line(const uint8_t *s, uint64_t n, MRec &R
     return m_end(L) ? PJ_REC_OK : PJ_REC_SYNTAX;
 }
 
+// A block's records, staged: the input bytes [g0, a1) (g0 = the first
+// record's start rounded down to 16 bytes, a1 = the last record's end) in
+// LDS when they fit the tile, read with 16-byte loads (exact at the input's
+// end).  Every record is then read from LDS; a block that does not fit reads
+// from global memory.
+struct MStage {
+    const uint8_t *tile;
+    uint64_t g0;
+    bool staged;
+    __device__ __forceinline__ const uint8_t *at(const ModelDecParams &P, uint64_t a) const {
+        return staged ? tile + (a - g0) : P.in + a;
+    }
+};
+
+template <int BT, int TILE>
+__device__ __forceinline__ MStage m_stage(const ModelDecParams &P, uint8_t *tile, uint64_t b) {
+    const uint64_t l0 = b * BT, l1 = min(l0 + BT, P.lines);
+    const uint64_t a0 = P.line_start[l0], a1 = P.line_start[l1] - 1, g0 = a0 & ~15ull;
+    const bool staged = a1 - g0 <= (uint64_t)TILE;
+    if (staged) {
+        const uint32_t nch = (uint32_t)((a1 - g0 + 15) >> 4);
+        for (uint32_t c = threadIdx.x; c < nch; c += BT) {
+            const uint64_t g = g0 + 16ull * c;
+            uint4 v;
+            if (g + 16 <= P.len) v = *reinterpret_cast<const uint4 *>(P.in + g);
+            else {
+                uint32_t x[4] = {0, 0, 0, 0};
+                for (uint32_t j = 0; j < 16 && g + j < P.len; j++) x[j >> 2] |= (uint32_t)P.in[g + j] << (8 * (j & 3));
+                v = make_uint4(x[0], x[1], x[2], x[3]);
+            }
+            reinterpret_cast<uint4 *>(tile)[c] = v;
+        }
+    }
+    __syncthreads();
+    return MStage{tile, g0, staged};
+}
+
 // The record's counters: [0] valid, [1] invalid, [2 + k] decoded bytes of
 // string property k; and whether it is blank.
 template <int MODEL>
-__device__ __forceinline__ int m_read(const ModelDecParams &P, uint64_t l, MRec &R, uint64_t (&cnt)[MD_MAXK]) {
+__device__ __forceinline__ int m_read(const ModelDecParams &P, const MStage &S, uint64_t l, MRec &R,
+                                      uint64_t (&cnt)[MD_MAXK]) {
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) cnt[k] = 0;
     if (l >= P.lines) return -1;
     const uint64_t a = P.line_start[l], e = P.line_start[l + 1] - 1;
-    const int code = m_line<MODEL>(P.in + a, e - a, R);
+    const int code = m_line<MODEL>(S.at(P, a), e - a, R);
     if (code == PJ_REC_OK) {
         cnt[0] = 1;
 #pragma unroll
         for (int k = 0; k < MSchema<MODEL>::N; k++)
-            if (MSchema<MODEL>::prop(k).kind == K_STR) cnt[2 + k] = R.slen[k];
+            if (MSchema<MODEL>::kind(k) == K_STR) cnt[2 + k] = R.slen[k];
     } else cnt[1] = 1;
     return code;
 }
 
-template <int MODEL, int BT>
+template <int MODEL, int BT, int TILE>
 __global__ __launch_bounds__(BT) void k_mdec_count(ModelDecParams P) {
     __shared__ uint64_t sh[BT / 64 + 2];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 16];
     const uint64_t b = blockIdx.x, l = b * BT + threadIdx.x;
+    const MStage S = m_stage<BT, TILE>(P, tile, b);
     MRec R;
     uint64_t cnt[MD_MAXK];
-    const int code = m_read<MODEL>(P, l, R, cnt);
+    const int code = m_read<MODEL>(P, S, l, R, cnt);
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
@@ -508,13 +594,15 @@ __global__ __launch_bounds__(BT) void k_mdec_scan(ModelDecParams P) {
         for (int k = 0; k < MD_MAXK; k++) P.totals[k] = carry[k];
 }
 
-template <int MODEL, int BT>
+template <int MODEL, int BT, int TILE>
 __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
     __shared__ uint64_t sh[BT / 64 + 2];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 16];
     const uint64_t b = blockIdx.x, l = b * BT + threadIdx.x;
+    const MStage S = m_stage<BT, TILE>(P, tile, b);
     MRec R;
     uint64_t cnt[MD_MAXK], at[MD_MAXK];
-    const int code = m_read<MODEL>(P, l, R, cnt);
+    const int code = m_read<MODEL>(P, S, l, R, cnt);
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
@@ -536,12 +624,12 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
     const uint64_t a = P.line_start[l];
 #pragma unroll
     for (int k = 0; k < MSchema<MODEL>::N; k++) {
-        const int kind = MSchema<MODEL>::prop(k).kind;
+        const int kind = MSchema<MODEL>::kind(k);
         if (kind == K_STR) {
             const uint64_t s0 = at[2 + k], s1 = s0 + R.slen[k];
             if (fits) static_cast<uint64_t *>(o.col[k])[row + 1] = s1;
             if (R.slen[k] && s1 <= o.cap_bytes[k]) {
-                MLine L{P.in + a, P.line_start[l + 1] - 1 - a, R.spos[k]};
+                MLine L{S.at(P, a), P.line_start[l + 1] - 1 - a, R.spos[k]};
                 MOut w{o.bytes[k] + s0};
                 (void)m_string(L, w);
             }
@@ -556,20 +644,22 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
 }  // namespace
 }  // namespace pj
 
-constexpr int MDEC_BT = 256;
+// 128 records per block, staged in a 32 KiB tile (about 250 bytes per
+// record fit; longer blocks read global memory)
+constexpr int MDEC_BT = 128, MDEC_TILE = 32768;
 int pj_decode_model_block() { return MDEC_BT; }
 
 hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_t st) {
     const unsigned g = (unsigned)P.nblocks;
     if (!g) return hipSuccess;
     if (model == PJ_MODEL_ORDER)
-        hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_ORDER, MDEC_BT>), dim3(g), dim3(MDEC_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
-        hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_USER, MDEC_BT>), dim3(g), dim3(MDEC_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_USER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     hipLaunchKernelGGL(pj::k_mdec_scan<MDEC_BT>, dim3(1), dim3(MDEC_BT), 0, st, P);
     if (model == PJ_MODEL_ORDER)
-        hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_ORDER, MDEC_BT>), dim3(g), dim3(MDEC_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
-        hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_USER, MDEC_BT>), dim3(g), dim3(MDEC_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_USER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     return hipGetLastError();
 }
