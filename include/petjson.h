@@ -223,6 +223,10 @@ pj_status pj_encode_bound(const pj_pet_columns *cols, int format, uint64_t *boun
 pj_status pj_encode_by_status_device(pj_ctx *ctx, const pj_pet_columns *cols, uint32_t status_mask,
                                      int format, uint8_t *out, uint64_t out_cap, uint64_t *out_len,
                                      uint64_t *n_selected);
+/* Same as pj_encode_by_status_device with host pointers. */
+pj_status pj_encode_by_status_host(pj_ctx *ctx, const pj_pet_columns *cols, uint32_t status_mask,
+                                   int format, uint8_t *out, uint64_t out_cap, uint64_t *out_len,
+                                   uint64_t *n_selected);
 /* Same as pj_encode_device with host pointers. */
 pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
                          uint8_t *out, uint64_t out_cap, uint64_t *out_len);
@@ -341,6 +345,13 @@ pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_t *in, uint
                                  pj_model_columns *out, uint64_t *err_line, uint8_t *err_code,
                                  uint64_t err_cap, pj_decode_result *res);
 void      pj_decode_model_bounds(int model, uint64_t len, pj_model_columns *caps_out);
+/* The same two calls with host pointers (the columns, the text and the
+ * error lists in host memory; the device work is staged by the library). */
+pj_status pj_encode_model_host(pj_ctx *ctx, int model, const pj_model_columns *cols, int format,
+                               uint8_t *out, uint64_t out_cap, uint64_t *out_len);
+pj_status pj_decode_model_host(pj_ctx *ctx, int model, const uint8_t *in, uint64_t len, int array,
+                               pj_model_columns *out, uint64_t *err_line, uint8_t *err_code,
+                               uint64_t err_cap, pj_decode_result *res);
 
 #ifdef __cplusplus
 }

@@ -564,24 +564,65 @@ pj_status pj_encode_size_device(pj_ctx *ctx, const pj_pet_columns *cols, int for
     return encode_impl(ctx, cols, format, nullptr, 0, out_len, true);
 }
 
+}  // extern "C"
+
+namespace {
+// Host Pet columns copied into the context's input staging buffer; *dc
+// receives the same column set with device pointers.
+pj_status stage_pet_cols(pj_ctx *ctx, const pj_pet_columns *cols, pj_pet_columns *dc) {
+    pj_status s;
+    Layout L;
+    host_layout(cols, &L);
+    PJ_HIP(ctx->stage_in.ensure(L.total));
+    uint8_t *base = static_cast<uint8_t *>(ctx->stage_in.p);
+    void *hp[17], *dp[17];
+    pj_pet_columns hc = *cols;
+    *dc = *cols;
+    col_ptrs(&hc, hp);
+    for (int k = 0; k < 17; k++) {
+        dp[k] = hp[k] ? base + L.off[k] : nullptr;
+        if (hp[k] && L.size[k] && (s = h2d(ctx, dp[k], hp[k], L.size[k]))) return s;
+    }
+    set_col_ptrs(dc, dp);
+    return PJ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+pj_status pj_encode_by_status_host(pj_ctx *ctx, const pj_pet_columns *cols, uint32_t status_mask, int format,
+                                   uint8_t *out, uint64_t out_cap, uint64_t *out_len, uint64_t *n_selected) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if ((s = check_enc_cols(cols))) return s;
+    pj_pet_columns dc;
+    if ((s = stage_pet_cols(ctx, cols, &dc))) return s;
+    uint64_t need = 0;
+    s = pj_encode_by_status_device(ctx, &dc, status_mask, format, nullptr, 0, &need, n_selected);
+    if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
+    *out_len = need;
+    if (need > out_cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    if (need == 0) return PJ_OK;
+    if (!out) return fail(PJ_ERR_INVALID_ARG, "null output");
+    PJ_HIP(ctx->stage_out.ensure(need + 4));
+    uint64_t got = 0;
+    if ((s = pj_encode_by_status_device(ctx, &dc, status_mask, format, static_cast<uint8_t *>(ctx->stage_out.p), need,
+                                        &got, n_selected)))
+        return s;
+    if ((s = d2h(ctx, out, ctx->stage_out.p, got))) return s;
+    *out_len = got;
+    return PJ_OK;
+}
+
 pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t out_cap,
                          uint64_t *out_len) {
     pj_status s = bind(ctx);
     if (s) return s;
     if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
     if (cols->n_pets && (s = check_enc_cols(cols))) return s;
-    Layout L;
-    host_layout(cols, &L);
-    PJ_HIP(ctx->stage_in.ensure(L.total));
-    uint8_t *base = static_cast<uint8_t *>(ctx->stage_in.p);
-    void *hp[17], *dp[17];
-    pj_pet_columns hc = *cols, dc = *cols;
-    col_ptrs(&hc, hp);
-    for (int k = 0; k < 17; k++) {
-        dp[k] = hp[k] ? base + L.off[k] : nullptr;
-        if (hp[k] && L.size[k] && (s = h2d(ctx, dp[k], hp[k], L.size[k]))) return s;
-    }
-    set_col_ptrs(&dc, dp);
+    pj_pet_columns dc;
+    if ((s = stage_pet_cols(ctx, cols, &dc))) return s;
     uint64_t need = 0;
     if ((s = pj_encode_size_device(ctx, &dc, format, &need))) return s;
     *out_len = need;
@@ -1225,4 +1266,127 @@ extern "C" void pj_decode_model_bounds(int model, uint64_t len, pj_model_columns
     c->cap_n = len / 3 + 1;
     for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++)
         c->cap_bytes[k] = model_ok(model) && k < model_props(model) && model_str(model, k) ? len : 0;
+}
+
+// ------------------------------------------------ Order and User, host memory
+namespace {
+// Bytes of column k of n records (string properties: the n + 1 offsets),
+// and of its string bytes.
+uint64_t model_col_bytes(int model, int k, uint64_t n) {
+    if (model_str(model, k)) return (n + 1) * 8;
+    const bool wide = k == 0 || (model == PJ_MODEL_ORDER && k == 1);       // int64 ids
+    const bool i32 = (model == PJ_MODEL_ORDER && k == 2) || (model == PJ_MODEL_USER && k == 7);
+    return n * (wide ? 8 : i32 ? 4 : 1);
+}
+}  // namespace
+
+extern "C" pj_status pj_encode_model_host(pj_ctx *ctx, int model, const pj_model_columns *cols, int format,
+                                          uint8_t *out, uint64_t out_cap, uint64_t *out_len) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (!model_ok(model)) return fail(PJ_ERR_INVALID_ARG, "unknown model");
+    const uint64_t n = cols->n;
+    if (n && (s = check_model_cols(model, cols, false))) return s;
+    // staging layout: present, then each column and its bytes
+    pj_model_columns dc = *cols;
+    uint64_t off = 0, o_present = 0, o_col[PJ_MODEL_MAX_PROPS] = {}, o_bytes[PJ_MODEL_MAX_PROPS] = {},
+             nbytes[PJ_MODEL_MAX_PROPS] = {};
+    if (cols->present) { o_present = off; off += align256(n + 4); }
+    for (int k = 0; n && k < model_props(model); k++) {
+        o_col[k] = off;
+        off += align256(model_col_bytes(model, k, n) + 4);
+        if (model_str(model, k)) {
+            nbytes[k] = static_cast<const uint64_t *>(cols->col[k])[n];
+            o_bytes[k] = off;
+            off += align256(nbytes[k] + 8);
+        }
+    }
+    PJ_HIP(ctx->stage_in.ensure(off + 256));
+    uint8_t *base = static_cast<uint8_t *>(ctx->stage_in.p);
+    if (cols->present) {
+        dc.present = base + o_present;
+        if ((s = h2d(ctx, dc.present, cols->present, n))) return s;
+    }
+    for (int k = 0; n && k < model_props(model); k++) {
+        dc.col[k] = base + o_col[k];
+        if ((s = h2d(ctx, dc.col[k], cols->col[k], model_col_bytes(model, k, n)))) return s;
+        if (model_str(model, k)) {
+            dc.bytes[k] = base + o_bytes[k];
+            if ((s = h2d(ctx, dc.bytes[k], cols->bytes[k], nbytes[k]))) return s;
+        }
+    }
+    uint64_t need = 0;
+    s = pj_encode_model_device(ctx, model, &dc, format, nullptr, 0, &need);
+    if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
+    *out_len = need;
+    if (need > out_cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    if (need == 0) return PJ_OK;
+    if (!out) return fail(PJ_ERR_INVALID_ARG, "null output");
+    PJ_HIP(ctx->stage_out.ensure(need + 4));
+    uint64_t got = 0;
+    if ((s = pj_encode_model_device(ctx, model, &dc, format, static_cast<uint8_t *>(ctx->stage_out.p), need, &got)))
+        return s;
+    if ((s = d2h(ctx, out, ctx->stage_out.p, got))) return s;
+    *out_len = got;
+    return PJ_OK;
+}
+
+extern "C" pj_status pj_decode_model_host(pj_ctx *ctx, int model, const uint8_t *in, uint64_t len, int array,
+                                          pj_model_columns *out, uint64_t *err_line, uint8_t *err_code,
+                                          uint64_t err_cap, pj_decode_result *res) {
+    pj_status s = bind(ctx);
+    if (s) return s;
+    if (!out || !res) return fail(PJ_ERR_INVALID_ARG, "null argument");
+    if (!model_ok(model)) return fail(PJ_ERR_INVALID_ARG, "unknown model");
+    if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
+    if ((s = check_model_cols(model, out, true))) return s;
+    if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
+    // device outputs sized by the caller's capacities, then the errors
+    const uint64_t cap = out->cap_n;
+    pj_model_columns dc = *out;
+    uint64_t off = 0, o_col[PJ_MODEL_MAX_PROPS] = {}, o_bytes[PJ_MODEL_MAX_PROPS] = {};
+    const uint64_t o_present = off;
+    off += align256(cap + 4);
+    for (int k = 0; k < model_props(model); k++) {
+        o_col[k] = off;
+        off += align256(model_col_bytes(model, k, cap) + 8);
+        if (model_str(model, k)) {
+            o_bytes[k] = off;
+            off += align256(out->cap_bytes[k] + 8);
+        }
+    }
+    const uint64_t o_el = off, o_ec = o_el + align256(err_cap * 8 + 8);
+    off = o_ec + align256(err_cap + 8);
+    PJ_HIP(ctx->stage_out.ensure(off + 256));
+    PJ_HIP(ctx->stage_in.ensure(len + 64));
+    uint8_t *ob = static_cast<uint8_t *>(ctx->stage_out.p), *D = static_cast<uint8_t *>(ctx->stage_in.p);
+    dc.present = ob + o_present;
+    for (int k = 0; k < model_props(model); k++) {
+        dc.col[k] = ob + o_col[k];
+        if (model_str(model, k)) dc.bytes[k] = ob + o_bytes[k];
+    }
+    if (len && (s = h2d(ctx, D, in, len))) return s;
+    uint64_t *del = reinterpret_cast<uint64_t *>(ob + o_el);
+    uint8_t *dec = ob + o_ec;
+    s = pj_decode_model_device(ctx, model, D, len, array, &dc, err_cap ? del : nullptr, err_cap ? dec : nullptr,
+                               err_cap, res);
+    if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
+    const pj_status ds = s;
+    // what was written: the rows that fit, their string bytes, the errors listed
+    const uint64_t rows = dc.n;
+    out->n = rows;
+    for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) out->n_bytes[k] = dc.n_bytes[k];
+    pj_status t;
+    if ((t = d2h(ctx, out->present, dc.present, rows))) return t;
+    for (int k = 0; k < model_props(model); k++) {
+        if (model_str(model, k)) {
+            if ((t = d2h(ctx, out->col[k], dc.col[k], (rows + 1) * 8))) return t;
+            const uint64_t nb = std::min(dc.n_bytes[k], out->cap_bytes[k]);
+            if ((t = d2h(ctx, out->bytes[k], dc.bytes[k], nb))) return t;
+        } else if ((t = d2h(ctx, out->col[k], dc.col[k], model_col_bytes(model, k, rows)))) return t;
+    }
+    const uint64_t ne = std::min(res->n_errors, err_cap);
+    if (ne && ((t = d2h(ctx, err_line, del, ne * 8)) || (t = d2h(ctx, err_code, dec, ne)))) return t;
+    return ds == PJ_OK ? PJ_OK : fail(PJ_ERR_CAPACITY, "capacity too small (sizes needed are in the result)");
 }

@@ -165,6 +165,13 @@ def load_lib():
         L.pj_encode_by_status_device.argtypes = [vp, C.POINTER(PetColumnsStruct), C.c_uint32, i32, vp, u64,
                                                  C.POINTER(u64), C.POINTER(u64)]
         L.pj_encode_by_status_device.restype = i32
+        L.pj_encode_by_status_host.argtypes = L.pj_encode_by_status_device.argtypes
+        L.pj_encode_by_status_host.restype = i32
+        L.pj_encode_model_host.argtypes = [vp, i32, C.POINTER(ModelColumnsStruct), i32, vp, u64, C.POINTER(u64)]
+        L.pj_encode_model_host.restype = i32
+        L.pj_decode_model_host.argtypes = [vp, i32, vp, u64, i32, C.POINTER(ModelColumnsStruct), vp, vp, u64,
+                                           C.POINTER(DecodeResult)]
+        L.pj_decode_model_host.restype = i32
         L.pj_encode_model_device.argtypes = [vp, i32, C.POINTER(ModelColumnsStruct), i32, vp, u64, C.POINTER(u64)]
         L.pj_encode_model_device.restype = i32
         L.pj_decode_model_device.argtypes = [vp, i32, vp, u64, i32, C.POINTER(ModelColumnsStruct), vp, vp, u64,
@@ -754,6 +761,57 @@ def _encode_by_status(self, cols: Columns, mask: int, fmt: int = FORMAT_ARRAY, o
     return out[: n.value], m.value
 
 
+def _encode_by_status_host(self, cols: Columns, mask: int, fmt: int = FORMAT_ARRAY):
+    """pj_encode_by_status_host: host columns in, (bytes, count) out."""
+    s = cols.struct()
+    n, m = C.c_uint64(0), C.c_uint64(0)
+    rc = self.L.pj_encode_by_status_host(self.ctx, C.byref(s), mask, fmt, None, 0, C.byref(n), C.byref(m))
+    if rc not in (PJ_OK, PJ_ERR_CAPACITY):
+        self._check(rc)
+    out = np.empty(max(1, n.value), np.uint8)
+    self._check(self.L.pj_encode_by_status_host(self.ctx, C.byref(s), mask, fmt, C.c_void_p(out.ctypes.data),
+                                                out.size, C.byref(n), C.byref(m)))
+    return out[: n.value].tobytes(), m.value
+
+
+def _model_encode_host(self, cols: ModelColumns, fmt: int = FORMAT_ARRAY) -> bytes:
+    """pj_encode_model_host: host columns in, the JSON bytes out."""
+    s = cols.struct()
+    n = C.c_uint64(0)
+    rc = self.L.pj_encode_model_host(self.ctx, cols.model, C.byref(s), fmt, None, 0, C.byref(n))
+    if rc not in (PJ_OK, PJ_ERR_CAPACITY):
+        self._check(rc)
+    out = np.empty(max(1, n.value), np.uint8)
+    self._check(self.L.pj_encode_model_host(self.ctx, cols.model, C.byref(s), fmt, C.c_void_p(out.ctypes.data),
+                                            out.size, C.byref(n)))
+    return out[: n.value].tobytes()
+
+
+def _model_decode_host(self, model: int, data: bytes, array: bool = False, caps=None, err_cap=None):
+    """pj_decode_model_host: bytes in, (host columns, error indices, error
+    codes, DecodeResult) out."""
+    n = len(data)
+    cap_n, cap_bytes = caps or decode_model_bounds(model, n)
+    cols = alloc_model_columns(model, cap_n, cap_bytes)
+    if err_cap is None:
+        err_cap = n + 1
+    el = np.zeros(max(err_cap, 1), np.uint64)
+    ec = np.zeros(max(err_cap, 1), np.uint8)
+    buf = np.frombuffer(data, np.uint8) if n else np.zeros(1, np.uint8)
+    s = cols.struct()
+    res = DecodeResult()
+    self._check(self.L.pj_decode_model_host(self.ctx, model, C.c_void_p(buf.ctypes.data), n, int(array), C.byref(s),
+                                            C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap,
+                                            C.byref(res)))
+    cols.n = int(s.n)
+    cols.n_bytes = [int(s.n_bytes[k]) for k in range(MODEL_MAX_PROPS)]
+    ne = int(res.n_errors)
+    return cols.to_host(), el[:ne].copy(), ec[:ne].copy(), res
+
+
 Codec.encode_by_status = _encode_by_status
+Codec.encode_by_status_host = _encode_by_status_host
+Codec.encode_model_host = _model_encode_host
+Codec.decode_model_host = _model_decode_host
 Codec.encode_model = _model_encode
 Codec.decode_model = _model_decode

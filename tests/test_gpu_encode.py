@@ -392,3 +392,12 @@ def test_encode_by_status_capacity_and_no_status_column(codec):
     assert m == cols.n_pets and got.cpu().numpy().tobytes() == orc.encode(cols, pj.FORMAT_ARRAY)
     got, m = codec.encode_by_status(d, 0b0111, pj.FORMAT_ARRAY)
     assert m == 0 and got.cpu().numpy().tobytes() == b"[]"
+
+
+def test_encode_by_status_host_matches_oracle(codec):
+    cols = pj.generate(3, 40_000)
+    cols.arrays["status"][::5] = pj.STATUS_NULL
+    for mask, fmt in ((1, pj.FORMAT_ARRAY), (0b1010, pj.FORMAT_PRETTY), (0xF, pj.FORMAT_NDJSON)):
+        got, m = codec.encode_by_status_host(cols, mask, fmt)
+        want, wm = orc.encode_by_status(cols, mask, fmt)
+        assert m == wm and got == want, (mask, fmt)

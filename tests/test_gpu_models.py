@@ -146,3 +146,30 @@ def test_model_decode_capacity(codec):
     with pytest.raises(pj.PetJsonError) as ei:
         codec.decode_model(pj.MODEL_USER, t, caps=(100, cap_b))
     assert ei.value.status == pj.PJ_ERR_CAPACITY
+
+
+@pytest.mark.parametrize("model", [pj.MODEL_ORDER, pj.MODEL_USER])
+def test_model_host_entry_points_match_oracle(codec, model):
+    """pj_encode_model_host / pj_decode_model_host: host columns and text,
+    the device work staged by the library."""
+    cols = pj.generate_model(model, 50_000, seed=21, null_rate=0.2)
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
+        assert codec.encode_model_host(cols, fmt) == orc.encode_model(cols, fmt), fmt
+    rnd = random.Random(model)
+    lines = orc.encode_model(cols, pj.FORMAT_NDJSON).split(b"\n")[:-1]
+    lines = [_mutate(rnd, x) if i % 7 == 0 else x for i, x in enumerate(lines)]
+    data = b"\n".join(lines) + b"\n"
+    rc, rcols, rel, rec, rres = orc.decode_model(model, data)
+    gcols, gel, gec, gres = codec.decode_model_host(model, data)
+    assert (gres.n_lines, gres.n_pets, gres.n_errors) == (rres.n_lines, rres.n_pets, rres.n_errors)
+    assert np.array_equal(gel, rel) and np.array_equal(gec, rec)
+    assert from_model_columns(gcols) == from_model_columns(rcols)
+    assert np.array_equal(gcols.present, rcols.present)
+    # too small a string capacity: the sizes needed come back with the error
+    cap_n, cap_b = pj.decode_model_bounds(model, len(data))
+    k = next(k for k, (_, kind) in enumerate(pj.MODEL_PROPS[model]) if kind == "str")
+    cap_b = list(cap_b)
+    cap_b[k] = 10
+    with pytest.raises(pj.PetJsonError) as ei:
+        codec.decode_model_host(model, data, caps=(cap_n, cap_b))
+    assert ei.value.status == pj.PJ_ERR_CAPACITY
