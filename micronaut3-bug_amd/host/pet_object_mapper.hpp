@@ -16,6 +16,7 @@
 // (MyEntityConfig.java:37-39).
 #pragma once
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <initializer_list>
@@ -196,8 +197,155 @@ inline std::vector<Pet> from_columns(const pj_pet_columns &c) {
     return out;
 }
 
+// The petstore's Order and User schemas (petstore.json:937-971, 824-857):
+// every property optional, an empty optional is null.
+enum class OrderStatus : uint8_t { PLACED = 0, APPROVED = 1, DELIVERED = 2 };
+struct Order {
+    std::optional<int64_t> id, petId;
+    std::optional<int32_t> quantity;
+    std::optional<std::string> shipDate;   // the date-time text as written
+    std::optional<OrderStatus> status;
+    std::optional<bool> complete;
+    bool operator==(const Order &o) const {
+        return id == o.id && petId == o.petId && quantity == o.quantity && shipDate == o.shipDate &&
+               status == o.status && complete == o.complete;
+    }
+};
+struct User {
+    std::optional<int64_t> id;
+    std::optional<std::string> username, firstName, lastName, email, password, phone;
+    std::optional<int32_t> userStatus;
+    bool operator==(const User &o) const {
+        return id == o.id && username == o.username && firstName == o.firstName && lastName == o.lastName &&
+               email == o.email && password == o.password && phone == o.phone && userStatus == o.userStatus;
+    }
+};
+
+// One pj_model_columns set in host vectors: per property a value column
+// (string properties: n + 1 offsets) and a byte column, and the present bits.
+struct ModelColumnSet {
+    int model = 0;
+    uint64_t n = 0;
+    std::vector<uint8_t> present;
+    std::vector<std::vector<uint8_t>> col, bytes;   // raw storage of each column
+    ModelColumnSet(int m, uint64_t cap, uint64_t cap_bytes) : model(m), present(cap + 1), col(PJ_MODEL_MAX_PROPS),
+                                                             bytes(PJ_MODEL_MAX_PROPS) {
+        for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) {
+            col[k].resize((cap + 1) * 8);
+            bytes[k].resize(cap_bytes + 8);
+        }
+    }
+    pj_model_columns view(uint64_t cap_n = 0, uint64_t cap_bytes = 0) {
+        pj_model_columns v;
+        std::memset(&v, 0, sizeof v);
+        v.n = n;
+        v.present = present.data();
+        for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) {
+            v.col[k] = col[k].data();
+            v.bytes[k] = bytes[k].data();
+            v.cap_bytes[k] = cap_bytes;
+        }
+        v.cap_n = cap_n;
+        return v;
+    }
+    template <class T> T *as(int k) { return reinterpret_cast<T *>(col[k].data()); }
+    void put_str(int k, uint64_t i, uint64_t &fill, const std::optional<std::string> &v) {
+        if (v) {
+            std::memcpy(bytes[k].data() + fill, v->data(), v->size());
+            fill += v->size();
+        }
+        as<uint64_t>(k)[i + 1] = fill;
+    }
+    std::optional<std::string> get_str(int k, uint64_t i, bool on) {
+        if (!on) return std::nullopt;
+        const uint64_t *o = as<uint64_t>(k);
+        return std::string(reinterpret_cast<const char *>(bytes[k].data()) + o[i], o[i + 1] - o[i]);
+    }
+};
+
+inline uint64_t text_bytes(const std::optional<std::string> &s) { return s ? s->size() : 0; }
+
+inline ModelColumnSet to_model_columns(const std::vector<Order> &v) {
+    uint64_t nb = 0;
+    for (const Order &o : v) nb += text_bytes(o.shipDate);
+    ModelColumnSet c(PJ_MODEL_ORDER, v.size(), nb);
+    c.n = v.size();
+    uint64_t fill = 0;
+    for (uint64_t i = 0; i < v.size(); i++) {
+        const Order &o = v[i];
+        c.present[i] = (uint8_t)((o.id ? 1 : 0) | (o.petId ? 2 : 0) | (o.quantity ? 4 : 0) | (o.shipDate ? 8 : 0) |
+                                 (o.status ? 16 : 0) | (o.complete ? 32 : 0));
+        c.as<int64_t>(0)[i] = o.id.value_or(0);
+        c.as<int64_t>(1)[i] = o.petId.value_or(0);
+        c.as<int32_t>(2)[i] = o.quantity.value_or(0);
+        c.put_str(3, i, fill, o.shipDate);
+        c.as<uint8_t>(4)[i] = o.status ? (uint8_t)*o.status : 0;
+        c.as<uint8_t>(5)[i] = o.complete.value_or(false) ? 1 : 0;
+    }
+    return c;
+}
+
+inline ModelColumnSet to_model_columns(const std::vector<User> &v) {
+    uint64_t nb = 0;                                 // every column gets room for all the text
+    for (const User &u : v)
+        nb += text_bytes(u.username) + text_bytes(u.firstName) + text_bytes(u.lastName) + text_bytes(u.email) +
+              text_bytes(u.password) + text_bytes(u.phone);
+    ModelColumnSet c(PJ_MODEL_USER, v.size(), nb);
+    c.n = v.size();
+    uint64_t fill[PJ_MODEL_MAX_PROPS] = {};
+    for (uint64_t i = 0; i < v.size(); i++) {
+        const User &u = v[i];
+        const std::optional<std::string> *str[6] = {&u.username, &u.firstName, &u.lastName, &u.email, &u.password,
+                                                    &u.phone};
+        uint8_t p = (uint8_t)((u.id ? 1 : 0) | (u.userStatus ? 128 : 0));
+        for (int k = 1; k <= 6; k++) {
+            if (*str[k - 1]) p |= (uint8_t)(1u << k);
+            c.put_str(k, i, fill[k], *str[k - 1]);
+        }
+        c.present[i] = p;
+        c.as<int64_t>(0)[i] = u.id.value_or(0);
+        c.as<int32_t>(7)[i] = u.userStatus.value_or(0);
+    }
+    return c;
+}
+
+inline std::vector<Order> orders_from(ModelColumnSet &c) {
+    std::vector<Order> v(c.n);
+    for (uint64_t i = 0; i < c.n; i++) {
+        const uint8_t p = c.present[i];
+        Order &o = v[i];
+        if (p & 1) o.id = c.as<int64_t>(0)[i];
+        if (p & 2) o.petId = c.as<int64_t>(1)[i];
+        if (p & 4) o.quantity = c.as<int32_t>(2)[i];
+        o.shipDate = c.get_str(3, i, p & 8);
+        if (p & 16) o.status = (OrderStatus)c.as<uint8_t>(4)[i];
+        if (p & 32) o.complete = c.as<uint8_t>(5)[i] != 0;
+    }
+    return v;
+}
+
+inline std::vector<User> users_from(ModelColumnSet &c) {
+    std::vector<User> v(c.n);
+    for (uint64_t i = 0; i < c.n; i++) {
+        const uint8_t p = c.present[i];
+        User &u = v[i];
+        if (p & 1) u.id = c.as<int64_t>(0)[i];
+        std::optional<std::string> *str[6] = {&u.username, &u.firstName, &u.lastName, &u.email, &u.password,
+                                              &u.phone};
+        for (int k = 1; k <= 6; k++) *str[k - 1] = c.get_str(k, i, (p >> k) & 1);
+        if (p & 128) u.userStatus = c.as<int32_t>(7)[i];
+    }
+    return v;
+}
+
 // Result of reading NDJSON: the valid records in input order plus the line
 // index and PJ_REC_* code of each invalid one.
+template <class T> struct ReadResultOf {
+    std::vector<T> values;
+    std::vector<uint64_t> error_lines;
+    std::vector<uint8_t> error_codes;
+};
+
 struct ReadResult {
     std::vector<Pet> values;
     std::vector<uint64_t> error_lines;
@@ -270,9 +418,78 @@ class PetObjectMapper {
         return std::move(r.values);
     }
 
+    // GET /pet/findByStatus (petstore.json:106-140): the List<Pet> response
+    // body of the pets whose status is in the mask (bit 0 available, the
+    // query's default; 1 pending; 2 sold; 3 no status).
+    std::vector<uint8_t> findPetsByStatus(const std::vector<Pet> &pets, uint32_t status_mask = 1,
+                                          pj_format fmt = PJ_FORMAT_ARRAY) {
+        ColumnSet cs = to_columns(pets);
+        pj_pet_columns v = cs.view();
+        uint64_t bound = 0, got = 0, count = 0;
+        check(pj_encode_bound(&v, fmt, &bound));       // bounds any selection too
+        std::vector<uint8_t> out(bound);
+        check(pj_encode_by_status_host(ctx_, &v, status_mask, fmt, out.data(), out.size(), &got, &count));
+        out.resize(got);
+        return out;
+    }
+
+    // writeValueAsBytes(List<Order>) / (List<User>).
+    std::vector<uint8_t> writeValueAsBytes(const std::vector<Order> &v, pj_format fmt = PJ_FORMAT_ARRAY) {
+        ModelColumnSet c = to_model_columns(v);
+        return write_model(c, fmt);
+    }
+    std::vector<uint8_t> writeValueAsBytes(const std::vector<User> &v, pj_format fmt = PJ_FORMAT_ARRAY) {
+        ModelColumnSet c = to_model_columns(v);
+        return write_model(c, fmt);
+    }
+
+    // readValue over NDJSON Orders / Users (or one array document when
+    // array is true): the valid records and the invalid lines.
+    ReadResultOf<Order> readOrders(const uint8_t *in, uint64_t len, bool array = false) {
+        ReadResultOf<Order> r;
+        ModelColumnSet c = read_model(PJ_MODEL_ORDER, in, len, array, r.error_lines, r.error_codes);
+        r.values = orders_from(c);
+        return r;
+    }
+    ReadResultOf<User> readUsers(const uint8_t *in, uint64_t len, bool array = false) {
+        ReadResultOf<User> r;
+        ModelColumnSet c = read_model(PJ_MODEL_USER, in, len, array, r.error_lines, r.error_codes);
+        r.values = users_from(c);
+        return r;
+    }
+
     pj_ctx *context() { return ctx_; }
 
   private:
+    std::vector<uint8_t> write_model(ModelColumnSet &c, pj_format fmt) {
+        pj_model_columns v = c.view();
+        uint64_t need = 0;
+        const pj_status st = pj_encode_model_host(ctx_, c.model, &v, fmt, nullptr, 0, &need);
+        if (st != PJ_OK && st != PJ_ERR_CAPACITY) check(st);
+        std::vector<uint8_t> out(need);
+        uint64_t got = 0;
+        check(pj_encode_model_host(ctx_, c.model, &v, fmt, out.data(), out.size(), &got));
+        out.resize(got);
+        return out;
+    }
+    ModelColumnSet read_model(int model, const uint8_t *in, uint64_t len, bool array,
+                              std::vector<uint64_t> &error_lines, std::vector<uint8_t> &error_codes) {
+        pj_model_columns caps;
+        std::memset(&caps, 0, sizeof caps);
+        pj_decode_model_bounds(model, len, &caps);
+        ModelColumnSet c(model, caps.cap_n, len);
+        pj_model_columns v = c.view(caps.cap_n, len);
+        const uint64_t err_cap = len + 1;                // every line may be an error
+        error_lines.resize(err_cap);
+        error_codes.resize(err_cap);
+        pj_decode_result res;
+        check(pj_decode_model_host(ctx_, model, in, len, array ? 1 : 0, &v, error_lines.data(), error_codes.data(),
+                                   err_cap, &res));
+        error_lines.resize(res.n_errors);
+        error_codes.resize(res.n_errors);
+        c.n = v.n;
+        return c;
+    }
     ReadResult read(const uint8_t *in, uint64_t len, bool array) {
         pj_pet_columns caps;
         std::memset(&caps, 0, sizeof caps);

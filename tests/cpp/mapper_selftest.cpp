@@ -77,6 +77,50 @@ static std::vector<Pet> normalised(std::vector<Pet> v) {
     return v;
 }
 
+static std::vector<Order> sample_orders(int n, unsigned seed) {
+    std::mt19937_64 rng(seed);
+    std::vector<Order> v(n);
+    for (Order &o : v) {
+        if (rng() % 5) o.id = (int64_t)rng();
+        if (rng() % 5) o.petId = (int64_t)(rng() % 100000);
+        if (rng() % 5) o.quantity = (int32_t)(rng() % 2001) - 1000;
+        if (rng() % 5) o.shipDate = "2026-0" + std::to_string(1 + rng() % 9) + "-1" + std::to_string(rng() % 10) +
+                                    "T10:00:00.000Z";
+        if (rng() % 5) o.status = (OrderStatus)(rng() % 3);
+        if (rng() % 5) o.complete = rng() % 2 == 0;
+    }
+    return v;
+}
+
+static std::vector<User> sample_users(int n, unsigned seed) {
+    std::mt19937_64 rng(seed);
+    auto word = [&](const char *pre) { return std::string(pre) + std::to_string(rng() % 100000) + "\xC3\xA9\"\n"; };
+    std::vector<User> v(n);
+    for (User &u : v) {
+        if (rng() % 5) u.id = (int64_t)rng();
+        if (rng() % 5) u.username = word("u");
+        if (rng() % 5) u.firstName = word("f");
+        if (rng() % 5) u.lastName = word("l");
+        if (rng() % 5) u.email = word("e@");
+        if (rng() % 5) u.password = word("p");
+        if (rng() % 5) u.phone = word("+");
+        if (rng() % 5) u.userStatus = (int32_t)(rng() % 7);
+    }
+    return v;
+}
+
+template <class T> static std::string oracle_model_json(const std::vector<T> &v, int fmt) {
+    ModelColumnSet c = to_model_columns(v);
+    pj_model_columns m = c.view();
+    pj_options o;
+    pj_default_options(&o);
+    uint64_t n = 0;
+    or_encode_model(c.model, &m, &o, fmt, nullptr, 0, &n);
+    std::string s(n, '\0');
+    or_encode_model(c.model, &m, &o, fmt, reinterpret_cast<uint8_t *>(&s[0]), n, &n);
+    return s;
+}
+
 #define CHECK(c)                                                        \
     do {                                                                \
         if (!(c)) {                                                     \
@@ -99,6 +143,13 @@ int main(int argc, char **argv) {
     one[0].status = StatusEnum::SOLD;
     CHECK(oracle_json(one, PJ_FORMAT_ARRAY) == "[{\"id\":10,\"name\":\"doggie\",\"photoUrls\":[],\"status\":\"sold\"}]");
     CHECK(fromValue("pending") == StatusEnum::PENDING);
+    // Order / User packing round trips
+    std::vector<Order> orders = sample_orders(500, 3);
+    std::vector<User> users = sample_users(500, 4);
+    {
+        ModelColumnSet oc = to_model_columns(orders), uc = to_model_columns(users);
+        CHECK(orders_from(oc) == orders && users_from(uc) == users);
+    }
     bool threw = false;
     try { fromValue("lost"); } catch (const std::invalid_argument &) { threw = true; }
     CHECK(threw);
@@ -139,6 +190,40 @@ int main(int argc, char **argv) {
         try { m.readArray(arr.data(), arr.size() - 1); }
         catch (const SerdeException &e) { thrown = e.status(); }
         CHECK(thrown == PJ_ERR_SYNTAX);
+    }
+    if (gpu) {
+        PetObjectMapper &m = PetObjectMapper::getDefault();
+        // pretty printing, and findPetsByStatus's body against the oracle
+        std::vector<uint8_t> pretty = m.writeValueAsBytes(pets, PJ_FORMAT_PRETTY);
+        CHECK(std::string(pretty.begin(), pretty.end()) == oracle_json(pets, PJ_FORMAT_PRETTY));
+        for (uint32_t mask : {1u, 6u, 15u}) {
+            ColumnSet cs = to_columns(pets);
+            pj_pet_columns v = cs.view();
+            pj_options o;
+            pj_default_options(&o);
+            uint64_t n = 0, cnt = 0;
+            or_encode_by_status(&v, &o, mask, PJ_FORMAT_ARRAY, nullptr, 0, &n, &cnt);
+            std::string want(n, '\0');
+            or_encode_by_status(&v, &o, mask, PJ_FORMAT_ARRAY, reinterpret_cast<uint8_t *>(&want[0]), n, &n, &cnt);
+            std::vector<uint8_t> got = m.findPetsByStatus(pets, mask);
+            CHECK(std::string(got.begin(), got.end()) == want);
+        }
+        // Order / User: write against the oracle, read back
+        for (int fmt : {PJ_FORMAT_ARRAY, PJ_FORMAT_NDJSON, PJ_FORMAT_PRETTY}) {
+            std::vector<uint8_t> ob = m.writeValueAsBytes(orders, (pj_format)fmt);
+            std::vector<uint8_t> ub = m.writeValueAsBytes(users, (pj_format)fmt);
+            CHECK(std::string(ob.begin(), ob.end()) == oracle_model_json(orders, fmt));
+            CHECK(std::string(ub.begin(), ub.end()) == oracle_model_json(users, fmt));
+            const bool arr = fmt != PJ_FORMAT_NDJSON;
+            ReadResultOf<Order> ro = m.readOrders(ob.data(), ob.size(), arr);
+            ReadResultOf<User> ru = m.readUsers(ub.data(), ub.size(), arr);
+            CHECK(ro.values == orders && ro.error_lines.empty());
+            CHECK(ru.values == users && ru.error_lines.empty());
+        }
+        std::string bad = "{\"quantity\":2147483648}\n{\"status\":\"lost\"}\n{\"id\":7}\n";
+        ReadResultOf<Order> rb = m.readOrders(reinterpret_cast<const uint8_t *>(bad.data()), bad.size());
+        CHECK(rb.values.size() == 1 && rb.values[0].id == 7 && rb.error_lines.size() == 2);
+        CHECK(rb.error_codes[0] == PJ_REC_NUMBER && rb.error_codes[1] == PJ_REC_BAD_STATUS);
     }
     std::printf("mapper selftest ok (%s)\n", gpu ? "gpu" : "cpu");
     return 0;
