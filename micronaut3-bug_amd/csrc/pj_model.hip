@@ -571,27 +571,27 @@ __global__ __launch_bounds__(BT) void k_mdec_count(ModelDecParams P) {
     if (code == PJ_REC_EMPTY) atomicAdd(reinterpret_cast<unsigned long long *>(P.totals + MD_MAXK), 1ull);
 }
 
-// One workgroup: the block sums in order, BT blocks per round.
+// One workgroup: thread t takes R = ceil(nblocks / BT) consecutive blocks,
+// sums them, and a block scan of those sums gives each thread the offsets
+// its blocks start from.
 template <int BT>
 __global__ __launch_bounds__(BT) void k_mdec_scan(ModelDecParams P) {
     __shared__ uint64_t sh[BT / 64 + 2];
-    uint64_t carry[MD_MAXK];
+    const uint64_t R = (P.nblocks + BT - 1) / BT, b0 = threadIdx.x * R, b1 = min(b0 + R, P.nblocks);
 #pragma unroll
-    for (int k = 0; k < MD_MAXK; k++) carry[k] = 0;
-    for (uint64_t r = 0; r < P.nblocks; r += BT) {
-        const uint64_t b = r + threadIdx.x;
-#pragma unroll
-        for (int k = 0; k < MD_MAXK; k++) {
-            const uint64_t v = b < P.nblocks ? P.bagg[b * MD_MAXK + k] : 0;
-            uint64_t tot;
-            const uint64_t pre = block_excl_scan<BT>(v, sh, &tot);
-            if (b < P.nblocks) P.bbase[b * MD_MAXK + k] = carry[k] + pre;
-            carry[k] += tot;
-            __syncthreads();
+    for (int k = 0; k < MD_MAXK; k++) {
+        uint64_t sum = 0;
+        for (uint64_t b = b0; b < b1; b++) sum += P.bagg[b * MD_MAXK + k];
+        uint64_t tot;
+        uint64_t run = block_excl_scan<BT>(sum, sh, &tot);
+        for (uint64_t b = b0; b < b1; b++) {
+            const uint64_t v = P.bagg[b * MD_MAXK + k];
+            P.bbase[b * MD_MAXK + k] = run;
+            run += v;
         }
+        if (threadIdx.x == 0) P.totals[k] = tot;
+        __syncthreads();
     }
-    if (threadIdx.x == 0)
-        for (int k = 0; k < MD_MAXK; k++) P.totals[k] = carry[k];
 }
 
 template <int MODEL, int BT, int TILE>
@@ -656,7 +656,7 @@ hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_
         hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
         hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_USER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
-    hipLaunchKernelGGL(pj::k_mdec_scan<MDEC_BT>, dim3(1), dim3(MDEC_BT), 0, st, P);
+    hipLaunchKernelGGL(pj::k_mdec_scan<1024>, dim3(1), dim3(1024), 0, st, P);
     if (model == PJ_MODEL_ORDER)
         hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
