@@ -1211,7 +1211,8 @@ extern "C" pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_
     uint64_t *X = nullptr, lines = 0;
     if ((s = index_stage(ctx, in, len, array != 0, P, X, &lines))) return s;
     const uint64_t nb = (lines + pj_decode_model_block() - 1) / pj_decode_model_block();
-    PJ_HIP(ctx->scan.ensure((2 * nb * MD_MAXK + MD_MAXK + 1) * sizeof(uint64_t)));
+    const uint64_t nchunks = (nb + 1023) / 1024;     // the scan's chunks of 1024 blocks
+    PJ_HIP(ctx->scan.ensure((2 * nb * MD_MAXK + nchunks * MD_MAXK + MD_MAXK + 1) * sizeof(uint64_t)));
     uint64_t *SB = static_cast<uint64_t *>(ctx->scan.p);
     ModelDecParams M;
     std::memset(&M, 0, sizeof M);
@@ -1226,6 +1227,7 @@ extern "C" pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_
     M.totals = SB;
     M.bagg = SB + MD_MAXK + 1;
     M.bbase = M.bagg + nb * MD_MAXK;
+    M.csum = M.bbase + nb * MD_MAXK;
     M.nblocks = nb;
     if ((s = mark(ctx))) return s;
     PJ_HIP(pj_launch_fill_u64(SB, MD_MAXK + 1, 0, ctx->stream));

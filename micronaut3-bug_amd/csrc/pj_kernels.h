@@ -54,7 +54,8 @@ struct ModelDecParams {
     uint8_t *err_code;
     uint64_t err_cap;
     uint64_t *bagg;            // [nblocks * MD_MAXK] block totals
-    uint64_t *bbase;           // [nblocks * MD_MAXK] block first offsets
+    uint64_t *bbase;           // [nblocks * MD_MAXK] block first offsets within their chunk
+    uint64_t *csum;            // [nchunks * MD_MAXK] chunk first offsets
     uint64_t *totals;          // [MD_MAXK + 1] sums (the last: blank records)
     uint64_t nblocks;
 };

@@ -6,7 +6,7 @@
 //   k_mdec_count  reads each record and sums, per block of records, the
 //                 valid ones, the invalid ones and the decoded bytes of each
 //                 string property;
-//   k_mdec_scan   turns those sums into each block's first offsets;
+//   k_mdec_scan_* turn those sums into each block's first offsets;
 //   k_mdec_write  reads each record again and writes its values, or its
 //                 error slot, at the offsets a block scan gives.
 // The grammar and binding rules are the Pet decoder's: RFC 8259 with
@@ -571,27 +571,47 @@ __global__ __launch_bounds__(BT) void k_mdec_count(ModelDecParams P) {
     if (code == PJ_REC_EMPTY) atomicAdd(reinterpret_cast<unsigned long long *>(P.totals + MD_MAXK), 1ull);
 }
 
-// One workgroup: thread t takes R = ceil(nblocks / BT) consecutive blocks,
-// sums them, and a block scan of those sums gives each thread the offsets
-// its blocks start from.
-template <int BT>
-__global__ __launch_bounds__(BT) void k_mdec_scan(ModelDecParams P) {
-    __shared__ uint64_t sh[BT / 64 + 2];
-    const uint64_t R = (P.nblocks + BT - 1) / BT, b0 = threadIdx.x * R, b1 = min(b0 + R, P.nblocks);
+// The block sums scanned in two levels: k_mdec_scan_chunks scans each chunk
+// of MD_CHUNK blocks (one block per thread) into bbase and stores the
+// chunk's totals; k_mdec_scan_tops (one workgroup) scans the chunk totals
+// into csum and the grand totals.  A block's first offsets are then
+// csum[its chunk] + bbase[the block].
+constexpr int MD_CHUNK = 1024;
+
+__global__ __launch_bounds__(MD_CHUNK) void k_mdec_scan_chunks(ModelDecParams P) {
+    __shared__ uint64_t sh[MD_CHUNK / 64 + 2];
+    const uint64_t g = blockIdx.x, b = g * MD_CHUNK + threadIdx.x;
+    const bool in = b < P.nblocks;
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
-        uint64_t sum = 0;
-        for (uint64_t b = b0; b < b1; b++) sum += P.bagg[b * MD_MAXK + k];
         uint64_t tot;
-        uint64_t run = block_excl_scan<BT>(sum, sh, &tot);
-        for (uint64_t b = b0; b < b1; b++) {
-            const uint64_t v = P.bagg[b * MD_MAXK + k];
-            P.bbase[b * MD_MAXK + k] = run;
-            run += v;
-        }
-        if (threadIdx.x == 0) P.totals[k] = tot;
+        const uint64_t pre = block_excl_scan<MD_CHUNK>(in ? P.bagg[b * MD_MAXK + k] : 0ull, sh, &tot);
+        if (in) P.bbase[b * MD_MAXK + k] = pre;
+        if (threadIdx.x == 0) P.csum[g * MD_MAXK + k] = tot;
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(MD_CHUNK) void k_mdec_scan_tops(ModelDecParams P) {
+    __shared__ uint64_t sh[MD_CHUNK / 64 + 2];
+    const uint64_t nc = (P.nblocks + MD_CHUNK - 1) / MD_CHUNK;
+    uint64_t carry[MD_MAXK];
+#pragma unroll
+    for (int k = 0; k < MD_MAXK; k++) carry[k] = 0;
+    for (uint64_t r = 0; r < nc; r += MD_CHUNK) {
+        const uint64_t c = r + threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < MD_MAXK; k++) {
+            const uint64_t v = c < nc ? P.csum[c * MD_MAXK + k] : 0;
+            uint64_t tot;
+            const uint64_t pre = block_excl_scan<MD_CHUNK>(v, sh, &tot);
+            __syncthreads();
+            if (c < nc) P.csum[c * MD_MAXK + k] = carry[k] + pre;
+            carry[k] += tot;
+        }
+    }
+    if (threadIdx.x == 0)
+        for (int k = 0; k < MD_MAXK; k++) P.totals[k] = carry[k];
 }
 
 template <int MODEL, int BT, int TILE>
@@ -606,7 +626,7 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
-        at[k] = P.bbase[b * MD_MAXK + k] + block_excl_scan<BT>(cnt[k], sh, &tot);
+        at[k] = P.csum[b / MD_CHUNK * MD_MAXK + k] + P.bbase[b * MD_MAXK + k] + block_excl_scan<BT>(cnt[k], sh, &tot);
         __syncthreads();
     }
     if (code < 0) return;
@@ -656,7 +676,9 @@ hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_
         hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
         hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_USER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
-    hipLaunchKernelGGL(pj::k_mdec_scan<1024>, dim3(1), dim3(1024), 0, st, P);
+    hipLaunchKernelGGL(pj::k_mdec_scan_chunks, dim3((g + pj::MD_CHUNK - 1) / pj::MD_CHUNK), dim3(pj::MD_CHUNK), 0, st,
+                       P);
+    hipLaunchKernelGGL(pj::k_mdec_scan_tops, dim3(1), dim3(pj::MD_CHUNK), 0, st, P);
     if (model == PJ_MODEL_ORDER)
         hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
