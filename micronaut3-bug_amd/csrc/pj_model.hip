@@ -82,7 +82,24 @@ __device__ __forceinline__ bool m_u4(MLine &L, uint32_t *cu) {
 // A string starting at its opening quote: escapes (\uXXXX pairs joined,
 // lone surrogates rejected), no raw controls, UTF-8 lead bytes C0-DF /
 // E0-EF / F0-F7 each with its 10xxxxxx continuations.
-__device__ __forceinline__ int m_string(MLine &L, MOut &o) {
+// The writing pass's string output: the decoded bytes gather in a register
+// and leave as 8-byte stores at any address, the tail exact.
+struct MStore {
+    StoreSink ss;
+    uint64_t k = 0;
+    __device__ __forceinline__ explicit MStore(uint8_t *dst) { ss.init(dst); }
+    __device__ __forceinline__ void put(uint32_t b) {
+        ss.put8(b & 0xFF, 1);
+        k++;
+    }
+    __device__ __forceinline__ void put8(uint64_t x) {
+        ss.put8(x, 8);
+        k += 8;
+    }
+    __device__ __forceinline__ void finish() { ss.finish(); }
+};
+
+template <class O> __device__ __forceinline__ int m_string(MLine &L, O &o) {
     L.p++;
     for (;;) {
         // 8 bytes at a time while none is a quote, a backslash, a control
@@ -650,8 +667,9 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
             if (fits) static_cast<uint64_t *>(o.col[k])[row + 1] = s1;
             if (R.slen[k] && s1 <= o.cap_bytes[k]) {
                 MLine L{S.at(P, a), P.line_start[l + 1] - 1 - a, R.spos[k]};
-                MOut w{o.bytes[k] + s0};
+                MStore w(o.bytes[k] + s0);
                 (void)m_string(L, w);
+                w.finish();
             }
         } else if (fits) {
             if (kind == K_I64) static_cast<int64_t *>(o.col[k])[row] = R.v[k];
