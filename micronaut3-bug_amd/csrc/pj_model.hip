@@ -449,6 +449,13 @@ template <int MODEL, int F> __device__ __forceinline__ int m_value(MLine &L, MRe
     return PJ_REC_OK;
 }
 
+// Property f's value, through the m_value instance of each property (so
+// every index into R stays static).
+template <int MODEL, int F = 0> __device__ __forceinline__ int m_value_of(MLine &L, MRec &R, int f) {
+    if constexpr (F >= MSchema<MODEL>::N) return PJ_REC_OK;
+    else return f == F ? m_value<MODEL, F>(L, R) : m_value_of<MODEL, F + 1>(L, R, f);
+}
+
 // One record [s, s + n): its PJ_REC_* code, and its values in R.
 template <int MODEL> __device__ __forceinline__ int m_line(const uint8_t *s, uint64_t n, MRec &R) {
     MLine L{s, n, 0};
@@ -479,21 +486,11 @@ template <int MODEL> __device__ __forceinline__ int m_line(const uint8_t *s, uin
             m_skip_ws(L);
             if (m_end(L)) return PJ_REC_SYNTAX;
             const int f = key.k <= 16 ? m_prop_of<MODEL>(key) : -1;
-            switch (f) {
-            case 0: e = m_value<MODEL, 0>(L, R); break;
-            case 1: e = m_value<MODEL, 1>(L, R); break;
-            case 2: e = m_value<MODEL, 2>(L, R); break;
-            case 3: e = m_value<MODEL, 3>(L, R); break;
-            case 4: e = m_value<MODEL, 4>(L, R); break;
-            case 5: e = m_value<MODEL, 5>(L, R); break;
-            case 6: e = MSchema<MODEL>::N > 6 ? m_value<MODEL, 6 % MSchema<MODEL>::N>(L, R) : PJ_REC_OK; break;
-            case 7: e = MSchema<MODEL>::N > 7 ? m_value<MODEL, 7 % MSchema<MODEL>::N>(L, R) : PJ_REC_OK; break;
-            default: {
+            if (f >= 0) e = m_value_of<MODEL>(L, R, f);
+            else {
                 uint64_t np;
                 e = m_skip(L.s, L.n, L.p, 1, &np);
                 L.p = np;
-                break;
-            }
             }
             if (e) return e;
             m_skip_ws(L);
@@ -609,19 +606,20 @@ __global__ __launch_bounds__(MD_CHUNK) void k_mdec_scan_chunks(ModelDecParams P)
     }
 }
 
-__global__ __launch_bounds__(MD_CHUNK) void k_mdec_scan_tops(ModelDecParams P) {
-    __shared__ uint64_t sh[MD_CHUNK / 64 + 2];
+constexpr int MD_TOPS = 256;   // threads of k_mdec_scan_tops (room in registers for the carries)
+__global__ __launch_bounds__(MD_TOPS) void k_mdec_scan_tops(ModelDecParams P) {
+    __shared__ uint64_t sh[MD_TOPS / 64 + 2];
     const uint64_t nc = (P.nblocks + MD_CHUNK - 1) / MD_CHUNK;
     uint64_t carry[MD_MAXK];
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) carry[k] = 0;
-    for (uint64_t r = 0; r < nc; r += MD_CHUNK) {
+    for (uint64_t r = 0; r < nc; r += MD_TOPS) {
         const uint64_t c = r + threadIdx.x;
 #pragma unroll
         for (int k = 0; k < MD_MAXK; k++) {
             const uint64_t v = c < nc ? P.csum[c * MD_MAXK + k] : 0;
             uint64_t tot;
-            const uint64_t pre = block_excl_scan<MD_CHUNK>(v, sh, &tot);
+            const uint64_t pre = block_excl_scan<MD_TOPS>(v, sh, &tot);
             __syncthreads();
             if (c < nc) P.csum[c * MD_MAXK + k] = carry[k] + pre;
             carry[k] += tot;
@@ -696,7 +694,7 @@ hipError_t pj_launch_decode_model(const ModelDecParams &P, int model, hipStream_
         hipLaunchKernelGGL((pj::k_mdec_count<PJ_MODEL_USER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     hipLaunchKernelGGL(pj::k_mdec_scan_chunks, dim3((g + pj::MD_CHUNK - 1) / pj::MD_CHUNK), dim3(pj::MD_CHUNK), 0, st,
                        P);
-    hipLaunchKernelGGL(pj::k_mdec_scan_tops, dim3(1), dim3(pj::MD_CHUNK), 0, st, P);
+    hipLaunchKernelGGL(pj::k_mdec_scan_tops, dim3(1), dim3(pj::MD_TOPS), 0, st, P);
     if (model == PJ_MODEL_ORDER)
         hipLaunchKernelGGL((pj::k_mdec_write<PJ_MODEL_ORDER, MDEC_BT, MDEC_TILE>), dim3(g), dim3(MDEC_BT), 0, st, P);
     else
