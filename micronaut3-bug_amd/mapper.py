@@ -1,4 +1,5 @@
-"""ObjectMapper-style surface over libpetjson for Pet objects.
+"""ObjectMapper-style surface over libpetjson for Pet objects (and the
+petstore's Order and User records, as dicts).
 
 Mirrors io.micronaut.serde.ObjectMapper as the reference uses it:
 ObjectMapper.getDefault() (reference service/MyEntityService.java:45),
@@ -63,5 +64,77 @@ class PetObjectMapper:
                                                     f"Pet (PJ_REC code {int(r.error_codes[0])})")
         return r.values
 
+    def find_pets_by_status(self, pets: List[Pet], status_mask: int = 1, fmt: int = pj.FORMAT_ARRAY) -> bytes:
+        """GET /pet/findByStatus (petstore.json:106-140): the response body of
+        the pets whose status is in the mask (bit 0 available, the query's
+        default; 1 pending; 2 sold; 3 no status)."""
+        body, _ = self.codec.encode_by_status_host(to_columns(pets), status_mask, fmt)
+        return body
+
+    def write_orders(self, orders: List[dict], fmt: int = pj.FORMAT_ARRAY) -> bytes:
+        """writeValueAsBytes(List<Order>): records as dicts of the Order
+        properties (petstore.json:937-971); a missing or None one is null."""
+        return self.codec.encode_model_host(_model_columns(pj.MODEL_ORDER, orders), fmt)
+
+    def write_users(self, users: List[dict], fmt: int = pj.FORMAT_ARRAY) -> bytes:
+        """writeValueAsBytes(List<User>) (petstore.json:824-857)."""
+        return self.codec.encode_model_host(_model_columns(pj.MODEL_USER, users), fmt)
+
+    def read_orders(self, data: bytes, array: bool = False) -> ReadResult:
+        return self._read_model(pj.MODEL_ORDER, data, array)
+
+    def read_users(self, data: bytes, array: bool = False) -> ReadResult:
+        return self._read_model(pj.MODEL_USER, data, array)
+
+    def _read_model(self, model: int, data: bytes, array: bool) -> ReadResult:
+        cols, el, ec, res = self.codec.decode_model_host(model, data, array)
+        return ReadResult(_model_records(cols), el, ec)
+
     def close(self):
         self.codec.close()
+
+
+def _model_columns(model: int, records: List[dict]) -> pj.ModelColumns:
+    """Order / User dicts as host columns (None or missing: null)."""
+    props = pj.MODEL_PROPS[model]
+    n = len(records)
+    present = np.zeros(n, np.uint8)
+    col, byt = [], []
+    for k, (name, kind) in enumerate(props):
+        vals = [r.get(name) for r in records]
+        for i, v in enumerate(vals):
+            if v is not None:
+                present[i] |= 1 << k
+        if kind == "str":
+            bs = [v.encode("utf-8") if isinstance(v, str) else (v or b"") for v in vals]
+            off = np.zeros(n + 1, np.uint64)
+            off[1:] = np.cumsum([len(b) for b in bs], dtype=np.uint64) if n else []
+            col.append(off)
+            byt.append(np.frombuffer(b"".join(bs), np.uint8).copy())
+        else:
+            if kind == "enum":
+                vals = [pj.ORDER_STATUS.index(v) if v is not None else 0 for v in vals]
+            col.append(np.array([int(v or 0) for v in vals], pj.KIND_DTYPE[kind]))
+            byt.append(None)
+    return pj.ModelColumns(model, n, present, col, byt)
+
+
+def _model_records(c: pj.ModelColumns) -> List[dict]:
+    """Host columns back to dicts of the non-null properties."""
+    out = []
+    for i in range(c.n):
+        r = {}
+        for k, (name, kind) in enumerate(c.props):
+            if not (int(c.present[i]) >> k) & 1:
+                continue
+            v = c.col[k]
+            if kind == "str":
+                r[name] = c.bytes[k][int(v[i]): int(v[i + 1])].tobytes().decode("utf-8", "surrogateescape")
+            elif kind == "enum":
+                r[name] = pj.ORDER_STATUS[int(v[i])]
+            elif kind == "bool":
+                r[name] = bool(v[i])
+            else:
+                r[name] = int(v[i])
+        out.append(r)
+    return out

@@ -49,3 +49,24 @@ def test_python_mapper_write_read():
     r = m.read_value(b + b'{"name":1,"photoUrls":[]}\n')
     assert [norm_pet(p) for p in r.values] == [norm_pet(p) for p in pets]
     assert list(r.error_lines) == [2] and list(r.error_codes) == [pj.REC_TYPE]
+
+
+@pytest.mark.gpu
+def test_python_mapper_orders_users_and_find_by_status():
+    from mapper import PetObjectMapper, _model_columns
+    m = PetObjectMapper.get_default()
+    orders = [{"id": 1, "petId": 7, "quantity": 2, "shipDate": "2026-01-02T03:04:05Z", "status": "approved",
+               "complete": True}, {"id": 2}, {}]
+    users = [{"id": 9, "username": "ué\"", "userStatus": -3}, {"email": "a@b"}]
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON, pj.FORMAT_PRETTY):
+        ob, ub = m.write_orders(orders, fmt), m.write_users(users, fmt)
+        assert ob == orc.encode_model(_model_columns(pj.MODEL_ORDER, orders), fmt)
+        assert ub == orc.encode_model(_model_columns(pj.MODEL_USER, users), fmt)
+        ro = m.read_orders(ob, array=fmt != pj.FORMAT_NDJSON)
+        ru = m.read_users(ub, array=fmt != pj.FORMAT_NDJSON)
+        assert ro.values == orders and len(ro.error_lines) == 0
+        assert ru.values == users and len(ru.error_lines) == 0
+    pets = [Pet(name="a", photo_urls=[], status=StatusEnum.AVAILABLE), Pet(name="b", photo_urls=[]),
+            Pet(name="c", photo_urls=["u"], status=StatusEnum.SOLD)]
+    assert m.find_pets_by_status(pets) == orc.encode(to_columns(pets[:1]), pj.FORMAT_ARRAY)
+    assert m.find_pets_by_status(pets, 0b1100) == orc.encode(to_columns(pets[1:]), pj.FORMAT_ARRAY)
