@@ -401,3 +401,13 @@ def test_encode_by_status_host_matches_oracle(codec):
         got, m = codec.encode_by_status_host(cols, mask, fmt)
         want, wm = orc.encode_by_status(cols, mask, fmt)
         assert m == wm and got == want, (mask, fmt)
+
+
+def test_config1_gpu_output_matches_committed_digest(codec):
+    """BASELINE configs[0] on the GPU hashes to the committed digests."""
+    d = load("config1_digest.json")
+    dev = pj.generate(1, d["records"]).to_device()
+    for name, fmt in (("array", pj.FORMAT_ARRAY), ("ndjson", pj.FORMAT_NDJSON), ("pretty", pj.FORMAT_PRETTY)):
+        b = codec.encode(dev, fmt).cpu().numpy().tobytes()
+        assert len(b) == d["digests"][name]["bytes"]
+        assert hashlib.sha256(b).hexdigest() == d["digests"][name]["sha256"], name

@@ -377,3 +377,15 @@ def test_encode_by_status_is_encode_of_the_selected_records(config):
             got, m = orc.encode_by_status(cols, mask, fmt)
             assert m == len(chosen)
             assert got == orc.encode(to_columns(chosen), fmt), (mask, fmt)
+
+
+def test_config1_digest_is_pinned():
+    """the generator and the checker together reproduce
+    the committed digests (tests/golden/config1_digest.json)."""
+    import hashlib
+    d = load("config1_digest.json")
+    cols = pj.generate(1, d["records"])
+    for name, fmt in (("array", pj.FORMAT_ARRAY), ("ndjson", pj.FORMAT_NDJSON), ("pretty", pj.FORMAT_PRETTY)):
+        b = orc.encode(cols, fmt)
+        assert len(b) == d["digests"][name]["bytes"]
+        assert hashlib.sha256(b).hexdigest() == d["digests"][name]["sha256"], name
