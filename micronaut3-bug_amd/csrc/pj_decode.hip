@@ -1111,6 +1111,9 @@ __device__ __forceinline__ void rec_counts(const LineRec &r, uint64_t *v) {
 constexpr int PJ_BAIL = -1;
 // line kinds of the split decode (above the code in the line's info word)
 constexpr uint32_t LK_GENERAL = 1u << 8, LK_WAVE = 1u << 9, LK_BAD = 1u << 10;
+// a line the bitmap-free pass left to k_dec_measure_long (long, or a full
+// tape): its counters are missing from its block's scan until k_dec_fixup
+constexpr uint32_t LK_DEFER = 1u << 11;
 constexpr int PJ_TAPE_FULL = -2;  // valid so far, more items than the line tape holds: read by the wave
 
 // bit k set iff byte k of x equals c
@@ -2410,7 +2413,11 @@ __device__ __forceinline__ void load_tile(const DecParams &P, uint8_t *tile, uin
 // into sh_ls, and the block cut into sub-tiles: maximal runs of lines whose
 // bytes fit the LDS tile (normally one), their first lines in sh_sub.
 // Returns the number of sub-tiles.  All threads.
-template <int TILE>
+// With LONG > 0, a block that does not fit the tile whole gives each line
+// longer than LONG a sub-tile of its own, marked SUB_SKIP: such lines are
+// read elsewhere, so the sub-tile is never loaded.
+constexpr uint16_t SUB_SKIP = 0x8000;
+template <int TILE, int LONG = 0>
 __device__ __forceinline__ uint32_t block_subtiles(const DecParams &P, uint64_t l0, uint32_t cnt, uint64_t *sh_ls,
                                                    uint16_t *sh_sub, uint32_t *sh_nsub) {
     const uint32_t t = threadIdx.x;
@@ -2421,11 +2428,17 @@ __device__ __forceinline__ uint32_t block_subtiles(const DecParams &P, uint64_t 
         uint32_t j = 0;
         if (min(sh_ls[cnt], P.len) - (sh_ls[0] & ~15ull) <= TILE) sh_sub[j++] = 0;
         else {
+            auto is_long = [&](uint32_t k) { return LONG > 0 && sh_ls[k + 1] - 1 - sh_ls[k] > (uint64_t)LONG; };
             for (uint32_t k = 0; k < cnt;) {
+                if (is_long(k)) {
+                    sh_sub[j++] = (uint16_t)k | SUB_SKIP;
+                    k++;
+                    continue;
+                }
                 sh_sub[j++] = (uint16_t)k;
                 const uint64_t a = sh_ls[k] & ~15ull;
                 uint32_t k2 = k + 1;
-                while (k2 < cnt && min(sh_ls[k2 + 1], P.len) - a <= TILE) k2++;
+                while (k2 < cnt && !is_long(k2) && min(sh_ls[k2 + 1], P.len) - a <= TILE) k2++;
                 k = k2;
             }
         }
@@ -2481,9 +2494,10 @@ __device__ __noinline__ int run_line_measure(const DecParams &P, const Src S, ui
 }
 
 // BM false (split decode only): no bitmaps in LDS, so more workgroups share
-// a CU; a block that holds a line for the wave path (long, or too many items
-// for its tape) gives up before it writes anything and joins P.bm_list, whose
-// blocks k_dec_block_bm then reads with the bitmaps.
+// a CU.  A line for the wave path (long, or too many items for its tape) is
+// deferred: it enters the block's scan with zero counters, goes to
+// P.long_list for k_dec_measure_long, and its block joins P.bm_list, whose
+// offsets k_dec_fixup then corrects.
 template <int BT, int TILE, int LONG, int LPB, bool TAPE, bool BM>
 __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
     static_assert(LONG < 65536, "tape positions of per-thread lines are 16-bit");
@@ -2504,7 +2518,7 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
     const uint32_t cnt = (uint32_t)min((uint64_t)LPB, P.lines - l0);
     const uint64_t l = l0 + t;
     const bool live = t < cnt;
-    const uint32_t nsub = block_subtiles<TILE>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
+    const uint32_t nsub = block_subtiles<TILE, BM ? 0 : LONG>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
     uint64_t gs = 0;
     uint32_t n = 0;
     if (live) {
@@ -2512,13 +2526,6 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
         n = (uint32_t)(sh_ls[t + 1] - 1 - gs);
     }
     bool longl = n > (uint32_t)LONG;               // read by the owning wave (also: tape full)
-    if constexpr (!BM) {
-        if (block_any(longl, &sh_any)) {
-            if (t == 0) P.bm_list[atomicAdd(P.bm_count, 1ull)] = b;
-            return;
-        }
-    }
-    bool handover = false;                          // (!BM) a tape filled up: the block is handed over
     // ---- pass 0: validate and measure, sub-tile by sub-tile
     LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
     int code = 0;
@@ -2526,7 +2533,8 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
     uint32_t s0 = 0;                                // tile offset of this thread's line
     uint64_t ta0 = 0, ttb = 0;                      // its sub-tile
     for (uint32_t j = 0; j < nsub; j++) {
-        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
+        if (sh_sub[j] & SUB_SKIP) continue;         // (!BM) one long line: deferred
+        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1] & ~SUB_SKIP;
         const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
         const bool sub_over = tb > TILE;            // one line, longer than the tile
         const bool mine = live && t >= ka && t < kb;
@@ -2557,12 +2565,6 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
                     need_gen = code == PJ_BAIL;
                 }
             }
-            if constexpr (!BM) {
-                if (block_any(mine && longl, &sh_any)) {
-                    handover = true;
-                    break;
-                }
-            }
             // long lines: the wave of the owning thread reads them together,
             // over the bitmaps, which only sub-tiles holding one build
             if (BM && block_any(mine && longl, &sh_any)) {
@@ -2587,7 +2589,7 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
                     if (bad) code = PJ_REC_STRING;  // provisional: k_dec_errcode settles it
                 }
             }
-            for (uint64_t m = __ballot(mine && !bad && longl); m; m &= m - 1) {
+            for (uint64_t m = BM ? __ballot(mine && !bad && longl) : 0ull; m; m &= m - 1) {
                 const int k = __builtin_ctzll(m);
                 const uint32_t ks0 = (uint32_t)__shfl((int)s0, k, 64), kn = (uint32_t)__shfl((int)n, k, 64);
                 LineRec rr{0, 0, 0, 0, 0, 0, 0, 0};
@@ -2598,7 +2600,7 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
                     need_gen = cc == PJ_BAIL;
                 }
             }
-        } else if (mine) {
+        } else if (BM && mine) {                    // (!BM: such a line is long, so deferred)
             over = true;
             need_gen = true;
         }
@@ -2615,18 +2617,16 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
         }
         __syncthreads();                            // the tile is reused by the next sub-tile
     }
+    const bool defer = !BM && live && longl;
     if constexpr (!BM) {
-        if (handover) {
-            if (t == 0) P.bm_list[atomicAdd(P.bm_count, 1ull)] = b;
-            return;
-        }
+        if (block_any(defer, &sh_any) && t == 0) P.bm_list[atomicAdd(P.bm_count, 1ull)] = b;
     }
     if (general) atomicAdd(P.gq_count, 1ull);       // diagnostics: lines off the fast path
     r.code = live ? (uint32_t)code : 0;
     if (live && code == PJ_REC_EMPTY) atomicAdd(P.empty_count, 1ull);
     // ---- scans and look-back
     uint64_t v[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (live) rec_counts(r, v);
+    if (live && !defer) rec_counts(r, v);
     uint32_t pos[PJ_DEC_NCNT];                      // block-relative: a block's columns stay below 2^32 bytes
     uint64_t agg[PJ_DEC_NCNT];
     {
@@ -2646,10 +2646,12 @@ __device__ __forceinline__ void dec_block(DecParams &P, const uint64_t b) {
 #pragma unroll
             for (int k = 0; k < PJ_DEC_NCNT; k++) P.lpos[k * L + l] = pos[k];
             const bool wave = longl && !general && !bad && code == 0;
-            P.lpos[PJ_DEC_NCNT * L + l] = (uint32_t)code | (general ? LK_GENERAL : 0u) | (wave ? LK_WAVE : 0u) |
-                                          (bad ? LK_BAD : 0u);
-            // lines of the whole wave or the general parser are written by k_dec_long
-            if (code == 0 && (wave || general)) P.long_list[atomicAdd(P.long_count, 1ull)] = l;
+            P.lpos[PJ_DEC_NCNT * L + l] = defer ? LK_DEFER
+                                                : (uint32_t)code | (general ? LK_GENERAL : 0u) | (wave ? LK_WAVE : 0u) |
+                                                      (bad ? LK_BAD : 0u);
+            // lines of the whole wave or the general parser are written by
+            // k_dec_long (deferred ones once k_dec_measure_long has read them)
+            if (defer || (code == 0 && (wave || general))) P.long_list[atomicAdd(P.long_count, 1ull)] = l;
         }
         if (t < PJ_DEC_NCNT) {
             uint64_t x = 0;
@@ -2769,20 +2771,101 @@ __global__ __launch_bounds__(BT, BM ? 2 : 3) void k_dec_block(DecParams P) {
     dec_block<BT, TILE, LONG, LPB, TAPE, BM>(P, sh_blk);
 }
 
-// The blocks the bitmap-free pass handed over, read with the bitmaps: a
-// fixed grid claims them one at a time (their costs differ widely; the list
-// is empty in most calls).
-template <int BT, int TILE, int LONG, int LPB>
-__global__ __launch_bounds__(BT, 2) void k_dec_block_bm(DecParams P) {
-    __shared__ uint64_t sh_i;
-    const uint64_t cnt = *P.bm_count;
-    for (;;) {
-        if (threadIdx.x == 0) sh_i = atomicAdd(P.bm_count + 1, 1ull);
-        __syncthreads();
-        const uint64_t i = sh_i;
-        if (i >= cnt) break;
-        dec_block<BT, TILE, LONG, LPB, true, true>(P, P.bm_list[i]);
-        __syncthreads();                            // LDS is reused by the next block
+// The lines the bitmap-free pass deferred, one 64-thread workgroup per line
+// at a time: the line is tiled into LDS with its bitmaps, checked for bad
+// bytes and read by the wave-parallel walk (a line longer than the tile, or
+// one the walk does not recognise, by the general parser on one thread).
+// Its 8 counters go to tape words 0-7, its code and kind to its info word;
+// LK_DEFER stays set for k_dec_fixup.
+template <int TILE>
+__global__ __launch_bounds__(64) void k_dec_measure_long(DecParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
+    __shared__ uint64_t spec[TILE / 64 + 1];
+    __shared__ uint64_t badm[TILE / 64 + 1];
+    __shared__ uint64_t sh_scan[1];
+    const uint64_t cnt = *P.long_count, L = P.lines;
+    const uint32_t t = threadIdx.x;
+    for (uint64_t i = blockIdx.x; i < cnt; i += gridDim.x) {
+        const uint64_t l = P.long_list[i];
+        const uint32_t info = __builtin_amdgcn_readfirstlane(P.lpos[PJ_DEC_NCNT * L + l]);
+        if (!(info & LK_DEFER)) continue;           // a general line of the validating pass
+        const uint64_t gs = P.line_start[l], ge = P.line_start[l + 1];
+        const uint32_t n = (uint32_t)(ge - 1 - gs);
+        const uint64_t a0 = gs & ~15ull, tb = min(ge, P.len) - a0;
+        const uint32_t s0 = (uint32_t)(gs - a0);
+        LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+        int code = 0;
+        bool general = false, bad = false;
+        LineInfo Li;
+        if (tb > TILE) {
+            general = true;
+            if (t == 0) code = run_line_measure(P, Src{P.in, P.len, nullptr}, gs, n, &Li);
+        } else {
+            const uint32_t nw = (uint32_t)((tb + 63) >> 6);
+            load_tile<64>(P, tile, a0, gs, tb, nw);
+            __syncthreads();
+            if (P.array_doc && t == 0) tile[s0 + n] = '\n';
+            __syncthreads();
+            tile_bitmaps<64>(tile, nw, spec, badm, sh_scan);
+            __syncthreads();
+            bad = line_bad(badm, nw, s0, n);
+            if (bad) code = PJ_REC_STRING;          // provisional: k_dec_errcode settles it
+            else {
+                code = fline_wave<false>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, s0, n, r, nullptr, nullptr);
+                if (code == PJ_BAIL) {
+                    general = true;
+                    if (t == 0) code = run_line_measure(P, Src{tile, tb, nullptr}, s0, n, &Li);
+                }
+            }
+        }
+        if (t == 0) {
+            if (general && !code) {
+                r.name_len = Li.name_len; r.cat_len = Li.has_cat ? Li.cat_len : 0; r.n_urls = Li.n_urls;
+                r.url_bytes = Li.url_bytes; r.n_tags = Li.n_tags; r.tag_bytes = Li.tag_bytes;
+            }
+            r.code = (uint32_t)code;
+            uint64_t v[PJ_DEC_NCNT];
+            rec_counts(r, v);
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) P.tape[k * L + l] = v[k];
+            const bool wave = !general && !bad && code == 0;
+            P.lpos[PJ_DEC_NCNT * L + l] = (uint32_t)code | LK_DEFER | (general ? LK_GENERAL : 0u) |
+                                          (wave ? LK_WAVE : 0u) | (bad ? LK_BAD : 0u);
+            if (general) atomicAdd(P.gq_count, 1ull);
+        }
+        __syncthreads();                            // the tile is reused by the next line
+    }
+}
+
+// The blocks holding deferred lines: each line's offsets inside its block
+// gain the counters of the deferred lines before it, and the block's totals
+// gain theirs.  Runs after k_dec_measure_long, before the block scan.
+template <int BT, int LPB>
+__global__ __launch_bounds__(BT) void k_dec_fixup(DecParams P) {
+    static_assert(LPB <= BT, "one line per thread");
+    __shared__ uint32_t sh_scan[PJ_DEC_NCNT * (BT / 64)];
+    const uint64_t cnt = *P.bm_count, L = P.lines;
+    const uint32_t t = threadIdx.x;
+    for (uint64_t i = blockIdx.x; i < cnt; i += gridDim.x) {
+        const uint64_t b = P.bm_list[i], l0 = b * LPB, l = l0 + t;
+        const bool live = t < LPB && l < L;
+        const uint32_t info = live ? P.lpos[PJ_DEC_NCNT * L + l] : 0u;
+        const bool def = (info & LK_DEFER) != 0;
+        uint32_t v[PJ_DEC_NCNT], ex[PJ_DEC_NCNT], tot[PJ_DEC_NCNT];
+#pragma unroll
+        for (int k = 0; k < PJ_DEC_NCNT; k++) v[k] = def ? (uint32_t)P.tape[k * L + l] : 0u;
+        block_excl_scan_n<BT, PJ_DEC_NCNT>(v, ex, tot, sh_scan);
+        if (live) {
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++)
+                if (ex[k]) P.lpos[k * L + l] += ex[k];
+        }
+        if (t < PJ_DEC_NCNT) {
+            uint64_t x = 0;
+#pragma unroll
+            for (int k = 0; k < PJ_DEC_NCNT; k++) x = k == (int)t ? tot[k] : x;
+            P.bagg[b * PJ_DEC_NCNT + t] += x;
+        }
     }
 }
 
@@ -2859,7 +2942,7 @@ __global__ __launch_bounds__(BT) void k_dec_bscan(DecParams P) {
 // sub-tiles), and each thread writes its fast-path line from its tape at the
 // offsets the scan gave.  Invalid lines get their error slot; lines of the
 // whole wave or the general parser are left to k_dec_long.
-template <int BT, int TILE, int LPB>
+template <int BT, int TILE, int LPB, int LONG>
 __global__ __launch_bounds__(BT, 2) void k_dec_write(DecParams P) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
     __shared__ uint64_t sh_ls[LPB + 1];
@@ -2871,7 +2954,7 @@ __global__ __launch_bounds__(BT, 2) void k_dec_write(DecParams P) {
     const uint64_t l = l0 + t;
     const bool live = t < cnt;
     const pj_pet_columns &o = P.o;
-    const uint32_t nsub = block_subtiles<TILE>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
+    const uint32_t nsub = block_subtiles<TILE, LONG>(P, l0, cnt, sh_ls, sh_sub, &sh_nsub);
     if (b == 0 && t == 0) {
         o.name_off[0] = 0; o.cat_name_off[0] = 0; o.photo_off[0] = 0; o.tag_off[0] = 0;
         o.url_off[0] = 0; o.tag_name_off[0] = 0;
@@ -2905,7 +2988,8 @@ __global__ __launch_bounds__(BT, 2) void k_dec_write(DecParams P) {
     uint64_t tw[TAPE_PRE];
     if (fastl) tape_prefetch(Tape{P.tape + l, L}, tw);
     for (uint32_t j = 0; j < nsub; j++) {
-        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1];
+        if (sh_sub[j] & SUB_SKIP) continue;         // one long line: written by k_dec_long
+        const uint32_t ka = sh_sub[j], kb = sh_sub[j + 1] & ~SUB_SKIP;
         const uint64_t g0 = sh_ls[ka], a0 = g0 & ~15ull, g1 = min(sh_ls[kb], P.len), tb = g1 - a0;
         if (tb <= TILE) {                           // a longer sub-tile is one line of the general parser
             load_tile<BT>(P, tile, a0, g0, tb, (uint32_t)((tb + 63) >> 6));
@@ -2939,7 +3023,9 @@ __global__ __launch_bounds__(64) void k_dec_long(DecParams P) {
         const uint64_t l = P.long_list[i];
         const uint64_t gs = P.line_start[l], ge = P.line_start[l + 1];
         const uint32_t n = (uint32_t)(ge - 1 - gs);
-        if (P.lpos[PJ_DEC_NCNT * L + l] & LK_GENERAL) {
+        const uint32_t info = __builtin_amdgcn_readfirstlane(P.lpos[PJ_DEC_NCNT * L + l]);
+        if (info & 0xFF) continue;                  // a deferred line found invalid
+        if (info & LK_GENERAL) {
             // the general parser, from the input (the measuring walk, then the writing walk)
             if (threadIdx.x == 0) {
                 uint64_t gp[PJ_DEC_NCNT];
@@ -3083,7 +3169,7 @@ hipError_t pj_launch_dec_bscan(const DecParams &P, hipStream_t st) {
 }
 
 hipError_t pj_launch_dec_write(const DecParams &P, hipStream_t st) {
-    hipLaunchKernelGGL((pj::k_dec_write<DEC_LINE_BT, DEC_WTILE, DEC_LPB>), dim3((unsigned)P.nblocks), dim3(DEC_LINE_BT), 0,
+    hipLaunchKernelGGL((pj::k_dec_write<DEC_LINE_BT, DEC_WTILE, DEC_LPB, DEC_LONG>), dim3((unsigned)P.nblocks), dim3(DEC_LINE_BT), 0,
                        st, P);
     return hipGetLastError();
 }
@@ -3097,11 +3183,12 @@ hipError_t pj_launch_dec_parse(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.lines + DEC_LPB - 1) / DEC_LPB;
     if (P.tape) {
         // every block without bitmaps (five workgroups per CU), then the
-        // blocks it handed over with them
+        // lines it deferred, then its offsets corrected for them
         hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_FTILE, DEC_LONG, DEC_LPB, true, false>), dim3((unsigned)g),
                            dim3(DEC_LINE_BT), 0, st, P);
-        hipLaunchKernelGGL((pj::k_dec_block_bm<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB>),
-                           dim3((unsigned)(g < 1024 ? g : 1024)), dim3(DEC_LINE_BT), 0, st, P);
+        hipLaunchKernelGGL((pj::k_dec_measure_long<DEC_TILE>), dim3(1024), dim3(64), 0, st, P);
+        hipLaunchKernelGGL((pj::k_dec_fixup<DEC_LINE_BT, DEC_LPB>), dim3((unsigned)(g < 1024 ? g : 1024)),
+                           dim3(DEC_LINE_BT), 0, st, P);
     } else
         hipLaunchKernelGGL((pj::k_dec_block<DEC_LINE_BT, DEC_TILE, DEC_LONG, DEC_LPB, false>), dim3((unsigned)g),
                            dim3(DEC_LINE_BT), 0, st, P);

@@ -110,8 +110,8 @@ struct DecParams {
     // look-back words bstate); the writer kernels then need no waiting
     uint32_t *lpos;
     uint64_t *bagg, *bbase, *bstate;
-    uint64_t *bm_list;         // split decode: blocks handed to the bitmap pass (nblocks entries)
-    unsigned long long *bm_count;  // [0] blocks in bm_list, [1] blocks claimed by the bitmap pass
+    uint64_t *bm_list;         // split decode: blocks holding deferred lines (nblocks entries)
+    unsigned long long *bm_count;  // [0] blocks in bm_list, [1] unused
     uint64_t nblocks;          // line blocks of the validating kernel
     uint64_t *long_list;       // lines read by a whole wave, written by k_dec_long
     unsigned long long *long_count;
