@@ -296,10 +296,10 @@ def test_decode_long_lines_wave_parallel(codec):
 
 def test_decode_tape_full_lines_hand_over(codec):
     """Short lines with more url and tag words than a line's tape holds (27)
-    go to the wave path: the bitmap-free validating pass hands their block to
-    the bitmap pass before writing anything, also when such a line sits in
-    a block's second sub-tile (blocks of 104 lines of about 400 bytes), and
-    next to lines the general parser reads.  Against the oracle."""
+    go to the wave path: the bitmap-free validating pass defers them after
+    writing part of their tape, also when such a line sits in a block's
+    second sub-tile (blocks of 104 lines of about 400 bytes), and next to
+    lines the general parser reads.  Against the oracle."""
     rnd = random.Random(7)
 
     def rec(i, nu, nt, pad):
@@ -322,6 +322,51 @@ def test_decode_tape_full_lines_hand_over(codec):
     data = b"\n".join(lines + mut) + b"\n"
     ref = orc.decode(data)
     for shift in (0, 5):
+        assert_same(gpu_decode(codec, data, shift=shift), ref)
+
+
+def test_decode_deferred_lines_fix_offsets(codec):
+    """Long lines deferred by the bitmap-free pass, at every kind of place in
+    their blocks (first, last, several in a row, one per block, most of a
+    block), and of every kind: valid, valid with escapes and many tags, a bad
+    byte inside a string, a status outside the enum, whitespace the wave walk
+    leaves to the general parser, longer than the tile, an unknown key.  The
+    short lines after them take their offsets from k_dec_fixup; the error
+    slots too.  Against the oracle, with the input at two alignments."""
+    rnd = random.Random(11)
+
+    def short(i):
+        return ('{"id":%d,"name":"s%d","photoUrls":["p"],"tags":[{"id":%d,"name":"x"}],"status":"sold"}'
+                % (i, i, i)).encode()
+
+    def long_line(i, kind):
+        name = "L" * rnd.randrange(1100, 4000)
+        tags = ",".join('{"id":%d,"name":"t\\u00e9%d"}' % (k, k) for k in range(rnd.randrange(0, 60)))
+        body = '"id":%d,"name":"%s","photoUrls":["a\\nb"],"tags":[%s],"status":"pending"' % (i, name, tags)
+        if kind == 1:
+            body = body.replace("LLLL", "L\x01LL", 1)                # a raw control byte in a string
+        elif kind == 2:
+            body = body.replace('"pending"', '"lost"')                # not in the enum
+        elif kind == 3:
+            body = body.replace('"tags":', '"tags" : ')              # whitespace: the general parser
+        elif kind == 4:
+            body = body.replace(name, "W" * 40000)                     # over the tile
+        elif kind == 5:
+            body = '"extra":{"k":[1,2,{"z":null}]},' + body           # an unknown key
+        return ("{" + body + "}").encode()
+
+    lines = []
+    for blk in range(40):
+        pat = blk % 5
+        for j in range(104):
+            i = len(lines)
+            longp = (pat == 0 and j in (0, 103)) or (pat == 1 and 10 <= j < 14) or (pat == 2 and j == 50) \
+                or (pat == 3 and j % 3 != 1)
+            lines.append(long_line(i, rnd.randrange(6)) if longp else short(i))
+    data = b"\n".join(lines) + b"\n"
+    ref = orc.decode(data)
+    assert ref[3].n_errors > 20
+    for shift in (0, 7):
         assert_same(gpu_decode(codec, data, shift=shift), ref)
 
 
