@@ -2183,8 +2183,10 @@ __device__ __noinline__ int fline_wave(const PJ_LDS uint8_t *tile, const PJ_LDS 
 // bitmap (unescaped quotes | backslashes) and a per-word flag for raw control
 // characters or malformed UTF-8 inside strings.  Each thread owns a
 // contiguous run of words; the in-string carry between runs comes from a
-// block scan of (newline seen, quote parity).
-template <int BT>
+// block scan of (newline seen, quote parity).  With BAD false only the
+// specials bitmap is built (one pass, no scan): enough to walk a line known
+// to be valid.
+template <int BT, bool BAD = true>
 __device__ __forceinline__ void tile_bitmaps(const uint8_t *tile, uint32_t nw, uint64_t *spec, uint64_t *qu,
                                              uint64_t *sh) {
     const uint32_t t = threadIdx.x;
@@ -2229,6 +2231,7 @@ __device__ __forceinline__ void tile_bitmaps(const uint8_t *tile, uint32_t nw, u
         } else par = __builtin_popcountll(Qu) & 1;
         summ = idx_combine(summ, (N ? 2ull : 0ull) | par);
     }
+    if constexpr (!BAD) return;
     uint64_t tot;
     const uint64_t carry0 = block_excl_scan_idx<BT>(summ, sh, &tot);
     // pass 2: in-string mask, faults inside strings
@@ -3044,7 +3047,7 @@ __global__ __launch_bounds__(64) void k_dec_long(DecParams P) {
         __syncthreads();
         if (P.array_doc && threadIdx.x == 0) tile[gs + n - a0] = '\n';
         __syncthreads();
-        tile_bitmaps<64>(tile, nw, spec, badm, sh_scan);
+        tile_bitmaps<64, false>(tile, nw, spec, badm, sh_scan);  // the line is valid: specials only
         __syncthreads();
         const uint64_t pb = l / LPB;
         uint64_t base[PJ_DEC_NCNT];
