@@ -67,6 +67,38 @@ def test_array_roundtrip_gpu(codec, config):
     assert_same(doc, gpu_array(codec, doc), orc.decode_array(doc))
 
 
+def test_array_deferred_long_elements(codec):
+    """Elements over 1 KiB among short ones, so the validating pass defers
+    them to the one-wave kernels: valid ones (escapes, many tags), a raw
+    control byte in a string, a status outside the enum, whitespace the
+    wave walk leaves to the general parser, one longer than the tile.  The
+    separators around them vary.  Against the oracle."""
+    rnd = random.Random(23)
+
+    def elem(i):
+        if rnd.random() < 0.8:
+            return ('{"id":%d,"name":"s%d","photoUrls":[],"status":"sold"}' % (i, i)).encode()
+        kind = rnd.randrange(5)
+        name = "N" * rnd.randrange(1100, 3000)
+        tags = ",".join('{"id":%d,"name":"t\\t%d"}' % (k, k) for k in range(rnd.randrange(0, 40)))
+        body = '"id":%d,"name":"%s","photoUrls":["x"],"tags":[%s],"status":"available"' % (i, name, tags)
+        if kind == 1:
+            body = body.replace("NNNN", "N\x02NN", 1)
+        elif kind == 2:
+            body = body.replace('"available"', '"gone"')
+        elif kind == 3:
+            body = body.replace('"photoUrls":', '"photoUrls" :')
+        elif kind == 4:
+            body = body.replace(name, "Z" * 36000)
+        return ("{" + body + "}").encode()
+
+    doc = join_array([elem(i) for i in range(700)], rnd)
+    ref = orc.decode_array(doc)
+    assert ref[0] == pj.PJ_OK and ref[4].n_errors > 10
+    for shift in (0, 3):
+        assert_same(doc, gpu_array(codec, doc, shift=shift), ref)
+
+
 def test_array_host_entry_point(codec):
     doc = orc.encode(pj.generate(3, 3000), pj.FORMAT_ARRAY)
     cols, el, ec, res = codec.decode_array_host(doc)
