@@ -209,6 +209,12 @@ pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n) {
 }
 
 bool nested_cols(const pj_pet_columns *c) { return c->cat_id || c->photo_off || c->tag_off; }
+// PETJSON_ENC_TWO_PASS=1 writes nested records at the offsets of the
+// measuring pass instead of with the single pass (kept to compare the two).
+bool enc_two_pass() {
+    const char *e = std::getenv("PETJSON_ENC_TWO_PASS");
+    return e && e[0] == '1';
+}
 
 pj_status check_enc_cols(const pj_pet_columns *c) {
     if (c->n_pets == 0) return PJ_OK;
@@ -282,6 +288,13 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     const bool pretty = format == PJ_FORMAT_PRETTY;
     const uint64_t bt = (uint64_t)(pretty ? pj_encode_pretty_records() : pj_encode_block_records(nested_cols(cols)));
     const uint64_t nblk = (n + bt - 1) / bt;
+    // Nested records: the size alone comes from the measuring pass
+    // (k_enc_measure), which also gives every block its bounds and offset.
+    // The bytes come from the single pass, each block placed by its own
+    // look-back; it measured faster than the measuring pass followed by a
+    // writer at the given offsets (PETJSON_ENC_TWO_PASS=1).  The fixed
+    // scratch of the no-allocation entry point holds only the single pass.
+    const bool two_pass = !pretty && nested_cols(cols) && !fixed_scratch && (count_only || enc_two_pass());
     uint64_t *sc;
     if (fixed_scratch) {
         if (n > PJ_NOALLOC_MAX_RECORDS(nested_cols(cols)) || nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
@@ -290,7 +303,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
                                                 std::to_string(PJ_NOALLOC_MAX_RECORDS(nested_cols(cols))) + ")");
         sc = ctx->noalloc_scratch;
     } else {
-        PJ_HIP(ctx->scan.ensure((nblk + 3 + 128) * sizeof(uint64_t)));
+        PJ_HIP(ctx->scan.ensure((nblk + 3 + 128 + (two_pass ? GEO_WORDS * nblk : 0)) * sizeof(uint64_t)));
         sc = static_cast<uint64_t *>(ctx->scan.p);
     }
     EncParams P;
@@ -308,6 +321,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.nfall = reinterpret_cast<unsigned long long *>(sc + 2);
     P.state = sc + 3;
     P.dummy = reinterpret_cast<uint32_t *>(sc + 3 + nblk);   // 128 u64 = PJ_BLOCK dwords
+    uint64_t *geo = two_pass ? sc + 3 + nblk + 128 : nullptr;
     // Nested records run on persistent workgroups that claim their blocks by
     // ticket.  Flat blocks run one per workgroup in launch order (no ticket
     // atomic on the critical path) with bounded look-back waits: should a
@@ -320,7 +334,15 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
         PJ_HIP(pj_launch_fill_u64(sc, nblk + 3, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
         if (pretty) PJ_HIP(pj_launch_encode_rows(P, true, ctx->stream));
-        else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
+        else if (two_pass) {
+            P.geo = geo;
+            PJ_HIP(pj_launch_encode_measure(P, ctx->stream));
+            if (!count_only) {
+                if ((s = mark(ctx))) return s;
+                P.geo = geo;
+                PJ_HIP(pj_launch_encode(P, true, false, ctx->stream));
+            }
+        } else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
         if ((s = mark(ctx))) return s;
         PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));

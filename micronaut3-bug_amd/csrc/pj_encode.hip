@@ -214,18 +214,30 @@ template <class S> __device__ __forceinline__ void esc_bytes(S &s, uint64_t x, i
     }
     if (m > done) s.put8(x >> (8 * done), m - done);
 }
-__device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint32_t) {
+// Bytes the escapes of the bytes of x selected by keep add to them: one for
+// each byte needing an escape, four more for the controls other than
+// \b \t \n \f \r (which take six bytes, the rest two).
+__device__ __forceinline__ uint32_t esc_extra(uint64_t x, uint64_t keep) {
     constexpr uint64_t L7 = 0x7F7F7F7F7F7F7F7Full, H = 0x8080808080808080ull;
-    const uint64_t keep = m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1);
     const uint64_t sp = special_mask(x) & keep & H;
-    // controls other than \b \t \n \f \r take six bytes, the rest two
     const uint64_t lo = x & L7;
     const uint64_t lt20 = ~((lo + 0x6060606060606060ull) | x) & H;
     const uint64_t ge8 = (lo + 0x7878787878787878ull) & H, lt14 = ~(lo + 0x7272727272727272ull) & H;
     const uint64_t y = x ^ 0x0B0B0B0B0B0B0B0Bull;
     const uint64_t eq11 = ~(((y & L7) + L7) | y) & H;
     const uint64_t lng = lt20 & ~(ge8 & lt14 & ~eq11) & keep;
-    s.n += (uint64_t)(m + __builtin_popcountll(sp) + 4 * __builtin_popcountll(lng));
+    return (uint32_t)(__builtin_popcountll(sp) + 4 * __builtin_popcountll(lng));
+}
+__device__ __forceinline__ void esc_bytes(CountSink &s, uint64_t x, int m, uint32_t) {
+    const uint64_t keep = m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1);
+    s.n += (uint64_t)m + esc_extra(x, keep);
+}
+// The escape bytes of a string in global memory (esc_extra over its bytes).
+__device__ __forceinline__ uint64_t str_extra(const uint8_t *p, uint64_t len) {
+    uint64_t e = 0, k = 0;
+    for (; k + 8 <= len; k += 8) e += esc_extra(ldu64(p + k), ~0ull);
+    if (k < len) e += esc_extra(ld_tail(p + k, (int)(len - k)), (1ull << (8 * (len - k))) - 1);
+    return e;
 }
 
 // The string bytes of a staged slice, read as aligned LDS qwords joined by a
@@ -319,11 +331,15 @@ struct ColSrc {
     // of the staging buffer (from sbase) holds a byte that needs an escape
     const uint64_t *plain = nullptr;
     const uint8_t *sbase = nullptr;
+    // lengths only, bytes not read: every string counts as escape-free (the
+    // measuring kernel adds the escapes of all bytes separately)
+    bool all_plain = false;
 };
 
 // Whether staged bytes [p, p + len) need no escape: every 16-byte chunk they
 // touch is clear in the chunk bitmap (a set chunk may belong to a neighbour).
 __device__ __forceinline__ bool staged_plain(const ColSrc &X, const uint8_t *p, uint64_t len) {
+    if (X.all_plain) return true;
     if (!X.plain || len == 0) return X.plain != nullptr;
     const uint32_t a = (uint32_t)(p - X.sbase), c0 = a >> 4, c1 = (a + (uint32_t)len - 1) >> 4;
     for (uint32_t w = c0 >> 6; w <= (c1 >> 6); w++) {
@@ -837,8 +853,10 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 // level (url and tag item ranges, name and category name byte ranges),
 // lanes 0-3 then the url and tag name byte ranges those select.  Laid out
 // as [0] first url item, [1] end, [2] first tag item, [3] end, then
-// (first byte, end) of the name, category name, url and tag name columns.
-constexpr int NX = 12;
+// (first byte, end) of the name, category name, url and tag name columns;
+// [12] the block's output offset when the bounds and offsets are given
+// (P.geo).
+constexpr int NX = GEO_WORDS;
 template <bool NESTED, int R>
 __device__ __forceinline__ uint64_t bounds_l1(const EncParams &P, uint64_t nb, uint32_t l) {
     const pj_pet_columns &c = P.c;
@@ -861,10 +879,18 @@ __device__ __forceinline__ void bounds_store(uint64_t *nx, uint64_t v1, uint64_t
     if (l < 8) nx[l] = v1;
     if (l < 4) nx[8 + l] = v2;
 }
-// The first wave claims the next block by ticket and stores its number and
-// bounds (lane l of the wave).
+// The first wave claims the next block, by ticket, and stores its number and
+// bounds (lane l of the wave).  With the bounds and offsets given (P.geo)
+// the next block is the static successor cur + gridDim.x and its GEO_WORDS
+// words are one load away.
 template <bool NESTED, int R>
-__device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uint64_t *nb, uint32_t l) {
+__device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uint64_t *nb, uint32_t l, uint64_t cur) {
+    if (P.geo) {
+        const uint64_t n1 = cur + gridDim.x;
+        if (l < (uint32_t)GEO_WORDS && n1 < (P.n + R - 1) / R) nx[l] = P.geo[GEO_WORDS * n1 + l];
+        if (l == 0) *nb = n1;
+        return;
+    }
     unsigned long long tk = 0;
     if (l == 0) tk = atomicAdd(P.ticket, 1ull);
     const uint64_t n1 = (uint64_t)__shfl((long long)tk, 0);
@@ -1020,11 +1046,15 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     // ---- the first block: its number and bounds, then its loads
     if (t < 64) {
         unsigned long long tk = 0;
-        const bool by_id = !PERSIST && P.order_by_id;
+        const bool by_id = (!PERSIST && P.order_by_id) || P.geo;
         if (!by_id && t == 0) tk = atomicAdd(P.ticket, 1ull);
         const uint64_t b0 = by_id ? (uint64_t)blockIdx.x : (uint64_t)__shfl((long long)tk, 0);
-        const uint64_t v1 = bounds_l1<NESTED, R>(P, b0, t);
-        bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
+        if (P.geo) {
+            if (t < (uint32_t)GEO_WORDS && b0 < nblk) sh_nx[t] = P.geo[GEO_WORDS * b0 + t];
+        } else {
+            const uint64_t v1 = bounds_l1<NESTED, R>(P, b0, t);
+            bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
+        }
         if (t == 0) sh_nb = b0;
     }
     __syncthreads();
@@ -1044,6 +1074,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
 #endif
         EPROF(0);
         const Geo g = block_geo<NESTED, R, INCAP, UCAP, GCAP>(sh_nx, b);
+        const uint64_t gbase = sh_nx[12];               // given offset (P.geo)
         uint64_t nb = 0;
         // the flat tile starts zeroed: writers merge the qwords they share with an OR
         if (!NESTED)
@@ -1175,7 +1206,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         }
         // ---- block scan, publish the aggregate
         if (!(NESTED && fast)) pre = block_excl_scan<BT>(len, sh_scan, &agg);
-        if (t == 0) lb_publish(P.state, b, agg);
+        if (t == 0 && !P.geo) lb_publish(P.state, b, agg);
         // (the copy-out reads up to 32 bytes past the block's bytes)
         const bool fits = fast && agg + 32 <= TILE;
         if (!fits && t == 0 && P.nfall) atomicAdd(P.nfall, 1ull);    // blocks off the tile path
@@ -1255,7 +1286,9 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         // that consecutive tickets start at nearly the same time and a
         // look-back finds its predecessors published) and its bounds fetched
         // by the first wave while the others copy the tile out
-        if (t < 64) {
+        if (P.geo) {
+            if (t == 0) sh_base = gbase;
+        } else if (t < 64) {
             const uint64_t excl = lb_resolve(P.state, b, agg, !PERSIST && P.order_by_id ? P.spin_limit : 0, P.ticket);
             if (t == 0) {
                 sh_base = excl;
@@ -1270,7 +1303,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         // starts soon after its ticket
         const bool early = fits || P.count_only;
         if (PERSIST && early && t < 64) {
-            claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
+            claim_next<NESTED, R>(P, sh_nx, &sh_nb, t, b);
             EPROF(6);
         }
         const uint64_t base = sh_base;
@@ -1326,13 +1359,211 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             }
         }
         if (!PERSIST) break;
-        if (!early && t < 64) claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
+        if (!early && t < 64) claim_next<NESTED, R>(P, sh_nx, &sh_nb, t, b);
         // the next block's loads (record, item and staging values)
         __syncthreads();
         nb = sh_nb;
         if (nb < nblk)
             enc_prefetch<NESTED, BT, R, NI, SV>(P, block_geo<NESTED, R, INCAP, UCAP, GCAP>(sh_nx, nb), rv, iv, sv);
         b = nb;
+    }
+}
+
+// Nested records, first of two passes: the exact output length of every
+// block of R records (the blocks k_encode writes), and every block's bounds
+// and output offset (GEO_WORDS words at P.geo[GEO_WORDS * b]); *P.total gets
+// the whole length.  k_encode then writes the blocks at those offsets with
+// no look-back of its own.  A workgroup measures K consecutive blocks; the
+// groups are chained by a decoupled look-back (state[g]), taken by ticket so
+// that a look-back only ever waits on running groups.  There is no LDS tile
+// and no staging: per record and per item, the fixed bytes and the digit
+// counts come from the column values, every string counted as if it needed
+// no escape, and one coalesced pass over the 16-byte chunks of the group's
+// slices of the four byte columns adds the escapes of all their bytes, each
+// byte to its block.  The escapes of bytes that are not written (a null
+// name, an omitted category, photoUrls or tags list, a tag name flagged
+// absent) are taken back by the thread that owns them.  Every load of the
+// first round (records, items, chunks) is issued before any is used.
+template <int BT, int R, int K, int UN>
+__global__ __launch_bounds__(BT) void k_enc_measure(EncParams P) {
+    constexpr int RG = R * K, NW = BT / 64;
+    static_assert(RG <= BT, "one record per thread");
+    // block boundaries j = 0..K: url item, tag item, then the first byte of
+    // the name, category name, url and tag name columns
+    __shared__ uint64_t bd[K + 1][6];
+    __shared__ uint64_t sh_red[NW][K];
+    __shared__ uint64_t sh_g;
+    const uint32_t t = threadIdx.x;
+    const pj_pet_columns &c = P.c;
+    const uint64_t nblk = (P.n + R - 1) / R, ngrp = (nblk + K - 1) / K;
+    if (t < 64) {
+        unsigned long long tk = 0;
+        if (t == 0) tk = atomicAdd(P.ticket, 1ull);
+        const uint64_t g = (uint64_t)__shfl((long long)tk, 0);
+        // lane l < 4 (K + 1): boundary j = l / 4, offset column l % 4
+        const uint32_t j = t >> 2, k = t & 3;
+        const uint64_t r = min(g * RG + (uint64_t)j * R, P.n);
+        uint64_t v1 = 0;
+        if (j <= (uint32_t)K) {
+            const uint64_t *o = k == 0 ? c.photo_off : k == 1 ? c.tag_off : k == 2 ? c.name_off
+                                                                      : (c.cat_id ? c.cat_name_off : nullptr);
+            v1 = o ? o[r] : 0;
+            bd[j][k] = v1;
+        }
+        // then the url and tag name bytes those item boundaries select
+        if (j <= (uint32_t)K && k < 2) {
+            const uint64_t *o2 = k == 0 ? (c.photo_off ? c.url_off : nullptr) : (c.tag_off ? c.tag_name_off : nullptr);
+            bd[j][4 + k] = o2 ? o2[v1] : 0;
+        }
+        if (t == 0) sh_g = g;
+    }
+    __syncthreads();
+    const uint64_t g = sh_g, r0 = g * RG, i = r0 + t;
+    ColSrc XP{c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes, 0, 0, 0, 0};
+    XP.all_plain = true;
+    uint64_t acc[K];
+#pragma unroll
+    for (int j = 0; j < K; j++) acc[j] = 0;
+    // the chunks: column k's group slice [bd[0][..], bd[K][..]) from its
+    // aligned start, the four slices end to end
+    const uint8_t *srcs[4] = {c.name_bytes, c.cat_name_bytes, c.url_bytes, c.tag_name_bytes};
+    uint64_t lo16[4], cend[5];
+    cend[0] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint64_t lo = bd[0][2 + k], hi = bd[K][2 + k];
+        lo16[k] = lo & ~15ull;
+        cend[k + 1] = cend[k] + (hi > lo ? (((hi + 15) & ~15ull) - lo16[k]) >> 4 : 0);
+    }
+    uint4 x[UN];
+    auto load_chunks = [&](uint64_t j0) {
+#pragma unroll
+        for (int u = 0; u < UN; u++) {
+            const uint64_t j = j0 + (uint64_t)u * BT;
+            x[u] = make_uint4(0, 0, 0, 0);
+            if (j < cend[4]) {
+                const int k = j >= cend[1] ? (j >= cend[2] ? (j >= cend[3] ? 3 : 2) : 1) : 0;
+                x[u] = *reinterpret_cast<const uint4 *>(srcs[k] + lo16[k] + 16 * (j - cend[k]));
+            }
+        }
+    };
+    load_chunks(t);
+    const uint64_t U0 = bd[0][0], U = bd[K][0] - U0, G0 = bd[0][1], G = bd[K][1] - G0;
+    const bool live = t < (uint32_t)RG && i < P.n;
+    RecVals v{};
+    if (live) v = load_rec<true>(P, i);
+    UrlItem u1{};
+    TagItem g1{};
+    if (t < U) u1 = load_url(P, U0 + t);
+    if (t < G) g1 = load_tag(P, G0 + t);
+    // the block of item q (of column k: 0 urls, 1 tags)
+    auto blk_of = [&](int k, uint64_t q) {
+        int j = 0;
+#pragma unroll
+        for (int m = 1; m < K; m++) j += q >= bd[m][k] ? 1 : 0;
+        return j;
+    };
+    auto add = [&](int j, uint64_t w) {
+#pragma unroll
+        for (int m = 0; m < K; m++) acc[m] += j == m ? w : 0;
+    };
+    // records
+    if (live) {
+        CountSink s;
+        rec_head<true>(s, P, XP, i, v);
+        name_unit(s, P, XP, nullptr, (uint32_t)(v.nb - v.na),
+                  (v.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (v.u1 == v.u0 ? 0x80u : 0u));
+        rec_tags_open<true>(s, P, v);
+        rec_tail(s, P, i, v);
+        uint64_t n = s.n;
+        // bytes in the slices that this record does not write
+        if (!(v.fl & PJ_PET_HAS_NAME) && v.nb > v.na) n -= str_extra(c.name_bytes + v.na, v.nb - v.na);
+        const bool cat_w = (v.fl & PJ_PET_HAS_CATEGORY) && (v.cf & PJ_SUB_HAS_NAME);
+        if (c.cat_id && !cat_w && v.cb > v.ca) n -= str_extra(c.cat_name_bytes + v.ca, v.cb - v.ca);
+        if (!(v.fl & PJ_PET_HAS_PHOTOURLS))
+            for (uint64_t u = v.u0; u < v.u1; u++) {
+                const UrlItem it = load_url(P, u);
+                n -= (it.b - it.a) + 3 + str_extra(c.url_bytes + it.a, it.b - it.a);
+            }
+        if (!(v.fl & PJ_PET_HAS_TAGS))
+            for (uint64_t q = v.t0; q < v.t1; q++) {
+                const TagItem it = load_tag(P, q);
+                CountSink cs;
+                emit_tag_v(cs, P, XP, it, false);
+                n -= cs.n + ((it.tf & PJ_SUB_HAS_NAME) ? str_extra(c.tag_name_bytes + it.a, it.b - it.a) : 0);
+            }
+        add((int)(t / R), n);
+    }
+    // items, counted as written
+    auto url_n = [&](const UrlItem &it) { return (it.b - it.a) + 3; };
+    auto tag_n = [&](const TagItem &it) {
+        CountSink cs;
+        emit_tag_v(cs, P, XP, it, false);
+        uint64_t n = cs.n;
+        if (!(it.tf & PJ_SUB_HAS_NAME) && it.b > it.a) n -= str_extra(c.tag_name_bytes + it.a, it.b - it.a);
+        return n;
+    };
+    if (t < U) add(blk_of(0, U0 + t), url_n(u1));
+    for (uint64_t k = t + BT; k < U; k += BT) add(blk_of(0, U0 + k), url_n(load_url(P, U0 + k)));
+    if (t < G) add(blk_of(1, G0 + t), tag_n(g1));
+    for (uint64_t k = t + BT; k < G; k += BT) add(blk_of(1, G0 + k), tag_n(load_tag(P, G0 + k)));
+    // the escapes of every byte of the four slices, each to its block
+    for (uint64_t j0 = t;; ) {
+#pragma unroll
+        for (int u = 0; u < UN; u++) {
+            const uint64_t j = j0 + (uint64_t)u * BT;
+            if (j >= cend[4]) break;
+            const int k = j >= cend[1] ? (j >= cend[2] ? (j >= cend[3] ? 3 : 2) : 1) : 0;
+            const uint64_t gb = lo16[k] + 16 * (j - cend[k]);
+            const uint64_t lo = ((uint64_t)x[u].y << 32) | x[u].x, hi = ((uint64_t)x[u].w << 32) | x[u].z;
+            // the blocks' byte ranges split the chunk; bytes outside the
+            // group slice belong to none
+#pragma unroll
+            for (int m = 0; m < K; m++) {
+                const uint64_t bl = bd[m][2 + k], bh = bd[m + 1][2 + k];
+                if (bh <= gb || bl >= gb + 16 || bh <= bl) continue;
+                const uint32_t a = bl > gb ? (uint32_t)(bl - gb) : 0u, e = bh < gb + 16 ? (uint32_t)(bh - gb) : 16u;
+                const uint64_t m0 = (a < 8 ? ~0ull << (8 * a) : 0ull) & (e >= 8 ? ~0ull : (1ull << (8 * e)) - 1);
+                const uint64_t m1 = (a <= 8 ? ~0ull : ~0ull << (8 * (a - 8))) &
+                                    (e >= 16 ? ~0ull : e <= 8 ? 0ull : (1ull << (8 * (e - 8))) - 1);
+                acc[m] += esc_extra(lo, m0) + esc_extra(hi, m1);
+            }
+        }
+        j0 += (uint64_t)UN * BT;
+        if (j0 >= cend[4]) break;
+        load_chunks(j0);
+    }
+    // block totals
+    const uint32_t w = t >> 6;
+#pragma unroll
+    for (int m = 0; m < K; m++) {
+        const uint64_t s = wave_sum(acc[m]);
+        if ((t & 63) == 0) sh_red[w][m] = s;
+    }
+    __syncthreads();
+    if (t < 64) {
+        uint64_t blen[K], agg = 0;
+#pragma unroll
+        for (int m = 0; m < K; m++) {
+            blen[m] = 0;
+#pragma unroll
+            for (int q = 0; q < NW; q++) blen[m] += sh_red[q][m];
+            agg += blen[m];
+        }
+        const uint64_t excl = lookback(P.state, g, agg);
+        if (t == 0 && g == ngrp - 1) *P.total = excl + agg;
+        // each block's bounds and offset for the writer
+        uint64_t base = excl;
+#pragma unroll
+        for (int m = 0; m < K; m++) {
+            const uint64_t b = g * K + m;
+            if (b < nblk && t < (uint32_t)GEO_WORDS) {
+                const uint32_t f = t < 12 ? (t < 4 ? t >> 1 : 2 + ((t - 4) >> 1)) : 0;
+                const uint64_t val = t == 12 ? base : bd[m + (t & 1)][f];
+                P.geo[GEO_WORDS * b + t] = val;
+            }
+            base += blen[m];
+        }
     }
 }
 
@@ -1675,6 +1906,18 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                                  ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
     return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>,
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
+}
+
+// The measuring pass: ENC_MEAS_K blocks per workgroup of 512 threads.
+constexpr int ENC_MEAS_BT = 512, ENC_MEAS_K = 4, ENC_MEAS_UN = 8;
+uint64_t pj_encode_measure_groups(uint64_t n) {
+    const uint64_t nblk = (n + ENC_NEST_R - 1) / ENC_NEST_R;
+    return (nblk + ENC_MEAS_K - 1) / ENC_MEAS_K;
+}
+hipError_t pj_launch_encode_measure(const EncParams &P, hipStream_t st) {
+    hipLaunchKernelGGL((pj::k_enc_measure<ENC_MEAS_BT, ENC_NEST_R, ENC_MEAS_K, ENC_MEAS_UN>),
+                       dim3((unsigned)pj_encode_measure_groups(P.n)), dim3(ENC_MEAS_BT), 0, st, P);
+    return hipGetLastError();
 }
 
 // 512-record blocks: measured fastest (256 with three workgroups per CU

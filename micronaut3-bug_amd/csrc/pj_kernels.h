@@ -22,7 +22,11 @@ struct EncParams {
     uint32_t *dummy;           // PJ_BLOCK scratch dwords (shared first dwords land here)
     unsigned long long *nfall; // blocks whose records did not fit the LDS tile (counted)
     const uint64_t *sel;       // one-thread-per-record kernel: output record j is record sel[j] (or j)
+    uint64_t *geo;             // nested writer, two passes: block b's bounds and output offset
+                               // (GEO_WORDS words at geo[GEO_WORDS * b], from k_enc_measure);
+                               // blocks then run in static order with no look-back
 };
+constexpr int GEO_WORDS = 13;
 
 // Order / User encode (pj_encode_model_device): one thread per record,
 // blocks claimed by ticket, decoupled look-back.
@@ -139,6 +143,7 @@ enum { C_PETS = 0, C_NAMEB, C_CATB, C_URLS, C_URLB, C_TAGS, C_TAGB, C_ERRS, PJ_D
 hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);
 hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);   // p[0, n) += v
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
+hipError_t pj_launch_encode_measure(const EncParams &P, hipStream_t st);
 int pj_encode_block_records(bool nested);
 // one thread per output record (pretty output, or a selection of records)
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);

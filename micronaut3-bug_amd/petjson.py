@@ -407,9 +407,11 @@ class Codec:
         self._check(self.L.pj_encode_size_device(self.ctx, C.byref(s), fmt, C.byref(n)))
         return n.value
 
-    def encode(self, cols: Columns, fmt: int = FORMAT_ARRAY, out=None):
+    def encode(self, cols: Columns, fmt: int = FORMAT_ARRAY, out=None, two_pass=False):
         """Encode device columns; returns a uint8 torch tensor (a view of `out`
-        when given) holding exactly the JSON bytes."""
+        when given) holding exactly the JSON bytes.  two_pass: nested records
+        are written at the offsets of the measuring pass rather than by the
+        single pass (the library reads PETJSON_ENC_TWO_PASS on every call)."""
         import torch
         if out is None:
             need = self.encode_size(cols, fmt)
@@ -418,7 +420,18 @@ class Codec:
         s = cols.struct()
         n = C.c_uint64(0)
         cap = out.numel()
-        self._check(self.L.pj_encode_device(self.ctx, C.byref(s), fmt, C.c_void_p(out.data_ptr()), cap, C.byref(n)))
+        old = os.environ.get("PETJSON_ENC_TWO_PASS")
+        if two_pass:
+            os.environ["PETJSON_ENC_TWO_PASS"] = "1"
+        try:
+            self._check(self.L.pj_encode_device(self.ctx, C.byref(s), fmt, C.c_void_p(out.data_ptr()), cap,
+                                                C.byref(n)))
+        finally:
+            if two_pass:
+                if old is None:
+                    del os.environ["PETJSON_ENC_TWO_PASS"]
+                else:
+                    os.environ["PETJSON_ENC_TWO_PASS"] = old
         return out[: n.value]
 
     def encode_noalloc(self, cols: Columns, out, fmt: int = FORMAT_ARRAY):
