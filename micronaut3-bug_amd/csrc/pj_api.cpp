@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "petjson.h"
+#include "pj_host_lock.h"
 #include "pj_kernels.h"
 
 namespace {
@@ -162,8 +163,11 @@ void par_copy(void *d, const void *s, size_t n) {
     for (auto &x : th) x.join();
 }
 
-// Host -> device; the context stream waits for the data before its next work.
-pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n) {
+// Host -> device; returns when the data is on the device.  With order_stream
+// the context stream also waits for it before its next work; a second host
+// thread copying while the context stream runs passes false, so that the
+// work the main thread is queueing meanwhile does not wait for its copy.
+pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n, bool order_stream = true) {
     if (!n) return PJ_OK;
     pj_status s = xfer_init(c);
     if (s) return s;
@@ -176,7 +180,7 @@ pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n) {
         PJ_HIP(hipEventRecord(c->bev[b], c->xs));
     }
     PJ_HIP(hipEventRecord(c->xev, c->xs));
-    PJ_HIP(hipStreamWaitEvent(c->stream, c->xev, 0));
+    if (order_stream) PJ_HIP(hipStreamWaitEvent(c->stream, c->xev, 0));
     // the bounce buffers are reused by the next copy: wait for the last DMAs
     PJ_HIP(hipEventSynchronize(c->xev));
     return PJ_OK;
@@ -296,12 +300,16 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // scratch of the no-allocation entry point holds only the single pass.
     const bool two_pass = !pretty && nested_cols(cols) && !fixed_scratch && (count_only || enc_two_pass());
     uint64_t *sc;
+    std::unique_lock<std::mutex> noalloc_guard;
     if (fixed_scratch) {
         if (n > PJ_NOALLOC_MAX_RECORDS(nested_cols(cols)) || nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
             return fail(PJ_ERR_INVALID_ARG, "pj_encode_device_noalloc: " + std::to_string(n) +
                                                 " records exceed the fixed scratch (at most " +
                                                 std::to_string(PJ_NOALLOC_MAX_RECORDS(nested_cols(cols))) + ")");
         sc = ctx->noalloc_scratch;
+        // every call on this GPU shares the array: one call at a time, until
+        // its stream has drained (the lock is released when this returns)
+        noalloc_guard = std::unique_lock<std::mutex>(pj::noalloc_lock(ctx->device));
     } else {
         PJ_HIP(ctx->scan.ensure((nblk + 3 + 128 + (two_pass ? GEO_WORDS * nblk : 0)) * sizeof(uint64_t)));
         sc = static_cast<uint64_t *>(ctx->scan.p);
@@ -1002,7 +1010,9 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
             if (ctx->seg_in[k ^ 1].ensure(b2 - a2 + 16) != hipSuccess) return fail(PJ_ERR_DEVICE, "segment buffer");
             copier = std::thread([&, k, a2, b2] {
                 s2 = bind(ctx);                       // (HIP's current device is per thread)
-                if (!s2) s2 = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[k ^ 1].p), in + a2, b2 - a2);
+                // (returns once the segment is on the device; the thread is
+                // joined before the segment is decoded)
+                if (!s2) s2 = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[k ^ 1].p), in + a2, b2 - a2, false);
                 if (s2) e2 = pj_last_error();
             });
         }

@@ -10,7 +10,7 @@
 //     bytes each; tags Poisson(1.5) capped at 5; name len U[4,32] with 5% of
 //     characters from {'"', '\\', '\n', '\t', U+00E9, U+0001}; ids 50% U[0,999],
 //     50% full-range int64 (INT64_MIN / INT64_MAX forced now and then).
-//  5  as 3 but name length log-normal (median 12, sigma 1.5, capped at 4 KiB)
+//  5  as 3 but name length log-normal (median 12, sigma 1.5, uncapped)
 //     with 30% of characters escape-heavy / multi-byte (incl. 4-byte code
 //     points); 1% of records have 8-16 KiB names and 200 tags.
 #include "pj_gen.h"
