@@ -226,6 +226,25 @@ def skew_workload(codec, n, steps, warmup, with_decode):
         same = res.n_errors == 0 and all(np.array_equal(h[k], cols[k]) for k in pj.COLS if cols[k] is not None)
         r.update({"decode_ms_per_step": dwall * 1e3, "roundtrip_bit_exact": bool(same),
                   "decode_alg_GBps": (out_bytes + in_bytes) / dwall / 1e9})
+        # the same lines with 0.1% corrupted: the invalid lines' first-error
+        # codes (k_dec_errcode, the last kernel of the call) against the
+        # generator's list of what it corrupted
+        host = text.cpu().numpy().copy()
+        lines, codes = pj.corrupt_ndjson(host, 0x5EED5, 0.001)
+        bad = torch.from_numpy(host).cuda()
+        del host
+        dms, ems = [], []
+        for _ in range(max(2, steps // 2)):
+            dcols, el, ec, res = codec.decode(bad, err_cap=2 * len(lines))
+            tm = codec.timings()
+            dms.append(tm[0])
+            ems.append(tm[-1])
+        ok = (res.n_errors == len(lines) and np.array_equal(el.cpu().numpy().astype(np.uint64), lines) and
+              np.array_equal(ec.cpu().numpy(), codes))
+        r["corrupted_decode"] = {"invalid_lines": int(len(lines)), "errors_match_generator": bool(ok),
+                                 "decode_pipeline_ms": sum(dms[1:]) / len(dms[1:]),
+                                 "k_dec_errcode_ms": sum(ems[1:]) / len(ems[1:])}
+        del bad
     del dev, out
     torch.cuda.empty_cache()
     return r

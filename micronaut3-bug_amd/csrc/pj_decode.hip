@@ -3075,31 +3075,81 @@ __global__ __launch_bounds__(64) void k_dec_long(DecParams P) {
 }
 
 // ---------------------------------------------------------------- error codes
-// Lines found invalid from the bitmaps alone: the code of the first error
-// reading left to right comes from the byte-by-byte general parser.  One
-// workgroup per queued line at a time (grid-stride over the queue, whose
-// length every thread reads after the parse kernel has finished); lines up to
-// ERR_STAGE bytes are staged in LDS.
-template <int BT, int ERR_STAGE>
+// Lines found invalid from the bitmaps: a raw control character or malformed
+// UTF-8 inside one of their strings.  The line's code is that of the first
+// error reading left to right.  Every byte before the first bad byte p is
+// valid where it stands, and p lies inside a string, so that error is the
+// first error met in the line cut short at p: an error
+// before p keeps its code, and otherwise the string holding p runs past the
+// cut, which is PJ_REC_STRING, the code the bad byte gives (a line whose
+// only bad byte is its terminator, in an unterminated string, is cut at its
+// end).  The cut line is read by the wave-parallel walk over the tile's
+// specials bitmap, which returns the codes the serial walk returns; the
+// shapes it leaves to the general parser are read on one thread, strings
+// skipped through the same bitmap rather than byte by byte.  One workgroup per
+// queued line at a time (grid-stride over the queue, whose length every
+// thread reads after the parse kernel has finished): the line is tiled, its
+// bitmaps built, p found, and one thread parses.  A line longer than the
+// tile goes through the byte-by-byte parser from global memory.
+template <int BT, int TILE>
 __global__ __launch_bounds__(BT) void k_dec_errcode(DecParams P) {
-    __shared__ __attribute__((aligned(16))) uint8_t buf[ERR_STAGE + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TILE + 64];
+    __shared__ uint64_t spec[TILE / 64 + 1];
+    __shared__ uint64_t badm[TILE / 64 + 1];
+    __shared__ uint64_t sh_scan[1];
+    __shared__ uint32_t sh_cut;
     const uint64_t cnt = *P.dq_count;
+    const uint32_t t = threadIdx.x;
     for (uint64_t i = blockIdx.x; i < cnt; i += gridDim.x) {
         const uint64_t e = P.dq[i];
         const uint64_t l = P.err_line[e];
-        const uint64_t gs = P.line_start[l];
-        const uint32_t n = (uint32_t)(P.line_start[l + 1] - 1 - gs);
-        const bool staged = n <= ERR_STAGE;
-        if (staged)
-            for (uint32_t j = threadIdx.x; j < n; j += BT) buf[j] = P.in[gs + j];
+        const uint64_t gs = P.line_start[l], ge = P.line_start[l + 1];
+        const uint32_t n = (uint32_t)(ge - 1 - gs);
+        const uint64_t a0 = gs & ~15ull, tb = min(ge, P.len) - a0;
+        const uint32_t s0 = (uint32_t)(gs - a0);
+        if (tb > TILE) {
+            if (t == 0) {
+                LineInfo L;
+                P.err_code[e] = (uint8_t)run_line(P, Src{P.in, P.len, nullptr}, gs, n, true, false, L, nullptr);
+            }
+            continue;
+        }
+        const uint32_t nw = (uint32_t)((tb + 63) >> 6);
+        load_tile<BT>(P, tile, a0, gs, tb, nw);
         __syncthreads();
-        if (threadIdx.x == 0) {
-            LineInfo L;
-            const Src S = staged ? Src{buf, n, nullptr} : Src{P.in, P.len, nullptr};
-            const int code = run_line(P, S, staged ? 0 : gs, n, true, false, L, nullptr);
-            P.err_code[e] = (uint8_t)code;
+        if (P.array_doc && t == 0) tile[s0 + n] = '\n';
+        if (t == 0) sh_cut = n;
+        __syncthreads();
+        tile_bitmaps<BT>(tile, nw, spec, badm, sh_scan);
+        __syncthreads();
+        // the first bad byte of the line
+        for (uint32_t k = (s0 >> 6) + t; k <= ((s0 + n) >> 6) && k < nw; k += BT) {
+            uint64_t m = badm[k];
+            if (k == (s0 >> 6)) m &= ~0ull << (s0 & 63);
+            if (m) {
+                const uint32_t at = 64 * k + (uint32_t)__builtin_ctzll(m);
+                if (at < s0 + n) atomicMin(&sh_cut, at - s0);
+            }
         }
         __syncthreads();
+        // (a line whose only bad byte is its terminator, an unterminated
+        // string, is read whole: it holds no bad byte)
+        const uint32_t cut = sh_cut, ce = s0 + cut;
+        // nothing past the cut is seen: its specials are dropped
+        for (uint32_t k = (ce >> 6) + t; k < nw; k += BT) spec[k] &= k == (ce >> 6) ? ~(~0ull << (ce & 63)) : 0ull;
+        __syncthreads();
+        // the wave-parallel walk (the cut line holds no bad byte); the shapes
+        // it leaves to the general parser, on one thread
+        LineRec r{0, 0, 0, 0, 0, 0, 0, 0};
+        int code = fline_wave<false>((const PJ_LDS uint8_t *)tile, (const PJ_LDS uint64_t *)spec, s0, cut, r, nullptr, nullptr);
+        if (t == 0) {
+            if (code == PJ_BAIL) {
+                LineInfo L;
+                code = run_line(P, Src{tile, tb, spec}, s0, cut, false, false, L, nullptr);
+            }
+            P.err_code[e] = (uint8_t)code;
+        }
+        __syncthreads();                            // the tile is reused by the next line
     }
 }
 
@@ -3158,7 +3208,7 @@ hipError_t pj_launch_arr_frame(const DecParams &P, hipStream_t st) {
 }
 
 hipError_t pj_launch_dec_errcode(const DecParams &P, hipStream_t st) {
-    hipLaunchKernelGGL((pj::k_dec_errcode<64, 8192>), dim3(8192), dim3(64), 0, st, P);
+    hipLaunchKernelGGL((pj::k_dec_errcode<64, DEC_TILE>), dim3(8192), dim3(64), 0, st, P);
     return hipGetLastError();
 }
 
