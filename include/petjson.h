@@ -233,16 +233,18 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
 
 /* Same as pj_encode_device, but allocates nothing: no hipMalloc / hipFree
  * or allocating library routine runs inside the call.  No counterpart in the
- * reference; it is for callers that cannot allocate (code under HIP graph
- * capture, tight serving loops, harnesses that forbid allocation).  Its
+ * reference; it is for callers that cannot allocate (tight serving loops,
+ * harnesses that forbid allocation).  The call is synchronous: it waits for
+ * its stream and reads the length back, so it cannot be recorded into a HIP
+ * graph.  Its
  * scratch (block look-back words) lives in a fixed device array of
  * PJ_NOALLOC_SCRATCH_WORDS 64-bit words per GPU, held until the process
  * ends, so n_pets is limited to PJ_NOALLOC_MAX_RECORDS(nested) where nested
  * means any of the category / photoUrls / tags groups is present; larger
  * inputs return PJ_ERR_INVALID_ARG.  Every call on one GPU shares that
- * GPU's array (each call clears what it needs), so calls that overlap on
- * one GPU — two contexts on two threads — race and must be serialised by
- * the caller. */
+ * GPU's array (each call clears what it needs); calls on one GPU from
+ * different threads or contexts are serialised inside the library by a
+ * per-GPU host lock held until the call's stream has drained. */
 #define PJ_NOALLOC_SCRATCH_WORDS (1u << 20)
 #define PJ_NOALLOC_MAX_RECORDS(nested) \
     ((uint64_t)(PJ_NOALLOC_SCRATCH_WORDS - 131) * ((nested) ? 96u : 256u))

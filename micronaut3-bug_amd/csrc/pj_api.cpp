@@ -820,6 +820,21 @@ pj_status decode_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_colum
     DecParams P;
     uint64_t *X = nullptr, lines = 0;
     if ((s = index_stage(ctx, in, len, array, P, X, &lines))) return s;
+    P.lines = lines;
+    if (len >= PJ_DEC_MAX_BLOCK_SPAN && lines) {
+        // the lines of one block must span less than 4 GiB (32-bit offsets
+        // inside a block); only an input that long can break it
+        PJ_HIP(pj_launch_fill_u64(X + 15, 1, 0, ctx->stream));
+        PJ_HIP(pj_launch_dec_span_check(P, X + 15, ctx->stream));
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, X + 15, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->pinned[0]) {
+            ctx->n_ev = 0;
+            return fail(PJ_ERR_INVALID_ARG, "lines of 4 GiB or more in one block of " +
+                                                std::to_string(pj_dec_parse_block()) + " lines (offsets inside a "
+                                                "block are 32-bit)");
+        }
+    }
     P.o = *out;
     P.err_line = err_line;
     P.err_code = err_code;

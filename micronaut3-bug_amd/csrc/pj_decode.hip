@@ -3187,6 +3187,22 @@ int pj_dec_index_block() { return DEC_IDX_BT * DEC_IDX_R; }
 constexpr int DEC_LPB = PJ_DEC_LPB;
 int pj_dec_parse_block() { return DEC_LPB; }
 
+namespace pj {
+// Sets *flag when some line block spans PJ_DEC_MAX_BLOCK_SPAN bytes or more.
+__global__ void k_dec_span_check(const uint64_t *ls, uint64_t lines, uint64_t lpb, uint64_t *flag) {
+    const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (!dec_block_span_ok(ls, lines, lpb, b)) *flag = 1;
+}
+}  // namespace pj
+
+hipError_t pj_launch_dec_span_check(const DecParams &P, uint64_t *flag, hipStream_t st) {
+    const uint64_t nb = (P.lines + DEC_LPB - 1) / DEC_LPB;
+    if (!nb) return hipSuccess;
+    hipLaunchKernelGGL(pj::k_dec_span_check, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, P.line_start,
+                       P.lines, (uint64_t)DEC_LPB, flag);
+    return hipGetLastError();
+}
+
 hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     const uint64_t g = (P.nblk64 + DEC_IDX_BT * DEC_IDX_R - 1) / (DEC_IDX_BT * DEC_IDX_R);
     hipLaunchKernelGGL((pj::k_dec_lines<DEC_IDX_BT, DEC_IDX_R>), dim3((unsigned)g), dim3(DEC_IDX_BT), 0, st, P);

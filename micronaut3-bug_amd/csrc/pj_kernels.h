@@ -174,3 +174,14 @@ int pj_dec_index_block();
 // u64); resolved once per device, with that device current.
 hipError_t pj_noalloc_scratch_init(int device, uint64_t **ptr);
 int pj_dec_parse_block();
+// The Pet decode keeps each line's output offsets inside its line block as
+// 32-bit values, so the bytes of a block's lines must stay below 4 GiB (a
+// line of 4 GiB or more is refused with them).  Block b holds lines
+// [b lpb, (b + 1) lpb); line l spans [ls[l], ls[l + 1]).  Checked by
+// k_dec_span_check when the input is that long (PJ_ERR_INVALID_ARG).
+constexpr uint64_t PJ_DEC_MAX_BLOCK_SPAN = (1ull << 32) - (1ull << 20);
+__host__ __device__ inline bool dec_block_span_ok(const uint64_t *ls, uint64_t lines, uint64_t lpb, uint64_t b) {
+    const uint64_t l0 = b * lpb, l1 = l0 + lpb < lines ? l0 + lpb : lines;
+    return l0 >= lines || ls[l1] - ls[l0] < PJ_DEC_MAX_BLOCK_SPAN;
+}
+hipError_t pj_launch_dec_span_check(const DecParams &P, uint64_t *flag, hipStream_t st);
