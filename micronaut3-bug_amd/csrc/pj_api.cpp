@@ -347,6 +347,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
             PJ_HIP(pj_launch_encode_measure(P, ctx->stream));
             if (!count_only) {
                 if ((s = mark(ctx))) return s;
+                PJ_HIP(pj_launch_fill_u64(sc, 1, 0, ctx->stream));   // the writer's tickets
                 P.geo = geo;
                 PJ_HIP(pj_launch_encode(P, true, false, ctx->stream));
             }

@@ -881,12 +881,13 @@ __device__ __forceinline__ void bounds_store(uint64_t *nx, uint64_t v1, uint64_t
 }
 // The first wave claims the next block, by ticket, and stores its number and
 // bounds (lane l of the wave).  With the bounds and offsets given (P.geo)
-// the next block is the static successor cur + gridDim.x and its GEO_WORDS
-// words are one load away.
+// its GEO_WORDS words are one load away.
 template <bool NESTED, int R>
-__device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uint64_t *nb, uint32_t l, uint64_t cur) {
+__device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uint64_t *nb, uint32_t l) {
     if (P.geo) {
-        const uint64_t n1 = cur + gridDim.x;
+        unsigned long long tk0 = 0;
+        if (l == 0) tk0 = atomicAdd(P.ticket, 1ull);
+        const uint64_t n1 = (uint64_t)__shfl((long long)tk0, 0);
         if (l < (uint32_t)GEO_WORDS && n1 < (P.n + R - 1) / R) nx[l] = P.geo[GEO_WORDS * n1 + l];
         if (l == 0) *nb = n1;
         return;
@@ -1046,7 +1047,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     // ---- the first block: its number and bounds, then its loads
     if (t < 64) {
         unsigned long long tk = 0;
-        const bool by_id = (!PERSIST && P.order_by_id) || P.geo;
+        const bool by_id = !PERSIST && P.order_by_id;
         if (!by_id && t == 0) tk = atomicAdd(P.ticket, 1ull);
         const uint64_t b0 = by_id ? (uint64_t)blockIdx.x : (uint64_t)__shfl((long long)tk, 0);
         if (P.geo) {
@@ -1303,7 +1304,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         // starts soon after its ticket
         const bool early = fits || P.count_only;
         if (PERSIST && early && t < 64) {
-            claim_next<NESTED, R>(P, sh_nx, &sh_nb, t, b);
+            claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
             EPROF(6);
         }
         const uint64_t base = sh_base;
@@ -1359,7 +1360,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             }
         }
         if (!PERSIST) break;
-        if (!early && t < 64) claim_next<NESTED, R>(P, sh_nx, &sh_nb, t, b);
+        if (!early && t < 64) claim_next<NESTED, R>(P, sh_nx, &sh_nb, t);
         // the next block's loads (record, item and staging values)
         __syncthreads();
         nb = sh_nb;
