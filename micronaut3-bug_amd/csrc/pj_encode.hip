@@ -186,13 +186,11 @@ __device__ __forceinline__ uint64_t special_mask(uint64_t x) {
 // branches: \" \\ \b \t \n \f \r, else \u00XX (hex digits a-f in the case
 // hexa selects).
 __device__ __forceinline__ uint64_t esc_seq(uint32_t c, uint32_t hexa, int *len) {
-    uint32_t e = c;                                   // '"' and '\\' escape as themselves
-    e = c == 8 ? 'b' : e;
-    e = c == 9 ? 't' : e;
-    e = c == 10 ? 'n' : e;
-    e = c == 12 ? 'f' : e;
-    e = c == 13 ? 'r' : e;
-    const bool shrt = c == '"' || c == '\\' || c == 8 || c == 9 || c == 10 || c == 12 || c == 13;
+    // '"' and '\\' escape as themselves; the controls 8 9 10 12 13 as b t n f r,
+    // read from a packed table (bits 8..13 of 0x3700 mark them short)
+    constexpr uint64_t SHORTS = pack8("btn\0fr", 6);
+    const bool shrt = c >= 0x20 || ((0x3700u >> (c & 31)) & 1u);
+    const uint32_t e = c >= 0x20 ? c : (uint32_t)(SHORTS >> (8 * ((c - 8) & 7))) & 0xFFu;
     const uint32_t lo = c & 15, hc = lo < 10 ? '0' + lo : hexa + lo - 10;
     const uint64_t u6 = pack8("\\u00", 4) | ((uint64_t)('0' + (c >> 4)) << 32) | ((uint64_t)hc << 40);
     *len = shrt ? 2 : 6;
