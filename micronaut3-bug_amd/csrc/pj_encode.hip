@@ -161,14 +161,42 @@ template <class S> __device__ __forceinline__ void emit_long(S &s, int64_t v) {
     s.put8(eight_digits(c2), 8);
 }
 
+// |v| as three groups of eight decimal digits, most significant first
+// (g0 < 1845), and the leading nonzero group with the digits after it (16,
+// 8 or 0).  Same work for every value, so lanes with short and long ids do
+// not run separate paths.
+struct LongGroups {
+    uint32_t g0, g1, g2;
+    uint32_t top;      // the leading nonzero group (g2 when all are zero)
+    int after;         // digits after it: 16, 8 or 0
+};
+__device__ __forceinline__ LongGroups long_groups(int64_t v) {
+    const uint64_t u = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
+    const uint64_t q = u / 100000000ull;
+    LongGroups r;
+    r.g2 = (uint32_t)(u - q * 100000000ull);
+    r.g0 = (uint32_t)(q / 100000000ull);
+    r.g1 = (uint32_t)(q - (uint64_t)r.g0 * 100000000ull);
+    r.top = r.g0 ? r.g0 : r.g1 ? r.g1 : r.g2;
+    r.after = r.g0 ? 16 : r.g1 ? 8 : 0;
+    return r;
+}
+// Long.toString(v) into the LDS tile: the leading group's digits, then the
+// full groups after it, each piece stored whole (a piece of no bytes stores
+// nothing the next piece does not overwrite).
+__device__ __forceinline__ void emit_long(LdsSinkU &s, int64_t v) {
+    const LongGroups G = long_groups(v);
+    s.put8('-', v < 0 ? 1 : 0);
+    const int nt = digits32(G.top);
+    s.put8(eight_digits(G.top) >> (8 * (8 - nt)), nt);
+    s.put8(eight_digits(G.g0 ? G.g1 : G.g2), G.after ? 8 : 0);
+    s.put8(eight_digits(G.g2), G.after == 16 ? 8 : 0);
+}
+
 // Length only (no digit strings built).
 __device__ __forceinline__ void emit_long(CountSink &s, int64_t v) {
-    uint64_t u = v < 0 ? 0ull - (uint64_t)v : (uint64_t)v;
-    int n = v < 0;
-    if (u < 100000000ull) n += digits32((uint32_t)u);
-    else if (u < 10000000000000000ull) n += 8 + digits32((uint32_t)(u / 100000000ull));
-    else n += 16 + digits32((uint32_t)(u / 10000000000000000ull));
-    s.n += (uint64_t)n;
+    const LongGroups G = long_groups(v);
+    s.n += (uint64_t)((v < 0 ? 1 : 0) + G.after + digits32(G.top));
 }
 
 // ----------------------------------------------------------------- strings
