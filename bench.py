@@ -121,19 +121,72 @@ def decode_workload(codec, n, steps, warmup):
     kern["k_dec_lines_GBps"] = in_bytes / (kern["k_dec_lines_ms"] * 1e-3) / 1e9
     kern["alg_frac_hbm_kernels"] = (in_bytes + out_bytes) / (ksum * 1e-3) / 1e9 / HBM_PEAK_GBPS
     # the host entry point on the same text (PCIe-inclusive; not the headline)
-    host = host_text if host_text is not None else data.cpu().numpy().tobytes()
-    codec.decode_host(host, caps=caps, err_cap=max(16, 2 * len(lines)))
-    th = time.perf_counter()
-    codec.decode_host(host, caps=caps, err_cap=max(16, 2 * len(lines)))
-    th = time.perf_counter() - th
+    del bufs
+    torch.cuda.empty_cache()
+    hostr = host_decode_rates(codec, np.frombuffer(host_text, np.uint8), caps, max(16, 2 * len(lines)), int(res.n_pets))
     r = {"records": int(res.n_lines), "records_per_s": res.n_lines / wall, "ms_per_step": wall * 1e3,
          "input_bytes": in_bytes, "output_bytes": out_bytes, "input_GBps": in_bytes / wall / 1e9,
          "alg_GBps": (in_bytes + out_bytes) / wall / 1e9,
          "alg_frac_hbm": (in_bytes + out_bytes) / wall / 1e9 / HBM_PEAK_GBPS,
          "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
          "lines_general_parser": int(res.n_general), "kernels": kern,
-         "host_entry_point": {"decode_host_ms": th * 1e3, "input_GBps": in_bytes / th / 1e9}}
+         "host_entry_point": hostr}
     return r
+
+
+def host_decode_rates(codec, text, caps, err_cap, n_pets, reps=3):
+    """pj_decode_host on host input, outputs preallocated (and touched): with
+    pageable buffers (copied through the library's pinned bounce buffers)
+    and with pinned ones (pj_host_alloc, moved by DMA directly), beside
+    plain pinned H2D / D2H copies of the input's size.  Medians of reps."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    import petjson as pj
+    N = int(text.size)
+    med = lambda v: sorted(v)[len(v) // 2]
+    pin = torch.empty(N, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(N, dtype=torch.uint8, device="cuda")
+    h2d, d2h = [], []
+    for _ in range(reps):
+        torch.cuda.synchronize(); t0 = time.perf_counter(); d.copy_(pin, non_blocking=True); torch.cuda.synchronize()
+        h2d.append(N / (time.perf_counter() - t0) / 1e9)
+        t0 = time.perf_counter(); pin.copy_(d, non_blocking=True); torch.cuda.synchronize()
+        d2h.append(N / (time.perf_counter() - t0) / 1e9)
+    del pin, d
+    torch.cuda.empty_cache()
+    cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
+    sizes = {"id": cp, "flags": cp, "status": cp, "name_off": cp + 1, "name_bytes": caps["cap_name_bytes"],
+             "cat_id": cp, "cat_flags": cp, "cat_name_off": cp + 1, "cat_name_bytes": caps["cap_cat_name_bytes"],
+             "photo_off": cp + 1, "url_off": cu + 1, "url_bytes": caps["cap_url_bytes"], "tag_off": cp + 1,
+             "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
+    out = {}
+    for kind in ("pageable", "pinned"):
+        alloc = (lambda n, t: np.ones(max(1, n), t)) if kind == "pageable" else pj.host_array
+        inp = text if kind == "pageable" else alloc(N, np.uint8)
+        if kind == "pinned":
+            inp[:] = text
+        cols = pj.Columns(0, {k: alloc(v, pj.DTYPES[k]) for k, v in sizes.items()}, dict(caps))
+        for a in cols.arrays.values():
+            a[:] = 1
+        el, ec = alloc(err_cap, np.uint64), alloc(err_cap, np.uint8)
+        ms, ok = [], True
+        for _ in range(reps + 1):
+            st = cols.struct()
+            res = pj.DecodeResult()
+            t0 = time.perf_counter()
+            rc = codec.L.pj_decode_host(codec.ctx, C.c_void_p(inp.ctypes.data), N, C.byref(st),
+                                        C.c_void_p(el.ctypes.data), C.c_void_p(ec.ctypes.data), err_cap, C.byref(res))
+            ms.append((time.perf_counter() - t0) * 1e3)
+            ok = ok and rc == 0 and res.n_pets == n_pets
+        m = med(ms[1:])
+        out["decode_host_" + kind] = {"ms": m, "input_GBps": N / m / 1e6, "ok": bool(ok)}
+        del cols, inp, el, ec
+    out["pinned_h2d_copy_GBps"] = med(h2d)
+    out["pinned_d2h_copy_GBps"] = med(d2h)
+    out["pinned_decode_frac_of_h2d_copy"] = out["decode_host_pinned"]["input_GBps"] / out["pinned_h2d_copy_GBps"]
+    out["pageable_decode_frac_of_h2d_copy"] = out["decode_host_pageable"]["input_GBps"] / out["pinned_h2d_copy_GBps"]
+    return out
 
 
 def _timed(fn, budget_s, threads):

@@ -251,6 +251,15 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
 pj_status pj_encode_device_noalloc(pj_ctx *ctx, const pj_pet_columns *cols, int format,
                                    uint8_t *out, uint64_t out_cap, uint64_t *out_len);
 
+/* Pinned (page-locked) host memory for the *_host entry points.  Inputs and
+ * outputs that lie in it move by DMA straight between the caller's buffer
+ * and the device; other host memory is copied through the library's pinned
+ * bounce buffers first.  No counterpart in the reference; it is for callers
+ * that stage their bytes in memory they allocate once (a Java caller would
+ * wrap it in a MemorySegment).  Returns NULL when the allocation fails. */
+void       *pj_host_alloc(uint64_t n);
+void        pj_host_free(void *p);
+
 /* ------------------------------------------------------------------ decode */
 /* Parse NDJSON (one Pet per line) into columns (readValue per line).
  * Valid records are written in input order; invalid ones are skipped and

@@ -58,6 +58,16 @@ struct DevBuf {
 
 constexpr int MAX_EV = 12;
 
+// A copy engine between pageable host memory and the device: its own copy
+// stream, two pinned bounce buffers and their events.
+struct Xfer {
+    hipStream_t s = nullptr;
+    uint8_t *bounce[2] = {nullptr, nullptr};
+    hipEvent_t bev[2] = {nullptr, nullptr};
+    hipEvent_t done = nullptr;
+    size_t chunk = 0;
+};
+
 inline uint64_t align256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
 }  // namespace
@@ -71,16 +81,14 @@ struct pj_ctx {
     DevBuf index;       // decode: special bitmap, bad flags, line starts
     DevBuf stage_in;    // host path: input staging
     DevBuf stage_out;   // host path: output staging
+    DevBuf stage_out2;  // streamed host decode: the other segment's output staging
     DevBuf tape;        // decode: per-line results of the validating walk
     DevBuf seg_in[2];   // streamed host decode: input segments (double buffer)
     uint64_t *pinned = nullptr;   // 64 u64 of pinned host memory for results
-    // host entry points: a copy stream, two pinned bounce buffers and their
-    // events (made on first use)
-    hipStream_t xs = nullptr;
-    uint8_t *bounce[2] = {nullptr, nullptr};
-    hipEvent_t bev[2] = {nullptr, nullptr};
-    hipEvent_t xev = nullptr;
-    size_t xchunk = 0;
+    // host entry points: one copy engine per direction (made on first use),
+    // so that a copy in and a copy out can run at once
+    Xfer xin, xout;
+    hipEvent_t seg_ready = nullptr;   // streamed decode: a segment's columns are final
     uint64_t *noalloc_scratch = nullptr;  // this device's fixed encode scratch (device address)
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
@@ -134,16 +142,26 @@ size_t xfer_chunk() {
     return v;
 }
 
-pj_status xfer_init(pj_ctx *c) {
-    if (c->xs) return PJ_OK;
-    c->xchunk = xfer_chunk();
-    PJ_HIP(hipStreamCreateWithFlags(&c->xs, hipStreamNonBlocking));
+pj_status xfer_init(Xfer &x) {
+    if (x.s) return PJ_OK;
+    x.chunk = xfer_chunk();
+    PJ_HIP(hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking));
     for (int b = 0; b < 2; b++) {
-        PJ_HIP(hipHostMalloc((void **)&c->bounce[b], c->xchunk, hipHostMallocDefault));
-        PJ_HIP(hipEventCreateWithFlags(&c->bev[b], hipEventDisableTiming));
+        PJ_HIP(hipHostMalloc((void **)&x.bounce[b], x.chunk, hipHostMallocDefault));
+        PJ_HIP(hipEventCreateWithFlags(&x.bev[b], hipEventDisableTiming));
     }
-    PJ_HIP(hipEventCreateWithFlags(&c->xev, hipEventDisableTiming));
+    PJ_HIP(hipEventCreateWithFlags(&x.done, hipEventDisableTiming));
     return PJ_OK;
+}
+void xfer_free(Xfer &x) {
+    if (x.s) (void)hipStreamSynchronize(x.s);
+    for (int b = 0; b < 2; b++) {
+        if (x.bounce[b]) (void)hipHostFree(x.bounce[b]);
+        if (x.bev[b]) (void)hipEventDestroy(x.bev[b]);
+    }
+    if (x.done) (void)hipEventDestroy(x.done);
+    if (x.s) (void)hipStreamDestroy(x.s);
+    x = Xfer{};
 }
 
 // n bytes from s to d on up to 16 host threads (at least 4 MiB each).
@@ -163,51 +181,78 @@ void par_copy(void *d, const void *s, size_t n) {
     for (auto &x : th) x.join();
 }
 
+// Whether host bytes [p, p + n) are pinned memory (pj_host_alloc, or any
+// hipHostMalloc): such bytes move by DMA straight from / to the caller's
+// buffer, with no copy through the bounce buffers.
+bool pinned_host(const void *p, size_t n) {
+    for (const void *q : {p, static_cast<const void *>(static_cast<const uint8_t *>(p) + n - 1)}) {
+        hipPointerAttribute_t a;
+        if (hipPointerGetAttributes(&a, q) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        if (a.type != hipMemoryTypeHost) return false;
+    }
+    return true;
+}
+
 // Host -> device; returns when the data is on the device.  With order_stream
 // the context stream also waits for it before its next work; a second host
 // thread copying while the context stream runs passes false, so that the
 // work the main thread is queueing meanwhile does not wait for its copy.
 pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n, bool order_stream = true) {
     if (!n) return PJ_OK;
-    pj_status s = xfer_init(c);
+    Xfer &x = c->xin;
+    pj_status s = xfer_init(x);
     if (s) return s;
-    for (size_t off = 0, i = 0; off < n; off += c->xchunk, i++) {
-        const size_t k = std::min(c->xchunk, n - off);
+    if (pinned_host(host, n)) PJ_HIP(hipMemcpyAsync(dev, host, n, hipMemcpyHostToDevice, x.s));
+    else for (size_t off = 0, i = 0; off < n; off += x.chunk, i++) {
+        const size_t k = std::min(x.chunk, n - off);
         const int b = (int)(i & 1);
-        if (i >= 2) PJ_HIP(hipEventSynchronize(c->bev[b]));      // the DMA that last read this buffer is done
-        par_copy(c->bounce[b], static_cast<const uint8_t *>(host) + off, k);
-        PJ_HIP(hipMemcpyAsync(static_cast<uint8_t *>(dev) + off, c->bounce[b], k, hipMemcpyHostToDevice, c->xs));
-        PJ_HIP(hipEventRecord(c->bev[b], c->xs));
+        if (i >= 2) PJ_HIP(hipEventSynchronize(x.bev[b]));      // the DMA that last read this buffer is done
+        par_copy(x.bounce[b], static_cast<const uint8_t *>(host) + off, k);
+        PJ_HIP(hipMemcpyAsync(static_cast<uint8_t *>(dev) + off, x.bounce[b], k, hipMemcpyHostToDevice, x.s));
+        PJ_HIP(hipEventRecord(x.bev[b], x.s));
     }
-    PJ_HIP(hipEventRecord(c->xev, c->xs));
-    if (order_stream) PJ_HIP(hipStreamWaitEvent(c->stream, c->xev, 0));
+    PJ_HIP(hipEventRecord(x.done, x.s));
+    if (order_stream) PJ_HIP(hipStreamWaitEvent(c->stream, x.done, 0));
     // the bounce buffers are reused by the next copy: wait for the last DMAs
-    PJ_HIP(hipEventSynchronize(c->xev));
+    PJ_HIP(hipEventSynchronize(x.done));
     return PJ_OK;
 }
 
-// Device -> host, after the context stream's work so far; returns when the
-// bytes are in host memory.
-pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n) {
+// Device -> host, after the work the event `after` marks (by default the
+// context stream's work so far); returns when the bytes are in host memory.
+pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n, hipEvent_t after = nullptr) {
     if (!n) return PJ_OK;
-    pj_status s = xfer_init(c);
+    Xfer &x = c->xout;
+    pj_status s = xfer_init(x);
     if (s) return s;
-    PJ_HIP(hipEventRecord(c->xev, c->stream));
-    PJ_HIP(hipStreamWaitEvent(c->xs, c->xev, 0));
-    const size_t chunks = (n + c->xchunk - 1) / c->xchunk;
+    if (!after) {
+        PJ_HIP(hipEventRecord(x.done, c->stream));
+        after = x.done;
+    }
+    PJ_HIP(hipStreamWaitEvent(x.s, after, 0));
+    if (pinned_host(host, n)) {
+        PJ_HIP(hipMemcpyAsync(host, dev, n, hipMemcpyDeviceToHost, x.s));
+        PJ_HIP(hipEventRecord(x.bev[0], x.s));
+        PJ_HIP(hipEventSynchronize(x.bev[0]));
+        return PJ_OK;
+    }
+    const size_t chunks = (n + x.chunk - 1) / x.chunk;
     auto issue = [&](size_t i) -> pj_status {
-        const size_t off = i * c->xchunk, k = std::min(c->xchunk, n - off);
-        PJ_HIP(hipMemcpyAsync(c->bounce[i & 1], static_cast<const uint8_t *>(dev) + off, k, hipMemcpyDeviceToHost, c->xs));
-        PJ_HIP(hipEventRecord(c->bev[i & 1], c->xs));
+        const size_t off = i * x.chunk, k = std::min(x.chunk, n - off);
+        PJ_HIP(hipMemcpyAsync(x.bounce[i & 1], static_cast<const uint8_t *>(dev) + off, k, hipMemcpyDeviceToHost, x.s));
+        PJ_HIP(hipEventRecord(x.bev[i & 1], x.s));
         return PJ_OK;
     };
     if ((s = issue(0))) return s;
     for (size_t i = 0; i < chunks; i++) {
         // the other buffer's host copy (chunk i - 1) is done: start chunk i + 1's DMA into it
         if (i + 1 < chunks && (s = issue(i + 1))) return s;
-        PJ_HIP(hipEventSynchronize(c->bev[i & 1]));
-        const size_t off = i * c->xchunk;
-        par_copy(static_cast<uint8_t *>(host) + off, c->bounce[i & 1], std::min(c->xchunk, n - off));
+        PJ_HIP(hipEventSynchronize(x.bev[i & 1]));
+        const size_t off = i * x.chunk;
+        par_copy(static_cast<uint8_t *>(host) + off, x.bounce[i & 1], std::min(x.chunk, n - off));
     }
     return PJ_OK;
 }
@@ -480,18 +525,15 @@ void pj_destroy(pj_ctx *c) {
     c->index.release();
     c->stage_in.release();
     c->stage_out.release();
+    c->stage_out2.release();
     c->tape.release();
     c->seg_in[0].release();
     c->seg_in[1].release();
     for (auto &e : c->ev) if (e) (void)hipEventDestroy(e);
     if (c->pinned) (void)hipHostFree(c->pinned);
-    if (c->xs) (void)hipStreamSynchronize(c->xs);
-    for (int b = 0; b < 2; b++) {
-        if (c->bounce[b]) (void)hipHostFree(c->bounce[b]);
-        if (c->bev[b]) (void)hipEventDestroy(c->bev[b]);
-    }
-    if (c->xev) (void)hipEventDestroy(c->xev);
-    if (c->xs) (void)hipStreamDestroy(c->xs);
+    xfer_free(c->xin);
+    xfer_free(c->xout);
+    if (c->seg_ready) (void)hipEventDestroy(c->seg_ready);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -962,6 +1004,19 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
                            uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array);
 }
 
+extern "C" void *pj_host_alloc(uint64_t n) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, n ? n : 1, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+extern "C" void pj_host_free(void *p) {
+    if (p) (void)hipHostFree(p);
+}
+
 extern "C" pj_status pj_decode_host(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out,
                                     uint64_t *err_line, uint8_t *err_code, uint64_t err_cap,
                                     pj_decode_result *res) {
@@ -976,22 +1031,47 @@ extern "C" pj_status pj_decode_array_host(pj_ctx *ctx, const uint8_t *in, uint64
 
 namespace {
 // Streamed host decode: an NDJSON input of more than stream_above() bytes
-// is decoded in segments of about segment_bytes(), cut after a newline.
-// Segment k + 1 is copied in (on the copy stream, by a second host thread)
-// while segment k decodes; segment k's columns then go to the caller's
-// arrays at the running offsets, its offset arrays and error line numbers
-// shifted on the device first.  Device memory is bounded by the segment
-// size, not the input's.
+// is decoded in segments of about segment_bytes(), cut after a newline, in
+// a three-stage pipeline: while segment k decodes on the context stream, a
+// host thread copies segment k + 1 in (copy engine xin) and another copies
+// segment k - 1's columns out (copy engine xout) to the caller's arrays at
+// the running offsets, its offset arrays and error line numbers shifted on
+// the device first.  Both copy directions run at once (PCIe is full
+// duplex), each through its own pinned bounce buffers.  Device memory is
+// bounded by two segments and their outputs, not by the input.
 uint64_t segment_bytes() {
     if (const char *e = std::getenv("PETJSON_DECODE_SEGMENT")) {
         const unsigned long long v = std::strtoull(e, nullptr, 10);
         if (v) return v;
     }
-    return 1ull << 30;
+    return 256ull << 20;
 }
 uint64_t stream_above() {
     if (std::getenv("PETJSON_DECODE_SEGMENT")) return segment_bytes();
-    return 16ull << 30;
+    return 2 * segment_bytes();
+}
+
+// Device layout of one segment's outputs: the 17 columns (sized for n
+// input bytes) and the error list (ce entries).
+struct SegOut {
+    uint64_t off[20];
+    uint64_t cp, cu, ct;
+    pj_pet_columns dc;
+};
+SegOut seg_layout(uint64_t n, uint64_t ce) {
+    SegOut L;
+    std::memset(&L.dc, 0, sizeof L.dc);
+    pj_decode_bounds(n, &L.dc);
+    L.cp = L.dc.cap_pets;
+    L.cu = L.dc.cap_urls;
+    L.ct = L.dc.cap_tags;
+    const uint64_t cp = L.cp, cu = L.cu, ct = L.ct;
+    const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, L.dc.cap_name_bytes, cp * 8, cp, (cp + 1) * 8,
+                             L.dc.cap_cat_name_bytes, (cp + 1) * 8, (cu + 1) * 8, L.dc.cap_url_bytes, (cp + 1) * 8,
+                             ct * 8, ct, (ct + 1) * 8, L.dc.cap_tag_name_bytes, ce * 8, ce};
+    L.off[0] = 0;
+    for (int j = 0; j < 19; j++) L.off[j + 1] = L.off[j] + align256(sz[j] + 8);
+    return L;
 }
 
 pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
@@ -1007,117 +1087,143 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
         return q ? (uint64_t)(static_cast<const uint8_t *>(q) - in) + 1 : len;
     };
     std::memset(res, 0, sizeof *res);
+    if (!ctx->seg_ready) PJ_HIP(hipEventCreateWithFlags(&ctx->seg_ready, hipEventDisableTiming));
     uint64_t base[PJ_DEC_NCNT] = {0, 0, 0, 0, 0, 0, 0, 0};   // rows, bytes and items written before the segment
     uint64_t lines = 0;
     bool over = false;                 // the caller's capacities ran out: only counting from there
     pj_status s = PJ_OK;
+    DevBuf *stage[2] = {&ctx->stage_out, &ctx->stage_out2};
+    // buffers for a full segment, sized once (a longer segment, cut after a
+    // long line, grows them)
+    const uint64_t ce0 = seg / 16 + 16;   // the error list: a first guess, redone once with the count
+    PJ_HIP(ctx->seg_in[0].ensure(std::min(seg, len) + 16));
+    PJ_HIP(ctx->seg_in[1].ensure(std::min(seg, len) + 16));
+    {
+        const SegOut L = seg_layout(std::min(seg, len), ce0);
+        PJ_HIP(stage[0]->ensure(L.off[19]));
+        PJ_HIP(stage[1]->ensure(L.off[19]));
+    }
+    // a host thread's result
+    struct Job {
+        std::thread th;
+        pj_status st = PJ_OK;
+        std::string err;
+        pj_status join() {
+            if (th.joinable()) th.join();
+            const pj_status r = st;
+            st = PJ_OK;
+            return r;
+        }
+    };
+    Job cin, cout;
+    auto finish = [&](pj_status r) -> pj_status {
+        const pj_status a1 = cin.join(), a2 = cout.join();
+        if (r) return r;
+        if (a1) return fail(a1, cin.err);
+        if (a2) return fail(a2, cout.err);
+        return PJ_OK;
+    };
     uint64_t a = 0, b = seg_end(0);
     // the first segment in
-    PJ_HIP(ctx->seg_in[0].ensure(b - a + 16));
-    if ((s = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[0].p), in, b - a))) return s;
+    if ((s = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[0].p), in, b - a, false))) return s;
     for (int k = 0; a < len; k ^= 1) {
         const uint64_t n = b - a;
         const uint64_t a2 = b, b2 = b < len ? seg_end(b) : b;
         // the next segment in, while this one decodes
-        pj_status s2 = PJ_OK;
-        std::string e2;
-        std::thread copier;
         if (a2 < len) {
-            if (ctx->seg_in[k ^ 1].ensure(b2 - a2 + 16) != hipSuccess) return fail(PJ_ERR_DEVICE, "segment buffer");
-            copier = std::thread([&, k, a2, b2] {
-                s2 = bind(ctx);                       // (HIP's current device is per thread)
-                // (returns once the segment is on the device; the thread is
-                // joined before the segment is decoded)
-                if (!s2) s2 = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[k ^ 1].p), in + a2, b2 - a2, false);
-                if (s2) e2 = pj_last_error();
+            if (ctx->seg_in[k ^ 1].ensure(b2 - a2 + 16) != hipSuccess) return finish(fail(PJ_ERR_DEVICE, "segment buffer"));
+            cin.th = std::thread([&, k, a2, b2] {
+                pj_status r = bind(ctx);               // (HIP's current device is per thread)
+                if (!r) r = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[k ^ 1].p), in + a2, b2 - a2, false);
+                if (r) cin.err = pj_last_error();
+                cin.st = r;
             });
         }
-        // this segment: columns sized for it, on the device
-        pj_pet_columns dc;
-        std::memset(&dc, 0, sizeof dc);
-        pj_decode_bounds(n, &dc);
-        const uint64_t cp = dc.cap_pets, cu = dc.cap_urls, ct = dc.cap_tags;
-        uint64_t ce = n / 16 + 16;           // the error list: a first guess, redone once with the count
-      again:
-        const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, dc.cap_name_bytes, cp * 8, cp, (cp + 1) * 8,
-                                 dc.cap_cat_name_bytes, (cp + 1) * 8, (cu + 1) * 8, dc.cap_url_bytes, (cp + 1) * 8,
-                                 ct * 8, ct, (ct + 1) * 8, dc.cap_tag_name_bytes, ce * 8, ce};
-        uint64_t off[20];
-        off[0] = 0;
-        for (int j = 0; j < 19; j++) off[j + 1] = off[j] + align256(sz[j] + 8);
-        hipError_t he = ctx->stage_out.ensure(off[19]);
+        // this segment: columns sized for it in this slot's staging (segment
+        // k - 2's copy-out, which used it, was joined one segment ago)
+        uint64_t ce = ce0;
+        SegOut L;
         pj_decode_result r;
-        if (he == hipSuccess) {
-            uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
+      again:
+        L = seg_layout(n, ce);
+        if (stage[k]->ensure(L.off[19]) != hipSuccess) return finish(fail(PJ_ERR_DEVICE, "segment columns: out of device memory"));
+        uint8_t *D = static_cast<uint8_t *>(stage[k]->p);
+        {
             void *dp[17];
-            for (int j = 0; j < 17; j++) dp[j] = D + off[j];
-            set_col_ptrs(&dc, dp);
-            uint64_t *del = reinterpret_cast<uint64_t *>(D + off[17]);
-            uint8_t *dec = D + off[18];
-            s = decode_impl(ctx, static_cast<uint8_t *>(ctx->seg_in[k].p), n, &dc, del, dec, ce, &r);
-            if (s == PJ_ERR_CAPACITY && r.n_errors > ce) {
-                ce = r.n_errors;
-                goto again;
-            }
-            if (s == PJ_OK) {
-                const uint64_t T[PJ_DEC_NCNT] = {r.n_pets, r.name_bytes, r.cat_name_bytes, r.n_urls,
-                                                 r.url_bytes, r.n_tags, r.tag_name_bytes, r.n_errors};
-                over = over || base[C_PETS] + T[C_PETS] > out->cap_pets ||
-                       base[C_NAMEB] + T[C_NAMEB] > out->cap_name_bytes ||
-                       base[C_CATB] + T[C_CATB] > out->cap_cat_name_bytes ||
-                       base[C_URLS] + T[C_URLS] > out->cap_urls || base[C_URLB] + T[C_URLB] > out->cap_url_bytes ||
-                       base[C_TAGS] + T[C_TAGS] > out->cap_tags ||
-                       base[C_TAGB] + T[C_TAGB] > out->cap_tag_name_bytes || base[C_ERRS] + T[C_ERRS] > err_cap;
-                if (!over) {
-                    // offsets and error lines shifted past the earlier segments, then out
-                    const hipError_t h = [&] {
-                        hipError_t x;
-                        const uint64_t np = T[C_PETS];
-                        if ((x = pj_launch_add_u64(dc.name_off, np + 1, base[C_NAMEB], ctx->stream)) ||
-                            (x = pj_launch_add_u64(dc.cat_name_off, np + 1, base[C_CATB], ctx->stream)) ||
-                            (x = pj_launch_add_u64(dc.photo_off, np + 1, base[C_URLS], ctx->stream)) ||
-                            (x = pj_launch_add_u64(dc.tag_off, np + 1, base[C_TAGS], ctx->stream)) ||
-                            (x = pj_launch_add_u64(dc.url_off, T[C_URLS] + 1, base[C_URLB], ctx->stream)) ||
-                            (x = pj_launch_add_u64(dc.tag_name_off, T[C_TAGS] + 1, base[C_TAGB], ctx->stream)) ||
-                            (x = pj_launch_add_u64(del, T[C_ERRS], lines, ctx->stream)))
-                            return x;
-                        return hipStreamSynchronize(ctx->stream);
-                    }();
-                    if (h != hipSuccess) s = fail(PJ_ERR_DEVICE, std::string("segment offsets: ") + hipGetErrorString(h));
-                }
-            }
-        } else s = fail(PJ_ERR_DEVICE, "segment columns: out of device memory");
-        if (copier.joinable()) copier.join();  // the copy stream and bounce buffers are free again
-        if (s) return s;
-        if (s2) return fail(s2, e2);
+            for (int j = 0; j < 17; j++) dp[j] = D + L.off[j];
+            set_col_ptrs(&L.dc, dp);
+        }
+        uint64_t *del = reinterpret_cast<uint64_t *>(D + L.off[17]);
+        uint8_t *dec = D + L.off[18];
+        s = decode_impl(ctx, static_cast<uint8_t *>(ctx->seg_in[k].p), n, &L.dc, del, dec, ce, &r);
+        if (s == PJ_ERR_CAPACITY && r.n_errors > ce) {
+            ce = r.n_errors;
+            goto again;
+        }
+        if (s) return finish(s);
+        const uint64_t T[PJ_DEC_NCNT] = {r.n_pets, r.name_bytes, r.cat_name_bytes, r.n_urls,
+                                         r.url_bytes, r.n_tags, r.tag_name_bytes, r.n_errors};
+        over = over || base[C_PETS] + T[C_PETS] > out->cap_pets || base[C_NAMEB] + T[C_NAMEB] > out->cap_name_bytes ||
+               base[C_CATB] + T[C_CATB] > out->cap_cat_name_bytes || base[C_URLS] + T[C_URLS] > out->cap_urls ||
+               base[C_URLB] + T[C_URLB] > out->cap_url_bytes || base[C_TAGS] + T[C_TAGS] > out->cap_tags ||
+               base[C_TAGB] + T[C_TAGB] > out->cap_tag_name_bytes || base[C_ERRS] + T[C_ERRS] > err_cap;
+        // segment k - 1's copy-out is done before this one's starts (one
+        // copy engine out); its staging slot is then free for segment k + 1
+        if (const pj_status c1 = cout.join()) return finish(fail(c1, cout.err));
         if (!over) {
-            const uint64_t np = r.n_pets, nu = r.n_urls, nt = r.n_tags;
+            // offsets and error lines shifted past the earlier segments, then out
+            const uint64_t np = T[C_PETS];
+            hipError_t x;
+            if ((x = pj_launch_add_u64(L.dc.name_off, np + 1, base[C_NAMEB], ctx->stream)) ||
+                (x = pj_launch_add_u64(L.dc.cat_name_off, np + 1, base[C_CATB], ctx->stream)) ||
+                (x = pj_launch_add_u64(L.dc.photo_off, np + 1, base[C_URLS], ctx->stream)) ||
+                (x = pj_launch_add_u64(L.dc.tag_off, np + 1, base[C_TAGS], ctx->stream)) ||
+                (x = pj_launch_add_u64(L.dc.url_off, T[C_URLS] + 1, base[C_URLB], ctx->stream)) ||
+                (x = pj_launch_add_u64(L.dc.tag_name_off, T[C_TAGS] + 1, base[C_TAGB], ctx->stream)) ||
+                (x = pj_launch_add_u64(del, T[C_ERRS], lines, ctx->stream)) ||
+                (x = hipEventRecord(ctx->seg_ready, ctx->stream)))
+                return finish(fail(PJ_ERR_DEVICE, std::string("segment offsets: ") + hipGetErrorString(x)));
             // host destination of each column: its element at the running base
             void *hp[17];
             col_ptrs(out, hp);
+            const uint64_t nu = r.n_urls, nt = r.n_tags;
             const uint64_t bp = base[C_PETS], bu = base[C_URLS], bt = base[C_TAGS];
+            struct Piece { uint8_t *dst; const uint8_t *src; uint64_t n; };
+            std::vector<Piece> pieces;
             const uint64_t dst_off[17] = {bp * 8, bp, bp, bp * 8, base[C_NAMEB], bp * 8, bp, bp * 8, base[C_CATB],
                                           bp * 8, bu * 8, base[C_URLB], bp * 8, bt * 8, bt, bt * 8, base[C_TAGB]};
             const uint64_t used[17] = {np * 8, np, np, (np + 1) * 8, r.name_bytes, np * 8, np, (np + 1) * 8,
                                        r.cat_name_bytes, (np + 1) * 8, (nu + 1) * 8, r.url_bytes, (np + 1) * 8,
                                        nt * 8, nt, (nt + 1) * 8, r.tag_name_bytes};
-            void *dp[17];
-            col_ptrs(&dc, dp);
             for (int j = 0; j < 17; j++)
-                if (used[j] && (s = d2h(ctx, static_cast<uint8_t *>(hp[j]) + dst_off[j], dp[j], used[j]))) return s;
-            uint8_t *D = static_cast<uint8_t *>(ctx->stage_out.p);
-            if (r.n_errors && ((s = d2h(ctx, err_line + base[C_ERRS], D + off[17], r.n_errors * 8)) ||
-                               (s = d2h(ctx, err_code + base[C_ERRS], D + off[18], r.n_errors))))
-                return s;
+                if (used[j]) pieces.push_back({static_cast<uint8_t *>(hp[j]) + dst_off[j], D + L.off[j], used[j]});
+            if (r.n_errors) {
+                pieces.push_back({reinterpret_cast<uint8_t *>(err_line + base[C_ERRS]), D + L.off[17], r.n_errors * 8});
+                pieces.push_back({err_code + base[C_ERRS], D + L.off[18], r.n_errors});
+            }
+            // every piece waits for the event as recorded now, never for the
+            // context stream, where the next segment is being queued (the next
+            // record of the event comes after this thread is joined)
+            hipEvent_t ready = ctx->seg_ready;
+            cout.th = std::thread([&, pieces, ready] {
+                pj_status q = bind(ctx);
+                for (size_t j = 0; !q && j < pieces.size(); j++)
+                    q = d2h(ctx, pieces[j].dst, pieces[j].src, pieces[j].n, ready);
+                if (q) cout.err = pj_last_error();
+                cout.st = q;
+            });
         }
         base[C_PETS] += r.n_pets; base[C_NAMEB] += r.name_bytes; base[C_CATB] += r.cat_name_bytes;
         base[C_URLS] += r.n_urls; base[C_URLB] += r.url_bytes; base[C_TAGS] += r.n_tags;
         base[C_TAGB] += r.tag_name_bytes; base[C_ERRS] += r.n_errors;
         lines += r.n_lines;
         res->n_general += r.n_general;
+        // the next segment is on the device before it decodes
+        if (const pj_status c2 = cin.join()) return finish(fail(c2, cin.err));
         a = a2;
         b = b2;
     }
+    if ((s = finish(PJ_OK))) return s;
     res->n_lines = lines;
     res->n_pets = base[C_PETS]; res->name_bytes = base[C_NAMEB]; res->cat_name_bytes = base[C_CATB];
     res->n_urls = base[C_URLS]; res->url_bytes = base[C_URLB]; res->n_tags = base[C_TAGS];

@@ -111,7 +111,7 @@ _GEN = None
 EXPORTS = ["pj_create", "pj_destroy", "pj_default_options", "pj_set_options", "pj_last_error",
            "pj_last_timings", "pj_encode_device", "pj_encode_size_device", "pj_encode_host",
            "pj_decode_device", "pj_decode_host", "pj_decode_bounds", "pj_encode_device_noalloc",
-           "pj_decode_array_device", "pj_decode_array_host", "pj_encode_bound"]
+           "pj_decode_array_device", "pj_decode_array_host", "pj_encode_bound", "pj_host_alloc", "pj_host_free"]
 NOALLOC_SCRATCH_WORDS = 1 << 20
 
 
@@ -162,6 +162,9 @@ def load_lib():
                                       C.POINTER(DecodeResult)]
             getattr(L, f).restype = i32
         L.pj_decode_bounds.argtypes = [u64, C.POINTER(PetColumnsStruct)]
+        L.pj_host_alloc.argtypes = [u64]
+        L.pj_host_alloc.restype = vp
+        L.pj_host_free.argtypes = [vp]
         L.pj_encode_by_status_device.argtypes = [vp, C.POINTER(PetColumnsStruct), C.c_uint32, i32, vp, u64,
                                                  C.POINTER(u64), C.POINTER(u64)]
         L.pj_encode_by_status_device.restype = i32
@@ -180,6 +183,22 @@ def load_lib():
         L.pj_decode_model_bounds.argtypes = [i32, u64, C.POINTER(ModelColumnsStruct)]
         _LIB = L
     return _LIB
+
+
+def host_array(n: int, dtype) -> np.ndarray:
+    """A numpy array of n elements in pinned host memory (pj_host_alloc),
+    freed when the array is collected: inputs and outputs of the *_host
+    entry points placed in it move by DMA with no bounce copy."""
+    L = load_lib()
+    nbytes = max(1, int(n) * np.dtype(dtype).itemsize)
+    p = L.pj_host_alloc(nbytes)
+    if not p:
+        raise MemoryError(f"pj_host_alloc({nbytes}) failed")
+    buf = (C.c_uint8 * nbytes).from_address(p)
+    arr = np.frombuffer(buf, dtype=np.uint8, count=nbytes).view(dtype)[: int(n)]
+    import weakref
+    weakref.finalize(buf, L.pj_host_free, p)
+    return arr
 
 
 def load_gen():

@@ -78,16 +78,68 @@ print("streamed decode ok")
 """
 
 
-@pytest.mark.parametrize("segment", [1_000_003, 4_194_301])
-def test_host_decode_streamed_in_segments(segment):
-    """Inputs over PETJSON_DECODE_SEGMENT bytes (default: inputs over 16 GiB,
-    in 1 GiB segments) are decoded in segments cut after a newline, the next
-    one copied in while one decodes: columns, error lines and codes, and
-    totals equal the one-shot device decode.  The input holds blank lines,
-    1% corrupted lines, a 3 MB line longer than a segment, skewed records,
-    and a last line without its newline; capacities one short report
-    PJ_ERR_CAPACITY."""
+@pytest.mark.parametrize("segment,chunk", [(1_000_003, None), (4_194_301, 65537)])
+def test_host_decode_streamed_in_segments(segment, chunk):
+    """Inputs over PETJSON_DECODE_SEGMENT bytes (default: inputs over 512
+    MiB, in 256 MiB segments) are decoded in segments cut after a newline,
+    in a pipeline: the next segment copied in and the previous one's columns
+    copied out while one decodes.  Columns, error lines and codes, and totals
+    equal the one-shot device decode.  The input holds blank lines, 1%
+    corrupted lines, a 3 MB line longer than a segment, skewed records, and a
+    last line without its newline; capacities one short report
+    PJ_ERR_CAPACITY.  With small bounce chunks (PETJSON_XFER_CHUNK) both copy
+    directions cross many chunk boundaries while running at once."""
     env = dict(os.environ, PETJSON_DECODE_SEGMENT=str(segment),
                PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"), os.path.join(ROOT, "tests")]))
+    if chunk:
+        env["PETJSON_XFER_CHUNK"] = str(chunk)
     r = subprocess.run([sys.executable, "-c", STREAM], capture_output=True, text=True, env=env, timeout=240)
     assert r.returncode == 0 and "streamed decode ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
+
+
+PINNED = r"""
+import ctypes as C
+import numpy as np, torch
+import petjson as pj
+codec = pj.Codec(0)
+buf = codec.encode(pj.generate(3, 60000).to_device(), pj.FORMAT_NDJSON).cpu().numpy().copy()
+lines, codes = pj.corrupt_ndjson(buf, 7, 0.01)
+ref, el_r, ec_r, res_r = codec.decode(torch.from_numpy(buf).cuda())
+ref = ref.to_host()
+n = buf.size
+inp = pj.host_array(n, np.uint8)
+inp[:] = buf
+caps = pj.decode_bounds(n)
+cp, cu, ct = caps["cap_pets"], caps["cap_urls"], caps["cap_tags"]
+sizes = {"id": cp, "flags": cp, "status": cp, "name_off": cp + 1, "name_bytes": caps["cap_name_bytes"],
+         "cat_id": cp, "cat_flags": cp, "cat_name_off": cp + 1, "cat_name_bytes": caps["cap_cat_name_bytes"],
+         "photo_off": cp + 1, "url_off": cu + 1, "url_bytes": caps["cap_url_bytes"], "tag_off": cp + 1,
+         "tag_id": ct, "tag_flags": ct, "tag_name_off": ct + 1, "tag_name_bytes": caps["cap_tag_name_bytes"]}
+cols = pj.Columns(0, {k: pj.host_array(v, pj.DTYPES[k]) for k, v in sizes.items()}, dict(caps))
+el, ec = pj.host_array(4096, np.uint64), pj.host_array(4096, np.uint8)
+s = cols.struct()
+res = pj.DecodeResult()
+rc = codec.L.pj_decode_host(codec.ctx, C.c_void_p(inp.ctypes.data), n, C.byref(s), C.c_void_p(el.ctypes.data),
+                            C.c_void_p(ec.ctypes.data), 4096, C.byref(res))
+assert rc == 0, rc
+assert res.n_pets == res_r.n_pets and res.n_errors == res_r.n_errors == len(lines)
+host = codec._trim(cols, res).to_host()
+for k in pj.COLS:
+    assert np.array_equal(host[k], ref[k]), k
+assert np.array_equal(el[: res.n_errors], el_r.cpu().numpy()) and np.array_equal(ec[: res.n_errors], ec_r.cpu().numpy())
+codec.close()
+print("pinned decode ok")
+"""
+
+
+@pytest.mark.parametrize("segment", [None, 1_000_003])
+def test_host_decode_pinned_buffers(segment):
+    """Input and output columns in pinned memory (pj_host_alloc) move by
+    DMA with no bounce copy, one-shot and streamed: the columns, error lines
+    and codes equal the device decode's."""
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"),
+                                                      os.path.join(ROOT, "tests")]))
+    if segment:
+        env["PETJSON_DECODE_SEGMENT"] = str(segment)
+    r = subprocess.run([sys.executable, "-c", PINNED], capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0 and "pinned decode ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
