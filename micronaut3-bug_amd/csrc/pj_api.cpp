@@ -775,8 +775,11 @@ bool dec_cols_ok(const pj_pet_columns *o) {
 // one array document, built in ctx->index (X: its header words; 2 holds the
 // record count).  Fills P's index fields (and zeroes the rest of P); the
 // record count goes to *lines.  The array frame's verdict is checked here.
+// With `cut` (array documents only) the frame is only scanned, for a
+// document cut short: *cut gets the position of its last top-level comma
+// (~0 when it has none), and no frame check is made.
 pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, DecParams &P, uint64_t *&X,
-                      uint64_t *lines_out) {
+                      uint64_t *lines_out, uint64_t *cut = nullptr) {
     pj_status s;
     const uint64_t nblk64 = (len + 63) / 64;
     uint64_t ls_cap = len / 128 + 16;
@@ -834,6 +837,19 @@ pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, 
             PJ_HIP(hipStreamSynchronize(ctx->stream));
             if (array || !P.order_by_id || ctx->pinned[0] == 0) break;
             P.order_by_id = 0;
+        }
+        if (cut) {
+            const uint64_t nsep = ctx->pinned[16 + 3];
+            if (nsep + 2 > ls_cap) {       // the separators' starts did not all fit: grow and redo
+                ls_cap = nsep + 2;
+                continue;
+            }
+            *cut = ~0ull;
+            if (nsep) {
+                PJ_HIP(hipMemcpy(ctx->pinned, P.line_start + nsep, sizeof(uint64_t), hipMemcpyDeviceToHost));
+                *cut = ctx->pinned[0] - 1;
+            }
+            return PJ_OK;
         }
         if (array && ctx->pinned[16 + 4] == 0) {
             (void)finish_timing(ctx);
@@ -1074,8 +1090,43 @@ SegOut seg_layout(uint64_t n, uint64_t ce) {
     return L;
 }
 
+// Array documents stream too: segment k after the first is the bytes after
+// a top-level comma, behind a '[' written in front of them on the device.
+// Where the segment can end is only known once it is on the device: the
+// frame scan of the cut document gives its last top-level comma, which
+// becomes a ']' so that the segment is a whole document of the elements up
+// to it (a segment with no such comma is loaded again twice as long); the
+// next segment starts after that comma.  Its elements are numbered on from
+// the earlier segments', as lines are.  (A frame error is reported as by
+// the one-shot decode when it shows inside one segment's document.)
+pj_status array_segment(pj_ctx *ctx, const uint8_t *in, uint64_t len, uint64_t a, uint64_t seg, int k, DevBuf &buf,
+                        uint64_t *n, uint64_t *next) {
+    const uint64_t pre = k == 0 && a == 0 ? 0 : 1;
+    for (uint64_t Z = std::min(seg, len - a);; Z = std::min(2 * Z, len - a)) {
+        PJ_HIP(buf.ensure(pre + Z + 16));
+        uint8_t *D = static_cast<uint8_t *>(buf.p);
+        pj_status s;
+        if ((s = h2d(ctx, D + pre, in + a, Z))) return s;
+        if (pre) PJ_HIP(pj_launch_put_bytes(D, '[', 1, ctx->stream));
+        if (a + Z == len) {           // the document's own end
+            *n = pre + Z;
+            *next = len;
+            return PJ_OK;
+        }
+        DecParams P;
+        uint64_t *X, lines, cut = ~0ull;
+        if ((s = index_stage(ctx, D, pre + Z, true, P, X, &lines, &cut))) return s;
+        if (cut != ~0ull && cut >= pre) {
+            PJ_HIP(pj_launch_put_bytes(D + cut, ']', 1, ctx->stream));
+            *n = cut + 1;
+            *next = a + (cut - pre) + 1;
+            return PJ_OK;
+        }
+    }
+}
+
 pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_columns *out, uint64_t *err_line,
-                             uint8_t *err_code, uint64_t err_cap, pj_decode_result *res) {
+                             uint8_t *err_code, uint64_t err_cap, pj_decode_result *res, bool array) {
     const uint64_t seg = segment_bytes();
     // segments end after a newline (or at the end); a line longer than a
     // segment makes its segment longer
@@ -1123,14 +1174,21 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
         if (a2) return fail(a2, cout.err);
         return PJ_OK;
     };
-    uint64_t a = 0, b = seg_end(0);
+    uint64_t a = 0, b = 0;
+    uint64_t an = 0, anext = 0;      // arrays: this segment's bytes on the device, the next one's start
     // the first segment in
-    if ((s = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[0].p), in, b - a, false))) return s;
+    if (array) {
+        if ((s = array_segment(ctx, in, len, 0, seg, 0, ctx->seg_in[0], &an, &anext))) return s;
+    } else {
+        b = seg_end(0);
+        if ((s = h2d(ctx, static_cast<uint8_t *>(ctx->seg_in[0].p), in, b - a, false))) return s;
+    }
     for (int k = 0; a < len; k ^= 1) {
-        const uint64_t n = b - a;
-        const uint64_t a2 = b, b2 = b < len ? seg_end(b) : b;
-        // the next segment in, while this one decodes
-        if (a2 < len) {
+        const uint64_t n = array ? an : b - a;
+        const uint64_t a2 = array ? anext : b, b2 = array ? 0 : (b < len ? seg_end(b) : b);
+        // the next segment in, while this one decodes (NDJSON: its end is
+        // known on the host)
+        if (!array && a2 < len) {
             if (ctx->seg_in[k ^ 1].ensure(b2 - a2 + 16) != hipSuccess) return finish(fail(PJ_ERR_DEVICE, "segment buffer"));
             cin.th = std::thread([&, k, a2, b2] {
                 pj_status r = bind(ctx);               // (HIP's current device is per thread)
@@ -1155,7 +1213,7 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
         }
         uint64_t *del = reinterpret_cast<uint64_t *>(D + L.off[17]);
         uint8_t *dec = D + L.off[18];
-        s = decode_impl(ctx, static_cast<uint8_t *>(ctx->seg_in[k].p), n, &L.dc, del, dec, ce, &r);
+        s = decode_impl(ctx, static_cast<uint8_t *>(ctx->seg_in[k].p), n, &L.dc, del, dec, ce, &r, array);
         if (s == PJ_ERR_CAPACITY && r.n_errors > ce) {
             ce = r.n_errors;
             goto again;
@@ -1220,6 +1278,9 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
         res->n_general += r.n_general;
         // the next segment is on the device before it decodes
         if (const pj_status c2 = cin.join()) return finish(fail(c2, cin.err));
+        if (array && a2 < len) {
+            if ((s = array_segment(ctx, in, len, a2, seg, k ^ 1, ctx->seg_in[k ^ 1], &an, &anext))) return finish(s);
+        }
         a = a2;
         b = b2;
     }
@@ -1244,7 +1305,7 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
     if (len && !in) return fail(PJ_ERR_INVALID_ARG, "null input");
     if (!dec_cols_ok(out)) return fail(PJ_ERR_INVALID_ARG, "decode needs every column pointer");
     if (err_cap && (!err_line || !err_code)) return fail(PJ_ERR_INVALID_ARG, "null error arrays");
-    if (!array && len > stream_above()) return decode_host_stream(ctx, in, len, out, err_line, err_code, err_cap, res);
+    if (len > stream_above()) return decode_host_stream(ctx, in, len, out, err_line, err_code, err_cap, res, array);
     // device staging: input, then every output column sized by the capacities
     const uint64_t cp = out->cap_pets, cu = out->cap_urls, ct = out->cap_tags;
     const uint64_t sz[19] = {cp * 8, cp, cp, (cp + 1) * 8, out->cap_name_bytes, cp * 8, cp, (cp + 1) * 8,

@@ -143,3 +143,57 @@ def test_host_decode_pinned_buffers(segment):
         env["PETJSON_DECODE_SEGMENT"] = str(segment)
     r = subprocess.run([sys.executable, "-c", PINNED], capture_output=True, text=True, env=env, timeout=240)
     assert r.returncode == 0 and "pinned decode ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
+
+
+ARRAY_STREAM = r"""
+import numpy as np, torch
+import petjson as pj
+codec = pj.Codec(0)
+rng = np.random.default_rng(5)
+els = []
+for cfg, n in ((3, 30000), (5, 3000)):
+    lines = codec.encode(pj.generate(cfg, n).to_device(), pj.FORMAT_NDJSON).cpu().numpy().tobytes().split(b"\n")[:-1]
+    els += lines
+# invalid elements that keep the frame: an unknown status, a missing name
+for i in rng.choice(len(els), 300, replace=False):
+    e = els[i]
+    els[i] = e.replace(b'"status":"', b'"status":"x', 1) if i % 2 else e.replace(b'"name":', b'"nom":', 1)
+# separators, brackets, quotes and backslashes inside strings; a 3 MB element
+els.insert(7, b'{"name":"a,b],[c}{\\\\\\",","photoUrls":["[,]","\\\\"],"tags":[{"name":"]],,"}]}')
+els.insert(20000, b'{"id":9,"name":"' + b"L" * 3_000_000 + b'","photoUrls":[],"status":"sold"}')
+seps = [b",", b" ,\n  ", b",\n", b"\t,"]
+doc = b" \n[" + b"".join(e + seps[j % 4] for j, e in enumerate(els[:-1])) + els[-1] + b"\n] \n"
+d = torch.from_numpy(np.frombuffer(doc, np.uint8).copy()).cuda()
+ref, el_r, ec_r, res_r = codec.decode(d, array=True)
+ref = ref.to_host()
+host, el, ec, res = codec.decode_array_host(doc)
+assert res.n_lines == res_r.n_lines == len(els), (res.n_lines, res_r.n_lines, len(els))
+for k in ("n_pets", "n_errors", "name_bytes", "cat_name_bytes", "n_urls", "url_bytes", "n_tags", "tag_name_bytes"):
+    assert getattr(res, k) == getattr(res_r, k), (k, getattr(res, k), getattr(res_r, k))
+for k in pj.COLS:
+    assert np.array_equal(host[k], ref[k]), k
+assert np.array_equal(el, el_r.cpu().numpy()) and np.array_equal(ec, ec_r.cpu().numpy())
+# a broken frame is still a syntax error
+try:
+    codec.decode_array_host(doc.rsplit(b"]", 1)[0] + b"} \n")
+    raise SystemExit("expected a syntax error")
+except pj.PetJsonError as e:
+    assert e.status == pj.PJ_ERR_SYNTAX, e
+codec.close()
+print("streamed array ok")
+"""
+
+
+@pytest.mark.parametrize("segment", [999_983, 4_194_301])
+def test_host_array_document_streamed_in_segments(segment):
+    """pj_decode_array_host on one JSON array document over
+    PETJSON_DECODE_SEGMENT bytes decodes it in segments cut at top-level
+    commas found on the device (separators, brackets and escapes inside
+    strings, whitespace and newlines between elements, a 3 MB element longer
+    than a segment, invalid elements): columns, element indices, codes and
+    totals equal the one-shot device decode, and a broken frame is still
+    PJ_ERR_SYNTAX."""
+    env = dict(os.environ, PETJSON_DECODE_SEGMENT=str(segment),
+               PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"), os.path.join(ROOT, "tests")]))
+    r = subprocess.run([sys.executable, "-c", ARRAY_STREAM], capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0 and "streamed array ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
