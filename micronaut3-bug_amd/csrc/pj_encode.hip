@@ -874,6 +874,56 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
 
 // ------------------------------------------------------------------ kernel
 
+// Names longer than LN_MIN bytes in tile-path blocks are counted and written
+// by a whole wave, one 8-byte word per lane; the record's own lane writes
+// only the quotes and the photoUrls opener around the body.  One long
+// escape-heavy name then no longer holds its wave (a lane writing it alone
+// takes a loop step per escape).
+constexpr uint32_t LN_MIN = 48;
+
+// 8 staged bytes at any byte address: two aligned LDS reads joined
+__device__ __forceinline__ uint64_t lds_any8(const PJ_LDS uint8_t *p) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 7;
+    const PJ_LDS uint64_t *q = (const PJ_LDS uint64_t *)(p - sh);
+    const uint64_t a = q[0];
+    return sh ? (a >> (8 * sh)) | (q[1] << (64 - 8 * sh)) : a;
+}
+// The bytes the escapes of the len staged bytes at p add (all 64 lanes of
+// the wave call, with the same arguments).
+__device__ __forceinline__ uint32_t wave_esc_extra(const PJ_LDS uint8_t *p, uint32_t len) {
+    uint32_t e = 0;
+    for (uint32_t k = 8u * (uint32_t)lane_id(); k < len; k += 512) {
+        const uint32_t m = min(8u, len - k);
+        e += esc_extra(lds_any8(p + k), m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1));
+    }
+    return (uint32_t)wave_sum(e);
+}
+// The escaped bytes of the len staged bytes at p, written to the tile from
+// offset dst (all 64 lanes of the wave call, with the same arguments): lane
+// l takes word l of each 512-byte step, and a wave scan of the words'
+// escaped lengths places them.
+__device__ __forceinline__ void wave_str_body(uint8_t *tile, uint32_t dst, const PJ_LDS uint8_t *p, uint32_t len,
+                                              uint32_t hexa) {
+    for (uint32_t k0 = 0; k0 < len; k0 += 512) {
+        const uint32_t k = k0 + 8u * (uint32_t)lane_id();
+        uint64_t x = 0;
+        uint32_t m = 0, w = 0;
+        if (k < len) {
+            m = min(8u, len - k);
+            const uint64_t keep = m >= 8 ? ~0ull : ((1ull << (8 * m)) - 1);
+            x = lds_any8(p + k) & keep;
+            w = m + esc_extra(x, keep);
+        }
+        const uint32_t inc = wave_incl_scan32(w);
+        if (m) {
+            LdsSinkU s{tile, dst + inc - w, dst + inc};
+            if (w == m) s.put8(x, (int)m);
+            else esc_bytes(s, x, (int)m, hexa);
+        }
+        dst += (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+    }
+}
+
 // Where a block's records, items and string bytes lie: fetched for block nb
 // by the first wave in two dependent rounds.  Lanes 0-7 load the first
 // level (url and tag item ranges, name and category name byte ranges),
@@ -1047,6 +1097,9 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
     __shared__ uint64_t splain[(INCAP / 16 + 63) / 64];  // staged 16-byte chunks that hold a byte to escape
     __shared__ uint64_t sh_nx[NX], sh_nb, sh_base, sh_len;
     __shared__ uint32_t sh_nbig;
+    // NESTED fast blocks: the records whose name the waves write together
+    __shared__ uint8_t sh_ln[RA];
+    __shared__ uint32_t sh_nln;
     // hybrid blocks (NESTED): the large records in record order, with their
     // block offsets, lengths and tile offsets; fast blocks keep each record's
     // head unit index, name offset in the staged slice and name length in
@@ -1082,7 +1135,10 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             const uint64_t v1 = bounds_l1<NESTED, R>(P, b0, t);
             bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
         }
-        if (t == 0) sh_nb = b0;
+        if (t == 0) {
+            sh_nb = b0;
+            sh_nln = 0;
+        }
     }
     __syncthreads();
     uint64_t b = sh_nb;
@@ -1147,6 +1203,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     sh_bpre[t] = (uint32_t)(rv.na - g.lo16[0]);
                     sh_blen[t] = (uint32_t)(rv.nb - rv.na);
                     rn_f[t] = (uint8_t)((rv.fl & (PJ_PET_HAS_NAME | PJ_PET_HAS_PHOTOURLS)) | (rv.u1 == rv.u0 ? 0x80u : 0u));
+                    if ((rv.fl & PJ_PET_HAS_NAME) && rv.nb - rv.na > LN_MIN) sh_ln[atomicAdd(&sh_nln, 1u)] = (uint8_t)t;
                     const uint32_t uf = rec_has_urls(rv) ? ITEM_ON : 0u, gf = rec_has_tags<NESTED>(rv) ? ITEM_ON : 0u;
                     for (uint32_t k = ul0; k < ul1; k++)
                         uinfo[k] = (hidx + 2 + k - ul0) | uf | (k + 1 == ul1 ? ITEM_LAST : 0u);
@@ -1169,9 +1226,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     ulen[hidx + 3 + nu + nt] = (uint32_t)ct.n;
                 }
                 if (t >= (uint32_t)name0<R>() && t - name0<R>() < nrec) {
-                    const uint32_t r = t - name0<R>();
+                    const uint32_t r = t - name0<R>(), f = rn_f[r];
                     CountSink cs;
-                    name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                    if ((f & PJ_PET_HAS_NAME) && sh_blen[r] > LN_MIN) {
+                        // the body's escapes are added by the waves below
+                        cs.n = sh_blen[r] + 2;
+                        rec_urls_open(cs, f, (f & 0x80u) != 0);
+                    } else name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
                     ulen[sh_big[r] + 1] = (uint32_t)cs.n;
                 }
 #pragma unroll
@@ -1191,6 +1252,17 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     }
                 }
                 __syncthreads();
+                if (sh_nln) {
+                    // long names: the escapes of their bodies, one name per wave
+                    for (uint32_t k = t >> 6; k < sh_nln; k += BT / 64) {
+                        const uint32_t r = sh_ln[k];
+                        const uint8_t *p = XL.name + sh_bpre[r];
+                        if (staged_plain(XL, p, sh_blen[r])) continue;
+                        const uint32_t e = wave_esc_extra((const PJ_LDS uint8_t *)p, sh_blen[r]);
+                        if ((t & 63) == 0) ulen[sh_big[r] + 1] += e;
+                    }
+                    __syncthreads();
+                }
                 const uint32_t NU = 4 * nrec + (uint32_t)(U + G);
                 lds_excl_scan<BT>(ulen, NU, sh_scan);
                 agg = ulen[NU];
@@ -1277,9 +1349,18 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     ts.finish();
                 }
                 if (t >= (uint32_t)name0<R>() && t - name0<R>() < nrec) {
-                    const uint32_t r = t - name0<R>();
-                    LdsSink ns{tile, ulen[sh_big[r] + 1], ulen[sh_big[r] + 2]};
-                    name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], rn_f[r]);
+                    const uint32_t r = t - name0<R>(), f = rn_f[r];
+                    const uint32_t u0 = ulen[sh_big[r] + 1], u1 = ulen[sh_big[r] + 2];
+                    LdsSink ns{tile, u0, u1};
+                    if ((f & PJ_PET_HAS_NAME) && sh_blen[r] > LN_MIN) {
+                        // a long name: its body is left to the waves below
+                        CountSink oc;
+                        rec_urls_open(oc, f, (f & 0x80u) != 0);
+                        ns.put_byte('"');
+                        ns.skip(u1 - u0 - 2 - (uint32_t)oc.n);
+                        ns.put_byte('"');
+                        rec_urls_open(ns, f, (f & 0x80u) != 0);
+                    } else name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
                     ns.finish();
                 }
 #pragma unroll
@@ -1300,6 +1381,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                         emit_tag_v(ls, P, XL, iv[j], (f & ITEM_LAST) != 0);
                         ls.finish();
                     }
+                }
+                // long names: their bodies, one name per wave (the tile is
+                // read only after the look-back's barrier)
+                for (uint32_t k = t >> 6; k < sh_nln; k += BT / 64) {
+                    const uint32_t r = sh_ln[k];
+                    wave_str_body(tile, ulen[sh_big[r] + 1] + 1, (const PJ_LDS uint8_t *)(XL.name + sh_bpre[r]), sh_blen[r],
+                                  P.hexa);
                 }
             } else if (live) {
                 LdsSink ls{tile, (uint32_t)pre};
@@ -1324,6 +1412,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         }
         __syncthreads();
         EPROF(5);
+        if (t == 0) sh_nln = 0;                         // (read for the last time before the barrier above)
         // a block with nothing left to write but its tile claims now; one
         // that still writes records after the look-back (fallback or
         // hybrid), once they are written, so that a claimed block always

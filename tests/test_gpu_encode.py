@@ -411,3 +411,44 @@ def test_config1_gpu_output_matches_committed_digest(codec):
         b = codec.encode(dev, fmt).cpu().numpy().tobytes()
         assert len(b) == d["digests"][name]["bytes"]
         assert hashlib.sha256(b).hexdigest() == d["digests"][name]["sha256"], name
+
+
+def _with_names(cols, lens, rng, esc_rate):
+    """cols with its names replaced: lengths from lens (cycled), bytes drawn
+    from letters, every byte that needs an escape and UTF-8 bytes."""
+    n = cols.n_pets
+    L = np.array([lens[i % len(lens)] for i in range(n)], np.uint64)
+    off = np.zeros(n + 1, np.uint64)
+    np.cumsum(L, out=off[1:])
+    letters = np.frombuffer(b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789 ", np.uint8)
+    special = np.array([0x22, 0x5C, 0x0A, 0x09, 0x08, 0x0C, 0x0D, 0x01, 0x1F, 0x1A, 0x00, 0x7F, 0xC3, 0xA9], np.uint8)
+    tot = int(off[-1])
+    b = rng.choice(letters, tot)
+    hit = rng.random(tot) < esc_rate
+    b[hit] = rng.choice(special, int(hit.sum()))
+    cols.arrays["name_off"] = off
+    cols.arrays["name_bytes"] = b
+    return cols
+
+
+@pytest.mark.parametrize("esc_rate", [0.0, 0.05, 0.3, 1.0])
+def test_encode_long_names_written_by_waves(codec, esc_rate):
+    """Names over 48 bytes in tile-path blocks have their escapes counted and
+    their bodies written by a whole wave, 8 bytes per lane, in 512-byte
+    steps: lengths around 48, 64 and 512, names past one step, null names
+    whose bytes still sit in the column, escapes at every offset."""
+    rng = np.random.default_rng(7 + int(esc_rate * 100))
+    lens = [0, 3, 47, 48, 49, 50, 55, 56, 57, 63, 64, 65, 71, 72, 100, 200, 20, 33]
+    cols = _with_names(pj.generate(3, 6_000), lens, rng, esc_rate)
+    flags = cols["flags"].copy()
+    flags[rng.random(cols.n_pets) < 0.05] &= ~np.uint8(pj.PET_HAS_NAME)
+    cols.arrays["flags"] = flags
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        ref = orc.encode(cols, fmt)
+        assert codec.encode_size(cols.to_device(), fmt) == len(ref)
+        assert gpu_encode(codec, cols, fmt) == ref, fmt
+    # a few names of one and two 512-byte steps among short ones
+    lens = [10] * 40 + [511, 512, 513, 700, 1023, 1024, 1025, 1100]
+    cols = _with_names(pj.generate(3, 3_000), lens, rng, esc_rate)
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt), fmt
