@@ -25,6 +25,7 @@
 // Output rules (jackson UTF8JsonGenerator via micronaut-serde, reference
 // build.gradle:104) and property order / inclusion (petstore.json:872-922)
 // are the ones restated by the CPU checker in oracle/pj_oracle.c.
+#include <map>
 #include <mutex>
 #include <type_traits>
 
@@ -1984,22 +1985,23 @@ namespace {
 // Workgroups of kernel K that the device holds at once (cached per device
 // and kernel): the persistent encode launches no more than that many, so
 // every launched workgroup is resident.
+// Workgroups of kern the current device holds at once, cached per device
+// and kernel (every encode kernel has the same type, so the kernel's address
+// is part of the key).
 template <class K> unsigned resident_groups(K kern, int threads) {
-    constexpr int MAXD = 64;
     static std::mutex mu;
-    static unsigned cache[MAXD] = {};
+    static std::map<std::pair<int, const void *>, unsigned> cache;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXD) return 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    const auto key = std::make_pair(dev, reinterpret_cast<const void *>(kern));
     std::lock_guard<std::mutex> lk(mu);
-    if (!cache[dev]) {
-        int per_cu = 0, cus = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 ||
-            cus <= 0)
-            return 0;
-        cache[dev] = (unsigned)(per_cu * cus);
-    }
-    return cache[dev];
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
+        return 0;
+    return cache[key] = (unsigned)(per_cu * cus);
 }
 template <class K>
 hipError_t launch_encode(K kern, int threads, const EncParams &P, uint64_t records, bool persistent, hipStream_t st) {

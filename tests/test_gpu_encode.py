@@ -243,6 +243,84 @@ def test_encode_hybrid_blocks_match_oracle(codec):
         assert (host[:cap][written] == ref[:cap][written]).all()
 
 
+def _offtile_cases():
+    """Blocks (96 records) that do not fit the tile path whole: medium names
+    past the staging buffer with a large record now and then, many large
+    records, a url larger than the staging buffer, control-byte names whose
+    output overflows the tile, large records side by side with ordinary
+    ones."""
+    import random
+    from model import Tag, from_columns
+    rnd = random.Random(11)
+    frag = [b"a", b"bc", b"\"", b"\\", b"\n", b"\x01", b"\x1f", b"\xc3\xa9", b"\xf0\x9f\x98\x80", b"xyz0123"]
+
+    def name(lo, hi):
+        out = b"".join(rnd.choice(frag) for _ in range(rnd.randrange(lo, hi)))
+        return out
+
+    cases = {}
+    # medium names everywhere, a large record now and then
+    pets = from_columns(pj.generate(3, 96 * 8), as_bytes=True)
+    for k, p in enumerate(pets):
+        p.name = name(20, 160)
+        if k % 53 == 7:
+            p.name = name(900, 2000)
+        if k % 71 == 3:
+            p.tags = [Tag(id=rnd.randrange(-10**15, 10**15), name=b"t%d" % j) for j in range(rnd.randrange(17, 40))]
+    cases["medium_names"] = pets
+    # a large record every 8th record
+    pets = from_columns(pj.generate(3, 96 * 3), as_bytes=True)
+    for k, p in enumerate(pets):
+        if k % 8 == 0:
+            p.name = name(600, 700)
+    cases["many_large"] = pets
+    # a record whose url alone overflows the staging buffer
+    pets = from_columns(pj.generate(3, 96 * 3), as_bytes=True)
+    pets[100].photo_urls = [b"https://" + b"u" * 20000]
+    pets[101].name = name(900, 1000)
+    cases["huge_url"] = pets
+    # names of control bytes (6 output bytes each): the output overflows the tile
+    pets = from_columns(pj.generate(3, 96 * 3), as_bytes=True)
+    for k, p in enumerate(pets[96:192]):
+        p.name = b"\x01" * 120
+    pets[150].name = name(900, 1000)
+    cases["tile_overflow"] = pets
+    # single ordinary records between large records
+    pets = from_columns(pj.generate(3, 96 * 2), as_bytes=True)
+    for k in range(0, 96 * 2, 2):
+        if k % 96 < 12:
+            pets[k].name = name(600, 700)
+    cases["alternating"] = pets
+    return cases
+
+
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_encode_offtile_blocks_match_oracle(codec, two_pass):
+    """Blocks that do not fit the tile path whole (hybrid blocks, and blocks
+    written one record per thread): against the oracle in both framings,
+    single pass and at measured offsets, with a capacity cut inside such a
+    block."""
+    for label, pets in _offtile_cases().items():
+        cols = to_columns(pets)
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            print(f"[offtile] {label} fmt={fmt} two_pass={two_pass}", flush=True)
+            ref = orc.encode(cols, fmt)
+            codec.set_options()
+            d = cols.to_device()
+            assert codec.encode_size(d, fmt) == len(ref), label
+            assert codec.encode(d, fmt, two_pass=two_pass).cpu().numpy().tobytes() == ref, (label, fmt)
+        if label == "medium_names" and not two_pass:
+            ref = np.frombuffer(orc.encode(cols, pj.FORMAT_NDJSON), np.uint8)
+            for cap in (len(ref) // 2, len(ref) - 7):
+                out = torch.full((len(ref),), 0xEE, dtype=torch.uint8, device="cuda")
+                with pytest.raises(pj.PetJsonError):
+                    codec.encode(d, pj.FORMAT_NDJSON, out=out[:cap])
+                host = out.cpu().numpy()
+                assert (host[cap:] == 0xEE).all()
+                written = host[:cap] != 0xEE
+                assert (host[:cap][written] == ref[:cap][written]).all()
+
+
 def test_encode_lookback_redo_in_ticket_order(codec, monkeypatch):
     """Flat blocks take their records in launch order and bound their
     look-back waits; a launch in which some wait ran out is redone with
