@@ -89,6 +89,7 @@ struct pj_ctx {
     // so that a copy in and a copy out can run at once
     Xfer xin, xout;
     hipEvent_t seg_ready = nullptr;   // streamed decode: a segment's columns are final
+    hipEvent_t seg_done[2] = {};      // streamed encode: a segment's bytes and length are final
     uint64_t *noalloc_scratch = nullptr;  // this device's fixed encode scratch (device address)
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
     hipEvent_t ev[MAX_EV] = {};
@@ -307,11 +308,22 @@ void set_enc_options(const pj_ctx *ctx, EncParams &P) {
 
 bool format_ok(int f) { return f == PJ_FORMAT_ARRAY || f == PJ_FORMAT_NDJSON || f == PJ_FORMAT_PRETTY; }
 
+// One segment of a streamed host encode (compact formats): the local index
+// of the input's first and last record (or ~0 when the segment holds
+// neither), and the pinned word that receives the segment's length before
+// the event is recorded.  encode_impl then returns as soon as the work is
+// queued.
+struct EncSeg {
+    uint64_t first, last;
+    uint64_t *len;
+    hipEvent_t done;
+};
+
 // fixed_scratch: encode into the device's fixed scratch array instead of
 // the context's growable buffer (pj_encode_device_noalloc); nothing is
 // allocated on that path.
 pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t cap,
-                      uint64_t *out_len, bool count_only, bool fixed_scratch = false) {
+                      uint64_t *out_len, bool count_only, bool fixed_scratch = false, const EncSeg *seg = nullptr) {
     pj_status s = bind(ctx);
     if (s) return s;
     if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
@@ -343,7 +355,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // look-back; it measured faster than the measuring pass followed by a
     // writer at the given offsets (PETJSON_ENC_TWO_PASS=1).  The fixed
     // scratch of the no-allocation entry point holds only the single pass.
-    const bool two_pass = !pretty && nested_cols(cols) && !fixed_scratch && (count_only || enc_two_pass());
+    const bool two_pass = !pretty && nested_cols(cols) && !fixed_scratch && !seg && (count_only || enc_two_pass());
     uint64_t *sc;
     std::unique_lock<std::mutex> noalloc_guard;
     if (fixed_scratch) {
@@ -363,6 +375,8 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     std::memset(&P, 0, sizeof P);
     P.c = *cols;
     P.n = n;
+    P.first = seg ? seg->first : 0;
+    P.last = seg ? seg->last : n - 1;
     P.format = format;
     set_enc_options(ctx, P);
     P.count_only = count_only ? 1 : 0;
@@ -380,7 +394,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // atomic on the critical path) with bounded look-back waits: should a
     // block wait past the bound (a predecessor not yet running), it flags
     // the launch, which is then redone with ticket-ordered blocks.
-    P.order_by_id = nested_cols(cols) || pretty ? 0 : 1;
+    P.order_by_id = nested_cols(cols) || pretty || seg ? 0 : 1;
     P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;
@@ -398,6 +412,11 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
             }
         } else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
         if ((s = mark(ctx))) return s;
+        if (seg) {
+            PJ_HIP(hipMemcpyAsync(seg->len, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+            PJ_HIP(hipEventRecord(seg->done, ctx->stream));
+            return PJ_OK;
+        }
         PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));
         if (!P.order_by_id || ctx->pinned[0] == 0 || attempt > 0) break;
@@ -534,6 +553,8 @@ void pj_destroy(pj_ctx *c) {
     xfer_free(c->xin);
     xfer_free(c->xout);
     if (c->seg_ready) (void)hipEventDestroy(c->seg_ready);
+    for (hipEvent_t e : c->seg_done)
+        if (e) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -609,6 +630,8 @@ pj_status pj_encode_by_status_device(pj_ctx *ctx, const pj_pet_columns *cols, ui
         return len > out_cap ? fail(PJ_ERR_CAPACITY, "output capacity too small") : PJ_OK;
     }
     P.n = m;
+    P.first = 0;
+    P.last = m - 1;
     P.sel = sel;
     P.ticket = reinterpret_cast<unsigned long long *>(ec);
     P.total = ec + 1;
@@ -659,6 +682,208 @@ pj_status stage_pet_cols(pj_ctx *ctx, const pj_pet_columns *cols, pj_pet_columns
     set_col_ptrs(dc, dp);
     return PJ_OK;
 }
+// ---- streamed host encode
+// pj_encode_host of an input over twice PETJSON_ENCODE_SEGMENT bytes of
+// columns (256 MiB by default; compact formats) runs in segments of records.
+// While segment k encodes on the context stream, a host thread copies
+// segment k + 1's column slices in (engine xin), and segment k - 1's bytes go
+// out (engine xout) to the caller's buffer at the running offset; PCIe is
+// full duplex, so the two copies run at once.  A segment's slices keep the
+// column layout: offsets stay absolute, and a slice indexed by them gets a
+// device pointer shifted back by its first offset.  Byte slices sit at the
+// address their first byte has in the input, modulo 16, with 16 bytes on
+// either side (the staging loads read aligned 16-byte chunks around them).
+uint64_t enc_segment_bytes() {
+    if (const char *e = std::getenv("PETJSON_ENCODE_SEGMENT")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v) return v;
+    }
+    return 256ull << 20;
+}
+
+// The column slices of records [r0, r1): per column (col_ptrs order) its
+// first byte in the host column, its size, its offset in the device buffer
+// and the shift of the device pointer.
+struct EncSlices {
+    uint64_t src[17], size[17], off[17], shift[17];
+    uint64_t total;
+};
+void enc_slices(const pj_pet_columns *c, uint64_t r0, uint64_t r1, EncSlices *E) {
+    const uint64_t m = r1 - r0;
+    const uint64_t u0 = c->photo_off ? c->photo_off[r0] : 0, u1 = c->photo_off ? c->photo_off[r1] : 0;
+    const uint64_t t0 = c->tag_off ? c->tag_off[r0] : 0, t1 = c->tag_off ? c->tag_off[r1] : 0;
+    void *hp[17];
+    pj_pet_columns hc = *c;
+    col_ptrs(&hc, hp);
+    // byte ranges of the string columns: [first byte, end)
+    const uint64_t nb0 = c->name_off[r0], nb1 = c->name_off[r1];
+    const uint64_t cb0 = c->cat_name_off ? c->cat_name_off[r0] : 0, cb1 = c->cat_name_off ? c->cat_name_off[r1] : 0;
+    const uint64_t ub0 = c->photo_off ? c->url_off[u0] : 0, ub1 = c->photo_off ? c->url_off[u1] : 0;
+    const uint64_t gb0 = c->tag_off ? c->tag_name_off[t0] : 0, gb1 = c->tag_off ? c->tag_name_off[t1] : 0;
+    const uint64_t src[17] = {r0 * 8, r0, r0, r0 * 8, nb0, r0 * 8, r0, r0 * 8, cb0,
+                              r0 * 8, u0 * 8, ub0, r0 * 8, t0 * 8, t0, t0 * 8, gb0};
+    const uint64_t size[17] = {m * 8, m, m, (m + 1) * 8, nb1 - nb0, m * 8, m, (m + 1) * 8, cb1 - cb0,
+                               (m + 1) * 8, (u1 - u0 + 1) * 8, ub1 - ub0, (m + 1) * 8, (t1 - t0) * 8, t1 - t0,
+                               (t1 - t0 + 1) * 8, gb1 - gb0};
+    // the columns indexed by item or byte offsets: the pointer moves back by
+    // the slice's first index (record columns are indexed from the segment's
+    // first record)
+    const uint64_t shift[17] = {0, 0, 0, 0, nb0, 0, 0, 0, cb0, 0, u0 * 8, ub0, 0, t0 * 8, t0, t0 * 8, gb0};
+    uint64_t o = 0;
+    for (int k = 0; k < 17; k++) {
+        const bool on = hp[k] != nullptr;
+        E->src[k] = src[k];
+        E->size[k] = on ? size[k] : 0;
+        E->shift[k] = shift[k];
+        o = align256(o) + 16;
+        o += (src[k] - o) & 15;                 // the same address mod 16 as in the input
+        E->off[k] = o;
+        o += E->size[k] + 16;
+    }
+    E->total = align256(o);
+}
+
+// Records [r0, r1) of host columns as a column set of their own (for
+// pj_encode_bound): record columns start at r0; offsets stay absolute.
+pj_pet_columns seg_view(const pj_pet_columns *c, uint64_t r0, uint64_t r1) {
+    pj_pet_columns v = *c;
+    v.n_pets = r1 - r0;
+    if (v.id) v.id += r0;
+    if (v.flags) v.flags += r0;
+    if (v.status) v.status += r0;
+    v.name_off += r0;
+    if (v.cat_id) v.cat_id += r0;
+    if (v.cat_flags) v.cat_flags += r0;
+    if (v.cat_name_off) v.cat_name_off += r0;
+    if (v.photo_off) v.photo_off += r0;
+    if (v.tag_off) v.tag_off += r0;
+    return v;
+}
+
+pj_status encode_host_stream(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8_t *out, uint64_t cap,
+                             uint64_t *out_len) {
+    const uint64_t n = cols->n_pets;
+    Layout L;
+    host_layout(cols, &L);
+    const uint64_t nseg = std::max<uint64_t>(2, (L.total + enc_segment_bytes() - 1) / enc_segment_bytes());
+    const uint64_t S = (n + nseg - 1) / nseg;
+    // buffers sized once for the largest segment: its slices, and its
+    // output (pj_encode_bound of its records)
+    uint64_t in_max = 0, out_max = 0;
+    for (uint64_t r0 = 0; r0 < n; r0 += S) {
+        const uint64_t r1 = std::min(n, r0 + S);
+        EncSlices E;
+        enc_slices(cols, r0, r1, &E);
+        pj_pet_columns hv = seg_view(cols, r0, r1);
+        uint64_t bound = 0;
+        pj_status s0 = pj_encode_bound(&hv, format, &bound);
+        if (s0) return s0;
+        in_max = std::max(in_max, E.total);
+        out_max = std::max(out_max, bound + 64);
+    }
+    DevBuf *stage[2] = {&ctx->stage_out, &ctx->stage_out2};
+    for (int k = 0; k < 2; k++) {
+        PJ_HIP(ctx->seg_in[k].ensure(in_max));
+        PJ_HIP(stage[k]->ensure(out_max));
+        if (!ctx->seg_done[k]) PJ_HIP(hipEventCreateWithFlags(&ctx->seg_done[k], hipEventDisableTiming));
+    }
+    struct Job {
+        std::thread th;
+        pj_status st = PJ_OK;
+        std::string err;
+        pj_status join() {
+            if (th.joinable()) th.join();
+            const pj_status r = st;
+            st = PJ_OK;
+            return r;
+        }
+    };
+    Job cin, cout;
+    auto finish = [&](pj_status r) -> pj_status {
+        const pj_status a1 = cin.join(), a2 = cout.join();
+        if (r) return r;
+        if (a1) return fail(a1, cin.err);
+        if (a2) return fail(a2, cout.err);
+        return PJ_OK;
+    };
+    // the slices of records [r0, r1) into slot k's input buffer
+    auto load = [&](int k, uint64_t r0, uint64_t r1) -> pj_status {
+        EncSlices E;
+        enc_slices(cols, r0, r1, &E);
+        void *hp[17];
+        pj_pet_columns hc = *cols;
+        col_ptrs(&hc, hp);
+        uint8_t *D = static_cast<uint8_t *>(ctx->seg_in[k].p);
+        for (int j = 0; j < 17; j++) {
+            if (!E.size[j]) continue;
+            const pj_status r = h2d(ctx, D + E.off[j], static_cast<const uint8_t *>(hp[j]) + E.src[j], E.size[j], false);
+            if (r) return r;
+        }
+        return PJ_OK;
+    };
+    pj_status s = load(0, 0, std::min(n, S));
+    if (s) return s;
+    uint64_t done = 0;                        // bytes of the segments before this one
+    int k = 0;
+    for (uint64_t r0 = 0; r0 < n; r0 += S, k ^= 1) {
+        const uint64_t r1 = std::min(n, r0 + S);
+        // segment k is on the device: its columns, shifted as its slices say
+        if (const pj_status c1 = cin.join()) return finish(fail(c1, cin.err));
+        EncSlices E;
+        enc_slices(cols, r0, r1, &E);
+        void *dp[17];
+        {
+            void *hp[17];
+            pj_pet_columns hc = *cols;
+            col_ptrs(&hc, hp);
+            const uintptr_t D = reinterpret_cast<uintptr_t>(ctx->seg_in[k].p);
+            for (int j = 0; j < 17; j++) dp[j] = hp[j] ? reinterpret_cast<void *>(D + E.off[j] - E.shift[j]) : nullptr;
+        }
+        pj_pet_columns dc = *cols;
+        set_col_ptrs(&dc, dp);
+        dc.n_pets = r1 - r0;
+        const EncSeg es{r0 == 0 ? 0 : ~0ull, r1 == n ? r1 - r0 - 1 : ~0ull, ctx->pinned + 48 + k, ctx->seg_done[k]};
+        uint64_t unused = 0;
+        if ((s = encode_impl(ctx, &dc, format, static_cast<uint8_t *>(stage[k]->p), out_max, &unused, false, false, &es)))
+            return finish(s);
+        // segment k + 1 in while k encodes (its slot's input was read by
+        // segment k - 1, whose encode is done: its length was read below)
+        if (r1 < n) {
+            const uint64_t a2 = r1, b2 = std::min(n, r1 + S);
+            const int k2 = k ^ 1;
+            cin.th = std::thread([&, k2, a2, b2] {
+                pj_status r = bind(ctx);               // (HIP's current device is per thread)
+                if (!r) r = load(k2, a2, b2);
+                if (r) cin.err = pj_last_error();
+                cin.st = r;
+            });
+        }
+        // segment k - 1's bytes are out, so its output slot is free again
+        if (const pj_status c2 = cout.join()) return finish(fail(c2, cout.err));
+        if (const hipError_t x = hipEventSynchronize(ctx->seg_done[k]))
+            return finish(fail(PJ_ERR_DEVICE, std::string("encode segment: ") + hipGetErrorString(x)));
+        const uint64_t len = ctx->pinned[48 + k];
+        // as much of segment k as fits the caller's buffer
+        const uint64_t w = done >= cap ? 0 : std::min(len, cap - done);
+        if (w) {
+            uint8_t *dst = out + done;
+            const void *src = stage[k]->p;
+            hipEvent_t ready = ctx->seg_done[k];     // (recorded again only after this thread is joined)
+            cout.th = std::thread([&, dst, src, w, ready] {
+                pj_status q = bind(ctx);
+                if (!q) q = d2h(ctx, dst, src, w, ready);
+                if (q) cout.err = pj_last_error();
+                cout.st = q;
+            });
+        }
+        done += len;
+    }
+    if ((s = finish(PJ_OK))) return s;
+    *out_len = done;
+    if (done > cap) return fail(PJ_ERR_CAPACITY, "output capacity too small");
+    return PJ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -694,6 +919,17 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, ui
     if (s) return s;
     if (!cols || !out_len) return fail(PJ_ERR_INVALID_ARG, "null argument");
     if (cols->n_pets && (s = check_enc_cols(cols))) return s;
+    if (cols->n_pets && format != PJ_FORMAT_PRETTY) {
+        if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
+        Layout L;
+        host_layout(cols, &L);
+        // (a segment size set in the environment streams anything above it)
+        const uint64_t above = std::getenv("PETJSON_ENCODE_SEGMENT") ? enc_segment_bytes() : 2 * enc_segment_bytes();
+        if (L.total > above) {
+            if (!out && out_cap) return fail(PJ_ERR_INVALID_ARG, "null output");
+            return encode_host_stream(ctx, cols, format, out, out_cap, out_len);
+        }
+    }
     pj_pet_columns dc;
     if ((s = stage_pet_cols(ctx, cols, &dc))) return s;
     uint64_t need = 0;

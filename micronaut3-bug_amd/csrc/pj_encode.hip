@@ -510,7 +510,7 @@ template <bool NESTED, class S>
 __device__ __forceinline__ void rec_head(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v) {
     const pj_pet_columns &c = P.c;
     const uint32_t fl = v.fl;
-    if (P.format != PJ_FORMAT_NDJSON) s.put_byte(i == 0 ? '[' : ',');
+    if (P.format != PJ_FORMAT_NDJSON) s.put_byte(i == P.first ? '[' : ',');
     bool first = true;
     s.put_byte('{');
     if (fl & PJ_PET_HAS_ID) { key(s, first); lit(s, "\"id\":"); emit_long(s, v.id); }
@@ -554,7 +554,7 @@ template <class S> __device__ __forceinline__ void rec_tail(S &s, const EncParam
     else if (P.incl[PJ_FIELD_PET_STATUS] == PJ_INCLUDE_ALWAYS) lit(s, ",\"status\":null}");
     else s.put_byte('}');
     if (P.format == PJ_FORMAT_NDJSON) s.put_byte('\n');
-    else if (i == P.n - 1) s.put_byte(']');
+    else if (i == P.last) s.put_byte(']');
 }
 
 __device__ __forceinline__ bool rec_has_urls(const RecVals &v) { return (v.fl & PJ_PET_HAS_PHOTOURLS) && v.u1 > v.u0; }
@@ -650,7 +650,7 @@ __device__ __forceinline__ void pp_sub(S &s, const EncParams &P, uint32_t fl, in
 template <class S> __device__ __forceinline__ void pp_rec(S &s, const EncParams &P, uint64_t i, const RecVals &v) {
     const pj_pet_columns &c = P.c;
     const uint32_t fl = v.fl;
-    if (i == 0) lit(s, "[ ");
+    if (i == P.first) lit(s, "[ ");
     else lit(s, ", ");
     bool first = true;
     s.put_byte('{');
@@ -697,7 +697,7 @@ template <class S> __device__ __forceinline__ void pp_rec(S &s, const EncParams 
         else lit(s, "\"status\" : \"sold\"");
     } else if (P.incl[PJ_FIELD_PET_STATUS] == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 2); lit(s, "\"status\" : null"); }
     pp_close(s, first, 0);
-    if (i == P.n - 1) lit(s, " ]");
+    if (i == P.last) lit(s, " ]");
 }
 
 // ---------------------------------------------------- large records, cooperatively
@@ -946,9 +946,12 @@ __device__ __forceinline__ uint64_t bounds_l1(const EncParams &P, uint64_t nb, u
                                  : (NESTED && c.cat_id ? c.cat_name_off : nullptr);
     return o ? o[r] : 0;
 }
-template <bool NESTED>
-__device__ __forceinline__ uint64_t bounds_l2(const EncParams &P, uint64_t v1, uint32_t l) {
-    if (!NESTED || l >= 4) return 0;
+// (A ticket past the last block loads nothing: its first-level words are 0,
+// and index 0 of the offset columns need not exist, as with the shifted
+// columns of a streamed host encode's segments.)
+template <bool NESTED, int R>
+__device__ __forceinline__ uint64_t bounds_l2(const EncParams &P, uint64_t nb, uint64_t v1, uint32_t l) {
+    if (!NESTED || l >= 4 || nb >= (P.n + R - 1) / R) return 0;
     const uint64_t *o = l < 2 ? (P.c.photo_off ? P.c.url_off : nullptr) : (P.c.tag_off ? P.c.tag_name_off : nullptr);
     return o ? o[v1] : 0;
 }
@@ -973,7 +976,7 @@ __device__ __forceinline__ void claim_next(const EncParams &P, uint64_t *nx, uin
     if (l == 0) tk = atomicAdd(P.ticket, 1ull);
     const uint64_t n1 = (uint64_t)__shfl((long long)tk, 0);
     const uint64_t v1 = bounds_l1<NESTED, R>(P, n1, l);
-    bounds_store(nx, v1, bounds_l2<NESTED>(P, v1, l), l);
+    bounds_store(nx, v1, bounds_l2<NESTED, R>(P, n1, v1, l), l);
     if (l == 0) *nb = n1;
 }
 
@@ -1134,7 +1137,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             if (t < (uint32_t)GEO_WORDS && b0 < nblk) sh_nx[t] = P.geo[GEO_WORDS * b0 + t];
         } else {
             const uint64_t v1 = bounds_l1<NESTED, R>(P, b0, t);
-            bounds_store(sh_nx, v1, bounds_l2<NESTED>(P, v1, t), t);
+            bounds_store(sh_nx, v1, bounds_l2<NESTED, R>(P, b0, v1, t), t);
         }
         if (t == 0) {
             sh_nb = b0;

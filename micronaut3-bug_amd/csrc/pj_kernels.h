@@ -7,6 +7,8 @@
 struct EncParams {
     pj_pet_columns c;          // device column pointers
     uint64_t n;                // records
+    uint64_t first, last;      // the local index of the input's first / last record (array
+                               // framing), or ~0 when a segment of the input holds none
     int format;                // pj_format
     uint8_t incl[PJ_FIELD_COUNT];  // pj_inclusion of each optional property (pj_field)
     uint32_t hexa;             // 'A' or 'a': first letter of hex escapes

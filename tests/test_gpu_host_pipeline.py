@@ -197,3 +197,69 @@ def test_host_array_document_streamed_in_segments(segment):
                PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"), os.path.join(ROOT, "tests")]))
     r = subprocess.run([sys.executable, "-c", ARRAY_STREAM], capture_output=True, text=True, env=env, timeout=240)
     assert r.returncode == 0 and "streamed array ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
+
+
+ENC_STREAM = r"""
+import ctypes as C
+import numpy as np
+import petjson as pj, oracle_py as orc
+from model import from_columns, to_columns
+codec = pj.Codec(0)
+cases = [(1, 20000), (2, 40000), (3, 30000), (5, 4000)]
+# a large record at a segment's first and last record
+pets = from_columns(pj.generate(3, 3000), as_bytes=True)
+for i in (0, 1499, 1500, 2999):
+    pets[i].name = b"\x01\\\"" * 700
+for cfg, n in cases + [(0, 0)]:
+    cols = pj.generate(cfg, n) if cfg else to_columns(pets)
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        want = orc.encode(cols, fmt)
+        got = codec.encode_host(cols, fmt)
+        assert got == want, (cfg, fmt, len(got), len(want))
+        # capacity cut: the bytes before it may be written, none after it
+        for cap in (len(want) - 1, len(want) // 2, 0):
+            out = np.full(len(want) + 16, 0xEE, np.uint8)
+            s, nn = cols.struct(), C.c_uint64(0)
+            rc = codec.L.pj_encode_host(codec.ctx, C.byref(s), fmt, C.c_void_p(out.ctypes.data), cap, C.byref(nn))
+            assert rc == pj.PJ_ERR_CAPACITY and nn.value == len(want), (cfg, fmt, cap, rc, nn.value)
+            assert (out[cap:] == 0xEE).all(), (cfg, fmt, cap)
+            w = out[:cap] != 0xEE
+            ref = np.frombuffer(want, np.uint8)[:cap]
+            assert (out[:cap][w] == ref[w]).all(), (cfg, fmt, cap)
+    # pinned columns and output (pj_host_alloc): DMA with no bounce copy
+    pc = pj.Columns(cols.n_pets, {}, dict(cols.caps))
+    for k, v in cols.arrays.items():
+        if v is None:
+            pc.arrays[k] = None
+            continue
+        a = pj.host_array(len(v), v.dtype)
+        a[:] = v
+        pc.arrays[k] = a
+    want = orc.encode(cols, pj.FORMAT_ARRAY)
+    out = pj.host_array(len(want) + 64, np.uint8)
+    s, nn = pc.struct(), C.c_uint64(0)
+    rc = codec.L.pj_encode_host(codec.ctx, C.byref(s), pj.FORMAT_ARRAY, C.c_void_p(out.ctypes.data), out.size, C.byref(nn))
+    assert rc == pj.PJ_OK and out[: nn.value].tobytes() == want, (cfg, rc)
+codec.close()
+print("streamed encode ok")
+"""
+
+
+@pytest.mark.parametrize("segment,chunk", [(99_991, 0), (1_000_003, 65537), (0, 0)])
+def test_host_encode_streamed_in_segments(segment, chunk):
+    """pj_encode_host on columns over PETJSON_ENCODE_SEGMENT bytes encodes
+    them in segments of records, each copied in while the one before it
+    encodes and out while the one after it encodes: the bytes equal the
+    oracle's in both framings (the array's brackets and separators across
+    segment boundaries, large escape-heavy records at a segment's first and
+    last record), a capacity cut writes nothing past it and reports the
+    size needed, and pinned columns and output give the same bytes.
+    segment 0: the default size, so these inputs take the one-shot path."""
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"),
+                                                      os.path.join(ROOT, "tests")]))
+    if segment:
+        env["PETJSON_ENCODE_SEGMENT"] = str(segment)
+    if chunk:
+        env["PETJSON_XFER_CHUNK"] = str(chunk)
+    r = subprocess.run([sys.executable, "-c", ENC_STREAM], capture_output=True, text=True, env=env, timeout=240)
+    assert r.returncode == 0 and "streamed encode ok" in r.stdout, r.stdout[-2000:] + r.stderr[-3000:]
