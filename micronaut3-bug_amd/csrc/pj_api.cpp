@@ -683,8 +683,10 @@ pj_status stage_pet_cols(pj_ctx *ctx, const pj_pet_columns *cols, pj_pet_columns
     return PJ_OK;
 }
 // ---- streamed host encode
-// pj_encode_host of an input over twice PETJSON_ENCODE_SEGMENT bytes of
-// columns (256 MiB by default; compact formats) runs in segments of records.
+// pj_encode_host of an input over 512 MiB of columns (compact formats) runs
+// in segments of records of about 256 MiB (PETJSON_ENCODE_SEGMENT sets the
+// size, and then anything over it streams; on the 0.35 GB flat benchmark
+// input, segments of 44 MB measured slower than one piece).
 // While segment k encodes on the context stream, a host thread copies
 // segment k + 1's column slices in (engine xin), and segment k - 1's bytes go
 // out (engine xout) to the caller's buffer at the running offset; PCIe is
@@ -699,6 +701,10 @@ uint64_t enc_segment_bytes() {
         if (v) return v;
     }
     return 256ull << 20;
+}
+uint64_t enc_stream_above() {
+    if (std::getenv("PETJSON_ENCODE_SEGMENT")) return enc_segment_bytes();
+    return 2 * enc_segment_bytes();
 }
 
 // The column slices of records [r0, r1): per column (col_ptrs order) its
@@ -765,7 +771,8 @@ pj_status encode_host_stream(pj_ctx *ctx, const pj_pet_columns *cols, int format
     const uint64_t n = cols->n_pets;
     Layout L;
     host_layout(cols, &L);
-    const uint64_t nseg = std::max<uint64_t>(2, (L.total + enc_segment_bytes() - 1) / enc_segment_bytes());
+    const uint64_t seg = enc_segment_bytes();
+    const uint64_t nseg = std::max<uint64_t>(2, (L.total + seg - 1) / seg);
     const uint64_t S = (n + nseg - 1) / nseg;
     // buffers sized once for the largest segment: its slices, and its
     // output (pj_encode_bound of its records)
@@ -923,9 +930,7 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format, ui
         if (!format_ok(format)) return fail(PJ_ERR_INVALID_ARG, "bad format");
         Layout L;
         host_layout(cols, &L);
-        // (a segment size set in the environment streams anything above it)
-        const uint64_t above = std::getenv("PETJSON_ENCODE_SEGMENT") ? enc_segment_bytes() : 2 * enc_segment_bytes();
-        if (L.total > above) {
+        if (L.total > enc_stream_above()) {
             if (!out && out_cap) return fail(PJ_ERR_INVALID_ARG, "null output");
             return encode_host_stream(ctx, cols, format, out, out_cap, out_len);
         }

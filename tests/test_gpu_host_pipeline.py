@@ -254,7 +254,7 @@ def test_host_encode_streamed_in_segments(segment, chunk):
     segment boundaries, large escape-heavy records at a segment's first and
     last record), a capacity cut writes nothing past it and reports the
     size needed, and pinned columns and output give the same bytes.
-    segment 0: the default size, so these inputs take the one-shot path."""
+    segment 0: the default sizes, under which these inputs take the one-shot path."""
     env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(ROOT, "micronaut3-bug_amd"),
                                                       os.path.join(ROOT, "tests")]))
     if segment:
