@@ -1685,6 +1685,13 @@ extern "C" pj_status pj_decode_model_device(pj_ctx *ctx, int model, const uint8_
     M.bbase = M.bagg + nb * MD_MAXK;
     M.csum = M.bbase + nb * MD_MAXK;
     M.nblocks = nb;
+    // the counting pass's record tape (one word per property and one for the
+    // record), while it stays under 16 GiB
+    const uint64_t tw = lines * (1 + (uint64_t)model_props(model));
+    if (decode_tape_enabled() && lines && tw * 8 <= (16ull << 30)) {
+        PJ_HIP(ctx->tape.ensure(tw * 8));
+        M.tape = static_cast<uint64_t *>(ctx->tape.p);
+    }
     if ((s = mark(ctx))) return s;
     PJ_HIP(pj_launch_fill_u64(SB, MD_MAXK + 1, 0, ctx->stream));
     for (int k = 0; k < model_props(model); k++)    // string offsets start at 0

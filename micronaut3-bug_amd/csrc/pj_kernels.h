@@ -64,6 +64,8 @@ struct ModelDecParams {
     uint64_t *csum;            // [nchunks * MD_MAXK] chunk first offsets
     uint64_t *totals;          // [MD_MAXK + 1] sums (the last: blank records)
     uint64_t nblocks;
+    uint64_t *tape;            // what the counting pass read of each record, for the writer
+                               // (word k of record l at tape[k * lines + l]), or null
 };
 
 // What the decode counting kernels learn about each line, read back by the

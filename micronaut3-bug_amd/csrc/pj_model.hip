@@ -387,6 +387,7 @@ template <int MODEL> __device__ __forceinline__ int m_prop_of(const MOut &k) {
 // One record's values as read (the last occurrence of each property).
 struct MRec {
     uint32_t present;
+    uint32_t sesc;                       // string properties whose value holds an escape
     int64_t v[PJ_MODEL_MAX_PROPS];
     uint64_t spos[PJ_MODEL_MAX_PROPS];   // string properties: the value's opening quote
     uint64_t slen[PJ_MODEL_MAX_PROPS];   // decoded bytes
@@ -420,6 +421,9 @@ template <int MODEL, int F> __device__ __forceinline__ int m_value(MLine &L, MRe
             if (KIND == K_STR) {
                 R.spos[f] = q;
                 R.slen[f] = o.k;
+                // escapes shorten the value: its raw bytes then differ from its decoded ones
+                if (L.p - q - 2 != o.k) R.sesc |= 1u << f;
+                else R.sesc &= ~(1u << f);
             } else {
                 int hit = -1;
 #pragma unroll
@@ -460,6 +464,7 @@ template <int MODEL, int F = 0> __device__ __forceinline__ int m_value_of(MLine 
 template <int MODEL> __device__ __forceinline__ int m_line(const uint8_t *s, uint64_t n, MRec &R) {
     MLine L{s, n, 0};
     R.present = 0;
+    R.sesc = 0;
 #pragma unroll
     for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) {
         R.v[k] = 0;
@@ -566,6 +571,26 @@ __device__ __forceinline__ int m_read(const ModelDecParams &P, const MStage &S, 
     return code;
 }
 
+// The record tape: word 0 holds the record's code (bits 0-7), its present
+// bits (8-15) and bit 16 when the record is 4 GiB or longer (its positions
+// do not fit the tape: the writer reads it again); word 1 + k holds property
+// k: an integer, enum or boolean value, or for a string its opening quote's
+// offset in the record (bits 0-31), its decoded length (32-62) and bit 63
+// when it holds an escape.
+constexpr uint64_t MT_WIDE = 1ull << 16, MT_ESC = 1ull << 63;
+template <int MODEL>
+__device__ __forceinline__ void m_tape_put(const ModelDecParams &P, uint64_t l, int code, const MRec &R) {
+    const uint64_t L = P.lines;
+    const bool wide = P.line_start[l + 1] - 1 - P.line_start[l] >= (1ull << 32);
+    P.tape[l] = ((uint64_t)code & 0xFF) | ((uint64_t)(R.present & 0xFF) << 8) | (wide ? MT_WIDE : 0ull);
+    if (code != PJ_REC_OK || wide) return;
+#pragma unroll
+    for (int k = 0; k < MSchema<MODEL>::N; k++)
+        P.tape[(1 + k) * L + l] = MSchema<MODEL>::kind(k) == K_STR
+                                      ? R.spos[k] | (R.slen[k] << 32) | (((R.sesc >> k) & 1) ? MT_ESC : 0ull)
+                                      : (uint64_t)R.v[k];
+}
+
 template <int MODEL, int BT, int TILE>
 __global__ __launch_bounds__(BT) void k_mdec_count(ModelDecParams P) {
     __shared__ uint64_t sh[BT / 64 + 2];
@@ -575,6 +600,7 @@ __global__ __launch_bounds__(BT) void k_mdec_count(ModelDecParams P) {
     MRec R;
     uint64_t cnt[MD_MAXK];
     const int code = m_read<MODEL>(P, S, l, R, cnt);
+    if (P.tape && l < P.lines) m_tape_put<MODEL>(P, l, code, R);
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
@@ -637,7 +663,30 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
     const MStage S = m_stage<BT, TILE>(P, tile, b);
     MRec R;
     uint64_t cnt[MD_MAXK], at[MD_MAXK];
-    const int code = m_read<MODEL>(P, S, l, R, cnt);
+    // the counting pass's tape, where it has one: the record's code, values
+    // and string positions without reading it again
+    const uint64_t w0 = P.tape && l < P.lines ? P.tape[l] : MT_WIDE;
+    const bool taped = !(w0 & MT_WIDE);
+    int code;
+    if (taped) {
+        code = (int)(w0 & 0xFF);
+        R.present = (uint32_t)(w0 >> 8) & 0xFF;
+        R.sesc = 0;
+#pragma unroll
+        for (int k = 0; k < MD_MAXK; k++) cnt[k] = 0;
+        cnt[code == PJ_REC_OK ? 0 : 1] = 1;
+#pragma unroll
+        for (int k = 0; k < MSchema<MODEL>::N; k++) {
+            const uint64_t x = code == PJ_REC_OK ? P.tape[(1 + k) * P.lines + l] : 0;
+            R.v[k] = (int64_t)x;
+            if (MSchema<MODEL>::kind(k) == K_STR) {
+                R.spos[k] = x & 0xFFFFFFFFull;
+                R.slen[k] = (x >> 32) & 0x7FFFFFFFull;
+                R.sesc |= (x & MT_ESC) ? 1u << k : 0u;
+                cnt[2 + k] = R.slen[k];
+            }
+        }
+    } else code = m_read<MODEL>(P, S, l, R, cnt);
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
@@ -664,9 +713,21 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
             const uint64_t s0 = at[2 + k], s1 = s0 + R.slen[k];
             if (fits) static_cast<uint64_t *>(o.col[k])[row + 1] = s1;
             if (R.slen[k] && s1 <= o.cap_bytes[k]) {
-                MLine L{S.at(P, a), P.line_start[l + 1] - 1 - a, R.spos[k]};
                 MStore w(o.bytes[k] + s0);
-                (void)m_string(L, w);
+                if (taped && !((R.sesc >> k) & 1)) {
+                    // no escape: the raw bytes are the value
+                    const uint8_t *src = S.at(P, a + R.spos[k] + 1);
+                    const uint64_t n = R.slen[k];
+                    uint64_t j = 0;
+                    for (; j + 8 <= n; j += 8) w.put8(ldu64(src + j));
+                    if (j < n) {
+                        const uint64_t x = ld_tail(src + j, (int)(n - j));
+                        for (uint64_t q = 0; q < n - j; q++) w.put((uint32_t)(x >> (8 * q)));
+                    }
+                } else {
+                    MLine L{S.at(P, a), P.line_start[l + 1] - 1 - a, R.spos[k]};
+                    (void)m_string(L, w);
+                }
                 w.finish();
             }
         } else if (fits) {

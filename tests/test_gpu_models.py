@@ -173,3 +173,33 @@ def test_model_host_entry_points_match_oracle(codec, model):
     with pytest.raises(pj.PetJsonError) as ei:
         codec.decode_model_host(model, data, caps=(cap_n, cap_b))
     assert ei.value.status == pj.PJ_ERR_CAPACITY
+
+
+@pytest.mark.parametrize("tape", ["1", "0"])
+def test_model_decode_tape_and_reparse_match_oracle(codec, monkeypatch, tape):
+    """The writing pass takes each record's code, values and string positions
+    from the counting pass's tape, copying escape-free strings raw and
+    decoding the others again; with PETJSON_DECODE_TAPE=0 it reads every
+    record again.  Both against the oracle: duplicate properties whose last
+    occurrence has or lacks escapes, escapes of every kind, multi-byte UTF-8
+    and mutated lines."""
+    monkeypatch.setenv("PETJSON_DECODE_TAPE", tape)
+    user = [b'{"username":"a\\nb","username":"plain","id":1}',
+            b'{"username":"plain","username":"a\\u00e9b\\"c\\\\d\\/e","id":2}',
+            b'{"email":"x\\/y","phone":"\\ud83d\\ude00 \xc3\xa9\xe2\x82\xac","password":"p\\tq\\r\\b\\f"}',
+            b'{"firstName":"' + b"z" * 300 + b'\\n","lastName":"' + b"y" * 301 + b'","userStatus":-2147483648}',
+            b'{"username":null,"username":"back","email":"e","email":null}']
+    rnd = random.Random(5)
+    cols = pj.generate_model(pj.MODEL_USER, 2000, seed=9, null_rate=0.2)
+    base = orc.encode_model(cols, pj.FORMAT_NDJSON, pj.INCLUDE_ALWAYS).split(b"\n")[:-1]
+    user += [_mutate(rnd, rnd.choice(base)) if i % 3 else rnd.choice(base) for i in range(6000)]
+    same_decode(codec, pj.MODEL_USER, b"\n".join(user))
+    order = [b'{"shipDate":"2024-01-01T00:00:00Z","shipDate":"2024\\u002d02","status":"placed"}',
+             b'{"shipDate":"a\\"b","shipDate":"plain","complete":true,"quantity":7}']
+    cols = pj.generate_model(pj.MODEL_ORDER, 2000, seed=8, null_rate=0.2)
+    base = orc.encode_model(cols, pj.FORMAT_NDJSON, pj.INCLUDE_ALWAYS).split(b"\n")[:-1]
+    order += [_mutate(rnd, rnd.choice(base)) if i % 3 else rnd.choice(base) for i in range(6000)]
+    same_decode(codec, pj.MODEL_ORDER, b"\n".join(order))
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_PRETTY):
+        data = orc.encode_model(cols, fmt, pj.INCLUDE_ALWAYS)
+        same_decode(codec, pj.MODEL_ORDER, data, array=True)
