@@ -453,4 +453,69 @@ struct WriteSink {
     }
 };
 
+// Global writes of a byte stream that starts at any address, one whole
+// aligned 32-byte sector at a time: bytes gather in a window of four qwords
+// that describes one aligned sector of the output, and a full window leaves
+// as two aligned 16-byte stores, so memory sees each sector written once
+// and whole (8-byte stores at any address cost a partial sector write each
+// when their line leaves L2 before it fills).  The first sector, shared
+// with the previous writer, and the last get exact stores of this writer's
+// bytes only, so neighbouring writers need no coordination.  Nothing is read.
+struct SectorSink {
+    uint8_t *sec;                 // the window's sector (32-byte aligned)
+    uint64_t w0, w1, w2, w3;
+    uint32_t o;                   // the window's next byte
+    uint32_t lo;                  // the window's first byte of this writer
+
+    __host__ __device__ __forceinline__ void init(uint8_t *p) {
+        sec = reinterpret_cast<uint8_t *>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)31);
+        o = lo = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 31);
+        w0 = w1 = w2 = w3 = 0;
+    }
+    // bytes [a, b) of the window, exactly
+    __host__ __device__ __forceinline__ void store_part(uint32_t a, uint32_t b) const {
+        const uint64_t w[4] = {w0, w1, w2, w3};
+#pragma unroll
+        for (uint32_t q = 0; q < 4; q++) {
+            const uint32_t qa = a > 8 * q ? a : 8 * q, qb = b < 8 * q + 8 ? b : 8 * q + 8;
+            if (qa >= qb) continue;
+            if (qb - qa == 8) stu64(sec + 8 * q, w[q]);
+            else st_tail(sec + qa, w[q] >> (8 * (qa - 8 * q)), qb - qa);
+        }
+    }
+    __host__ __device__ __forceinline__ void flush() {
+        if (lo) store_part(lo, 32);
+        else {
+            *reinterpret_cast<uint4 *>(sec) = make_uint4((uint32_t)w0, (uint32_t)(w0 >> 32), (uint32_t)w1, (uint32_t)(w1 >> 32));
+            *reinterpret_cast<uint4 *>(sec + 16) =
+                make_uint4((uint32_t)w2, (uint32_t)(w2 >> 32), (uint32_t)w3, (uint32_t)(w3 >> 32));
+        }
+        sec += 32;
+        lo = 0;
+    }
+    __host__ __device__ __forceinline__ void put8(uint64_t x, int k) {   // k (1..8) bytes of x
+        if (k < 8) x &= (1ull << (8 * k)) - 1;
+        const uint32_t j = o >> 3, sh = 8 * (o & 7);
+        const uint64_t a = x << sh, c = sh ? x >> (64 - sh) : 0;     // c: the bytes past qword j
+        w0 |= j == 0 ? a : 0;
+        w1 |= j == 1 ? a : (j == 0 ? c : 0);
+        w2 |= j == 2 ? a : (j == 1 ? c : 0);
+        w3 |= j == 3 ? a : (j == 2 ? c : 0);
+        o += (uint32_t)k;
+        if (o >= 32) {                     // (then j == 3, and c holds the bytes past the window)
+            flush();
+            o -= 32;
+            w0 = c;
+            w1 = w2 = w3 = 0;
+        }
+    }
+    __host__ __device__ __forceinline__ void put(uint32_t w, int k) { put8(w, k); }
+    __host__ __device__ __forceinline__ void put_byte(uint32_t b) { put8(b & 0xFF, 1); }
+    __host__ __device__ __forceinline__ void skip(uint32_t) {}
+    __host__ __device__ __forceinline__ uint32_t pos() const { return 0; }
+    __host__ __device__ __forceinline__ void finish() {
+        if (o > lo) store_part(lo, o);
+    }
+};
+
 }  // namespace pj

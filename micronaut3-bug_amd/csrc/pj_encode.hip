@@ -1728,7 +1728,8 @@ __global__ __launch_bounds__(BT) void k_encode_rows(EncParams P) {
     if (P.count_only || !live) return;
     const uint64_t at = sh_base + pre;
     if (at + cs.n > P.cap) return;
-    XSink xs{P.out + at, 0, 0};
+    SectorSink xs;
+    xs.init(P.out + at);
     if (PRETTY) pp_rec(xs, P, j, v);
     else emit_rec<true, true>(xs, P, XG, j, v, ri);
     xs.finish();
@@ -1910,7 +1911,8 @@ __global__ __launch_bounds__(BT) void k_encode_model(ModelEncParams P) {
     if (P.count_only || !live) return;
     const uint64_t at = sh_base + pre;
     if (at + cs.n > P.cap) return;
-    XSink xs{P.out + at, 0, 0};
+    SectorSink xs;
+    xs.init(P.out + at);
     m_rec<MODEL>(xs, P, i);
     xs.finish();
 }

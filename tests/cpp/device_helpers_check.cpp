@@ -178,6 +178,37 @@ static void check_write_sink() {
     }
 }
 
+// SectorSink: a record's bytes at any offset of a 32-byte aligned output,
+// in pieces of 1 to 8 bytes; the result equals the bytes, the buffer holds
+// exactly the sectors the record touches, and no byte outside [p, p + n)
+// changes.
+static void check_sector_sink() {
+    for (int it = 0; it < 40000; it++) {
+        const uint32_t n = (uint32_t)(it < 300 ? it % 100 : rng() % 700), p = (uint32_t)(rng() % 96);
+        std::vector<uint8_t> want(n);
+        for (auto &b : want) b = rbyte();
+        const uint32_t total = (p + n + 31) / 32 * 32 + 32;   // the sectors the record touches (and one more)
+        uint8_t *out = static_cast<uint8_t *>(std::aligned_alloc(32, total));
+        std::memset(out, 0xEE, total);
+        SectorSink s;
+        s.init(out + p);
+        uint32_t k = 0;
+        while (k < n) {
+            const uint32_t m = std::min<uint32_t>(n - k, 1 + (uint32_t)(rng() % 8));
+            uint64_t v = rng();                               // bytes past m must be ignored
+            std::memcpy(&v, want.data() + k, m);
+            if (m <= 4 && (rng() & 1)) s.put((uint32_t)v, (int)m);
+            else s.put8(v, (int)m);
+            k += m;
+        }
+        s.finish();
+        CHECK(n == 0 || std::memcmp(out + p, want.data(), n) == 0);
+        for (uint32_t j = 0; j < p; j++) CHECK(out[j] == 0xEE);
+        for (uint32_t j = p + n; j < total; j++) CHECK(out[j] == 0xEE);
+        std::free(out);
+    }
+}
+
 int main() {
     check_ld_tail();
     check_copy_from_lds();
@@ -186,6 +217,7 @@ int main() {
     check_tile_copy_out<192>();
     check_store_sink();
     check_write_sink();
+    check_sector_sink();
     std::printf("device helpers: all checks passed\n");
     return 0;
 }
