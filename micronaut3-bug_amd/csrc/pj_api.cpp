@@ -201,13 +201,27 @@ bool pinned_host(const void *p, size_t n) {
 // the context stream also waits for it before its next work; a second host
 // thread copying while the context stream runs passes false, so that the
 // work the main thread is queueing meanwhile does not wait for its copy.
-pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n, bool order_stream = true) {
+// With wait false a copy from pinned memory is only queued: h2d_wait then
+// waits for every copy queued so far, so that the slices of a column set
+// cost one wait, not one each.
+pj_status h2d_wait(pj_ctx *c, bool order_stream = true) {
+    Xfer &x = c->xin;
+    pj_status s = xfer_init(x);
+    if (s) return s;
+    PJ_HIP(hipEventRecord(x.done, x.s));
+    if (order_stream) PJ_HIP(hipStreamWaitEvent(c->stream, x.done, 0));
+    PJ_HIP(hipEventSynchronize(x.done));
+    return PJ_OK;
+}
+pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n, bool order_stream = true, bool wait = true) {
     if (!n) return PJ_OK;
     Xfer &x = c->xin;
     pj_status s = xfer_init(x);
     if (s) return s;
-    if (pinned_host(host, n)) PJ_HIP(hipMemcpyAsync(dev, host, n, hipMemcpyHostToDevice, x.s));
-    else for (size_t off = 0, i = 0; off < n; off += x.chunk, i++) {
+    if (pinned_host(host, n)) {
+        PJ_HIP(hipMemcpyAsync(dev, host, n, hipMemcpyHostToDevice, x.s));
+        if (!wait) return PJ_OK;
+    } else for (size_t off = 0, i = 0; off < n; off += x.chunk, i++) {
         const size_t k = std::min(x.chunk, n - off);
         const int b = (int)(i & 1);
         if (i >= 2) PJ_HIP(hipEventSynchronize(x.bev[b]));      // the DMA that last read this buffer is done
@@ -677,8 +691,9 @@ pj_status stage_pet_cols(pj_ctx *ctx, const pj_pet_columns *cols, pj_pet_columns
     col_ptrs(&hc, hp);
     for (int k = 0; k < 17; k++) {
         dp[k] = hp[k] ? base + L.off[k] : nullptr;
-        if (hp[k] && L.size[k] && (s = h2d(ctx, dp[k], hp[k], L.size[k]))) return s;
+        if (hp[k] && L.size[k] && (s = h2d(ctx, dp[k], hp[k], L.size[k], true, false))) return s;
     }
+    if ((s = h2d_wait(ctx))) return s;
     set_col_ptrs(dc, dp);
     return PJ_OK;
 }
@@ -823,10 +838,11 @@ pj_status encode_host_stream(pj_ctx *ctx, const pj_pet_columns *cols, int format
         uint8_t *D = static_cast<uint8_t *>(ctx->seg_in[k].p);
         for (int j = 0; j < 17; j++) {
             if (!E.size[j]) continue;
-            const pj_status r = h2d(ctx, D + E.off[j], static_cast<const uint8_t *>(hp[j]) + E.src[j], E.size[j], false);
+            const pj_status r =
+                h2d(ctx, D + E.off[j], static_cast<const uint8_t *>(hp[j]) + E.src[j], E.size[j], false, false);
             if (r) return r;
         }
-        return PJ_OK;
+        return h2d_wait(ctx, false);
     };
     pj_status s = load(0, 0, std::min(n, S));
     if (s) return s;
@@ -1771,16 +1787,17 @@ extern "C" pj_status pj_encode_model_host(pj_ctx *ctx, int model, const pj_model
     uint8_t *base = static_cast<uint8_t *>(ctx->stage_in.p);
     if (cols->present) {
         dc.present = base + o_present;
-        if ((s = h2d(ctx, dc.present, cols->present, n))) return s;
+        if ((s = h2d(ctx, dc.present, cols->present, n, true, false))) return s;
     }
     for (int k = 0; n && k < model_props(model); k++) {
         dc.col[k] = base + o_col[k];
-        if ((s = h2d(ctx, dc.col[k], cols->col[k], model_col_bytes(model, k, n)))) return s;
+        if ((s = h2d(ctx, dc.col[k], cols->col[k], model_col_bytes(model, k, n), true, false))) return s;
         if (model_str(model, k)) {
             dc.bytes[k] = base + o_bytes[k];
-            if ((s = h2d(ctx, dc.bytes[k], cols->bytes[k], nbytes[k]))) return s;
+            if ((s = h2d(ctx, dc.bytes[k], cols->bytes[k], nbytes[k], true, false))) return s;
         }
     }
+    if ((s = h2d_wait(ctx))) return s;
     uint64_t need = 0;
     s = pj_encode_model_device(ctx, model, &dc, format, nullptr, 0, &need);
     if (s != PJ_OK && s != PJ_ERR_CAPACITY) return s;
