@@ -238,7 +238,17 @@ pj_status h2d(pj_ctx *c, void *dev, const void *host, size_t n, bool order_strea
 
 // Device -> host, after the work the event `after` marks (by default the
 // context stream's work so far); returns when the bytes are in host memory.
-pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n, hipEvent_t after = nullptr) {
+// With wait false a copy into pinned memory is only queued: d2h_wait then
+// waits for every copy queued so far.
+pj_status d2h_wait(pj_ctx *c) {
+    Xfer &x = c->xout;
+    pj_status s = xfer_init(x);
+    if (s) return s;
+    PJ_HIP(hipEventRecord(x.bev[0], x.s));
+    PJ_HIP(hipEventSynchronize(x.bev[0]));
+    return PJ_OK;
+}
+pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n, hipEvent_t after = nullptr, bool wait = true) {
     if (!n) return PJ_OK;
     Xfer &x = c->xout;
     pj_status s = xfer_init(x);
@@ -250,9 +260,7 @@ pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n, hipEvent_t after
     PJ_HIP(hipStreamWaitEvent(x.s, after, 0));
     if (pinned_host(host, n)) {
         PJ_HIP(hipMemcpyAsync(host, dev, n, hipMemcpyDeviceToHost, x.s));
-        PJ_HIP(hipEventRecord(x.bev[0], x.s));
-        PJ_HIP(hipEventSynchronize(x.bev[0]));
-        return PJ_OK;
+        return wait ? d2h_wait(c) : PJ_OK;
     }
     const size_t chunks = (n + x.chunk - 1) / x.chunk;
     auto issue = [&](size_t i) -> pj_status {
@@ -1523,7 +1531,8 @@ pj_status decode_host_stream(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pe
             cout.th = std::thread([&, pieces, ready] {
                 pj_status q = bind(ctx);
                 for (size_t j = 0; !q && j < pieces.size(); j++)
-                    q = d2h(ctx, pieces[j].dst, pieces[j].src, pieces[j].n, ready);
+                    q = d2h(ctx, pieces[j].dst, pieces[j].src, pieces[j].n, ready, false);
+                if (!q) q = d2h_wait(ctx);
                 if (q) cout.err = pj_last_error();
                 cout.st = q;
             });
@@ -1592,9 +1601,11 @@ pj_status decode_host_impl(pj_ctx *ctx, const uint8_t *in, uint64_t len, pj_pet_
     col_ptrs(out, hp);
     pj_status t = PJ_OK;
     for (int k = 0; k < 17; k++)
-        if (used[k] && (t = d2h(ctx, hp[k], dp[k], used[k]))) return t;
+        if (used[k] && (t = d2h(ctx, hp[k], dp[k], used[k], nullptr, false))) return t;
     const uint64_t ne = std::min(res->n_errors, err_cap);
-    if (ne && ((t = d2h(ctx, err_line, del, ne * 8)) || (t = d2h(ctx, err_code, dec, ne)))) return t;
+    if (ne && ((t = d2h(ctx, err_line, del, ne * 8, nullptr, false)) || (t = d2h(ctx, err_code, dec, ne, nullptr, false))))
+        return t;
+    if ((t = d2h_wait(ctx))) return t;
     out->n_pets = np;
     return s;
 }
@@ -1860,15 +1871,17 @@ extern "C" pj_status pj_decode_model_host(pj_ctx *ctx, int model, const uint8_t 
     out->n = rows;
     for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) out->n_bytes[k] = dc.n_bytes[k];
     pj_status t;
-    if ((t = d2h(ctx, out->present, dc.present, rows))) return t;
+    if ((t = d2h(ctx, out->present, dc.present, rows, nullptr, false))) return t;
     for (int k = 0; k < model_props(model); k++) {
         if (model_str(model, k)) {
-            if ((t = d2h(ctx, out->col[k], dc.col[k], (rows + 1) * 8))) return t;
+            if ((t = d2h(ctx, out->col[k], dc.col[k], (rows + 1) * 8, nullptr, false))) return t;
             const uint64_t nb = std::min(dc.n_bytes[k], out->cap_bytes[k]);
-            if ((t = d2h(ctx, out->bytes[k], dc.bytes[k], nb))) return t;
-        } else if ((t = d2h(ctx, out->col[k], dc.col[k], model_col_bytes(model, k, rows)))) return t;
+            if ((t = d2h(ctx, out->bytes[k], dc.bytes[k], nb, nullptr, false))) return t;
+        } else if ((t = d2h(ctx, out->col[k], dc.col[k], model_col_bytes(model, k, rows), nullptr, false))) return t;
     }
     const uint64_t ne = std::min(res->n_errors, err_cap);
-    if (ne && ((t = d2h(ctx, err_line, del, ne * 8)) || (t = d2h(ctx, err_code, dec, ne)))) return t;
+    if (ne && ((t = d2h(ctx, err_line, del, ne * 8, nullptr, false)) || (t = d2h(ctx, err_code, dec, ne, nullptr, false))))
+        return t;
+    if ((t = d2h_wait(ctx))) return t;
     return ds == PJ_OK ? PJ_OK : fail(PJ_ERR_CAPACITY, "capacity too small (sizes needed are in the result)");
 }
