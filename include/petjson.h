@@ -247,7 +247,7 @@ pj_status pj_encode_host(pj_ctx *ctx, const pj_pet_columns *cols, int format,
  * per-GPU host lock held until the call's stream has drained. */
 #define PJ_NOALLOC_SCRATCH_WORDS (1u << 20)
 #define PJ_NOALLOC_MAX_RECORDS(nested) \
-    ((uint64_t)(PJ_NOALLOC_SCRATCH_WORDS - 131) * ((nested) ? 96u : 256u))
+    ((uint64_t)(PJ_NOALLOC_SCRATCH_WORDS - 132) * ((nested) ? 96u : 256u))
 pj_status pj_encode_device_noalloc(pj_ctx *ctx, const pj_pet_columns *cols, int format,
                                    uint8_t *out, uint64_t out_cap, uint64_t *out_len);
 

@@ -281,6 +281,10 @@ pj_status d2h(pj_ctx *c, void *host, const void *dev, size_t n, hipEvent_t after
 }
 
 bool nested_cols(const pj_pet_columns *c) { return c->cat_id || c->photo_off || c->tag_off; }
+uint64_t enc_big_cap() {
+    if (const char *e = std::getenv("PETJSON_ENC_BIG_CAP")) return std::strtoull(e, nullptr, 10);
+    return 1ull << 20;
+}
 // PETJSON_ENC_TWO_PASS=1 writes nested records at the offsets of the
 // measuring pass instead of with the single pass (kept to compare the two).
 bool enc_two_pass() {
@@ -378,10 +382,16 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     // writer at the given offsets (PETJSON_ENC_TWO_PASS=1).  The fixed
     // scratch of the no-allocation entry point holds only the single pass.
     const bool two_pass = !pretty && nested_cols(cols) && !fixed_scratch && !seg && (count_only || enc_two_pass());
+    // Nested records too large for the tile path (long names or lists) are
+    // written after the pass by k_enc_big, up to 2^20 of them per call (the
+    // rest by the pass itself; PETJSON_ENC_BIG_CAP sets another limit, 0 for
+    // none); the fixed scratch holds no such list.
+    const bool defer_big = nested_cols(cols) && !pretty && !count_only && !fixed_scratch;
+    const uint64_t big_cap = defer_big ? std::min<uint64_t>(n, enc_big_cap()) : 0;
     uint64_t *sc;
     std::unique_lock<std::mutex> noalloc_guard;
     if (fixed_scratch) {
-        if (n > PJ_NOALLOC_MAX_RECORDS(nested_cols(cols)) || nblk + 3 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
+        if (n > PJ_NOALLOC_MAX_RECORDS(nested_cols(cols)) || nblk + 4 + 128 > PJ_NOALLOC_SCRATCH_WORDS)
             return fail(PJ_ERR_INVALID_ARG, "pj_encode_device_noalloc: " + std::to_string(n) +
                                                 " records exceed the fixed scratch (at most " +
                                                 std::to_string(PJ_NOALLOC_MAX_RECORDS(nested_cols(cols))) + ")");
@@ -390,7 +400,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
         // its stream has drained (the lock is released when this returns)
         noalloc_guard = std::unique_lock<std::mutex>(pj::noalloc_lock(ctx->device));
     } else {
-        PJ_HIP(ctx->scan.ensure((nblk + 3 + 128 + (two_pass ? GEO_WORDS * nblk : 0)) * sizeof(uint64_t)));
+        PJ_HIP(ctx->scan.ensure((nblk + 4 + 128 + (two_pass ? GEO_WORDS * nblk : 0) + 2 * big_cap) * sizeof(uint64_t)));
         sc = static_cast<uint64_t *>(ctx->scan.p);
     }
     EncParams P;
@@ -404,13 +414,18 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.count_only = count_only ? 1 : 0;
     P.out = out;
     P.cap = count_only ? 0 : cap;
-    // scan buffer: ticket, total, fallback-block count, look-back words, dummy
+    // scan buffer: ticket, total, fallback-block count, large-record count,
+    // look-back words (these zeroed before each pass), dummy, block
+    // geometry (two passes), large-record list
     P.ticket = reinterpret_cast<unsigned long long *>(sc);
     P.total = sc + 1;
     P.nfall = reinterpret_cast<unsigned long long *>(sc + 2);
-    P.state = sc + 3;
-    P.dummy = reinterpret_cast<uint32_t *>(sc + 3 + nblk);   // 128 u64 = PJ_BLOCK dwords
-    uint64_t *geo = two_pass ? sc + 3 + nblk + 128 : nullptr;
+    P.big_count = reinterpret_cast<unsigned long long *>(sc + 3);
+    P.state = sc + 4;
+    P.dummy = reinterpret_cast<uint32_t *>(sc + 4 + nblk);   // 128 u64 = PJ_BLOCK dwords
+    uint64_t *geo = two_pass ? sc + 4 + nblk + 128 : nullptr;
+    P.big_list = sc + 4 + nblk + 128 + (two_pass ? GEO_WORDS * nblk : 0);
+    P.big_cap = big_cap;
     // Nested records run on persistent workgroups that claim their blocks by
     // ticket.  Flat blocks run one per workgroup in launch order (no ticket
     // atomic on the critical path) with bounded look-back waits: should a
@@ -420,7 +435,7 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
     P.spin_limit = spin_limit();
     for (int attempt = 0;; attempt++) {
         if ((s = mark(ctx))) return s;
-        PJ_HIP(pj_launch_fill_u64(sc, nblk + 3, 0, ctx->stream));
+        PJ_HIP(pj_launch_fill_u64(sc, nblk + 4, 0, ctx->stream));
         if ((s = mark(ctx))) return s;
         if (pretty) PJ_HIP(pj_launch_encode_rows(P, true, ctx->stream));
         else if (two_pass) {
@@ -431,8 +446,12 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
                 PJ_HIP(pj_launch_fill_u64(sc, 1, 0, ctx->stream));   // the writer's tickets
                 P.geo = geo;
                 PJ_HIP(pj_launch_encode(P, true, false, ctx->stream));
+                if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->stream));
             }
-        } else PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
+        } else {
+            PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
+            if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->stream));
+        }
         if ((s = mark(ctx))) return s;
         if (seg) {
             PJ_HIP(hipMemcpyAsync(seg->len, sc + 1, sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));

@@ -843,6 +843,52 @@ __device__ __forceinline__ uint64_t coop_rec(const EncParams &P, uint8_t *out, u
     return pos;
 }
 
+// The length of one large record, by the whole workgroup in one pass (every
+// thread gets it): the fixed pieces by thread 0, the name's escapes 16 bytes
+// per thread per round (all loads of a round issued before any is used), an
+// item per thread per round, and one block sum.  coop_rec's measuring mode
+// gives the same length with a scan per piece.
+template <bool NESTED, int BT>
+__device__ __forceinline__ uint64_t big_len(const EncParams &P, uint64_t i, const RecVals &v, uint64_t *sh) {
+    const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
+    const uint32_t t = threadIdx.x;
+    const bool has_name = (v.fl & PJ_PET_HAS_NAME) != 0;
+    uint64_t n = 0;
+    if (t == 0) {
+        CountSink cs;
+        rec_head<NESTED>(cs, P, XG, i, v);
+        rec_urls_open(cs, v);
+        rec_tags_open<NESTED>(cs, P, v);
+        rec_tail(cs, P, i, v);
+        n = cs.n + (has_name ? 2 : 0);
+    }
+    const uint64_t nl = has_name ? v.nb - v.na : 0;
+    const uint8_t *np = P.c.name_bytes + v.na;
+    for (uint64_t k = 16ull * t; k < nl; k += 16ull * BT) {
+        const uint32_t m = (uint32_t)min((uint64_t)16, nl - k);
+        const uint32_t m0 = min(m, 8u), m1 = m > 8 ? m - 8 : 0u;
+        const uint64_t x0 = m0 == 8 ? ldu64(np + k) : ld_tail(np + k, (int)m0);
+        const uint64_t x1 = m1 == 8 ? ldu64(np + k + 8) : m1 ? ld_tail(np + k + 8, (int)m1) : 0ull;
+        n += m + esc_extra(x0, m0 >= 8 ? ~0ull : ((1ull << (8 * m0)) - 1)) +
+             (m1 ? esc_extra(x1, m1 >= 8 ? ~0ull : ((1ull << (8 * m1)) - 1)) : 0u);
+    }
+    if (rec_has_urls(v))
+        for (uint64_t u = v.u0 + t; u < v.u1; u += BT) {
+            CountSink cs;
+            emit_url_v(cs, P, XG, load_url(P, u), u + 1 == v.u1);
+            n += cs.n;
+        }
+    if (rec_has_tags<NESTED>(v))
+        for (uint64_t g = v.t0 + t; g < v.t1; g += BT) {
+            CountSink cs;
+            emit_tag_v(cs, P, XG, load_tag(P, g), g + 1 == v.t1);
+            n += cs.n;
+        }
+    uint64_t tot;
+    block_excl_scan<BT>(n, sh, &tot);
+    return tot;
+}
+
 // A record handled cooperatively when its workgroup is on the fallback
 // path: a long name or a long list.
 #ifndef PJ_ENC_BIG_STR
@@ -871,6 +917,183 @@ __device__ __forceinline__ void lds_excl_scan(uint32_t *a, uint32_t n, uint64_t 
     }
     if (t == 0) a[n] = (uint32_t)tot;
     __syncthreads();
+}
+
+// ------------------------------------------------- large records, deferred
+// A nested pass lists each large record it has placed (record, output
+// offset) for k_enc_big, while the list has room: thread k takes a slot for
+// the block's large record k and marks it BIG_LISTED in big[k] (a record
+// index below 2^31 otherwise), so that the pass writes only the ones left
+// out.  The records that do not fit the output are not listed.  All
+// threads call; big[] is read after the barrier.
+constexpr uint32_t BIG_LISTED = 0x80000000u;
+__device__ __forceinline__ void defer_big(const EncParams &P, uint32_t *big, const uint32_t *bpre,
+                                          const uint32_t *blen, uint32_t nbig, uint64_t r0, uint64_t base) {
+    if (!P.big_cap || !nbig) return;               // (uniform)
+    const uint32_t t = threadIdx.x;
+    if (t < nbig) {
+        const uint64_t p = base + bpre[t];
+        if (p + blen[t] <= P.cap) {
+            const uint64_t k = atomicAdd(P.big_count, 1ull);
+            if (k < P.big_cap) {
+                P.big_list[2 * k] = r0 + big[t];
+                P.big_list[2 * k + 1] = p;
+                big[t] |= BIG_LISTED;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// One large record written at out by the whole workgroup, each string or
+// item loaded once.  The name in rounds of BT x 16 bytes, thread t taking
+// bytes 16t .. 16t + 15 of the round: their escaped lengths, one block scan,
+// then each byte's escape (1, 2 or 6 bytes) stored at its place in the LDS
+// stage with byte stores that need no branch on the byte's class, and the
+// round leaves with aligned 16-byte stores (tile_copy_out).  The url and
+// tag items one per thread per round, measured, scanned and written.  The
+// pieces and their order are those of coop_rec.
+#ifndef PJ_ENC_BIG_NB
+#define PJ_ENC_BIG_NB 16
+#endif
+constexpr int BIG_NB = PJ_ENC_BIG_NB;
+template <int BT> constexpr int big_stage_bytes() { return BT * BIG_NB * 6 + 64; }
+template <bool NESTED, int BT>
+__device__ __forceinline__ void big_rec(const EncParams &P, uint8_t *out, uint64_t i, const RecVals &v, uint8_t *stage,
+                                        uint64_t *sh) {
+    const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
+    const uint32_t t = threadIdx.x;
+    const bool has_name = (v.fl & PJ_PET_HAS_NAME) != 0;
+    const uint64_t nl = has_name ? v.nb - v.na : 0;
+    const uint8_t *np = P.c.name_bytes + v.na;
+    uint64_t pos;                                   // (uniform) bytes written before the current piece
+    {
+        CountSink cs;                               // (the same for every thread)
+        rec_head<NESTED>(cs, P, XG, i, v);
+        if (has_name) cs.put_byte('"');
+        if (t == 0) {
+            XSink xs{out, 0, 0};
+            rec_head<NESTED>(xs, P, XG, i, v);
+            if (has_name) xs.put_byte('"');
+            xs.finish();
+        }
+        pos = cs.n;
+    }
+    for (uint64_t r0 = 0; r0 < nl; r0 += (uint64_t)BT * BIG_NB) {
+        const uint64_t k = r0 + (uint64_t)BIG_NB * t;
+        const uint32_t m = k < nl ? (uint32_t)min((uint64_t)BIG_NB, nl - k) : 0u;
+        const uint32_t m0 = min(m, 8u), m1 = m > 8 ? m - 8 : 0u;
+        uint64_t x0 = 0, x1 = 0;
+        if (m0) x0 = m0 == 8 ? ldu64(np + k) : ld_tail(np + k, (int)m0);
+        if (m1) x1 = m1 == 8 ? ldu64(np + k + 8) : ld_tail(np + k + 8, (int)m1);
+        const uint64_t k0 = m0 >= 8 ? ~0ull : ((1ull << (8 * m0)) - 1), k1 = m1 >= 8 ? ~0ull : ((1ull << (8 * m1)) - 1);
+        const uint64_t len = m ? m + esc_extra(x0, k0) + (m1 ? esc_extra(x1, k1) : 0u) : 0u;
+        uint64_t tot;
+        uint32_t o = (uint32_t)block_excl_scan<BT>(len, sh, &tot);
+#pragma unroll
+        for (int j = 0; j < BIG_NB; j++) {
+            const uint32_t c = (uint32_t)((j < 8 ? x0 : x1) >> (8 * (j & 7))) & 0xFFu;
+            const bool on = (uint32_t)j < m;
+            const bool esc = c < 0x20u || c == 0x22u || c == 0x5Cu;
+            int L = 1;
+            const uint64_t e = esc ? esc_seq(c, P.hexa, &L) : (uint64_t)c;
+            const uint32_t n = on ? (uint32_t)L : 0u;
+#pragma unroll
+            for (int q = 0; q < 6; q++)
+                if ((uint32_t)q < n) stage[o + q] = (uint8_t)(e >> (8 * q));
+            o += n;
+        }
+        __syncthreads();
+        // (placed from the 16-byte aligned address below out, so that whole
+        // chunks leave with aligned stores)
+        const uint32_t oa = (uint32_t)((uintptr_t)out & 15);
+        tile_copy_out<BT>(stage, out - oa, pos + oa, pos + oa, pos + oa + tot, t);
+        __syncthreads();                            // the stage is written again by the next round
+        pos += tot;
+    }
+    // closing quote and photoUrls opener (every thread knows their length)
+    {
+        CountSink cs;
+        if (has_name) cs.put_byte('"');
+        rec_urls_open(cs, v);
+        if (t == 0) {
+            XSink xs{out + pos, 0, 0};
+            if (has_name) xs.put_byte('"');
+            rec_urls_open(xs, v);
+            xs.finish();
+        }
+        pos += cs.n;
+    }
+    if (rec_has_urls(v))
+        for (uint64_t r = v.u0; r < v.u1; r += BT) {
+            const uint64_t u = r + t;
+            UrlItem it{0, 0};
+            uint64_t len = 0;
+            if (u < v.u1) {
+                it = load_url(P, u);
+                CountSink cs;
+                emit_url_v(cs, P, XG, it, u + 1 == v.u1);
+                len = cs.n;
+            }
+            uint64_t tot;
+            const uint64_t off = block_excl_scan<BT>(len, sh, &tot);
+            if (u < v.u1) {
+                XSink xs{out + pos + off, 0, 0};
+                emit_url_v(xs, P, XG, it, u + 1 == v.u1);
+                xs.finish();
+            }
+            pos += tot;
+        }
+    {
+        CountSink cs;
+        rec_tags_open<NESTED>(cs, P, v);
+        if (t == 0) {
+            XSink xs{out + pos, 0, 0};
+            rec_tags_open<NESTED>(xs, P, v);
+            xs.finish();
+        }
+        pos += cs.n;
+    }
+    if (rec_has_tags<NESTED>(v))
+        for (uint64_t r = v.t0; r < v.t1; r += BT) {
+            const uint64_t g = r + t;
+            TagItem it{0, 0, 0, 0};
+            uint64_t len = 0;
+            if (g < v.t1) {
+                it = load_tag(P, g);
+                CountSink cs;
+                emit_tag_v(cs, P, XG, it, g + 1 == v.t1);
+                len = cs.n;
+            }
+            uint64_t tot;
+            const uint64_t off = block_excl_scan<BT>(len, sh, &tot);
+            if (g < v.t1) {
+                XSink xs{out + pos + off, 0, 0};
+                emit_tag_v(xs, P, XG, it, g + 1 == v.t1);
+                xs.finish();
+            }
+            pos += tot;
+        }
+    if (t == 0) {
+        XSink xs{out + pos, 0, 0};
+        rec_tail(xs, P, i, v);
+        xs.finish();
+    }
+}
+
+// The large records a nested pass listed, one per workgroup at a time, with
+// the whole GPU's workgroups on them instead of the pass's persistent ones.
+template <bool NESTED, int BT>
+__global__ __launch_bounds__(BT) void k_enc_big(EncParams P) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage[big_stage_bytes<BT>()];
+    __shared__ uint64_t sh_scan[BT / 64];
+    const uint64_t cnt = min((uint64_t)*P.big_count, P.big_cap);
+    for (uint64_t k = blockIdx.x; k < cnt; k += gridDim.x) {
+        const uint64_t i = P.big_list[2 * k], p = P.big_list[2 * k + 1];
+        const RecVals v = load_rec<NESTED>(P, i);
+        big_rec<NESTED, BT>(P, P.out + p, i, v, stage, sh_scan);
+        __syncthreads();                            // sh_scan is reused by the next record
+    }
 }
 
 // ------------------------------------------------------------------ kernel
@@ -1303,7 +1526,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             for (uint32_t k = 0; k < nbig; k++) {
                 const uint32_t r = big[k];
                 const RecVals bv = load_rec<NESTED>(P, r0 + r);
-                const uint64_t L = coop_rec<NESTED, BT>(P, nullptr, r0 + r, bv, sh_scan, &sh_len);
+                const uint64_t L = big_len<NESTED, BT>(P, r0 + r, bv, sh_scan);
                 if (t == r) len = L;
             }
         }
@@ -1444,9 +1667,10 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 const uint64_t lo = base + g_lo, hi = min(base + g_hi, P.cap);
                 if (lo < hi) tile_copy_out<BT>(tile, P.out, lo - t_lo, lo, hi, t);
             }
+            defer_big(P, sh_big, sh_bpre, sh_blen, nbig, r0, base);
             for (uint32_t k = 0; k < nbig; k++) {
                 const uint64_t p = base + sh_bpre[k];
-                if (p + sh_blen[k] > P.cap) continue;
+                if (p + sh_blen[k] > P.cap || (sh_big[k] & BIG_LISTED)) continue;
                 const RecVals bv = load_rec<NESTED>(P, r0 + sh_big[k]);
                 coop_rec<NESTED, BT>(P, P.out + p, r0 + sh_big[k], bv, sh_scan, &sh_len);
             }
@@ -1471,9 +1695,10 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 ws.finish();
             }
             const uint32_t fnbig = sh_nbig;
+            if (NESTED) defer_big(P, big, bpre, blen, fnbig, r0, base);
             for (uint32_t k = 0; k < fnbig; k++) {
                 const uint64_t p = base + bpre[k];
-                if (p + blen[k] > P.cap) continue;
+                if (p + blen[k] > P.cap || (NESTED && (big[k] & BIG_LISTED))) continue;
                 const RecVals bv = load_rec<NESTED>(P, r0 + big[k]);
                 coop_rec<NESTED, BT>(P, P.out + p, r0 + big[k], bv, sh_scan, &sh_len);
             }
@@ -2029,6 +2254,20 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                                  ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
     return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>,
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
+}
+
+// k_enc_big: one wave per large record (its time is latency: load, scan,
+// store chains, so the more records in flight the better), as many as the
+// GPU holds at once; with an empty list every workgroup returns at once.
+#ifndef PJ_ENC_BIG_BT
+#define PJ_ENC_BIG_BT 256
+#endif
+hipError_t pj_launch_encode_big(const EncParams &P, hipStream_t st) {
+    constexpr int BT = PJ_ENC_BIG_BT;
+    const unsigned res = resident_groups(pj::k_enc_big<true, BT>, BT);
+    if (!res) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((pj::k_enc_big<true, BT>), dim3(res), dim3(BT), 0, st, P);
+    return hipGetLastError();
 }
 
 // The measuring pass: ENC_MEAS_K blocks per workgroup of 512 threads.

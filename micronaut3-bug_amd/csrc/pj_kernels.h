@@ -27,6 +27,12 @@ struct EncParams {
     uint64_t *geo;             // nested writer, two passes: block b's bounds and output offset
                                // (GEO_WORDS words at geo[GEO_WORDS * b], from k_enc_measure);
                                // blocks then run in static order with no look-back
+    // nested writer: large records are listed (record, output offset) for
+    // k_enc_big to write after the pass; with big_cap 0, or once the list
+    // is full, the pass writes them itself
+    unsigned long long *big_count;  // zeroed
+    uint64_t *big_list;
+    uint64_t big_cap;
 };
 constexpr int GEO_WORDS = 13;
 
@@ -148,6 +154,8 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);   // p[0, n) += v
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 hipError_t pj_launch_encode_measure(const EncParams &P, hipStream_t st);
+// the large records a nested pass listed (P.big_list), one workgroup each
+hipError_t pj_launch_encode_big(const EncParams &P, hipStream_t st);
 int pj_encode_block_records(bool nested);
 // one thread per output record (pretty output, or a selection of records)
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);

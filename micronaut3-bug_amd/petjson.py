@@ -117,7 +117,7 @@ NOALLOC_SCRATCH_WORDS = 1 << 20
 
 def noalloc_max_records(nested: bool) -> int:
     """Largest n_pets pj_encode_device_noalloc accepts (PJ_NOALLOC_MAX_RECORDS)."""
-    return (NOALLOC_SCRATCH_WORDS - 131) * (96 if nested else 256)
+    return (NOALLOC_SCRATCH_WORDS - 132) * (96 if nested else 256)
 
 
 def lib_path() -> str:

@@ -334,6 +334,28 @@ def test_encode_lookback_redo_in_ticket_order(codec, monkeypatch):
             assert gpu_encode(codec, cols, fmt) == orc.encode(cols, fmt)
 
 
+@pytest.mark.parametrize("big_cap", ["0", "1", "5"])
+def test_encode_large_record_list_limits(codec, monkeypatch, big_cap):
+    """Large records of nested blocks are listed for a second kernel to
+    write (k_enc_big); those past the list's room are written by the pass
+    itself.  With no list, a list of one and of five slots (the default
+    holds 2^20) the bytes equal the oracle's, in blocks on and off the tile
+    path, in both framings and at measured offsets."""
+    monkeypatch.setenv("PETJSON_ENC_BIG_CAP", big_cap)
+    cases = dict(_offtile_cases())
+    cases["hybrid"] = _hybrid_pets()
+    for label, pets in cases.items():
+        cols = to_columns(pets)
+        d = cols.to_device()
+        for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+            print(f"[big_cap] {big_cap} {label} fmt={fmt}", flush=True)
+            ref = orc.encode(cols, fmt)
+            for two_pass in (False, True):
+                assert codec.encode(d, fmt, two_pass=two_pass).cpu().numpy().tobytes() == ref, (label, fmt, two_pass)
+    cols = pj.generate(5, 20_000)
+    assert gpu_encode(codec, cols, pj.FORMAT_NDJSON) == orc.encode(cols, pj.FORMAT_NDJSON)
+
+
 def test_encode_persistent_workgroups_many_rounds(codec):
     """Nested records run on persistent workgroups (as many as the device
     holds at once: 768 on one MI355X) that claim blocks of 96 records by
