@@ -92,6 +92,7 @@ struct pj_ctx {
     hipEvent_t seg_done[2] = {};      // streamed encode: a segment's bytes and length are final
     uint64_t *noalloc_scratch = nullptr;  // this device's fixed encode scratch (device address)
     bool flat_wide = false;       // flat encodes use the wide tile (records seen too long for the compact one)
+    bool big_seen = true;         // the last nested encode listed large records (k_enc_big gets a full grid)
     hipEvent_t ev[MAX_EV] = {};
     int n_ev = 0;
     float timings[MAX_EV] = {};
@@ -446,11 +447,11 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
                 PJ_HIP(pj_launch_fill_u64(sc, 1, 0, ctx->stream));   // the writer's tickets
                 P.geo = geo;
                 PJ_HIP(pj_launch_encode(P, true, false, ctx->stream));
-                if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->stream));
+                if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->big_seen, ctx->stream));
             }
         } else {
             PJ_HIP(pj_launch_encode(P, nested_cols(cols), ctx->flat_wide, ctx->stream));
-            if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->stream));
+            if (big_cap) PJ_HIP(pj_launch_encode_big(P, ctx->big_seen, ctx->stream));
         }
         if ((s = mark(ctx))) return s;
         if (seg) {
@@ -458,12 +459,14 @@ pj_status encode_impl(pj_ctx *ctx, const pj_pet_columns *cols, int format, uint8
             PJ_HIP(hipEventRecord(seg->done, ctx->stream));
             return PJ_OK;
         }
-        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 3 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
+        PJ_HIP(hipMemcpyAsync(ctx->pinned, sc, 4 * sizeof(uint64_t), hipMemcpyDeviceToHost, ctx->stream));
         PJ_HIP(hipStreamSynchronize(ctx->stream));
         if (!P.order_by_id || ctx->pinned[0] == 0 || attempt > 0) break;
         P.order_by_id = 0;                                      // redo in ticket order
         ctx->n_ev = 0;
     }
+    // the next nested encode's k_enc_big grid follows this one's large records
+    if (big_cap) ctx->big_seen = ctx->pinned[3] != 0;
     // flat records too long for the compact tile: later calls use the wide one
     if (!pretty && !nested_cols(cols) && !ctx->flat_wide && ctx->pinned[2] * 64 > nblk) ctx->flat_wide = true;
     if ((s = finish_timing(ctx))) return s;

@@ -2256,17 +2256,17 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
 }
 
-// k_enc_big: one wave per large record (its time is latency: load, scan,
-// store chains, so the more records in flight the better), as many as the
-// GPU holds at once; with an empty list every workgroup returns at once.
+// k_enc_big: one workgroup per large record, as many workgroups as the GPU
+// holds at once (full), or 64 when the caller expects an empty list (its
+// workgroups return at once; a longer list is still written, more slowly).
 #ifndef PJ_ENC_BIG_BT
 #define PJ_ENC_BIG_BT 256
 #endif
-hipError_t pj_launch_encode_big(const EncParams &P, hipStream_t st) {
+hipError_t pj_launch_encode_big(const EncParams &P, bool full, hipStream_t st) {
     constexpr int BT = PJ_ENC_BIG_BT;
     const unsigned res = resident_groups(pj::k_enc_big<true, BT>, BT);
     if (!res) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((pj::k_enc_big<true, BT>), dim3(res), dim3(BT), 0, st, P);
+    hipLaunchKernelGGL((pj::k_enc_big<true, BT>), dim3(full ? res : std::min(res, 64u)), dim3(BT), 0, st, P);
     return hipGetLastError();
 }
 

@@ -154,8 +154,10 @@ hipError_t pj_launch_fill_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t s
 hipError_t pj_launch_add_u64(uint64_t *p, uint64_t n, uint64_t v, hipStream_t st);   // p[0, n) += v
 hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStream_t st);
 hipError_t pj_launch_encode_measure(const EncParams &P, hipStream_t st);
-// the large records a nested pass listed (P.big_list), one workgroup each
-hipError_t pj_launch_encode_big(const EncParams &P, hipStream_t st);
+// the large records a nested pass listed (P.big_list), one workgroup each:
+// with full, as many workgroups as the GPU holds, else 64 (a launch that
+// expects an empty list costs less; any count is still written)
+hipError_t pj_launch_encode_big(const EncParams &P, bool full, hipStream_t st);
 int pj_encode_block_records(bool nested);
 // one thread per output record (pretty output, or a selection of records)
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);
