@@ -235,11 +235,23 @@ for cfg, n in cases + [(0, 0)]:
         a = pj.host_array(len(v), v.dtype)
         a[:] = v
         pc.arrays[k] = a
-    want = orc.encode(cols, pj.FORMAT_ARRAY)
-    out = pj.host_array(len(want) + 64, np.uint8)
-    s, nn = pc.struct(), C.c_uint64(0)
-    rc = codec.L.pj_encode_host(codec.ctx, C.byref(s), pj.FORMAT_ARRAY, C.c_void_p(out.ctypes.data), out.size, C.byref(nn))
-    assert rc == pj.PJ_OK and out[: nn.value].tobytes() == want, (cfg, rc)
+    # the same pinned columns 8 bytes off 16-byte alignment
+    pm = pj.Columns(cols.n_pets, {}, dict(cols.caps))
+    for k, v in cols.arrays.items():
+        if v is None:
+            pm.arrays[k] = None
+            continue
+        raw = pj.host_array(v.nbytes + 16, np.uint8)
+        a = raw[8: 8 + v.nbytes].view(v.dtype)
+        a[:] = v
+        pm.arrays[k] = a
+    for fmt in (pj.FORMAT_ARRAY, pj.FORMAT_NDJSON):
+        want = orc.encode(cols, fmt)
+        out = pj.host_array(len(want) + 64, np.uint8)
+        for cs in (pc, pm):
+            s, nn = cs.struct(), C.c_uint64(0)
+            rc = codec.L.pj_encode_host(codec.ctx, C.byref(s), fmt, C.c_void_p(out.ctypes.data), out.size, C.byref(nn))
+            assert rc == pj.PJ_OK and out[: nn.value].tobytes() == want, (cfg, fmt, cs is pm, rc)
 codec.close()
 print("streamed encode ok")
 """
