@@ -1515,8 +1515,42 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             isbig = live && rec_big<NESTED>(rv);
             if (live && !isbig) {
                 CountSink cs;
-                emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
+                if (NESTED) {
+                    // (the url and tag items are measured by a helper thread below)
+                    rec_head<NESTED>(cs, P, XG, i, rv);
+                    if (rv.fl & PJ_PET_HAS_NAME) emit_strx(cs, XG, XG.name + (rv.na - XG.nb), rv.nb - rv.na, P.hexa);
+                    rec_urls_open(cs, rv);
+                    rec_tags_open<NESTED>(cs, P, rv);
+                    rec_tail(cs, P, i, rv);
+                } else emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
                 len = cs.n;
+            }
+            if constexpr (NESTED) {
+                // The url and tag items of ordinary record r are measured by
+                // thread HELP0 + r of the otherwise idle waves, alongside its
+                // own thread: each record's chain of global reads is split in
+                // two (skewed encode 4.38 -> 3.98 ms).  The helper loads the
+                // record's offsets itself; ulen, unused off the tile path,
+                // carries the lengths.
+                constexpr uint32_t HELP0 = (uint32_t)((R + 63) / 64 * 64);
+                static_assert(HELP0 + R <= BT, "a helper thread per record");
+                const uint32_t r = t - HELP0;
+                if (t >= HELP0 && r < nrec) {
+                    const uint64_t ir = r0 + r;
+                    const uint32_t fl = c.flags ? c.flags[ir] : (uint32_t)PJ_PET_DEFAULT_FLAGS;
+                    const uint64_t u0 = c.photo_off ? c.photo_off[ir] : 0, u1 = c.photo_off ? c.photo_off[ir + 1] : 0;
+                    const uint64_t g0 = c.tag_off ? c.tag_off[ir] : 0, g1 = c.tag_off ? c.tag_off[ir + 1] : 0;
+                    // (rec_big, from the offsets)
+                    const bool big = c.name_off[ir + 1] - c.name_off[ir] > BIG_STR || u1 - u0 > BIG_ITEMS || g1 - g0 > BIG_ITEMS;
+                    CountSink cs;
+                    if (!big && (fl & PJ_PET_HAS_PHOTOURLS))
+                        for (uint64_t u = u0; u < u1; u++) emit_url_item(cs, P, XG, u, u + 1 == u1);
+                    if (!big && (fl & PJ_PET_HAS_TAGS))
+                        for (uint64_t g = g0; g < g1; g++) emit_tag_item(cs, P, XG, g, g + 1 == g1);
+                    ulen[r] = (uint32_t)cs.n;
+                }
+                __syncthreads();
+                if (live && !isbig) len += ulen[t];
             }
             uint64_t nb64;
             bidx = (uint32_t)block_excl_scan<BT>(isbig ? 1ull : 0ull, sh_scan, &nb64);
