@@ -949,8 +949,7 @@ __device__ __forceinline__ void defer_big(const EncParams &P, uint32_t *big, con
 // item loaded once.  The name in rounds of BT x 16 bytes, thread t taking
 // bytes 16t .. 16t + 15 of the round: their escaped lengths, one block scan,
 // then each byte's escape (1, 2 or 6 bytes) stored at its place in the LDS
-// stage with byte stores that need no branch on the byte's class, and the
-// round leaves with aligned 16-byte stores (tile_copy_out).  The url and
+// stage, and the round leaves with aligned 16-byte stores (tile_copy_out).  The url and
 // tag items one per thread per round, measured, scanned and written.  The
 // pieces and their order are those of coop_rec.
 #ifndef PJ_ENC_BIG_NB
@@ -998,9 +997,11 @@ __device__ __forceinline__ void big_rec(const EncParams &P, uint8_t *out, uint64
             int L = 1;
             const uint64_t e = esc ? esc_seq(c, P.hexa, &L) : (uint64_t)c;
             const uint32_t n = on ? (uint32_t)L : 0u;
-#pragma unroll
-            for (int q = 0; q < 6; q++)
-                if ((uint32_t)q < n) stage[o + q] = (uint8_t)(e >> (8 * q));
+            // at most three stores at any byte offset: the byte, the two-byte
+            // escape (or "\u" of a six-byte one) and "00XX"
+            if (n == 1) stage[o] = (uint8_t)e;
+            if (n >= 2) *reinterpret_cast<uint16_t *>(stage + o) = (uint16_t)e;
+            if (n == 6) *reinterpret_cast<uint32_t *>(stage + o + 2) = (uint32_t)(e >> 16);
             o += n;
         }
         __syncthreads();
