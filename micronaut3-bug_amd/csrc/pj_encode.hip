@@ -845,9 +845,9 @@ __device__ __forceinline__ uint64_t coop_rec(const EncParams &P, uint8_t *out, u
 
 // The length of one large record, by the whole workgroup in one pass (every
 // thread gets it): the fixed pieces by thread 0, the name's escapes 16 bytes
-// per thread per round (all loads of a round issued before any is used), an
-// item per thread per round, and one block sum.  coop_rec's measuring mode
-// gives the same length with a scan per piece.
+// per thread per step (both loads of a step issued before either is used),
+// an item per thread per round, and one block sum.  coop_rec's measuring
+// mode gives the same length with a scan per piece.
 template <bool NESTED, int BT>
 __device__ __forceinline__ uint64_t big_len(const EncParams &P, uint64_t i, const RecVals &v, uint64_t *sh) {
     const ColSrc XG{P.c.name_bytes, P.c.cat_name_bytes, P.c.url_bytes, P.c.tag_name_bytes, 0, 0, 0, 0};
@@ -949,9 +949,9 @@ __device__ __forceinline__ void defer_big(const EncParams &P, uint32_t *big, con
 // item loaded once.  The name in rounds of BT x 16 bytes, thread t taking
 // bytes 16t .. 16t + 15 of the round: their escaped lengths, one block scan,
 // then each byte's escape (1, 2 or 6 bytes) stored at its place in the LDS
-// stage, and the round leaves with aligned 16-byte stores (tile_copy_out).  The url and
-// tag items one per thread per round, measured, scanned and written.  The
-// pieces and their order are those of coop_rec.
+// stage, and the round leaves with aligned 16-byte stores (tile_copy_out).
+// The url and tag items one per thread per round, measured, scanned and
+// written.  The pieces and their order are those of coop_rec.
 #ifndef PJ_ENC_BIG_NB
 #define PJ_ENC_BIG_NB 16
 #endif
