@@ -174,13 +174,51 @@ def decode_workload(codec, n, steps, warmup):
     del bufs
     torch.cuda.empty_cache()
     hostr = host_decode_rates(codec, np.frombuffer(host_text, np.uint8), caps, max(16, 2 * len(lines)), int(res.n_pets))
+    del data
+    torch.cuda.empty_cache()
+    arr = array_decode_rates(codec, cols, caps, steps, warmup)
     r = {"records": int(res.n_lines), "records_per_s": res.n_lines / wall, "ms_per_step": wall * 1e3,
          "input_bytes": in_bytes, "output_bytes": out_bytes, "input_GBps": in_bytes / wall / 1e9,
          "alg_GBps": (in_bytes + out_bytes) / wall / 1e9,
          "alg_frac_hbm": (in_bytes + out_bytes) / wall / 1e9 / HBM_PEAK_GBPS,
          "invalid_records": int(res.n_errors), "errors_match_generator": bool(ok),
          "lines_general_parser": int(res.n_general), "kernels": kern,
-         "host_entry_point": hostr}
+         "host_entry_point": hostr, "array_document": arr}
+    return r
+
+
+def array_decode_rates(codec, cols, caps, steps, warmup):
+    """The same records as one JSON array document (readValue(bytes,
+    List<Pet>)): the frame kernels cut it into elements, then the line
+    stages decode them.  Columns compared with the generator's."""
+    import numpy as np
+    import torch
+    import petjson as pj
+    dev = cols.to_device()
+    doc = codec.encode(dev, pj.FORMAT_ARRAY)
+    del dev
+    torch.cuda.empty_cache()
+    bufs = codec.decode_buffers(caps, 16)
+    for _ in range(warmup):
+        codec.decode_array(doc, out=bufs)
+    torch.cuda.synchronize()
+    kms = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dcols, el, ec, res = codec.decode_array(doc, out=bufs)
+        kms.append(codec.timings()[0])                 # the whole pipeline, HIP events on the codec stream
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    h = dcols.to_host()
+    same = res.n_errors == 0 and all(np.array_equal(h[k], cols[k]) for k in pj.COLS if cols[k] is not None)
+    in_bytes = int(doc.numel())
+    out_bytes = sum(int(dcols[k].numel()) * dcols[k].element_size() for k in pj.COLS)
+    k = sum(kms) / len(kms)
+    r = {"records": int(res.n_pets), "input_bytes": in_bytes, "output_bytes": out_bytes, "ms_per_step": wall * 1e3,
+         "pipeline_ms": k, "alg_frac_hbm": (in_bytes + out_bytes) / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+         "roundtrip_bit_exact": bool(same)}
+    del doc, bufs, dcols
+    torch.cuda.empty_cache()
     return r
 
 

@@ -189,7 +189,7 @@ __device__ __forceinline__ FS fs_id() {
     FS f;
     f.out = 0xE4u;      // s -> s
 #pragma unroll
-    for (int k = 0; k < 4; k++) f.d[k] = f.mn[k] = 0;
+    for (int k = 0; k < 4; k++) f.d[k] = 0;
     return f;
 }
 __device__ __forceinline__ int32_t pick4(const int32_t *a, uint32_t k) {
@@ -204,7 +204,6 @@ __device__ __forceinline__ FS fs_cat(const FS &f, const FS &g) {
         const uint32_t s1 = (f.out >> (2 * k)) & 3;
         r.out |= ((g.out >> (2 * s1)) & 3) << (2 * k);
         r.d[k] = f.d[k] + pick4(g.d, s1);
-        r.mn[k] = min(f.mn[k], f.d[k] + pick4(g.mn, s1));
     }
     return r;
 }
@@ -271,9 +270,6 @@ __device__ __forceinline__ FS word_fs(const AMasks &M) {
     for (int s = 0; s < 4; s++) {
         const AWord a = arr_word(M, (uint32_t)s);
         f.d[s] = __builtin_popcountll(a.od) - __builtin_popcountll(a.cd);
-        int32_t mn = 0;
-        for (uint64_t m = a.cd; m; m &= m - 1) mn = min(mn, depth_at(a, (uint32_t)__builtin_ctzll(m)));
-        f.mn[s] = mn;
         f.out |= a.out << (2 * s);
     }
     return f;
@@ -359,17 +355,26 @@ __global__ __launch_bounds__(BT) void k_arr_frame(DecParams P) {
     const uint32_t sb = (uint32_t)bp & 3;
     uint32_t st0 = (ex.out >> (2 * sb)) & 3;
     int32_t dep0 = (int32_t)(uint32_t)(bp >> 32) + pick4(ex.d, sb);
-    // pass 1: count the separators; first / last non-whitespace; the close
+    // pass 1: the separators (a mask per word); first / last non-whitespace;
+    // the close
     uint64_t cnt = 0, first = ~0ull, lastp1 = 0, close = ~0ull;
+    uint64_t sep[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) sep[r] = 0;
     {
         uint32_t st = st0;
         int32_t dep = dep0;
+#pragma unroll
         for (int r = 0; r < R; r++) {
             const uint64_t w = w0 + r;
             if (w >= P.nblk64) break;
             const AMasks M = arr_masks(P.in + 64 * w, P.len - 64 * w);
             const AWord a = arr_word(M, st);
-            for (uint64_t m = a.md; m; m &= m - 1) cnt += dep + depth_at(a, (uint32_t)__builtin_ctzll(m)) == 1;
+            for (uint64_t m = a.md; m; m &= m - 1) {
+                const uint32_t i = (uint32_t)__builtin_ctzll(m);
+                if (dep + depth_at(a, i) == 1) sep[r] |= 1ull << i;
+            }
+            cnt += (uint64_t)__builtin_popcountll(sep[r]);
             if (close == ~0ull)
                 for (uint64_t m = a.cd; m; m &= m - 1) {
                     const uint32_t i = (uint32_t)__builtin_ctzll(m);
@@ -407,23 +412,12 @@ __global__ __launch_bounds__(BT) void k_arr_frame(DecParams P) {
     __syncthreads();
     // pass 2: element k + 1 starts after the k-th separator
     uint64_t idx = sh_pre + ex_cnt;
-    uint32_t st = st0;
-    int32_t dep = dep0;
-    for (int r = 0; r < R && cnt; r++) {
-        const uint64_t w = w0 + r;
-        if (w >= P.nblk64) break;
-        const AMasks M = arr_masks(P.in + 64 * w, P.len - 64 * w);
-        const AWord a = arr_word(M, st);
-        for (uint64_t m = a.md; m; m &= m - 1) {
-            const uint32_t i = (uint32_t)__builtin_ctzll(m);
-            if (dep + depth_at(a, i) == 1) {
-                if (1 + idx < P.ls_cap) P.line_start[1 + idx] = 64 * w + i + 1;
-                idx++;
-            }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        for (uint64_t m = sep[r]; m; m &= m - 1) {
+            if (1 + idx < P.ls_cap) P.line_start[1 + idx] = 64 * (w0 + r) + (uint64_t)__builtin_ctzll(m) + 1;
+            idx++;
         }
-        dep += __builtin_popcountll(a.od) - __builtin_popcountll(a.cd);
-        st = a.out;
-    }
 }
 // The frame's verdict (one thread): the first non-whitespace byte is '[',
 // the close is a ']' after it and nothing but whitespace follows.  Then

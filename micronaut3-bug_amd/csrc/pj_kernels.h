@@ -84,12 +84,11 @@ struct LineRec {
 
 // Summary of a stretch of an array document, for each of the four states it
 // may be entered in (bit 0 inside a string, bit 1 first byte escaped): the
-// exit state (2 bits each in out), the depth change and the lowest depth
-// reached.  Composed in order by the array frame kernels.
+// exit state (2 bits each in out) and the depth change.  Composed in order
+// by the array frame kernels.
 struct FS {
     uint32_t out;
     int32_t d[4];
-    int32_t mn[4];
 };
 
 struct DecParams {
