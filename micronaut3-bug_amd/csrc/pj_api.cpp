@@ -1073,14 +1073,16 @@ pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, 
     for (int attempt = 0; attempt < 2; attempt++) {
         const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
         // layout (u64 units): header 16 | dummy 32 | array frame scalars 8 |
-        //   state_idx gidx | (arrays: block summaries, entry states) | line_start ls_cap
+        //   state_idx gidx | (arrays: block summaries, entry states, per-thread
+        //   summaries) | line_start ls_cap
         // header: 0-1 tickets, 2 line count, 3 blank lines, 4-11 totals,
         //         12 lines off the fast path, 13 deferred error-code queue
         //         length, 14 lines for k_dec_long, 15 scan ticket
         const uint64_t o_dummy = 16, o_arr = 48, o_sidx = 56;
         const uint64_t ga = array ? pj_arr_blocks(nblk64) : 0;
         const uint64_t o_bsum = o_sidx + gidx, o_bpre = o_bsum + (ga * sizeof(FS) + 7) / 8;
-        const uint64_t o_ls = o_bpre + ga;
+        const uint64_t o_tsum = o_bpre + ga, ta = array ? pj_arr_threads(nblk64) : 0;
+        const uint64_t o_ls = o_tsum + (ta * sizeof(FS) + 7) / 8;
         PJ_HIP(ctx->index.ensure((o_ls + ls_cap) * 8 + 64));
         X = static_cast<uint64_t *>(ctx->index.p);
         std::memset(&P, 0, sizeof P);
@@ -1100,6 +1102,7 @@ pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, 
         P.arr = X + o_arr;
         P.arr_bsum = reinterpret_cast<FS *>(X + o_bsum);
         P.arr_bpre = X + o_bpre;
+        P.arr_tsum = reinterpret_cast<FS *>(X + o_tsum);
         // blocks in launch order with bounded look-back waits; a kernel
         // whose wait ran out (its ticket word set) is redone in ticket order
         P.order_by_id = 1;

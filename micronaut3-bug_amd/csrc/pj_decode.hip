@@ -306,6 +306,8 @@ __global__ __launch_bounds__(BT) void k_arr_sum(DecParams P) {
     }
     acc = block_fs_scan<BT>(acc, sh);
     if (t == BT - 1) P.arr_bsum[b] = acc;
+    // the thread's exclusive prefix in the block, for k_arr_frame
+    P.arr_tsum[b * BT + t] = t ? sh[t - 1] : fs_id();
 }
 // One workgroup: the state and depth each block is entered with, the
 // document being entered outside strings at depth 0.
@@ -332,7 +334,6 @@ __global__ __launch_bounds__(BT) void k_arr_scan(DecParams P, uint64_t nb) {
 // block each).
 template <int BT, int R>
 __global__ __launch_bounds__(BT) void k_arr_frame(DecParams P) {
-    __shared__ FS sh[BT];
     __shared__ uint64_t sh_scan[BT / 64];
     __shared__ uint64_t sh_blk, sh_pre, sh_mn[3];
     const uint32_t t = threadIdx.x;
@@ -342,15 +343,9 @@ __global__ __launch_bounds__(BT) void k_arr_frame(DecParams P) {
     }
     __syncthreads();
     const uint64_t b = sh_blk, w0 = (b * BT + t) * R;
-    // the thread's entry state: the block's, then its predecessors' words in the block
-    FS acc = fs_id();
-    for (int r = 0; r < R; r++) {
-        const uint64_t w = w0 + r;
-        if (w < P.nblk64) acc = fs_cat(acc, word_fs(arr_masks(P.in + 64 * w, P.len - 64 * w)));
-    }
-    block_fs_scan<BT>(acc, sh);
-    FS ex = fs_id();
-    if (t) ex = sh[t - 1];
+    // the thread's entry state: the block's, then its predecessors' words in
+    // the block (their summary, from k_arr_sum)
+    const FS ex = P.arr_tsum[b * BT + t];
     const uint64_t bp = P.arr_bpre[b];
     const uint32_t sb = (uint32_t)bp & 3;
     uint32_t st0 = (ex.out >> (2 * sb)) & 3;
@@ -3205,6 +3200,7 @@ hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
 
 constexpr int ARR_BT = 256, ARR_R = 4;
 uint64_t pj_arr_blocks(uint64_t nblk64) { return (nblk64 + ARR_BT * ARR_R - 1) / (ARR_BT * ARR_R); }
+uint64_t pj_arr_threads(uint64_t nblk64) { return pj_arr_blocks(nblk64) * ARR_BT; }
 
 hipError_t pj_launch_arr_frame(const DecParams &P, hipStream_t st) {
     const uint64_t g = pj_arr_blocks(P.nblk64);

@@ -136,6 +136,7 @@ struct DecParams {
     int array_doc;
     uint64_t *arr;
     FS *arr_bsum;
+    FS *arr_tsum;              // per thread of the frame kernels: the summary of its block's words before its own
     uint64_t *arr_bpre;
     unsigned long long *empty_count;   // lines that are blank (PJ_REC_EMPTY)
     // 1: block b of each kernel takes its input in launch order (no ticket
@@ -182,6 +183,7 @@ int pj_dec_bscan_block();
 // count into *n_lines, the verdict into arr[4])
 hipError_t pj_launch_arr_frame(const DecParams &P, hipStream_t st);
 uint64_t pj_arr_blocks(uint64_t nblk64);
+uint64_t pj_arr_threads(uint64_t nblk64);   // arr_tsum entries
 int pj_dec_index_block();
 // Device address of this GPU's fixed encode scratch (PJ_NOALLOC_SCRATCH_WORDS
 // u64); resolved once per device, with that device current.
