@@ -1071,7 +1071,10 @@ pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, 
     const uint64_t nblk64 = (len + 63) / 64;
     uint64_t ls_cap = len / 128 + 16;
     for (int attempt = 0; attempt < 2; attempt++) {
-        const uint64_t gidx = (nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block();
+        // look-back words: one per block of the kernel that builds the index
+        // (the newline index's, or the array frame's blocks)
+        const uint64_t ga = array ? pj_arr_blocks(nblk64) : 0;
+        const uint64_t gidx = std::max((nblk64 + pj_dec_index_block() - 1) / pj_dec_index_block(), ga);
         // layout (u64 units): header 16 | dummy 32 | array frame scalars 8 |
         //   state_idx gidx | (arrays: block summaries, entry states, per-thread
         //   summaries) | line_start ls_cap
@@ -1079,7 +1082,6 @@ pj_status index_stage(pj_ctx *ctx, const uint8_t *in, uint64_t len, bool array, 
         //         12 lines off the fast path, 13 deferred error-code queue
         //         length, 14 lines for k_dec_long, 15 scan ticket
         const uint64_t o_dummy = 16, o_arr = 48, o_sidx = 56;
-        const uint64_t ga = array ? pj_arr_blocks(nblk64) : 0;
         const uint64_t o_bsum = o_sidx + gidx, o_bpre = o_bsum + (ga * sizeof(FS) + 7) / 8;
         const uint64_t o_tsum = o_bpre + ga, ta = array ? pj_arr_threads(nblk64) : 0;
         const uint64_t o_ls = o_tsum + (ta * sizeof(FS) + 7) / 8;

@@ -3198,7 +3198,10 @@ hipError_t pj_launch_dec_index(const DecParams &P, hipStream_t st) {
     return hipGetLastError();
 }
 
-constexpr int ARR_BT = 256, ARR_R = 4;
+#ifndef PJ_ARR_R
+#define PJ_ARR_R 8
+#endif
+constexpr int ARR_BT = 256, ARR_R = PJ_ARR_R;
 uint64_t pj_arr_blocks(uint64_t nblk64) { return (nblk64 + ARR_BT * ARR_R - 1) / (ARR_BT * ARR_R); }
 uint64_t pj_arr_threads(uint64_t nblk64) { return pj_arr_blocks(nblk64) * ARR_BT; }
 
