@@ -515,6 +515,49 @@ template <int MODEL> __device__ __forceinline__ int m_line(const uint8_t *s, uin
     return m_end(L) ? PJ_REC_OK : PJ_REC_SYNTAX;
 }
 
+// Fast path: a record whose properties come in schema order (any of them
+// absent), with no whitespace, no unknown or repeated key and no error, read
+// as straight code: each property's `"key":` compared as a whole and its
+// value read by m_value.  Anything else gives M_SLOW, and the record is read
+// again by m_line, which decides its values or its first error; so whatever
+// this path accepts, m_line reads the same way.
+constexpr int M_SLOW = -1;
+template <int MODEL, int F> __device__ __forceinline__ bool m_key_is(const MLine &L, uint64_t q) {
+    const MProp k = MSchema<MODEL>::prop(F);
+    if (q + 3 + k.len > L.n || L.s[q] != '"' || L.s[q + 1 + k.len] != '"' || L.s[q + 2 + k.len] != ':') return false;
+    const uint32_t m0 = min(k.len, 8u), m1 = k.len > 8 ? k.len - 8 : 0u;
+    const uint64_t x0 = m0 == 8 ? ldu64(L.s + q + 1) : ld_tail(L.s + q + 1, (int)m0);
+    const uint64_t x1 = m1 ? ld_tail(L.s + q + 9, (int)m1) : 0ull;
+    return x0 == k.w0 && x1 == k.w1;
+}
+template <int MODEL, int F> __device__ __forceinline__ int m_fast_props(MLine &L, MRec &R, bool first) {
+    if constexpr (F >= MSchema<MODEL>::N) return PJ_REC_OK;
+    else {
+        if (L.p >= L.n) return M_SLOW;
+        if (L.s[L.p] == '}') return PJ_REC_OK;                 // the properties after it are absent
+        const uint64_t q = first ? L.p : L.p + 1;
+        if (!first && L.s[L.p] != ',') return M_SLOW;
+        if (!m_key_is<MODEL, F>(L, q)) return m_fast_props<MODEL, F + 1>(L, R, first);   // F is absent
+        L.p = q + 3 + MSchema<MODEL>::prop(F).len;
+        if (m_value<MODEL, F>(L, R) != PJ_REC_OK) return M_SLOW;
+        return m_fast_props<MODEL, F + 1>(L, R, false);
+    }
+}
+template <int MODEL> __device__ __forceinline__ int m_line_fast(const uint8_t *s, uint64_t n, MRec &R) {
+    MLine L{s, n, 1};
+    R.present = 0;
+    R.sesc = 0;
+#pragma unroll
+    for (int k = 0; k < PJ_MODEL_MAX_PROPS; k++) {
+        R.v[k] = 0;
+        R.slen[k] = 0;
+        R.spos[k] = 0;
+    }
+    if (n < 2 || s[0] != '{') return M_SLOW;
+    if (m_fast_props<MODEL, 0>(L, R, true) != PJ_REC_OK) return M_SLOW;
+    return L.p + 1 == n && s[L.p] == '}' ? PJ_REC_OK : M_SLOW;
+}
+
 // A block's records, staged: the input bytes [g0, a1) (g0 = the first
 // record's start rounded down to 16 bytes, a1 = the last record's end) in
 // LDS when they fit the tile, read with 16-byte loads (exact at the input's
@@ -561,7 +604,8 @@ __device__ __forceinline__ int m_read(const ModelDecParams &P, const MStage &S, 
     for (int k = 0; k < MD_MAXK; k++) cnt[k] = 0;
     if (l >= P.lines) return -1;
     const uint64_t a = P.line_start[l], e = P.line_start[l + 1] - 1;
-    const int code = m_line<MODEL>(S.at(P, a), e - a, R);
+    int code = m_line_fast<MODEL>(S.at(P, a), e - a, R);
+    if (code == M_SLOW) code = m_line<MODEL>(S.at(P, a), e - a, R);
     if (code == PJ_REC_OK) {
         cnt[0] = 1;
 #pragma unroll
