@@ -596,15 +596,17 @@ __device__ __forceinline__ MStage m_stage(const ModelDecParams &P, uint8_t *tile
 }
 
 // The record's counters: [0] valid, [1] invalid, [2 + k] decoded bytes of
-// string property k; and whether it is blank.
-template <int MODEL>
+// string property k; and whether it is blank.  FAST: through the fast path
+// first (the counting kernel; the writer reads records again only without
+// the tape, and keeps the smaller code).
+template <int MODEL, bool FAST = true>
 __device__ __forceinline__ int m_read(const ModelDecParams &P, const MStage &S, uint64_t l, MRec &R,
                                       uint64_t (&cnt)[MD_MAXK]) {
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) cnt[k] = 0;
     if (l >= P.lines) return -1;
     const uint64_t a = P.line_start[l], e = P.line_start[l + 1] - 1;
-    int code = m_line_fast<MODEL>(S.at(P, a), e - a, R);
+    int code = FAST ? m_line_fast<MODEL>(S.at(P, a), e - a, R) : M_SLOW;
     if (code == M_SLOW) code = m_line<MODEL>(S.at(P, a), e - a, R);
     if (code == PJ_REC_OK) {
         cnt[0] = 1;
@@ -730,7 +732,7 @@ __global__ __launch_bounds__(BT) void k_mdec_write(ModelDecParams P) {
                 cnt[2 + k] = R.slen[k];
             }
         }
-    } else code = m_read<MODEL>(P, S, l, R, cnt);
+    } else code = m_read<MODEL, false>(P, S, l, R, cnt);
 #pragma unroll
     for (int k = 0; k < MD_MAXK; k++) {
         uint64_t tot;
