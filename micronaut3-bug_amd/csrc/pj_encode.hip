@@ -1097,6 +1097,114 @@ __global__ __launch_bounds__(BT) void k_enc_big(EncParams P) {
     }
 }
 
+// ------------------------------------------------------- record units
+// The pieces the tile path cuts a record into (head, name with the
+// photoUrls opener, url items, tags opener, tag items, tail), compact or
+// PRETTY.  The pretty pieces are pp_rec's layout cut the same way: an item
+// is (" " for the first, ", " for the others) + its value (+ " ]" after the
+// last); every entry after the first is ",\n" + indentation.
+template <int F0, class S>
+__device__ __forceinline__ void pp_sub_x(S &s, const EncParams &P, const ColSrc &X, uint32_t fl, int64_t id,
+                                         const uint8_t *nm, uint64_t nlen) {
+    const uint32_t ii = P.incl[F0], ni = P.incl[F0 + 1];
+    bool first = true;
+    s.put_byte('{');
+    if (fl & PJ_SUB_HAS_ID) { pp_entry(s, first, 4); lit(s, "\"id\" : "); emit_long(s, id); }
+    else if (ii == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 4); lit(s, "\"id\" : null"); }
+    if (fl & PJ_SUB_HAS_NAME) {
+        if (nlen > 0 || ni != PJ_INCLUDE_NON_EMPTY) {
+            pp_entry(s, first, 4); lit(s, "\"name\" : "); emit_strx(s, X, nm, nlen, P.hexa);
+        }
+    } else if (ni == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 4); lit(s, "\"name\" : null"); }
+    pp_close(s, first, 2);
+}
+template <bool NESTED, bool PRETTY, class S>
+__device__ __forceinline__ void u_head(S &s, const EncParams &P, const ColSrc &X, uint64_t i, const RecVals &v) {
+    if constexpr (!PRETTY) rec_head<NESTED>(s, P, X, i, v);
+    else {
+        const uint32_t fl = v.fl;
+        if (i == P.first) lit(s, "[ ");
+        else lit(s, ", ");
+        bool first = true;
+        s.put_byte('{');
+        if (fl & PJ_PET_HAS_ID) { pp_entry(s, first, 2); lit(s, "\"id\" : "); emit_long(s, v.id); }
+        else if (P.incl[PJ_FIELD_PET_ID] == PJ_INCLUDE_ALWAYS) { pp_entry(s, first, 2); lit(s, "\"id\" : null"); }
+        if ((fl & PJ_PET_HAS_CATEGORY) && P.c.cat_id) {
+            pp_entry(s, first, 2);
+            lit(s, "\"category\" : ");
+            pp_sub_x<PJ_FIELD_CATEGORY_ID>(s, P, X, v.cf, v.cat_id, X.cat + (v.ca - X.cb), v.cb - v.ca);
+        } else if (P.incl[PJ_FIELD_PET_CATEGORY] == PJ_INCLUDE_ALWAYS) {
+            pp_entry(s, first, 2);
+            lit(s, "\"category\" : null");
+        }
+        pp_entry(s, first, 2);
+        if (fl & PJ_PET_HAS_NAME) lit(s, "\"name\" : ");
+        else lit(s, "\"name\" : null");
+    }
+}
+template <bool PRETTY, class S> __device__ __forceinline__ void u_urls_open(S &s, uint32_t fl, bool empty) {
+    if constexpr (!PRETTY) rec_urls_open(s, fl, empty);
+    else if (fl & PJ_PET_HAS_PHOTOURLS) {
+        lit(s, ",\n  \"photoUrls\" : [");
+        if (empty) lit(s, " ]");
+    } else lit(s, ",\n  \"photoUrls\" : null");
+}
+// f: the record's HAS_NAME and HAS_PHOTOURLS bits, 0x80 when it has no urls
+template <bool PRETTY, class S>
+__device__ __forceinline__ void u_name(S &s, const EncParams &P, const ColSrc &X, const uint8_t *nm, uint32_t nl,
+                                       uint32_t f) {
+    if (f & PJ_PET_HAS_NAME) emit_strx(s, X, nm, nl, P.hexa);
+    u_urls_open<PRETTY>(s, f, (f & 0x80u) != 0);
+}
+template <bool NESTED, bool PRETTY, class S>
+__device__ __forceinline__ void u_tags_open(S &s, const EncParams &P, const RecVals &v) {
+    if constexpr (!PRETTY) rec_tags_open<NESTED>(s, P, v);
+    else {
+        const uint32_t ti = P.incl[PJ_FIELD_PET_TAGS];
+        if (v.fl & PJ_PET_HAS_TAGS) {
+            if (v.t1 > v.t0 || ti != PJ_INCLUDE_NON_EMPTY) {
+                lit(s, ",\n  \"tags\" : [");
+                if (v.t1 == v.t0) lit(s, " ]");
+            }
+        } else if (ti == PJ_INCLUDE_ALWAYS) lit(s, ",\n  \"tags\" : null");
+    }
+}
+template <bool PRETTY, class S>
+__device__ __forceinline__ void u_tail(S &s, const EncParams &P, uint64_t i, const RecVals &v) {
+    if constexpr (!PRETTY) rec_tail(s, P, i, v);
+    else {
+        const uint32_t st = v.st;
+        if (st == 0) lit(s, ",\n  \"status\" : \"available\"");
+        else if (st == 1) lit(s, ",\n  \"status\" : \"pending\"");
+        else if (st == 2) lit(s, ",\n  \"status\" : \"sold\"");
+        else if (P.incl[PJ_FIELD_PET_STATUS] == PJ_INCLUDE_ALWAYS) lit(s, ",\n  \"status\" : null");
+        lit(s, "\n}");
+        if (i == P.last) lit(s, " ]");
+    }
+}
+template <bool PRETTY, class S>
+__device__ __forceinline__ void u_url(S &s, const EncParams &P, const ColSrc &X, const UrlItem &v, bool first,
+                                      bool last) {
+    if constexpr (!PRETTY) emit_url_v(s, P, X, v, last);
+    else {
+        if (first) s.put_byte(' ');
+        else lit(s, ", ");
+        emit_strx(s, X, X.url + (v.a - X.ub), v.b - v.a, P.hexa);
+        if (last) lit(s, " ]");
+    }
+}
+template <bool PRETTY, class S>
+__device__ __forceinline__ void u_tag(S &s, const EncParams &P, const ColSrc &X, const TagItem &v, bool first,
+                                      bool last) {
+    if constexpr (!PRETTY) emit_tag_v(s, P, X, v, last);
+    else {
+        if (first) s.put_byte(' ');
+        else lit(s, ", ");
+        pp_sub_x<PJ_FIELD_TAG_ID>(s, P, X, v.tf, v.id, X.tag + (v.a - X.tb), v.b - v.a);
+        if (last) lit(s, " ]");
+    }
+}
+
 // ------------------------------------------------------------------ kernel
 
 // Names longer than LN_MIN bytes in tile-path blocks are counted and written
@@ -1237,7 +1345,7 @@ __device__ __forceinline__ Geo block_geo(const uint64_t *nx, uint64_t b) {
 // thread t is list position t + j BT): heads of records 0..R-1 from position
 // 0, names from NAME0, url then tag items from ITEM0, each kind starting on
 // a wave boundary so that no wave runs two kinds of unit in one slot.
-constexpr uint32_t ITEM_ON = 1u << 31, ITEM_LAST = 1u << 30;
+constexpr uint32_t ITEM_ON = 1u << 31, ITEM_LAST = 1u << 30, ITEM_FIRST = 1u << 29;
 template <int R> constexpr int name0() { return (R + 63) / 64 * 64; }
 template <int R> constexpr int item0() { return (name0<R>() + R + 63) / 64 * 64; }
 
@@ -1302,8 +1410,9 @@ __device__ __forceinline__ void enc_prefetch(const EncParams &P, const Geo &g, R
 // workgroup measures and writes (slices of the string escaped in parallel
 // and placed by a block scan, items spread over the threads), so one
 // skewed record does not hold its workgroup for long.
-template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP, int WPE = 1>
+template <bool NESTED, int BT, int R, int TILE, int INCAP, int UCAP, int GCAP, int WPE = 1, bool PRETTY = false>
 __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
+    static_assert(!PRETTY || NESTED, "pretty output through the tile path: nested layout only");
     constexpr int UA = NESTED ? UCAP : 1, GA = NESTED ? GCAP : 1, RA = NESTED ? R : 1;
     // flat records write the tile with aligned stores only; nested ones,
     // whose many short items mostly land in edge qwords shared with a
@@ -1434,9 +1543,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     if ((rv.fl & PJ_PET_HAS_NAME) && rv.nb - rv.na > LN_MIN) sh_ln[atomicAdd(&sh_nln, 1u)] = (uint8_t)t;
                     const uint32_t uf = rec_has_urls(rv) ? ITEM_ON : 0u, gf = rec_has_tags<NESTED>(rv) ? ITEM_ON : 0u;
                     for (uint32_t k = ul0; k < ul1; k++)
-                        uinfo[k] = (hidx + 2 + k - ul0) | uf | (k + 1 == ul1 ? ITEM_LAST : 0u);
+                        uinfo[k] = (hidx + 2 + k - ul0) | uf | (k + 1 == ul1 ? ITEM_LAST : 0u) |
+                                   ((PRETTY && k == ul0) ? ITEM_FIRST : 0u);
                     for (uint32_t k = gl0; k < gl1; k++)
-                        ginfo[k] = (hidx + 3 + (ul1 - ul0) + k - gl0) | gf | (k + 1 == gl1 ? ITEM_LAST : 0u);
+                        ginfo[k] = (hidx + 3 + (ul1 - ul0) + k - gl0) | gf | (k + 1 == gl1 ? ITEM_LAST : 0u) |
+                                   ((PRETTY && k == gl0) ? ITEM_FIRST : 0u);
                 }
             }
             __syncthreads();
@@ -1446,9 +1557,9 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 if (live) {
                     const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
                     CountSink ch, cm, ct;
-                    rec_head<NESTED>(ch, P, XL, i, rv);
-                    rec_tags_open<NESTED>(cm, P, rv);
-                    rec_tail(ct, P, i, rv);
+                    u_head<NESTED, PRETTY>(ch, P, XL, i, rv);
+                    u_tags_open<NESTED, PRETTY>(cm, P, rv);
+                    u_tail<PRETTY>(ct, P, i, rv);
                     ulen[hidx] = (uint32_t)ch.n;
                     ulen[hidx + 2 + nu] = (uint32_t)cm.n;
                     ulen[hidx + 3 + nu + nt] = (uint32_t)ct.n;
@@ -1459,8 +1570,8 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     if ((f & PJ_PET_HAS_NAME) && sh_blen[r] > LN_MIN) {
                         // the body's escapes are added by the waves below
                         cs.n = sh_blen[r] + 2;
-                        rec_urls_open(cs, f, (f & 0x80u) != 0);
-                    } else name_unit(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
+                        u_urls_open<PRETTY>(cs, f, (f & 0x80u) != 0);
+                    } else u_name<PRETTY>(cs, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
                     ulen[sh_big[r] + 1] = (uint32_t)cs.n;
                 }
 #pragma unroll
@@ -1471,11 +1582,12 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     CountSink cs;
                     if (k < U) {
                         const uint32_t f = uinfo[k];
-                        if (f & ITEM_ON) emit_url_v(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, false);
+                        if (f & ITEM_ON)
+                            u_url<PRETTY>(cs, P, XL, UrlItem{iv[j].a, iv[j].b}, (f & ITEM_FIRST) != 0, (f & ITEM_LAST) != 0);
                         ulen[f & 0xFFFFu] = (uint32_t)cs.n;
                     } else if (k < U + G) {
                         const uint32_t f = ginfo[k - (uint32_t)U];
-                        if (f & ITEM_ON) emit_tag_v(cs, P, XL, iv[j], false);
+                        if (f & ITEM_ON) u_tag<PRETTY>(cs, P, XL, iv[j], (f & ITEM_FIRST) != 0, (f & ITEM_LAST) != 0);
                         ulen[f & 0xFFFFu] = (uint32_t)cs.n;
                     }
                 }
@@ -1513,10 +1625,11 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             // the large records in record order (the tile holds the list here
             // for the flat layout, which has no hybrid blocks)
             uint32_t *big = NESTED ? sh_big : reinterpret_cast<uint32_t *>(tile);
-            isbig = live && rec_big<NESTED>(rv);
+            isbig = !PRETTY && live && rec_big<NESTED>(rv);
             if (live && !isbig) {
                 CountSink cs;
-                if (NESTED) {
+                if constexpr (PRETTY) pp_rec(cs, P, i, rv);
+                else if (NESTED) {
                     // (the url and tag items are measured by a helper thread below)
                     rec_head<NESTED>(cs, P, XG, i, rv);
                     if (rv.fl & PJ_PET_HAS_NAME) emit_strx(cs, XG, XG.name + (rv.na - XG.nb), rv.nb - rv.na, P.hexa);
@@ -1526,7 +1639,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 } else emit_rec<NESTED, true>(cs, P, XG, i, rv, ri);
                 len = cs.n;
             }
-            if constexpr (NESTED) {
+            if constexpr (NESTED && !PRETTY) {
                 // The url and tag items of ordinary record r are measured by
                 // thread HELP0 + r of the otherwise idle waves, alongside its
                 // own thread: each record's chain of global reads is split in
@@ -1577,7 +1690,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
         // whole workgroup writes straight to global memory.
         bool hyb = false;
         uint64_t spre = 0;
-        if (NESTED && !fast) {
+        if (NESTED && !PRETTY && !fast) {
             uint64_t stot;
             spre = block_excl_scan<BT>(isbig ? 0ull : len, sh_scan, &stot);
             hyb = stot + 32 <= TILE;
@@ -1601,13 +1714,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                 if (live) {
                     const uint32_t nu = ul1 - ul0, nt = gl1 - gl0;
                     LdsSink hs{tile, ulen[hidx], ulen[hidx + 1]};
-                    rec_head<NESTED>(hs, P, XL, i, rv);
+                    u_head<NESTED, PRETTY>(hs, P, XL, i, rv);
                     hs.finish();
                     LdsSink ms{tile, ulen[hidx + 2 + nu], ulen[hidx + 3 + nu]};
-                    rec_tags_open<NESTED>(ms, P, rv);
+                    u_tags_open<NESTED, PRETTY>(ms, P, rv);
                     ms.finish();
                     LdsSink ts{tile, ulen[hidx + 3 + nu + nt], ulen[hidx + 4 + nu + nt]};
-                    rec_tail(ts, P, i, rv);
+                    u_tail<PRETTY>(ts, P, i, rv);
                     ts.finish();
                 }
                 if (t >= (uint32_t)name0<R>() && t - name0<R>() < nrec) {
@@ -1617,12 +1730,12 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                     if ((f & PJ_PET_HAS_NAME) && sh_blen[r] > LN_MIN) {
                         // a long name: its body is left to the waves below
                         CountSink oc;
-                        rec_urls_open(oc, f, (f & 0x80u) != 0);
+                        u_urls_open<PRETTY>(oc, f, (f & 0x80u) != 0);
                         ns.put_byte('"');
                         ns.skip(u1 - u0 - 2 - (uint32_t)oc.n);
                         ns.put_byte('"');
-                        rec_urls_open(ns, f, (f & 0x80u) != 0);
-                    } else name_unit(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
+                        u_urls_open<PRETTY>(ns, f, (f & 0x80u) != 0);
+                    } else u_name<PRETTY>(ns, P, XL, XL.name + sh_bpre[r], sh_blen[r], f);
                     ns.finish();
                 }
 #pragma unroll
@@ -1634,13 +1747,13 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
                         const uint32_t f = uinfo[k], u = f & 0xFFFFu;
                         if (!(f & ITEM_ON)) continue;
                         LdsSink ls{tile, ulen[u], ulen[u + 1]};
-                        emit_url_v(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, (f & ITEM_LAST) != 0);
+                        u_url<PRETTY>(ls, P, XL, UrlItem{iv[j].a, iv[j].b}, (f & ITEM_FIRST) != 0, (f & ITEM_LAST) != 0);
                         ls.finish();
                     } else if (k < U + G) {
                         const uint32_t f = ginfo[k - (uint32_t)U], u = f & 0xFFFFu;
                         if (!(f & ITEM_ON)) continue;
                         LdsSink ls{tile, ulen[u], ulen[u + 1]};
-                        emit_tag_v(ls, P, XL, iv[j], (f & ITEM_LAST) != 0);
+                        u_tag<PRETTY>(ls, P, XL, iv[j], (f & ITEM_FIRST) != 0, (f & ITEM_LAST) != 0);
                         ls.finish();
                     }
                 }
@@ -1715,7 +1828,7 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             uint32_t *big = reinterpret_cast<uint32_t *>(tile), *bpre = big + R, *blen = bpre + R;
             if (t == 0) sh_nbig = 0;
             __syncthreads();
-            const bool fbig = live && rec_big<NESTED>(rv);
+            const bool fbig = !PRETTY && live && rec_big<NESTED>(rv);    // (pretty: every record one thread each)
             if (fbig) {
                 const uint32_t k = atomicAdd(&sh_nbig, 1u);
                 big[k] = t;
@@ -1726,7 +1839,8 @@ __global__ __launch_bounds__(BT, WPE) void k_encode(EncParams P) {
             if (live && !fbig && base + pre + len <= P.cap) {
                 WriteSink ws;
                 ws.init(P.out, base + pre, P.dummy + t);
-                emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
+                if constexpr (PRETTY) pp_rec(ws, P, i, rv);
+                else emit_rec<NESTED, true>(ws, P, XG, i, rv, ri);
                 ws.finish();
             }
             const uint32_t fnbig = sh_nbig;
@@ -2289,6 +2403,16 @@ hipError_t pj_launch_encode(const EncParams &P, bool nested, bool wide, hipStrea
                                  ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
     return launch_encode(pj::k_encode<false, ENC_FLAT_BT, ENC_FLAT_R, ENC_FLAT_TILE, ENC_FLAT_IN, 1, 1, ENC_FLAT_WPE>,
                              ENC_FLAT_BT, P, ENC_FLAT_R, false, st);
+}
+
+// Pretty output of nested records through the tile path: 64 records per
+// block (a pretty record is about 350 bytes), otherwise the nested shape.
+constexpr int ENC_PRETTY_TILE_R = 64;
+int pj_encode_pretty_tile_records() { return ENC_PRETTY_TILE_R; }
+hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st) {
+    return launch_encode(pj::k_encode<true, ENC_NEST_BT, ENC_PRETTY_TILE_R, ENC_NEST_TILE, ENC_NEST_IN, ENC_NEST_UCAP,
+                                      ENC_NEST_GCAP, ENC_NEST_WPE, true>,
+                         ENC_NEST_BT, P, ENC_PRETTY_TILE_R, true, st);
 }
 
 // k_enc_big: one workgroup per large record, as many workgroups as the GPU

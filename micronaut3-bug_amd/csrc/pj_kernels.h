@@ -161,6 +161,10 @@ hipError_t pj_launch_encode_big(const EncParams &P, bool full, hipStream_t st);
 int pj_encode_block_records(bool nested);
 // one thread per output record (pretty output, or a selection of records)
 hipError_t pj_launch_encode_rows(const EncParams &P, bool pretty, hipStream_t st);
+// pretty output of nested records through the tiled encode (blocks of
+// pj_encode_pretty_tile_records() records)
+hipError_t pj_launch_encode_pretty(const EncParams &P, hipStream_t st);
+int pj_encode_pretty_tile_records();
 // indices of the records whose status is in mask into sel, their count into *P.total
 hipError_t pj_launch_select_status(const EncParams &P, uint32_t mask, uint64_t *sel, hipStream_t st);
 uint64_t pj_select_blocks(uint64_t n);   // workgroups (look-back words) of the selection kernel
