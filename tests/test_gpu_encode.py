@@ -92,6 +92,26 @@ def test_encode_misaligned_string_columns(codec):
         assert gpu_encode(codec, c2, pj.FORMAT_ARRAY) == orc.encode(cols, pj.FORMAT_ARRAY)
 
 
+def test_encode_into_misaligned_output(codec):
+    """An output buffer that starts off 16-byte alignment: the tile copy-out's
+    whole-line stores then fall at unaligned addresses.  Only the output's
+    bytes change, nothing before or after them."""
+    for config, n, fmt in ((3, 20_000, pj.FORMAT_ARRAY), (2, 30_000, pj.FORMAT_NDJSON),
+                           (5, 6_000, pj.FORMAT_NDJSON), (3, 8_000, pj.FORMAT_PRETTY)):
+        cols = pj.generate(config, n)
+        ref = np.frombuffer(orc.encode(cols, fmt), np.uint8)
+        d = cols.to_device()
+        buf = torch.full((ref.size + 64,), 0xEE, dtype=torch.uint8, device="cuda")
+        for off in (1, 3, 8, 13):
+            print(f"[encode misaligned out] config={config} fmt={fmt} off={off}", flush=True)
+            buf.fill_(0xEE)
+            got = codec.encode(d, fmt, out=buf[off:off + ref.size])
+            assert got.numel() == ref.size
+            host = buf.cpu().numpy()
+            assert (host[:off] == 0xEE).all() and (host[off + ref.size:] == 0xEE).all(), (config, fmt, off)
+            assert np.array_equal(host[off:off + ref.size], ref), (config, fmt, off)
+
+
 def test_encode_long_strings_and_all_bytes(codec):
     big = bytes(range(256)) * 70 + b"x" * 3
     pets = [pet_from_dict({"name": "n", "photoUrls": []})]
